@@ -1,0 +1,132 @@
+"""gehtp_amd — GEHTP's runlist engine on MI355X (gfx950), from Python.
+
+The product is ``libgehtp.so`` (C ABI in ``include/``). This module loads it with
+ctypes and mirrors the reference's host interface (``wt_parse``, ``wt_exec_run*``,
+``wt_exec_temp*`` ...; reference ``kernels/include/oplist_exec.h``) so Python code
+and tests drive the same entry points a C caller would.
+
+Loading fails loudly when the library has not been built: there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+from . import abi
+from .abi import (WT_ERR, WtBlob, WtExecStats, WtOpTs, load_library, opcodes)
+
+__all__ = ["abi", "WtBlob", "WtExecStats", "WtOpTs", "Engine", "ParsedBlob",
+           "WtParseError", "WtExecError", "load_library", "opcodes", "lib_path"]
+
+lib_path = Path(__file__).resolve().parent / "libgehtp.so"
+
+
+class WtParseError(RuntimeError):
+    def __init__(self, rc: int, msg: str):
+        super().__init__(f"wt_parse: {msg} ({rc})")
+        self.rc = rc
+
+
+class WtExecError(RuntimeError):
+    def __init__(self, rc: int, msg: str):
+        super().__init__(f"wt_exec: rc={rc}: {msg}")
+        self.rc = rc
+
+
+class ParsedBlob:
+    """A parsed blob: owns the byte buffer the wt_blob's weight_base points into."""
+
+    def __init__(self, lib, data: bytes):
+        self._buf = C.create_string_buffer(bytes(data), len(data))
+        self.size = len(data)
+        self.blob = WtBlob()
+        rc = lib.wt_parse(C.cast(self._buf, C.POINTER(C.c_uint8)), C.c_size_t(len(data)),
+                          C.byref(self.blob))
+        if rc != 0:
+            raise WtParseError(rc, lib.wt_err_str(rc).decode())
+
+    @property
+    def n_ops(self) -> int:
+        return self.blob.n_ops
+
+    @property
+    def n_slots(self) -> int:
+        return self.blob.n_slots
+
+
+class Engine:
+    """Process-wide engine (the library keeps one global instance, like the reference)."""
+
+    def __init__(self, path: str | Path | None = None):
+        self.lib = load_library(path or lib_path)
+
+    def parse(self, data: bytes) -> ParsedBlob:
+        return ParsedBlob(self.lib, data)
+
+    def _check(self, rc: int, err) -> None:
+        if rc != 0:
+            raise WtExecError(rc, err.value.decode(errors="replace"))
+
+    def run(self, pb: ParsedBlob, first: int = 0, count: int | None = None, timing: bool = False):
+        """wt_exec_run / wt_exec_run_range. Returns (engine_m, op_us list or None)."""
+        count = pb.n_ops - first if count is None else count
+        err = C.create_string_buffer(512)
+        m = C.c_uint32(0)
+        us = (C.c_int64 * max(count, 1))() if timing else None
+        if first == 0 and count == pb.n_ops:
+            rc = self.lib.wt_exec_run(C.byref(pb.blob), C.byref(m), us, err, 512)
+        else:
+            rc = self.lib.wt_exec_run_range(C.byref(pb.blob), first, count, C.byref(m), us, err, 512)
+        self._check(rc, err)
+        return m.value, (list(us) if timing else None)
+
+    def run_io(self, pb: ParsedBlob, inp: bytes | None, out_temp: int, out_bytes: int | None = None,
+               timing: bool = False):
+        """wt_exec_run_io: returns (output bytes, op_us or None)."""
+        err = C.create_string_buffer(512)
+        m = C.c_uint32(0)
+        us = (C.c_int64 * max(pb.n_ops, 1))() if timing else None
+        ibuf = C.create_string_buffer(bytes(inp), len(inp)) if inp is not None else None
+        cap = out_bytes if out_bytes is not None else 64 << 20
+        obuf = C.create_string_buffer(cap)
+        rc = self.lib.wt_exec_run_io(C.byref(pb.blob), ibuf, obuf, out_temp, C.byref(m), us, err, 512)
+        self._check(rc, err)
+        n = self.lib.wt_exec_temp_last_bytes(out_temp)
+        if n > cap:
+            raise WtExecError(-1, f"output temp {out_temp} has {n} bytes > buffer {cap}")
+        return obuf.raw[:n], (list(us) if timing else None)
+
+    def temp(self, tid: int) -> bytes:
+        """Bytes last written to temp tid (host copy)."""
+        n = self.lib.wt_exec_temp_last_bytes(tid)
+        p = self.lib.wt_exec_temp(tid)
+        if not p:
+            raise KeyError(f"temp {tid} not allocated")
+        return C.string_at(p, n)
+
+    def temp_bytes(self, tid: int) -> int:
+        return self.lib.wt_exec_temp_bytes(tid)
+
+    def temp_last_bytes(self, tid: int) -> int:
+        return self.lib.wt_exec_temp_last_bytes(tid)
+
+    def stats(self) -> WtExecStats:
+        st = WtExecStats()
+        self.lib.wt_exec_get_stats(C.byref(st))
+        return st
+
+    def shutdown(self) -> None:
+        self.lib.wt_exec_shutdown()
+
+    def state_reset(self) -> None:
+        self.lib.wt_exec_state_reset()
+
+    def set_ext_weights(self, buf) -> None:
+        self._ext = buf
+        self.lib.wt_exec_set_ext_weights(buf)
+
+    def set_trace(self, on: bool) -> None:
+        self.lib.wt_exec_set_trace(1 if on else 0)
+
+
+WT_ERR = WT_ERR

@@ -1,0 +1,119 @@
+// capi.cpp — kernel-level C entry points (include/gehtp_kernels.h).
+// Shapes and alignment are checked here so every launch stays inside its buffers.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "gehtp_kernels.h"
+#include "kernels.h"
+
+using namespace gehtp;
+
+namespace {
+
+inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+inline int rc(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline const __half* H(const void* p) { return static_cast<const __half*>(p); }
+inline __half* Hm(void* p) { return static_cast<__half*>(p); }
+
+bool w4g_args_ok(const void* x, uint32_t ldx, const void* wq, const void* ws, const void* y,
+                 uint32_t ldy, uint32_t N, uint32_t K) {
+    return x && wq && ws && y && K && K % 64 == 0 && ldx >= K && ldx % 8 == 0 && ldy >= N &&
+           al16(x) && al16(wq) && ((reinterpret_cast<uintptr_t>(ws) & 1u) == 0);
+}
+
+}  // namespace
+
+extern "C" {
+
+int gehtp_w4g_gemv(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y, uint32_t ldy,
+                   uint32_t M, uint32_t N, uint32_t K, void* stream) {
+    if (!w4g_args_ok(x, ldx, wq, ws, y, ldy, N, K) || M > kW4gGemvMaxM) return GEHTP_EINVAL;
+    return rc(launch_w4g_gemv(H(x), ldx, static_cast<const uint8_t*>(wq), H(ws), Hm(y), ldy, M, N, K, S(stream)));
+}
+
+int gehtp_w4g_gemm(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y, uint32_t ldy,
+                   uint32_t M, uint32_t N, uint32_t K, void* stream) {
+    if (!w4g_args_ok(x, ldx, wq, ws, y, ldy, N, K)) return GEHTP_EINVAL;
+    return rc(launch_w4g_gemm(H(x), ldx, static_cast<const uint8_t*>(wq), H(ws), Hm(y), ldy, M, N, K, S(stream)));
+}
+
+int gehtp_w4g_matmul(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y, uint32_t ldy,
+                     uint32_t M, uint32_t N, uint32_t K, void* stream) {
+    return M <= kW4gGemvMaxM ? gehtp_w4g_gemv(x, ldx, wq, ws, y, ldy, M, N, K, stream)
+                             : gehtp_w4g_gemm(x, ldx, wq, ws, y, ldy, M, N, K, stream);
+}
+
+int gehtp_w4g_dequant(const void* wq, const void* ws, void* w, uint32_t N, uint32_t K, void* stream) {
+    if (!wq || !ws || !w || K % 64 || !al16(wq) || !al16(w)) return GEHTP_EINVAL;
+    return rc(launch_w4g_dequant(static_cast<const uint8_t*>(wq), H(ws), Hm(w), N, K, S(stream)));
+}
+
+int gehtp_matmul_f16(const void* a, const void* w, void* y, uint32_t M, uint32_t K, uint32_t N_full,
+                     uint32_t n0, uint32_t N, uint32_t flags, void* stream) {
+    if (!a || !w || !y || (uint64_t)n0 + N > N_full) return GEHTP_EINVAL;
+    uint32_t Bn = flags >> 16;
+    if (!Bn || !(flags & 4u)) Bn = 1;
+    return rc(launch_matmul_f16(H(a), H(w), Hm(y), M, K, N_full, n0, N, flags & 1u, flags & 2u, Bn, S(stream)));
+}
+
+int gehtp_rmsnorm2(const void* x, const void* gamma, const void* beta, void* y, uint32_t rows, uint32_t rw,
+                   void* stream) {
+    if (!x || !gamma || !y || !rw || (rw % 8 == 0 && !al16(x))) return GEHTP_EINVAL;
+    return rc(launch_rmsnorm2(H(x), H(gamma), H(beta), Hm(y), rows, rw, S(stream)));
+}
+
+int gehtp_softmax(const void* x, void* y, uint32_t rows, uint32_t n, void* stream) {
+    if (!x || !y) return GEHTP_EINVAL;
+    return rc(launch_softmax(H(x), Hm(y), rows, n, S(stream)));
+}
+
+int gehtp_attn_prefill(const void* q, const void* k, const void* v, void* out, uint32_t S_, uint32_t Hh,
+                       uint32_t KVH, uint32_t hd, float scale, int causal, void* stream) {
+    if (!q || !k || !v || !out || hd != 128 || !KVH || Hh % KVH || !al16(q) || !al16(k) || !al16(v) ||
+        (reinterpret_cast<uintptr_t>(out) & 7u))
+        return GEHTP_EINVAL;
+    return rc(launch_attn_prefill(H(q), Hh * hd, H(k), H(v), KVH * hd, Hm(out), Hh * hd, S_, Hh, KVH, hd, scale,
+                                  causal != 0, S(stream)));
+}
+
+uint32_t gehtp_attn_decode_work_floats(uint32_t n_kv, uint32_t Hh, uint32_t hd) {
+    return attn_decode_work_floats(n_kv, Hh, hd);
+}
+
+int gehtp_attn_decode(const void* q, const void* ring, uint32_t state_bytes, void* out, uint32_t n_kv,
+                      uint32_t Hh, uint32_t KVH, uint32_t hd, float scale, void* work, uint32_t work_floats,
+                      void* stream) {
+    const uint32_t slot_bytes = KVH * hd * 4u;
+    if (!q || !ring || !out || !work || hd != 128 || !KVH || Hh % KVH || !slot_bytes ||
+        state_bytes % slot_bytes || !al16(q) || !al16(ring))
+        return GEHTP_EINVAL;
+    const uint32_t nslots = state_bytes / slot_bytes;
+    if (!n_kv || n_kv > nslots) return GEHTP_EINVAL;
+    return rc(launch_attn_decode(H(q), static_cast<const uint8_t*>(ring), slot_bytes, nslots, Hm(out), n_kv,
+                                 nullptr, Hh, KVH, hd, scale, static_cast<float*>(work), work_floats, S(stream)));
+}
+
+int gehtp_kv_append(void* ring, uint32_t state_bytes, const void* k, const void* v, uint32_t kv_elems,
+                    uint32_t n_tok, uint32_t pos, void* stream) {
+    const uint32_t slot_bytes = kv_elems * 4u;
+    if (!ring || !k || !v || !kv_elems || state_bytes % slot_bytes || pos == 0xFFFFFFFFu) return GEHTP_EINVAL;
+    return rc(launch_kv_append_n(static_cast<uint8_t*>(ring), slot_bytes, state_bytes / slot_bytes, H(k), H(v),
+                                 kv_elems, n_tok, pos, nullptr, S(stream)));
+}
+
+int gehtp_rope(const void* x, void* y, uint32_t n_tok, uint32_t n_heads, uint32_t hd, uint32_t pos0,
+               float theta, uint32_t row_stride, void* stream) {
+    if (!x || !y || !hd || hd % 2 || row_stride < n_heads * hd) return GEHTP_EINVAL;
+    return rc(launch_rope(H(x), Hm(y), n_tok, n_heads, hd, pos0, nullptr, theta, row_stride, S(stream)));
+}
+
+int gehtp_argmax(const void* x, uint32_t n, void* out, void* stream) {
+    if (!x || !out) return GEHTP_EINVAL;
+    return rc(launch_argmax(H(x), n, static_cast<int32_t*>(out), S(stream)));
+}
+
+const char* gehtp_version(void) { return "gehtp-gfx950 0.1"; }
+
+}  // extern "C"

@@ -1,0 +1,1059 @@
+// engine.cpp — the runlist engine: GEHTP's wt_exec_* ABI on one HIP device.
+//
+// Structure follows the reference engine (kernels/src/runtime/oplist_exec.c): a
+// process-wide singleton, temps addressed by id, the TEMPOFF static plan with a
+// bump fallback, persistent states, EXT_IN / EXT_WGT slots, and table dispatch by
+// opcode. What differs is where data lives and who computes:
+//   - the blob's weight region (and the external weight image) is copied to HBM
+//     once per blob; temps, states and the "VTCM" pool are HBM allocations;
+//   - each op enqueues gfx950 kernels on the engine stream; a run drains the stream
+//     before returning; there is no CPU compute path for any op;
+//   - KV ring bookkeeping (positions, counters) is mirrored on the host for the
+//     reference's hard-error checks, and on the device so kernels read positions.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "oplist_exec.h"
+#include "oplist_parse.h"
+
+namespace gehtp {
+
+int device_cu_count() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
+}  // namespace gehtp
+
+using namespace gehtp;
+
+namespace {
+
+constexpr uint32_t kMaxTemps = WT_EXEC_MAX_TEMPS;
+constexpr uint32_t kNone = 0xFFFFFFFFu;
+
+struct State {
+    uint8_t* dev = nullptr;
+    uint32_t bytes = 0;
+    uint32_t count = 0;            // host mirror of the auto-position counter
+    bool kv_ready = false;
+    uint32_t slot_bytes = 0, nslots = 0;
+    std::vector<uint32_t> posmap;  // slot -> absolute position (kNone = empty)
+};
+
+struct Engine {
+    bool ready = false;
+    hipStream_t stream = nullptr;
+
+    uint8_t* temps[kMaxTemps] = {};
+    uint32_t temp_bytes[kMaxTemps] = {};
+    uint32_t last_bytes[kMaxTemps] = {};
+    std::vector<uint8_t> mirror[kMaxTemps];
+
+    uint8_t* pool = nullptr;
+    uint32_t pool_cap = 0, pool_used = 0;
+    bool pool_owned = false;
+    std::vector<void*> retired_pools;   // earlier bump pools stay valid until shutdown
+    const uint32_t* static_offsets = nullptr;
+    uint32_t static_off_arr[kMaxTemps];
+    uint8_t* vtcm_pool = nullptr;
+    uint32_t vtcm_pool_size = 0;
+    uint32_t vtcm_off_arr[kMaxTemps];
+
+    uint32_t n_states = 0;
+    State st[WT_MAX_STATES];
+    bool states_loaded = false;
+    uint32_t* counters_dev = nullptr;   // one auto-position counter per state
+
+    // Device copy of the blob's weight region and its identity.
+    uint8_t* w_dev = nullptr;
+    size_t w_cap = 0;
+    uint64_t w_key = 0;
+    // External weight image.
+    const uint8_t* ext_host = nullptr;
+    uint8_t* ext_dev = nullptr;
+    size_t ext_cap = 0;
+    uint64_t ext_key = 0;
+    // Injected input for EXT_IN slots.
+    uint8_t* in_dev = nullptr;
+    size_t in_cap = 0;
+    bool in_active = false;
+
+    float* attn_work = nullptr;
+    uint32_t attn_work_floats = 0;
+
+    wt_exec_stats stats{};
+    wt_op_ts* ts = nullptr;
+    uint32_t ts_cap = 0;
+    bool trace = false;
+    const char* hook = nullptr;
+    std::vector<hipEvent_t> events;
+
+    Engine() {
+        std::fill(std::begin(static_off_arr), std::end(static_off_arr), kNone);
+        std::fill(std::begin(vtcm_off_arr), std::end(vtcm_off_arr), kNone);
+    }
+};
+
+Engine g;
+
+#define ERR(...) (std::snprintf(err, errn, __VA_ARGS__), -1)
+
+int ensure_ready(char* err, size_t errn) {
+    if (g.ready) return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return ERR("no HIP device visible");
+    if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess)
+        return ERR("hipStreamCreate failed");
+    if (hipMalloc(&g.counters_dev, WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
+        return ERR("counter alloc failed");
+    if (hipMemset(g.counters_dev, 0, WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
+        return ERR("counter clear failed");
+    g.ready = true;
+    return 0;
+}
+
+// 64-bit FNV-1a over a byte range.
+uint64_t fnv(uint64_t h, const void* p, size_t n) {
+    const uint8_t* b = static_cast<const uint8_t*>(p);
+    for (size_t i = 0; i < n; ++i) { h ^= b[i]; h *= 0x100000001b3ull; }
+    return h;
+}
+
+// Identity of a host byte image: pointer, size and sampled content (64 evenly spaced
+// 1 KiB windows plus the whole image when it is small), so a new blob that reuses an
+// old buffer address is still recognised as new.
+uint64_t image_key(const uint8_t* p, size_t n) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    h = fnv(h, &p, sizeof p);
+    h = fnv(h, &n, sizeof n);
+    if (n <= (4u << 20)) return fnv(h, p, n);
+    for (int i = 0; i < 64; ++i) {
+        const size_t off = (n - 1024) / 63 * (size_t)i;
+        h = fnv(h, p + off, 1024);
+    }
+    return h;
+}
+
+int upload(uint8_t** dev, size_t* cap, const uint8_t* host, size_t bytes, char* err, size_t errn) {
+    if (bytes > *cap) {
+        if (*dev) hipFree(*dev);
+        *dev = nullptr;
+        *cap = 0;
+        if (hipMalloc(reinterpret_cast<void**>(dev), bytes) != hipSuccess)
+            return ERR("device alloc of %zu bytes failed", bytes);
+        *cap = bytes;
+    }
+    if (bytes && hipMemcpy(*dev, host, bytes, hipMemcpyHostToDevice) != hipSuccess)
+        return ERR("weight upload failed");
+    return 0;
+}
+
+int ensure_weights(const wt_blob* b, char* err, size_t errn) {
+    uint64_t key = image_key(b->weight_base, b->weight_bytes);
+    key = fnv(key, b->slots, sizeof(wt_slot) * b->n_slots);
+    if (key != g.w_key || !g.w_dev) {
+        if (upload(&g.w_dev, &g.w_cap, b->weight_base, std::max<size_t>(b->weight_bytes, 16), err, errn))
+            return -1;
+        g.w_key = key;
+    }
+    size_t ext_need = 0;
+    for (uint32_t i = 0; i < b->n_slots; ++i)
+        if (b->slots[i].addr == WT_SLOT_EXT_WGT)
+            ext_need = std::max<size_t>(ext_need, b->slots[i].offset + b->slots[i].len);
+    if (ext_need && g.ext_host) {
+        const uint64_t ek = image_key(g.ext_host, ext_need);
+        if (ek != g.ext_key || !g.ext_dev) {
+            if (upload(&g.ext_dev, &g.ext_cap, g.ext_host, ext_need, err, errn)) return -1;
+            g.ext_key = ek;
+        }
+    }
+    return 0;
+}
+
+// ---- reference decoding (oplist_exec.c:175-213), returning DEVICE pointers ----
+uint8_t* slot_ptr(const wt_blob* b, uint32_t s) {
+    if (s >= b->n_slots) return nullptr;
+    const wt_slot& sl = b->slots[s];
+    if (sl.addr == WT_SLOT_EXT_IN && g.in_active) return g.in_dev;
+    if (sl.addr == WT_SLOT_EXT_WGT) return (g.ext_dev && g.ext_host) ? g.ext_dev + sl.offset : nullptr;
+    return g.w_dev + sl.offset;
+}
+
+uint8_t* ref_ptr(const wt_blob* b, uint32_t arg) {
+    if (arg & 0x8000u) return slot_ptr(b, arg & 0x7FFFu);
+    if ((arg & 0xE000u) == WT_REF_STATE_FLAG) {
+        const uint32_t s = arg & 0x1FFFu;
+        return s < g.n_states ? g.st[s].dev : nullptr;
+    }
+    if (arg & 0x4000u) {
+        const uint32_t t = arg & 0x3FFFu;
+        if (t < kMaxTemps && g.vtcm_pool && g.vtcm_off_arr[t] != kNone) return g.vtcm_pool + g.vtcm_off_arr[t];
+        return nullptr;
+    }
+    return arg < kMaxTemps ? g.temps[arg] : nullptr;
+}
+
+// f16 element count of a reference (oplist_exec.c:221-225).
+uint32_t ref_elem_count(const wt_blob* b, uint32_t arg) {
+    if (arg & 0x8000u) {
+        const uint32_t s = arg & 0x7FFFu;
+        return s < b->n_slots ? b->slots[s].count : 0;
+    }
+    if (arg & 0x4000u) return 0;
+    return arg < kMaxTemps ? g.last_bytes[arg] / 2u : 0;
+}
+
+// Byte capacity behind a reference, when known (0 = unknown).
+size_t ref_bytes(const wt_blob* b, uint32_t arg) {
+    if (arg & 0x8000u) {
+        const uint32_t s = arg & 0x7FFFu;
+        return s < b->n_slots ? b->slots[s].len : 0;
+    }
+    if ((arg & 0xE000u) == WT_REF_STATE_FLAG) {
+        const uint32_t s = arg & 0x1FFFu;
+        return s < g.n_states ? g.st[s].bytes : 0;
+    }
+    if (arg & 0x4000u) return 0;
+    return arg < kMaxTemps ? g.temp_bytes[arg] : 0;
+}
+
+// Temp allocation (oplist_exec.c:257-335): VTCM-plan temps, static-plan temps, then
+// a 128-byte aligned bump that only grows; earlier pools are kept alive.
+uint8_t* temp_get(uint32_t id, uint32_t bytes) {
+    if (id >= kMaxTemps) return nullptr;
+    if (g.vtcm_off_arr[id] != kNone) {
+        const uint32_t off = g.vtcm_off_arr[id];
+        if (!g.vtcm_pool || (uint64_t)off + bytes > g.vtcm_pool_size) return nullptr;
+        g.temps[id] = g.vtcm_pool + off;
+        g.temp_bytes[id] = bytes;
+        g.last_bytes[id] = bytes;
+        return g.temps[id];
+    }
+    if (g.static_offsets && g.pool) {
+        const uint32_t off = g.static_offsets[id];
+        if (off != kNone) {
+            if ((uint64_t)off + bytes > g.pool_used) return nullptr;
+            g.temps[id] = g.pool + off;
+            g.temp_bytes[id] = bytes;
+            g.last_bytes[id] = bytes;
+            return g.temps[id];
+        }
+    }
+    if (!g.temps[id] || g.temp_bytes[id] < bytes) {
+        const uint32_t aligned = (bytes + 127u) & ~127u;
+        if ((uint64_t)g.pool_used + aligned > g.pool_cap) {
+            if (g.static_offsets) return nullptr;   // static plan: reserve exhausted
+            uint64_t ncap = g.pool_cap ? g.pool_cap : (64u << 20);
+            while (ncap < (uint64_t)g.pool_used + aligned) ncap *= 2;
+            if (ncap > 0xFFFFFFFFull) return nullptr;
+            void* np = nullptr;
+            if (hipMalloc(&np, ncap) != hipSuccess) return nullptr;
+            if (g.pool && g.pool_owned) g.retired_pools.push_back(g.pool);
+            g.pool = static_cast<uint8_t*>(np);
+            g.pool_cap = (uint32_t)ncap;
+            g.pool_used = 0;
+            g.pool_owned = true;
+        }
+        g.temps[id] = g.pool + g.pool_used;
+        g.pool_used += aligned;
+        g.temp_bytes[id] = bytes;
+    }
+    g.last_bytes[id] = bytes;
+    return g.temps[id];
+}
+
+// TEMPOFF slot (oplist_exec.c:2012-2066): [cap][reserve: lo16 bump KB | hi16 VTCM KB][n][n x {tid,off,size}].
+int load_tempoff(const wt_blob* b, char* err, size_t errn) {
+    if (g.static_offsets) return 0;
+    std::fill(std::begin(g.static_off_arr), std::end(g.static_off_arr), kNone);
+    std::fill(std::begin(g.vtcm_off_arr), std::end(g.vtcm_off_arr), kNone);
+    for (uint32_t s = 0; s < b->n_slots; ++s) {
+        if (b->slots[s].addr != WT_SLOT_TEMPOFF) continue;
+        const uint8_t* p = b->weight_base + b->slots[s].offset;
+        const uint32_t len = b->slots[s].len;
+        if (len < 12u) return ERR("tempoff slot short");
+        uint32_t cap, reserve, n;
+        std::memcpy(&cap, p, 4);
+        std::memcpy(&reserve, p + 4, 4);
+        std::memcpy(&n, p + 8, 4);
+        if ((uint64_t)len < 12u + (uint64_t)n * 12u) return ERR("tempoff table short");
+        if (cap == 0 || cap > 0x80000000u) return ERR("tempoff cap bad");
+        const uint32_t vtcm_cap = (reserve >> 16) * 1024u;
+        reserve = (reserve & 0xFFFFu) * 1024u;
+        uint32_t tmp_static[kMaxTemps], tmp_vtcm[kMaxTemps];
+        std::fill(std::begin(tmp_static), std::end(tmp_static), kNone);
+        std::fill(std::begin(tmp_vtcm), std::end(tmp_vtcm), kNone);
+        for (uint32_t i = 0; i < n; ++i) {
+            uint32_t tid, off, sz;
+            std::memcpy(&tid, p + 12 + 12 * i, 4);
+            std::memcpy(&off, p + 16 + 12 * i, 4);
+            std::memcpy(&sz, p + 20 + 12 * i, 4);
+            const uint32_t t = tid & 0x3FFFu;
+            if (t >= kMaxTemps) return ERR("tempoff tid bad %u", t);
+            if (tid & WT_REF_VTCM_FLAG) {
+                if (vtcm_cap == 0 || (uint64_t)off + sz > vtcm_cap)
+                    return ERR("tempoff vtcm entry bad (tid %u off %u sz %u vtcm_cap %u)", t, off, sz, vtcm_cap);
+                tmp_vtcm[t] = off;
+            } else {
+                if ((uint64_t)off + sz > cap)
+                    return ERR("tempoff entry bad (tid %u off %u sz %u cap %u)", t, off, sz, cap);
+                tmp_static[t] = off;
+            }
+        }
+        void* pool = nullptr;
+        if (hipMalloc(&pool, (size_t)cap + reserve) != hipSuccess) return ERR("tempoff pool alloc");
+        if (g.pool && g.pool_owned) g.retired_pools.push_back(g.pool);
+        std::memcpy(g.static_off_arr, tmp_static, sizeof tmp_static);
+        std::memcpy(g.vtcm_off_arr, tmp_vtcm, sizeof tmp_vtcm);
+        g.pool = static_cast<uint8_t*>(pool);
+        g.pool_cap = cap + reserve;
+        g.pool_used = cap;
+        g.pool_owned = true;
+        g.static_offsets = g.static_off_arr;
+        if (vtcm_cap) {
+            void* vp = nullptr;
+            if (hipMalloc(&vp, vtcm_cap) != hipSuccess) return ERR("vtcm pool alloc");
+            g.vtcm_pool = static_cast<uint8_t*>(vp);
+            g.vtcm_pool_size = vtcm_cap;
+        }
+        break;
+    }
+    return 0;
+}
+
+// STATE slot (oplist_exec.c:2071-2102): [n][n x bytes], zeroed, process lifetime.
+int load_states(const wt_blob* b, char* err, size_t errn) {
+    if (g.states_loaded) return 0;
+    for (uint32_t s = 0; s < b->n_slots; ++s) {
+        if (b->slots[s].addr != WT_SLOT_STATE) continue;
+        const uint8_t* p = b->weight_base + b->slots[s].offset;
+        const uint32_t len = b->slots[s].len;
+        if (len < 4u) return ERR("state slot short");
+        uint32_t n;
+        std::memcpy(&n, p, 4);
+        if (n == 0 || n > WT_MAX_STATES || len < 4u + n * 4u)
+            return ERR("state slot table bad (n=%u len=%u)", n, len);
+        for (uint32_t i = 0; i < n; ++i) {
+            uint32_t bytes;
+            std::memcpy(&bytes, p + 4 + 4 * i, 4);
+            if (bytes == 0 || bytes > (1u << 30)) return ERR("state %u bytes bad %u", i, bytes);
+            void* d = nullptr;
+            if (hipMalloc(&d, bytes) != hipSuccess) return ERR("state %u alloc %u", i, bytes);
+            if (hipMemset(d, 0, bytes) != hipSuccess) return ERR("state %u clear", i);
+            g.st[i] = State{};
+            g.st[i].dev = static_cast<uint8_t*>(d);
+            g.st[i].bytes = bytes;
+        }
+        g.n_states = n;
+        break;
+    }
+    g.states_loaded = true;
+    return 0;
+}
+
+// KV geometry from the op's shape (oplist_exec.c:2119-2151).
+State* state_kv(uint32_t ref, uint32_t kv_elems, char* err, size_t errn) {
+    if ((ref & 0xE000u) != WT_REF_STATE_FLAG) {
+        std::snprintf(err, errn, "kv state_ref not 0x6000|idx (0x%X)", ref);
+        return nullptr;
+    }
+    const uint32_t i = ref & 0x1FFFu;
+    if (i >= g.n_states) { std::snprintf(err, errn, "kv state idx %u oob", i); return nullptr; }
+    State& s = g.st[i];
+    const uint32_t slot_bytes = kv_elems * 4u;
+    if (!s.kv_ready) {
+        if (slot_bytes < 256u || (slot_bytes & 127u) || s.bytes % slot_bytes) {
+            std::snprintf(err, errn, "kv state %u geometry bad (slot=%u total=%u)", i, slot_bytes, s.bytes);
+            return nullptr;
+        }
+        s.slot_bytes = slot_bytes;
+        s.nslots = s.bytes / slot_bytes;
+        s.posmap.assign(s.nslots, kNone);
+        s.kv_ready = true;
+    } else if (s.slot_bytes != slot_bytes) {
+        std::snprintf(err, errn, "kv state %u slot_bytes mismatch (%u vs %u)", i, s.slot_bytes, slot_bytes);
+        return nullptr;
+    }
+    return &s;
+}
+
+// Host-side lookup check for positions [0, n_kv) (kvcache.c:64-68): a miss is a hard error.
+int kv_check(const State& s, uint32_t n_kv, char* err, size_t errn) {
+    for (uint32_t p = 0; p < n_kv; ++p)
+        if (s.posmap[p % s.nslots] != p) return ERR("kv gather miss pos %u (state bug)", p);
+    return 0;
+}
+
+float f32_from_bits(uint32_t u) {
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// ---- op implementations ----
+struct Ctx {
+    const wt_blob* b;
+    const wt_op* op;
+    uint32_t* engine_m;
+    char* err;
+    size_t errn;
+};
+
+#define CHECK_LAUNCH(expr)                                                             \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess) return ERR("launch failed: %s", hipGetErrorString(e_));  \
+    } while (0)
+
+#define A(i) (cx.op->args[i])
+
+int op_nop(Ctx& cx) { (void)cx; g.stats.nop++; return 0; }
+
+int op_pin(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    if (A(0) >= cx.b->n_slots) return ERR("pin slot oob");
+    // Weights are resident in HBM from the first run: pinning is bookkeeping only.
+    g.stats.pin++;
+    g.stats.pin_skipped++;
+    return 0;
+}
+
+int op_matmul_f16(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const bool split = cx.op->opcode == OP_MATMUL_F16_SPLIT;
+    const uint32_t M = A(3), K = A(4);
+    const uint32_t N_full = A(5), n0 = split ? A(6) : 0, N = split ? A(7) : A(5);
+    const uint32_t flags = split ? A(8) : A(6);
+    uint32_t Bn = flags >> 16;
+    if (!Bn) Bn = 1;
+    const bool t0 = flags & 1u, t1 = flags & 2u, batched = flags & 4u;
+    if (!batched) Bn = 1;
+    if ((uint64_t)n0 + N > N_full) return ERR("matmul_f16 chunk [%u,+%u) beyond N_full %u", n0, N, N_full);
+    const __half* a = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const __half* w = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(1)));
+    const uint64_t ybytes = (uint64_t)M * N_full * Bn * 2u;
+    if (ybytes > 0xFFFFFFFFull) return ERR("matmul_f16 output too large");
+    // SPLIT chunks share the output temp: keep earlier chunks' columns.
+    __half* y = reinterpret_cast<__half*>(temp_get(A(2), (uint32_t)ybytes));
+    if (!a || !w || !y) return ERR("matmul_f16 ref fail");
+    const size_t abytes = ref_bytes(cx.b, A(0)), wbytes = ref_bytes(cx.b, A(1));
+    if (abytes && abytes < (uint64_t)M * K * Bn * 2u) return ERR("matmul_f16 a smaller than M*K");
+    if (wbytes && wbytes < (uint64_t)K * N_full * Bn * 2u) return ERR("matmul_f16 w smaller than K*N");
+    CHECK_LAUNCH(launch_matmul_f16(a, w, y, M, K, N_full, n0, N, t0, t1, Bn, g.stream));
+    return 0;
+}
+
+int op_matmul_w4g(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t M = A(4), K = A(5), N = A(6), group = A(7), flags = A(8);
+    if (group != 64) return ERR("w4g group %u unsupported (64 only)", group);
+    if (!(flags & 2u) || (flags & 0xFFFDu)) return ERR("w4g flags 0x%X unsupported (need t1)", flags);
+    if (K == 0 || K % 64) return ERR("w4g K=%u not a multiple of 64", K);
+    const uint32_t ldy = (flags >> 16) ? (flags >> 16) : N;
+    if (ldy < N) return ERR("w4g output stride %u < N %u", ldy, N);
+    const __half* a = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const uint8_t* wq = ref_ptr(cx.b, A(1));
+    const __half* ws = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(2)));
+    const uint64_t ybytes = ((uint64_t)(M ? M - 1 : 0) * ldy + N) * 2u;
+    __half* y = reinterpret_cast<__half*>(temp_get(A(3), (uint32_t)ybytes));
+    if (!a || !wq || !ws || !y) return ERR("w4g ref fail");
+    const size_t ab = ref_bytes(cx.b, A(0)), qb = ref_bytes(cx.b, A(1)), sb = ref_bytes(cx.b, A(2));
+    if (ab && ab < (uint64_t)M * K * 2u) return ERR("w4g activation smaller than M*K");
+    if (qb && qb < (uint64_t)N * K / 2u) return ERR("w4g weight slot %zu < N*K/2", qb);
+    if (sb && sb < (uint64_t)N * (K / 64) * 2u) return ERR("w4g scale slot %zu < N*K/64*2", sb);
+    if (((uintptr_t)a | (uintptr_t)wq) % 16) return ERR("w4g operands not 16-byte aligned");
+    g.stats.matmul++;
+    *cx.engine_m = M;
+    if (M <= kW4gGemvMaxM)
+        CHECK_LAUNCH(launch_w4g_gemv(a, K, wq, ws, y, ldy, M, N, K, g.stream));
+    else
+        CHECK_LAUNCH(launch_w4g_gemm(a, K, wq, ws, y, ldy, M, N, K, g.stream));
+    return 0;
+}
+
+int op_rmsnorm2(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t w_s = A(1) & 0x7FFFu, b_s = A(2) & 0x7FFFu, n = A(4);
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const __half* gw = reinterpret_cast<const __half*>(slot_ptr(cx.b, w_s));
+    const __half* bv = reinterpret_cast<const __half*>(slot_ptr(cx.b, b_s));
+    __half* y = reinterpret_cast<__half*>(temp_get(A(3), n * 2u));
+    if (!x || !gw || !y) return ERR("rmsnorm2 ref fail");
+    const uint32_t rw = cx.b->slots[w_s].len / 2u;
+    if (rw == 0 || n % rw) return ERR("rmsnorm2 shape n%u rw%u", n, rw);
+    if (bv && cx.b->slots[b_s].len < rw * 2u) return ERR("rmsnorm2 bias slot shorter than row");
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < (uint64_t)n * 2u) return ERR("rmsnorm2 input smaller than n");
+    g.stats.rmsnorm++;
+    CHECK_LAUNCH(launch_rmsnorm2(x, gw, bv, y, n / rw, rw, g.stream));
+    return 0;
+}
+
+int op_softmax(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t rows = A(2), n = A(3);
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    __half* y = reinterpret_cast<__half*>(temp_get(A(1), rows * n * 2u));
+    if (!x || !y) return ERR("softmax ref fail");
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < (uint64_t)rows * n * 2u) return ERR("softmax input smaller than rows*n");
+    CHECK_LAUNCH(launch_softmax(x, y, rows, n, g.stream));
+    return 0;
+}
+
+int op_binary(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    if (A(4) == 8) {   // SELECT [c, t, f, out, 8]
+        const __half* c = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+        const __half* t = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(1)));
+        const __half* f = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(2)));
+        const uint32_t cn = ref_elem_count(cx.b, A(0)), tn = ref_elem_count(cx.b, A(1));
+        const uint32_t fn = ref_elem_count(cx.b, A(2));
+        const uint32_t n = std::max(std::max(cn, tn), fn);
+        __half* y = reinterpret_cast<__half*>(temp_get(A(3), n * 2u));
+        if (!c || !t || !f || !y || n == 0) return ERR("select ref fail");
+        CHECK_LAUNCH(launch_select(c, cn, t, tn, f, fn, y, n, g.stream));
+        return 0;
+    }
+    const uint32_t n = A(3), sub = A(4);
+    const __half* a = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const __half* bb = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(1)));
+    __half* y = reinterpret_cast<__half*>(temp_get(A(2), n * 2u));
+    if (!a || !bb || !y) return ERR("binary ref fail");
+    const size_t ab = ref_bytes(cx.b, A(0)), bbytes = ref_bytes(cx.b, A(1));
+    if ((ab && ab < (uint64_t)n * 2u) || (bbytes && bbytes < (uint64_t)n * 2u))
+        return ERR("binary operand smaller than n");
+    CHECK_LAUNCH(launch_binary(a, bb, y, n, sub, g.stream));
+    return 0;
+}
+
+int op_add(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n = A(3);
+    const __half* a = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const __half* bb = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(1)));
+    __half* y = reinterpret_cast<__half*>(temp_get(A(2), n * 2u));
+    if (!a || !bb) return ERR("add ref empty");
+    if (!y) return ERR("add temp alloc");
+    const size_t ab = ref_bytes(cx.b, A(0)), bbytes = ref_bytes(cx.b, A(1));
+    if ((ab && ab < (uint64_t)n * 2u) || (bbytes && bbytes < (uint64_t)n * 2u))
+        return ERR("add operand smaller than n");
+    g.stats.add++;
+    CHECK_LAUNCH(launch_binary(a, bb, y, n, 0, g.stream));
+    return 0;
+}
+
+int op_unary(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n = A(2), sub = A(3);
+    if (sub > 16) return ERR("unary unknown subtype %u", sub);
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    __half* y = reinterpret_cast<__half*>(temp_get(A(1), n * 2u));
+    if (!x || !y) return ERR("unary ref fail");
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < (uint64_t)n * 2u) return ERR("unary input smaller than n");
+    CHECK_LAUNCH(launch_unary(x, y, n, sub, g.stream));
+    return 0;
+}
+
+int op_silu(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t x_t = A(0), n = A(2);
+    if (x_t >= kMaxTemps || !g.temps[x_t]) return ERR("silu src temp %u empty", x_t);
+    if (g.temp_bytes[x_t] != n * 2u)
+        return ERR("silu n_elem mismatch (%u vs face %u)", n, g.temp_bytes[x_t] / 2u);
+    __half* y = reinterpret_cast<__half*>(temp_get(A(1), n * 2u));
+    if (!y) return ERR("silu temp %u alloc", A(1));
+    g.stats.silu++;
+    CHECK_LAUNCH(launch_unary(reinterpret_cast<const __half*>(g.temps[x_t]), y, n, 12, g.stream));
+    return 0;
+}
+
+int op_argmax(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n = A(2);
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    int32_t* y = reinterpret_cast<int32_t*>(temp_get(A(1), 4u));
+    if (!x || !y) return ERR("argmax ref fail");
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < (uint64_t)n * 2u) return ERR("argmax input smaller than n");
+    CHECK_LAUNCH(launch_argmax(x, n, y, g.stream));
+    return 0;
+}
+
+int op_broadcast(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n = A(2), b_elems = A(3);
+    const uint32_t in_d[4] = {A(4), A(5), A(6), A(7)}, out_d[4] = {A(8), A(9), A(10), A(11)};
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    __half* y = reinterpret_cast<__half*>(temp_get(A(1), n * 2u));
+    if (!x || !y || b_elems == 0) return ERR("broadcast ref fail");
+    CHECK_LAUNCH(launch_broadcast(x, y, n, in_d, out_d, g.stream));
+    return 0;
+}
+
+int op_transpose_gen(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t rk = A(2);
+    const uint32_t dims[4] = {A(3), A(4), A(5), A(6)};
+    if (rk < 2 || rk > 4) return ERR("transpose_gen rank %u", rk);
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < rk; ++i) n *= dims[i];
+    for (uint32_t i = 0; i < rk; ++i)
+        if (((A(7) >> (8 * i)) & 0xFFu) >= rk) return ERR("transpose_gen perm bad");
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    __half* y = reinterpret_cast<__half*>(temp_get(A(1), (uint32_t)n * 2u));
+    if (!x || !y) return ERR("transpose_gen ref fail");
+    CHECK_LAUNCH(launch_transpose_gen(x, y, rk, dims, A(7), g.stream));
+    return 0;
+}
+
+int op_slice(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n_out = A(2), rk = A(3);
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    __half* y = reinterpret_cast<__half*>(temp_get(A(1), n_out * 2u));
+    if (!x || !y) return ERR("slice ref fail");
+    if (rk < 1 || rk > 3) return ERR("slice rank %u", rk);
+    uint32_t bb[3] = {A(4), A(5), A(6)}, ee[3] = {A(7), A(8), A(9)}, ss[3] = {A(10), A(11), A(12)};
+    uint32_t dd[3] = {A(13), A(14), A(15)}, od[3] = {1, 1, 1};
+    uint64_t prod = 1;
+    for (uint32_t ax = 0; ax < rk; ++ax) {
+        if (ss[ax] == 0) ss[ax] = 1;
+        const uint32_t span = ee[ax] > bb[ax] ? ee[ax] - bb[ax] : 0;
+        od[ax] = (span + ss[ax] - 1) / ss[ax];
+        prod *= od[ax];
+        if (od[ax] && (uint64_t)bb[ax] + (uint64_t)(od[ax] - 1) * ss[ax] >= dd[ax])
+            return ERR("slice axis %u reads beyond dim %u", ax, dd[ax]);
+    }
+    if (n_out > prod) return ERR("slice n_out %u exceeds slice size", n_out);
+    CHECK_LAUNCH(launch_slice(x, y, n_out, rk, bb, ss, dd, od, g.stream));
+    return 0;
+}
+
+int op_kv_append(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const __half* k = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const __half* v = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(1)));
+    const uint32_t kn = ref_elem_count(cx.b, A(0)), vn = ref_elem_count(cx.b, A(1));
+    if (!k || !v || !kn || kn != vn) return ERR("kv append ref fail");
+    State* s = state_kv(A(2), kn, err, errn);
+    if (!s) return -1;
+    const uint32_t si = A(2) & 0x1FFFu;
+    uint32_t pos = A(3), dev_pos = A(3);
+    if (pos == WT_KV_POS_AUTO) {
+        if (s->count >= s->nslots)
+            return ERR("kv append state %u count=%u >= nslots=%u (context too long)", si, s->count, s->nslots);
+        pos = s->count++;
+        dev_pos = 0xFFFFFFFFu;
+    }
+    s->posmap[pos % s->nslots] = pos;
+    CHECK_LAUNCH(launch_kv_append(s->dev, s->slot_bytes, s->nslots, k, v, kn, dev_pos,
+                                  g.counters_dev + si, g.stream));
+    return 0;
+}
+
+int op_kv_append_n(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n_tok = A(4), kv_elems = A(5);
+    const __half* k = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const __half* v = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(1)));
+    if (!k || !v || !kv_elems || !n_tok) return ERR("kv append_n ref fail");
+    const size_t kb = ref_bytes(cx.b, A(0)), vb = ref_bytes(cx.b, A(1));
+    if ((kb && kb < (uint64_t)n_tok * kv_elems * 2u) || (vb && vb < (uint64_t)n_tok * kv_elems * 2u))
+        return ERR("kv append_n k/v smaller than n_tok*kv_elems");
+    State* s = state_kv(A(2), kv_elems, err, errn);
+    if (!s) return -1;
+    const uint32_t si = A(2) & 0x1FFFu;
+    uint32_t pos = A(3), dev_pos = A(3);
+    if (pos == WT_KV_POS_AUTO) {
+        if ((uint64_t)s->count + n_tok > s->nslots)
+            return ERR("kv append_n state %u count=%u + %u > nslots=%u", si, s->count, n_tok, s->nslots);
+        pos = s->count;
+        s->count += n_tok;
+        dev_pos = 0xFFFFFFFFu;
+    }
+    for (uint32_t t = 0; t < n_tok; ++t) s->posmap[(pos + t) % s->nslots] = pos + t;
+    CHECK_LAUNCH(launch_kv_append_n(s->dev, s->slot_bytes, s->nslots, k, v, kv_elems, n_tok, dev_pos,
+                                    g.counters_dev + si, g.stream));
+    return 0;
+}
+
+int op_kv_gather(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    uint32_t n_kv = A(3);
+    const uint32_t H = A(4), KVH = A(5), hd = A(6);
+    if (!H || !KVH || !hd || H % KVH) return ERR("kv gather gqa bad (h=%u kvh=%u hd=%u)", H, KVH, hd);
+    State* s = state_kv(A(0), KVH * hd, err, errn);
+    if (!s) return -1;
+    uint32_t pstride = n_kv;
+    if (n_kv == WT_KV_POS_AUTO) {
+        if (s->count == 0 || s->count > s->nslots)
+            return ERR("kv gather state %u count=%u bad (append first?)", A(0) & 0x1FFFu, s->count);
+        n_kv = s->count;
+        pstride = s->nslots;
+    }
+    if (kv_check(*s, n_kv, err, errn)) return -1;
+    const uint64_t bytes = (uint64_t)H * hd * pstride * 2u;
+    if (bytes > 0xFFFFFFFFull) return ERR("kv gather output too large");
+    __half* kT = A(1) ? reinterpret_cast<__half*>(temp_get(A(1), (uint32_t)bytes)) : nullptr;
+    __half* vo = A(2) ? reinterpret_cast<__half*>(temp_get(A(2), (uint32_t)bytes)) : nullptr;
+    if ((!kT && A(1)) || (!vo && A(2))) return ERR("kv gather out alloc");
+    CHECK_LAUNCH(launch_kv_gather(s->dev, s->slot_bytes, s->nslots, kT, vo, n_kv, pstride, H, KVH, hd,
+                                  g.stream));
+    return 0;
+}
+
+int op_attn(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t S = A(4), H = A(5), KVH = A(6), hd = A(7), flags = A(9);
+    const float scale = f32_from_bits(A(8));
+    if (hd != 128) return ERR("attn head_dim %u unsupported (128 only)", hd);
+    if (!KVH || H % KVH) return ERR("attn heads %u not a multiple of kv heads %u", H, KVH);
+    const __half* q = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const __half* k = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(1)));
+    const __half* v = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(2)));
+    __half* o = reinterpret_cast<__half*>(temp_get(A(3), S * H * hd * 2u));
+    if (!q || !k || !v || !o) return ERR("attn ref fail");
+    const size_t qb = ref_bytes(cx.b, A(0)), kb = ref_bytes(cx.b, A(1)), vb = ref_bytes(cx.b, A(2));
+    if ((qb && qb < (uint64_t)S * H * hd * 2u) || (kb && kb < (uint64_t)S * KVH * hd * 2u) ||
+        (vb && vb < (uint64_t)S * KVH * hd * 2u))
+        return ERR("attn operand smaller than its shape");
+    CHECK_LAUNCH(launch_attn_prefill(q, H * hd, k, v, KVH * hd, o, H * hd, S, H, KVH, hd, scale,
+                                     flags & 1u, g.stream));
+    return 0;
+}
+
+int op_attn_decode(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    uint32_t n_kv = A(3);
+    const uint32_t H = A(4), KVH = A(5), hd = A(6);
+    const float scale = f32_from_bits(A(7));
+    if (hd != 128) return ERR("attn_decode head_dim %u unsupported (128 only)", hd);
+    if (!KVH || H % KVH) return ERR("attn_decode heads %u not a multiple of kv heads %u", H, KVH);
+    const uint32_t rep = H / KVH;
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return ERR("attn_decode group size %u unsupported", rep);
+    State* s = state_kv(A(1), KVH * hd, err, errn);
+    if (!s) return -1;
+    const bool autopos = n_kv == WT_KV_POS_AUTO;
+    if (autopos) n_kv = s->count;
+    if (n_kv == 0 || n_kv > s->nslots) return ERR("attn_decode n_kv %u bad (nslots %u)", n_kv, s->nslots);
+    if (kv_check(*s, n_kv, err, errn)) return -1;
+    const __half* q = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    __half* o = reinterpret_cast<__half*>(temp_get(A(2), H * hd * 2u));
+    if (!q || !o) return ERR("attn_decode ref fail");
+    const size_t qb = ref_bytes(cx.b, A(0));
+    if (qb && qb < (uint64_t)H * hd * 2u) return ERR("attn_decode q smaller than H*hd");
+    const uint32_t need = attn_decode_work_floats(autopos ? s->nslots : n_kv, H, hd);
+    if (need > g.attn_work_floats) {
+        if (g.attn_work) hipFree(g.attn_work);
+        g.attn_work = nullptr;
+        g.attn_work_floats = 0;
+        if (hipMalloc(&g.attn_work, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace alloc");
+        g.attn_work_floats = need;
+    }
+    CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o, n_kv,
+                                    autopos ? g.counters_dev + (A(1) & 0x1FFFu) : nullptr, H, KVH, hd,
+                                    scale, g.attn_work, g.attn_work_floats, g.stream));
+    return 0;
+}
+
+int op_rope(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n_tok = A(2), H = A(3), hd = A(4), pos0 = A(5), row_stride = A(7);
+    const float theta = f32_from_bits(A(6));
+    if (hd == 0 || hd % 2) return ERR("rope head_dim %u must be even", hd);
+    if (row_stride < H * hd) return ERR("rope row stride %u < heads*hd %u", row_stride, H * hd);
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const uint64_t bytes = (uint64_t)n_tok * row_stride * 2u;
+    __half* y = reinterpret_cast<__half*>(temp_get(A(1), (uint32_t)bytes));
+    if (!x || !y) return ERR("rope ref fail");
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < bytes) return ERR("rope input smaller than n_tok*row_stride");
+    const uint32_t* pos_dev = nullptr;
+    uint32_t base = pos0;
+    if ((pos0 & 0xFFFFE000u) == WT_REF_STATE_FLAG) {
+        const uint32_t si = pos0 & 0x1FFFu;
+        if (si >= g.n_states) return ERR("rope state %u oob", si);
+        pos_dev = g.counters_dev + si;
+        base = 0;
+    }
+    CHECK_LAUNCH(launch_rope(x, y, n_tok, H, hd, base, pos_dev, theta, row_stride, g.stream));
+    return 0;
+}
+
+int op_unsupported(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    return ERR("opcode %u has no HIP kernel in this build", (unsigned)cx.op->opcode);
+}
+
+typedef int (*OpFn)(Ctx&);
+
+struct Table {
+    OpFn fn[64];
+    Table() {
+        for (auto& f : fn) f = op_unsupported;
+        fn[OP_NOP] = op_nop;
+        fn[OP_PIN] = op_pin;
+        fn[OP_SILU_F16] = op_silu;
+        fn[OP_ADD_F16] = op_add;
+        fn[OP_UNARY_F16] = op_unary;
+        fn[OP_BINARY_F16] = op_binary;
+        fn[OP_SOFTMAX_F16] = op_softmax;
+        fn[OP_STRIDED_SLICE_F16] = op_slice;
+        fn[OP_ARGMAX_F16] = op_argmax;
+        fn[OP_KV_APPEND_F16] = op_kv_append;
+        fn[OP_KV_GATHER_F16] = op_kv_gather;
+        fn[OP_MATMUL_F16] = op_matmul_f16;
+        fn[OP_MATMUL_F16_SPLIT] = op_matmul_f16;
+        fn[OP_RMSNORM2_F16] = op_rmsnorm2;
+        fn[OP_BROADCAST_F16] = op_broadcast;
+        fn[OP_TRANSPOSE_GEN_F16] = op_transpose_gen;
+        fn[OP_MATMUL_W4G_F16] = op_matmul_w4g;
+        fn[OP_ATTN_F16] = op_attn;
+        fn[OP_ATTN_DECODE_F16] = op_attn_decode;
+        fn[OP_ROPE_F16] = op_rope;
+        fn[OP_KV_APPEND_N_F16] = op_kv_append_n;
+    }
+};
+const Table kTable;
+
+// Tensor dump hook "opidx:temp,..." (oplist_exec.c:108-166): host files /tmp/hook_<i>_<t>.f16.raw.
+void hook_dump(uint32_t ii) {
+    static const char* env_hook = nullptr;
+    static bool env_tried = false;
+    const char* hook = g.hook;
+    if (!hook) {
+        if (!env_tried) { env_hook = std::getenv("GEHTP_HOOK"); env_tried = true; }
+        hook = env_hook;
+    }
+    if (!hook || !hook[0]) return;
+    const char* tok = hook;
+    while (*tok) {
+        const char* comma = std::strchr(tok, ',');
+        const size_t len = comma ? (size_t)(comma - tok) : std::strlen(tok);
+        std::string item(tok, len);
+        const size_t colon = item.find(':');
+        if (colon != std::string::npos) {
+            const uint32_t hi = (uint32_t)std::strtoul(item.substr(0, colon).c_str(), nullptr, 0);
+            const uint32_t ht = (uint32_t)std::strtoul(item.substr(colon + 1).c_str(), nullptr, 0);
+            if (hi == ii && ht < kMaxTemps && g.temps[ht]) {
+                std::vector<uint8_t> host(g.last_bytes[ht]);
+                if (hipStreamSynchronize(g.stream) == hipSuccess &&
+                    hipMemcpy(host.data(), g.temps[ht], host.size(), hipMemcpyDeviceToHost) == hipSuccess) {
+                    char fn[128];
+                    std::snprintf(fn, sizeof fn, "/tmp/hook_%u_%u.f16.raw", hi, ht);
+                    if (FILE* f = std::fopen(fn, "wb")) {
+                        std::fwrite(host.data(), 1, host.size(), f);
+                        std::fclose(f);
+                    }
+                }
+            }
+        }
+        if (!comma) break;
+        tok = comma + 1;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, uint32_t* engine_m,
+                      int64_t* op_us, char* err, size_t errn) {
+    char dummy_err[8];
+    if (!err || !errn) { err = dummy_err; errn = sizeof dummy_err; }
+    uint32_t dummy_m = 0;
+    if (!engine_m) engine_m = &dummy_m;
+    if (!b) return ERR("null blob");
+    if ((uint64_t)first + count > b->n_ops) return ERR("range oob");
+    if (ensure_ready(err, errn)) return -1;
+    if (ensure_weights(b, err, errn)) return -1;
+    if (load_tempoff(b, err, errn)) return -1;
+    if (load_states(b, err, errn)) return -1;
+
+    const bool timed = op_us || (g.ts && g.ts_cap);
+    if (timed && g.events.size() < 2 * (size_t)count + 1) {
+        const size_t have = g.events.size();
+        g.events.resize(2 * (size_t)count + 1);
+        for (size_t i = have; i < g.events.size(); ++i)
+            if (hipEventCreate(&g.events[i]) != hipSuccess) return ERR("event create failed");
+    }
+    const bool sync_each = std::getenv("GEHTP_SYNC_EACH_OP") != nullptr;
+    if (timed && hipEventRecord(g.events[2 * (size_t)count], g.stream) != hipSuccess)
+        return ERR("event record failed");
+    for (uint32_t ii = 0; ii < count; ++ii) {
+        const uint32_t i = first + ii;
+        const wt_op* op = &b->ops[i];
+        if (timed) hipEventRecord(g.events[2 * ii], g.stream);
+        Ctx cx{b, op, engine_m, err, errn};
+        int rc = op->opcode < 64 ? kTable.fn[op->opcode](cx) : op_unsupported(cx);
+        if (timed) hipEventRecord(g.events[2 * ii + 1], g.stream);
+        if (g.trace)
+            std::fprintf(stderr, "[gehtp] op%u code=%u a=%u,%u,%u,%u rc=%d pool=%u\n", ii,
+                         (unsigned)op->opcode, op->args[0], op->args[1], op->args[2], op->args[3], rc,
+                         g.pool_used);
+        if (rc == 0 && sync_each) {
+            const hipError_t e = hipStreamSynchronize(g.stream);
+            if (e != hipSuccess) { std::snprintf(err, errn, "op %u: %s", i, hipGetErrorString(e)); rc = -1; }
+        }
+        g.stats.ops++;
+        if (rc == 0) hook_dump(ii);
+        if (rc) {
+            hipStreamSynchronize(g.stream);
+            return (int)i + 1;
+        }
+    }
+    const hipError_t e = hipStreamSynchronize(g.stream);
+    if (e != hipSuccess) return ERR("device error: %s", hipGetErrorString(e));
+    if (timed) {
+        for (uint32_t ii = 0; ii < count; ++ii) {
+            float ms = 0.0f, st_ms = 0.0f;
+            hipEventElapsedTime(&ms, g.events[2 * ii], g.events[2 * ii + 1]);
+            hipEventElapsedTime(&st_ms, g.events[2 * (size_t)count], g.events[2 * ii]);
+            if (op_us) op_us[ii] = (int64_t)std::llround(ms * 1000.0);
+            const uint32_t i = first + ii;
+            if (g.ts && i < g.ts_cap) {
+                g.ts[i].start_us = (uint32_t)std::llround(st_ms * 1000.0);
+                g.ts[i].dur_us = (uint32_t)std::llround(ms * 1000.0);
+                g.ts[i].dma_us = 0;
+                g.ts[i].dma_bytes = 0;
+                g.ts[i].engine = WT_ENG_HMX;
+            }
+        }
+    }
+    return 0;
+}
+
+int wt_exec_run(const struct wt_blob* b, uint32_t* engine_m, int64_t* op_us, char* err, size_t errn) {
+    g.stats = wt_exec_stats{};
+    return wt_exec_run_range(b, 0, b ? b->n_ops : 0, engine_m, op_us, err, errn);
+}
+
+int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, uint32_t out_temp,
+                   uint32_t* engine_m, int64_t* op_us, char* err, size_t errn) {
+    char dummy_err[8];
+    if (!err || !errn) { err = dummy_err; errn = sizeof dummy_err; }
+    if (!b) return ERR("null blob");
+    g.in_active = false;
+    if (in_ptr) {
+        if (ensure_ready(err, errn)) return -1;
+        size_t need = 0;
+        for (uint32_t i = 0; i < b->n_slots; ++i)
+            if (b->slots[i].addr == WT_SLOT_EXT_IN) need = std::max<size_t>(need, b->slots[i].len);
+        if (need) {
+            if (need > g.in_cap) {
+                if (g.in_dev) hipFree(g.in_dev);
+                g.in_dev = nullptr;
+                g.in_cap = 0;
+                if (hipMalloc(&g.in_dev, need) != hipSuccess) return ERR("input buffer alloc");
+                g.in_cap = need;
+            }
+            if (hipMemcpyAsync(g.in_dev, in_ptr, need, hipMemcpyHostToDevice, g.stream) != hipSuccess)
+                return ERR("input upload failed");
+            g.in_active = true;
+        }
+    }
+    int rc = wt_exec_run(b, engine_m, op_us, err, errn);
+    if (rc == 0 && out_ptr && out_temp < kMaxTemps && g.temps[out_temp]) {
+        if (hipMemcpy(out_ptr, g.temps[out_temp], g.last_bytes[out_temp], hipMemcpyDeviceToHost) != hipSuccess)
+            rc = ERR("output copy failed");
+    }
+    g.in_active = false;
+    return rc;
+}
+
+uint8_t* wt_exec_temp(uint32_t id) {
+    if (id >= kMaxTemps || !g.temps[id]) return nullptr;
+    std::vector<uint8_t>& m = g.mirror[id];
+    m.resize(std::max<uint32_t>(g.temp_bytes[id], 1));
+    if (g.stream) hipStreamSynchronize(g.stream);
+    if (hipMemcpy(m.data(), g.temps[id], g.temp_bytes[id], hipMemcpyDeviceToHost) != hipSuccess) return nullptr;
+    return m.data();
+}
+
+uint32_t wt_exec_temp_bytes(uint32_t id) { return id < kMaxTemps ? g.temp_bytes[id] : 0; }
+uint32_t wt_exec_temp_last_bytes(uint32_t id) { return id < kMaxTemps ? g.last_bytes[id] : 0; }
+
+void wt_exec_shutdown(void) {
+    if (g.stream) hipStreamSynchronize(g.stream);
+    g.stats = wt_exec_stats{};
+    if (g.pool && g.pool_owned) hipFree(g.pool);
+    for (void* p : g.retired_pools) hipFree(p);
+    g.retired_pools.clear();
+    g.pool = nullptr;
+    g.pool_cap = g.pool_used = 0;
+    g.pool_owned = false;
+    g.static_offsets = nullptr;
+    if (g.vtcm_pool) hipFree(g.vtcm_pool);
+    g.vtcm_pool = nullptr;
+    g.vtcm_pool_size = 0;
+    std::fill(std::begin(g.static_off_arr), std::end(g.static_off_arr), kNone);
+    std::fill(std::begin(g.vtcm_off_arr), std::end(g.vtcm_off_arr), kNone);
+    for (uint32_t i = 0; i < kMaxTemps; ++i) {
+        g.temps[i] = nullptr;
+        g.temp_bytes[i] = 0;
+        g.last_bytes[i] = 0;
+        std::vector<uint8_t>().swap(g.mirror[i]);
+    }
+    if (g.attn_work) hipFree(g.attn_work);
+    g.attn_work = nullptr;
+    g.attn_work_floats = 0;
+    // Weights stay resident (keyed by content); states persist until state_reset.
+}
+
+void wt_exec_state_reset(void) {
+    for (uint32_t i = 0; i < g.n_states; ++i) {
+        State& s = g.st[i];
+        if (s.dev) hipMemset(s.dev, 0, s.bytes);
+        s.count = 0;
+        if (s.kv_ready) std::fill(s.posmap.begin(), s.posmap.end(), kNone);
+    }
+    if (g.counters_dev) hipMemset(g.counters_dev, 0, WT_MAX_STATES * sizeof(uint32_t));
+}
+
+void wt_exec_pool_init(uint8_t* base, uint32_t total_cap, uint32_t static_cap, const uint32_t* offsets) {
+    if (base) {
+        if (g.pool && g.pool_owned) g.retired_pools.push_back(g.pool);
+        g.pool = base;
+        g.pool_cap = total_cap;
+        g.pool_used = static_cap ? static_cap : total_cap;
+        g.pool_owned = false;
+    }
+    g.static_offsets = offsets;
+}
+
+void wt_exec_get_stats(struct wt_exec_stats* st) {
+    if (st) *st = g.stats;
+}
+
+void wt_exec_set_ext_weights(const void* wgt_ptr) {
+    g.ext_host = static_cast<const uint8_t*>(wgt_ptr);
+}
+
+void wt_exec_set_ts(struct wt_op_ts* buf, uint32_t cap) {
+    g.ts = buf;
+    g.ts_cap = buf ? cap : 0;
+}
+
+void wt_exec_set_trace(int on) { g.trace = on != 0; }
+
+void wt_exec_set_hook(const char* spec) { g.hook = spec; }
+
+}  // extern "C"

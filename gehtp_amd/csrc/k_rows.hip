@@ -1,0 +1,529 @@
+// k_rows.hip — row-wise and element-wise runlist ops for gfx950.
+//
+// Arithmetic that the reference rounds through f16 at op boundaries is done here
+// with explicitly rounded operations (__fmul_rn / __fadd_rn / __fdiv_rn) so no
+// FMA contraction changes a result the reference's scalar path defines exactly.
+#include "kernels.h"
+
+#include <cmath>
+
+namespace gehtp {
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f(__half h) { return __half2float(h); }
+__device__ __forceinline__ __half f2h(float f) { return __float2half(f); }   // RNE
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// binary64 -> binary16, one RNE rounding (the reference builds RoPE tables this way).
+__device__ __forceinline__ uint16_t f64_to_f16_bits(double d) {
+    const uint64_t x = __builtin_bit_cast(uint64_t, d);
+    const uint16_t sign = (uint16_t)((x >> 48) & 0x8000u);
+    const int32_t dexp = (int32_t)((x >> 52) & 0x7ffu);
+    const uint64_t man = x & ((1ull << 52) - 1);
+    if (dexp == 0x7ff) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u : 0u));
+    const int32_t exp = dexp - 1008;
+    if (exp >= 31) return (uint16_t)(sign | 0x7c00u);
+    uint64_t kept, rem, halfway;
+    if (exp <= 0) {
+        if (exp < -10) return sign;
+        const uint64_t m = man | (1ull << 52);
+        const uint32_t shift = (uint32_t)(43 - exp);
+        kept = m >> shift;
+        rem = m & ((1ull << shift) - 1);
+        halfway = 1ull << (shift - 1);
+    } else {
+        kept = ((uint64_t)exp << 10) | (man >> 42);
+        rem = man & ((1ull << 42) - 1);
+        halfway = 1ull << 41;
+    }
+    if (rem > halfway || (rem == halfway && (kept & 1u))) kept++;
+    return (uint16_t)(sign | kept);
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm, one wavefront per row (reference exec_rmsnorm2, oplist_exec.c:1859-1871):
+// squares summed in double (each f32 square is exact in double), rms =
+// (float)sqrt(mean + 1e-6) in double, then f16(x / rms * g + b) with each step rounded.
+__global__ __launch_bounds__(256) void rmsnorm2_kernel(const __half* __restrict__ x,
+                                                       const __half* __restrict__ g,
+                                                       const __half* __restrict__ b,
+                                                       __half* __restrict__ y, uint32_t rows,
+                                                       uint32_t rw) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const __half* xr = x + (size_t)row * rw;
+    __half* yr = y + (size_t)row * rw;
+    double acc = 0.0;
+    const bool vec = (rw % 8 == 0);
+    if (vec) {
+        for (uint32_t i = lane * 8; i < rw; i += 512) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(xr + i);
+            const __half* hv = reinterpret_cast<const __half*>(&v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const double f = (double)h2f(hv[e]);
+                acc += f * f;
+            }
+        }
+    } else {
+        for (uint32_t i = lane; i < rw; i += 64) {
+            const double f = (double)h2f(xr[i]);
+            acc += f * f;
+        }
+    }
+    acc = wave_sum_d(acc);
+    const float rms = (float)sqrt(acc / (double)rw + 1e-6);
+    for (uint32_t i = lane; i < rw; i += 64) {
+        float v = __fdiv_rn(h2f(xr[i]), rms);
+        v = __fadd_rn(__fmul_rn(v, h2f(g[i])), b ? h2f(b[i]) : 0.0f);
+        yr[i] = f2h(v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Softmax, one workgroup per row, following exec_softmax's two forms
+// (oplist_exec.c:1163-1194 and kernels/src/hvx/hvx_softmax.c:81-93).
+__global__ __launch_bounds__(256) void softmax_kernel(const __half* __restrict__ x,
+                                                      __half* __restrict__ y, uint32_t n,
+                                                      int vector_form) {
+    __shared__ float red_f[4];
+    __shared__ double red_d[4];
+    const uint32_t row = blockIdx.x;
+    const __half* xr = x + (size_t)row * n;
+    __half* yr = y + (size_t)row * n;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    float mx = -INFINITY;
+    for (uint32_t i = tid; i < n; i += 256) mx = fmaxf(mx, h2f(xr[i]));
+    mx = wave_max_f(mx);
+    if (lane == 0) red_f[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    __syncthreads();
+
+    if (vector_form) {
+        double s = 0.0;
+        for (uint32_t i = tid; i < n; i += 256) s += (double)expf(__fsub_rn(h2f(xr[i]), mx));
+        s = wave_sum_d(s);
+        if (lane == 0) red_d[wave] = s;
+        __syncthreads();
+        const double sum = red_d[0] + red_d[1] + red_d[2] + red_d[3];
+        const float inv = sum > 0.0 ? (float)(1.0 / sum) : 0.0f;
+        for (uint32_t i = tid; i < n; i += 256)
+            yr[i] = f2h(__fmul_rn(expf(__fsub_rn(h2f(xr[i]), mx)), inv));
+    } else {
+        float s = 0.0f;
+        for (uint32_t i = tid; i < n; i += 256) s += expf(__fsub_rn(h2f(xr[i]), mx));
+        s = wave_sum_f(s);
+        if (lane == 0) red_f[wave] = s;
+        __syncthreads();
+        const float sum = red_f[0] + red_f[1] + red_f[2] + red_f[3];
+        for (uint32_t i = tid; i < n; i += 256) {
+            const __half e = f2h(expf(__fsub_rn(h2f(xr[i]), mx)));
+            yr[i] = f2h(__fdiv_rn(h2f(e), sum));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Element-wise binary ops, subtypes 0..5 (oplist_exec.c:1143-1158).
+__global__ void binary_kernel(const __half* __restrict__ a, const __half* __restrict__ b,
+                              __half* __restrict__ y, uint32_t n, uint32_t subtype) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float x0 = h2f(a[i]), x1 = h2f(b[i]);
+    float r = x0;
+    switch (subtype) {
+    case 0: r = __fadd_rn(x0, x1); break;
+    case 1: r = __fsub_rn(x0, x1); break;
+    case 2: r = __fmul_rn(x0, x1); break;
+    case 3: r = (x1 != 0.0f) ? __fdiv_rn(x0, x1) : 0.0f; break;
+    case 4: r = (x0 == x1) ? 1.0f : 0.0f; break;
+    case 5: r = ((uint32_t)x0 & (uint32_t)x1) ? 1.0f : 0.0f; break;
+    default: break;
+    }
+    y[i] = f2h(r);
+}
+
+__global__ void select_kernel(const __half* __restrict__ c, uint32_t cn, const __half* __restrict__ t,
+                              uint32_t tn, const __half* __restrict__ f, uint32_t fn,
+                              __half* __restrict__ y, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float cv = h2f(c[cn <= 1 ? 0 : (cn < n ? i % cn : i)]);
+    const float r = cv != 0.0f ? h2f(t[tn <= 1 ? 0 : (tn < n ? i % tn : i)])
+                               : h2f(f[fn <= 1 ? 0 : (fn < n ? i % fn : i)]);
+    y[i] = f2h(r);
+}
+
+// Element-wise unary ops, subtypes 0..16 (oplist_exec.c:1047-1078).
+__global__ void unary_kernel(const __half* __restrict__ x, __half* __restrict__ y, uint32_t n,
+                             uint32_t subtype) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = h2f(x[i]);
+    float r = v;
+    switch (subtype) {
+    case 0: r = -v; break;
+    case 1: r = expf(v); break;
+    case 2: r = v >= 0.0f ? __fsqrt_rn(v) : 0.0f; break;
+    case 3: r = v > 0.0f ? __fdiv_rn(1.0f, __fsqrt_rn(v)) : 0.0f; break;
+    case 4: r = v > 0.0f ? logf(v) : 0.0f; break;
+    case 5: r = fabsf(v); break;
+    case 6: r = sinf(v); break;
+    case 7: r = cosf(v); break;
+    case 8: r = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-v))); break;
+    case 9: r = tanhf(v); break;
+    case 10: {
+        const float v3 = __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, v), v), v);
+        const float t = tanhf(__fmul_rn(0.7978845608f, __fadd_rn(v, v3)));
+        r = __fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, t));
+        break;
+    }
+    case 11: r = fmaxf(0.0f, v); break;
+    case 12: r = __fdiv_rn(v, __fadd_rn(1.0f, expf(-v))); break;
+    case 13: r = v > 30.0f ? v : (v < -30.0f ? expf(v) : log1pf(expf(v))); break;
+    case 14: r = v; break;
+    case 15: r = (v != v) ? 1.0f : 0.0f; break;
+    case 16: r = (v == v && (v > 3.4e38f || v < -3.4e38f)) ? 1.0f : 0.0f; break;
+    default: break;
+    }
+    y[i] = f2h(r);
+}
+
+// ---------------------------------------------------------------------------
+// Argmax: first index of the strict maximum above -1e30 (oplist_exec.c:1990-2004).
+__global__ __launch_bounds__(1024) void argmax_kernel(const __half* __restrict__ x, uint32_t n,
+                                                      int32_t* __restrict__ out) {
+    __shared__ float sv[16];
+    __shared__ int32_t si[16];
+    float bv = -1e30f;
+    int32_t bi = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+        const float v = h2f(x[i]);
+        if (v > bv) { bv = v; bi = (int32_t)i; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int32_t oi = __shfl_xor(bi, off, 64);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    const uint32_t wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
+        out[0] = bi;
+    }
+}
+
+__global__ void copy_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    if (((uintptr_t)dst | (uintptr_t)src | n) % 16 == 0) {
+        for (; i < n / 16; i += stride)
+            reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(src)[i];
+    } else {
+        for (; i < n; i += stride) dst[i] = src[i];
+    }
+}
+
+__global__ void fill_zero_kernel(uint8_t* __restrict__ dst, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    if (((uintptr_t)dst | n) % 16 == 0) {
+        for (; i < n / 16; i += stride) reinterpret_cast<u32x4*>(dst)[i] = u32x4{0, 0, 0, 0};
+    } else {
+        for (; i < n; i += stride) dst[i] = 0;
+    }
+}
+
+// numpy broadcast with the reference's rank rules (oplist_exec.c:1876-1907).
+struct Dims4 { uint32_t v[4]; };
+__global__ void broadcast_kernel(const __half* __restrict__ x, __half* __restrict__ y, uint32_t n,
+                                 Dims4 in_d, Dims4 ostr, Dims4 istr, uint32_t r, uint32_t lead) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint32_t rem = i, in_lin = 0;
+    for (uint32_t d = 0; d < r; ++d) {
+        const uint32_t c = rem / ostr.v[d];
+        rem -= c * ostr.v[d];
+        if (d < lead) continue;
+        const uint32_t idim = in_d.v[d - lead];
+        if (idim > 1) in_lin += (c % idim) * istr.v[d - lead];
+    }
+    y[i] = x[in_lin];
+}
+
+// General C-order transpose, rank 2..4 (oplist_exec.c:1910-1948): input linear t
+// maps to output offset sum_ax ic[perm[ax]] * so[ax].
+__global__ void transpose_gen_kernel(const __half* __restrict__ x, __half* __restrict__ y,
+                                     uint32_t n, uint32_t rk, Dims4 si, Dims4 so, Dims4 perm) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n) return;
+    uint32_t rem = t, ic[4] = {0, 0, 0, 0};
+    for (uint32_t i = 0; i < rk; ++i) { ic[i] = rem / si.v[i]; rem -= ic[i] * si.v[i]; }
+    uint32_t ot = 0;
+    for (uint32_t ax = 0; ax < rk; ++ax) ot += ic[perm.v[ax]] * so.v[ax];
+    y[ot] = x[t];
+}
+
+// Strided slice, rank <= 3 (oplist_exec.c:1950-1988).
+__global__ void slice_kernel(const __half* __restrict__ x, __half* __restrict__ y, uint32_t n_out,
+                             uint32_t rk, Dims4 bb, Dims4 ss, Dims4 istr, Dims4 ostr) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_out) return;
+    uint32_t rem = i, in_lin = 0;
+    for (uint32_t ax = 0; ax < rk; ++ax) {
+        const uint32_t c = rem / ostr.v[ax];
+        rem -= c * ostr.v[ax];
+        in_lin += (bb.v[ax] + c * ss.v[ax]) * istr.v[ax];
+    }
+    y[i] = x[in_lin];
+}
+
+// RoPE, half split: for pair (i, i+hd/2) of each head,
+//   y_i = f16(f16(x_i c) + f16(-x_{i+h} s)),  y_{i+h} = f16(f16(x_{i+h} c) + f16(x_i s)),
+// with c, s = f16(cos/sin(pos * theta^(-2i/hd))) computed in double, as the
+// reference's mul/neg/concat/add chain with f16 tables does.
+__global__ void rope_kernel(const __half* __restrict__ x, __half* __restrict__ y, uint32_t n_tok,
+                            uint32_t n_heads, uint32_t hd, uint32_t pos0,
+                            const uint32_t* __restrict__ pos_dev, float theta, uint32_t row_stride) {
+    const uint32_t half = hd / 2;
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;   // (t, i)
+    if (idx >= n_tok * half) return;
+    const uint32_t t = idx / half, i = idx - t * half;
+    const uint32_t base = pos_dev ? *pos_dev + pos0 : pos0;
+    const double pos = (double)(base + t);
+    const double inv = 1.0 / pow((double)theta, (double)(2 * i) / (double)hd);
+    const float c = __half2float(__ushort_as_half(f64_to_f16_bits(cos(pos * inv))));
+    const float s = __half2float(__ushort_as_half(f64_to_f16_bits(sin(pos * inv))));
+    for (uint32_t h = 0; h < n_heads; ++h) {
+        const size_t o = (size_t)t * row_stride + (size_t)h * hd;
+        const float x1 = h2f(x[o + i]), x2 = h2f(x[o + i + half]);
+        const float a1 = h2f(f2h(__fmul_rn(x1, c))), b1 = h2f(f2h(__fmul_rn(-x2, s)));
+        const float a2 = h2f(f2h(__fmul_rn(x2, c))), b2 = h2f(f2h(__fmul_rn(x1, s)));
+        y[o + i] = f2h(__fadd_rn(a1, b1));
+        y[o + i + half] = f2h(__fadd_rn(a2, b2));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// KV ring append of n_tok tokens: workgroup t copies token t. The base position is
+// read by every workgroup before the last one to finish advances the device counter:
+// the counter is advanced by a separate single-thread kernel launched afterwards.
+__global__ __launch_bounds__(256) void kv_append_kernel(uint8_t* __restrict__ ring,
+                                                        uint32_t slot_bytes, uint32_t nslots,
+                                                        const __half* __restrict__ k,
+                                                        const __half* __restrict__ v,
+                                                        uint32_t kv_elems, uint32_t pos,
+                                                        const uint32_t* __restrict__ count) {
+    const uint32_t t = blockIdx.x;
+    const uint32_t base = (pos == 0xFFFFFFFFu) ? *count : pos;
+    const uint32_t slot = (base + t) % nslots;
+    __half* kf = reinterpret_cast<__half*>(ring + (size_t)slot * slot_bytes);
+    __half* vf = kf + kv_elems;
+    const __half* ks = k + (size_t)t * kv_elems;
+    const __half* vs = v + (size_t)t * kv_elems;
+    for (uint32_t i = threadIdx.x; i < kv_elems; i += 256) {
+        kf[i] = ks[i];
+        vf[i] = vs[i];
+    }
+}
+
+__global__ void counter_add_kernel(uint32_t* count, uint32_t n) { *count += n; }
+
+// KV gather with GQA expansion (oplist_exec.c:2183-2231): kT[h][d][p], v[h][p][d].
+__global__ void kv_gather_kernel(const uint8_t* __restrict__ ring, uint32_t slot_bytes,
+                                 uint32_t nslots, __half* __restrict__ kT, __half* __restrict__ vo,
+                                 uint32_t n_kv, uint32_t pstride, uint32_t H, uint32_t KVH,
+                                 uint32_t hd) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;   // (h, p, d)
+    const uint32_t total = H * pstride * hd;
+    if (idx >= total) return;
+    const uint32_t d = idx % hd;
+    const uint32_t p = (idx / hd) % pstride;
+    const uint32_t h = idx / (hd * pstride);
+    const uint32_t rep = H / KVH;
+    __half kval = __ushort_as_half(0), vval = __ushort_as_half(0);
+    if (p < n_kv) {
+        const uint32_t slot = p % nslots;
+        const __half* kf = reinterpret_cast<const __half*>(ring + (size_t)slot * slot_bytes);
+        kval = kf[(h / rep) * hd + d];
+        vval = kf[KVH * hd + (h / rep) * hd + d];
+    }
+    if (kT) kT[((size_t)h * hd + d) * pstride + p] = kval;
+    if (vo) vo[((size_t)h * pstride + p) * hd + d] = vval;
+}
+
+inline uint32_t blocks_for(size_t n, uint32_t bs) { return (uint32_t)((n + bs - 1) / bs); }
+
+}  // namespace
+
+hipError_t launch_rmsnorm2(const __half* x, const __half* g, const __half* b, __half* y,
+                           uint32_t rows, uint32_t rw, hipStream_t st) {
+    if (!rows) return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm2_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, st, x, g, b, y,
+                       rows, rw);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax(const __half* x, __half* y, uint32_t rows, uint32_t n, hipStream_t st) {
+    if (!rows || !n) return hipSuccess;
+    const int vector_form = (n % 32 == 0 && (size_t)rows * n >= 32) ? 1 : 0;
+    hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(256), 0, st, x, y, n, vector_form);
+    return hipGetLastError();
+}
+
+hipError_t launch_binary(const __half* a, const __half* b, __half* y, uint32_t n, uint32_t subtype,
+                         hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(binary_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, st, a, b, y, n, subtype);
+    return hipGetLastError();
+}
+
+hipError_t launch_select(const __half* c, uint32_t cn, const __half* t, uint32_t tn,
+                         const __half* f, uint32_t fn, __half* y, uint32_t n, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(select_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, st, c, cn, t, tn, f,
+                       fn, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_unary(const __half* x, __half* y, uint32_t n, uint32_t subtype, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(unary_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, st, x, y, n, subtype);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const __half* x, uint32_t n, int32_t* out, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, x, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t st) {
+    if (!bytes) return hipSuccess;
+    const size_t units = bytes % 16 == 0 ? bytes / 16 : bytes;
+    uint32_t grid = blocks_for(units, 256);
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(copy_kernel, dim3(grid), dim3(256), 0, st, static_cast<uint8_t*>(dst),
+                       static_cast<const uint8_t*>(src), bytes);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(void* dst, size_t bytes, hipStream_t st) {
+    if (!bytes) return hipSuccess;
+    const size_t units = bytes % 16 == 0 ? bytes / 16 : bytes;
+    uint32_t grid = blocks_for(units, 256);
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(grid), dim3(256), 0, st, static_cast<uint8_t*>(dst), bytes);
+    return hipGetLastError();
+}
+
+hipError_t launch_broadcast(const __half* x, __half* y, uint32_t n, const uint32_t in_d[4],
+                            const uint32_t out_d[4], hipStream_t st) {
+    if (!n) return hipSuccess;
+    uint32_t r = 4;
+    while (r > 0 && out_d[r - 1] == 1) r--;
+    if (r == 0) r = 1;
+    uint32_t ir = 4;
+    if (ir > r) ir = r;
+    Dims4 istr{{1, 1, 1, 1}}, ostr{{1, 1, 1, 1}}, ind{{in_d[0], in_d[1], in_d[2], in_d[3]}};
+    for (int i = (int)ir - 2; i >= 0; --i) istr.v[i] = istr.v[i + 1] * in_d[i + 1];
+    for (int i = (int)r - 2; i >= 0; --i) ostr.v[i] = ostr.v[i + 1] * out_d[i + 1];
+    hipLaunchKernelGGL(broadcast_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, st, x, y, n, ind,
+                       ostr, istr, r, r - ir);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_gen(const __half* x, __half* y, uint32_t rk, const uint32_t dims[4],
+                                uint32_t perm, hipStream_t st) {
+    uint32_t p[4] = {perm & 0xFFu, (perm >> 8) & 0xFFu, (perm >> 16) & 0xFFu, (perm >> 24) & 0xFFu};
+    Dims4 si{{1, 1, 1, 1}}, so{{1, 1, 1, 1}}, pm{{p[0], p[1], p[2], p[3]}};
+    size_t n = 1;
+    for (uint32_t i = 0; i < rk; ++i) n *= dims[i];
+    for (int i = (int)rk - 2; i >= 0; --i) {
+        si.v[i] = si.v[i + 1] * dims[i + 1];
+        const uint32_t pd = p[i + 1] >= rk ? 1u : dims[p[i + 1]];
+        so.v[i] = so.v[i + 1] * pd;
+    }
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(transpose_gen_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, st, x, y,
+                       (uint32_t)n, rk, si, so, pm);
+    return hipGetLastError();
+}
+
+hipError_t launch_slice(const __half* x, __half* y, uint32_t n_out, uint32_t rank,
+                        const uint32_t b[3], const uint32_t s[3], const uint32_t d[3],
+                        const uint32_t od[3], hipStream_t st) {
+    if (!n_out) return hipSuccess;
+    Dims4 bb{{b[0], b[1], b[2], 0}}, ss{{s[0], s[1], s[2], 1}}, istr{{1, 1, 1, 1}}, ostr{{1, 1, 1, 1}};
+    for (int i = (int)rank - 2; i >= 0; --i) {
+        istr.v[i] = istr.v[i + 1] * d[i + 1];
+        ostr.v[i] = ostr.v[i + 1] * od[i + 1];
+    }
+    hipLaunchKernelGGL(slice_kernel, dim3(blocks_for(n_out, 256)), dim3(256), 0, st, x, y, n_out,
+                       rank, bb, ss, istr, ostr);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(const __half* x, __half* y, uint32_t n_tok, uint32_t n_heads, uint32_t hd,
+                       uint32_t pos0, const uint32_t* pos_dev, float theta, uint32_t row_stride,
+                       hipStream_t st) {
+    const size_t n = (size_t)n_tok * (hd / 2);
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, st, x, y, n_tok, n_heads,
+                       hd, pos0, pos_dev, theta, row_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append_n(uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
+                              const __half* k, const __half* v, uint32_t kv_elems, uint32_t n_tok,
+                              uint32_t pos, uint32_t* count_dev, hipStream_t st) {
+    if (!n_tok) return hipSuccess;
+    hipLaunchKernelGGL(kv_append_kernel, dim3(n_tok), dim3(256), 0, st, ring, slot_bytes, nslots, k,
+                       v, kv_elems, pos, count_dev);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || pos != 0xFFFFFFFFu) return e;
+    hipLaunchKernelGGL(counter_add_kernel, dim3(1), dim3(1), 0, st, count_dev, n_tok);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append(uint8_t* ring, uint32_t slot_bytes, uint32_t nslots, const __half* k,
+                            const __half* v, uint32_t kv_elems, uint32_t pos, uint32_t* count_dev,
+                            hipStream_t st) {
+    return launch_kv_append_n(ring, slot_bytes, nslots, k, v, kv_elems, 1, pos, count_dev, st);
+}
+
+hipError_t launch_kv_gather(const uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
+                            __half* kT, __half* vo, uint32_t n_kv, uint32_t pstride, uint32_t H,
+                            uint32_t KVH, uint32_t hd, hipStream_t st) {
+    const size_t n = (size_t)H * pstride * hd;
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(kv_gather_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, st, ring, slot_bytes,
+                       nslots, kT, vo, n_kv, pstride, H, KVH, hd);
+    return hipGetLastError();
+}
+
+}  // namespace gehtp

@@ -1,0 +1,97 @@
+// kernels.h — host-side launchers of the gfx950 kernels (internal to libgehtp).
+//
+// Every launcher enqueues on the given stream and returns hipSuccess or the launch
+// error; shapes are validated by the caller (engine ops or the C-ABI entry points)
+// before a launcher is reached, so every launch stays inside its buffers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+
+namespace gehtp {
+
+// Number of compute units of the current device (cached).
+int device_cu_count();
+
+// ---- W4G (int4, group 64, fp16 scales) ----
+// y[m*ldy + n] = f16( sum_k x[m*ldx + k] * fp16(q[n,k] * s[n, k/64]) ), m < M.
+hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, const __half* ws,
+                           __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
+                           hipStream_t st);
+hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, const __half* ws,
+                           __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
+                           hipStream_t st);
+// w[n*K + k] = fp16(q * s) (bit-exact dequant; used by tests and the fp16 fallback).
+hipError_t launch_w4g_dequant(const uint8_t* wq, const __half* ws, __half* w,
+                              uint32_t N, uint32_t K, hipStream_t st);
+// Largest M the GEMV handles; larger M goes to the MFMA GEMM.
+constexpr uint32_t kW4gGemvMaxM = 4;
+
+// ---- fp16 x fp16 matmul, reference OP_MATMUL_F16 semantics ----
+// y[b][m][n0+n] over batch b < Bn; a [Bn][M][K] (or [K][M] when t0), w [Bn][K][N_full]
+// (or [Bn][N_full][K] when t1); f32 accumulate, f16 out.
+hipError_t launch_matmul_f16(const __half* a, const __half* w, __half* y,
+                             uint32_t M, uint32_t K, uint32_t N_full, uint32_t n0, uint32_t N,
+                             bool t0, bool t1, uint32_t Bn, hipStream_t st);
+
+// ---- row ops ----
+// One wavefront per row: y = f16(x / (float)sqrt(mean(x^2) + 1e-6) * g + b); b may be null.
+hipError_t launch_rmsnorm2(const __half* x, const __half* g, const __half* b, __half* y,
+                           uint32_t rows, uint32_t rw, hipStream_t st);
+// Row softmax with exec_softmax's dispatch (vector path when n % 32 == 0).
+hipError_t launch_softmax(const __half* x, __half* y, uint32_t rows, uint32_t n, hipStream_t st);
+hipError_t launch_binary(const __half* a, const __half* b, __half* y, uint32_t n, uint32_t subtype,
+                         hipStream_t st);
+// SELECT: y[i] = c[i%cn]!=0 ? t[i%tn] : f[i%fn] (scalar operands broadcast), n = max counts.
+hipError_t launch_select(const __half* c, uint32_t cn, const __half* t, uint32_t tn,
+                         const __half* f, uint32_t fn, __half* y, uint32_t n, hipStream_t st);
+hipError_t launch_unary(const __half* x, __half* y, uint32_t n, uint32_t subtype, hipStream_t st);
+hipError_t launch_argmax(const __half* x, uint32_t n, int32_t* out, hipStream_t st);
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t st);
+hipError_t launch_fill_zero(void* dst, size_t bytes, hipStream_t st);
+hipError_t launch_broadcast(const __half* x, __half* y, uint32_t n, const uint32_t in_d[4],
+                            const uint32_t out_d[4], hipStream_t st);
+hipError_t launch_transpose_gen(const __half* x, __half* y, uint32_t rank, const uint32_t dims[4],
+                                uint32_t perm, hipStream_t st);
+hipError_t launch_slice(const __half* x, __half* y, uint32_t n_out, uint32_t rank,
+                        const uint32_t b[3], const uint32_t s[3], const uint32_t d[3],
+                        const uint32_t od[3], hipStream_t st);
+// Rotary embedding, half-split layout; position of token t = base + t where
+// base = pos0 or, when pos_dev is non-null, *pos_dev (device counter) + pos0.
+hipError_t launch_rope(const __half* x, __half* y, uint32_t n_tok, uint32_t n_heads, uint32_t hd,
+                       uint32_t pos0, const uint32_t* pos_dev, float theta, uint32_t row_stride,
+                       hipStream_t st);
+
+// ---- KV ring (slot-major, slot = [K face | V face], each KVH*hd fp16) ----
+// Writes k, v (kv_elems each) into slot (*count_dev or pos) % nslots and, for the
+// automatic form, increments *count_dev. pos == UINT32_MAX selects the counter.
+hipError_t launch_kv_append(uint8_t* ring, uint32_t slot_bytes, uint32_t nslots, const __half* k,
+                            const __half* v, uint32_t kv_elems, uint32_t pos, uint32_t* count_dev,
+                            hipStream_t st);
+// n_tok tokens (row stride kv_elems) at positions base..base+n_tok-1, base = pos or,
+// when pos == UINT32_MAX, *count_dev (then advanced by n_tok).
+hipError_t launch_kv_append_n(uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
+                              const __half* k, const __half* v, uint32_t kv_elems, uint32_t n_tok,
+                              uint32_t pos, uint32_t* count_dev, hipStream_t st);
+// kT [H][hd][pstride], v [H][pstride][hd]; positions >= n_kv of the pstride are zero.
+hipError_t launch_kv_gather(const uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
+                            __half* kT, __half* vo, uint32_t n_kv, uint32_t pstride, uint32_t H,
+                            uint32_t KVH, uint32_t hd, hipStream_t st);
+
+// ---- attention ----
+// Flash prefill: q [S][H][hd] (row stride ldq), k/v [S][KVH][hd] (row stride ldkv),
+// out [S][H][hd] (row stride ldo); hd == 128.
+hipError_t launch_attn_prefill(const __half* q, uint32_t ldq, const __half* k, const __half* v,
+                               uint32_t ldkv, __half* out, uint32_t ldo, uint32_t S, uint32_t H,
+                               uint32_t KVH, uint32_t hd, float scale, bool causal,
+                               hipStream_t st);
+// Split-KV decode: q [H][hd]; K/V read from the ring for positions [0, n_kv) where
+// n_kv = n_kv_host, or *count_dev when count_dev is non-null.
+hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slot_bytes,
+                              uint32_t nslots, __half* out, uint32_t n_kv_host,
+                              const uint32_t* count_dev, uint32_t H, uint32_t KVH, uint32_t hd,
+                              float scale, float* work, uint32_t work_floats, hipStream_t st);
+// Floats of workspace launch_attn_decode needs for n_kv positions.
+uint32_t attn_decode_work_floats(uint32_t max_kv, uint32_t H, uint32_t hd);
+
+}  // namespace gehtp

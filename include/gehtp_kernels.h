@@ -1,0 +1,74 @@
+/* gehtp_kernels.h — kernel-level C entry points of libgehtp (gfx950).
+ *
+ * These have no single counterpart in the reference ABI: they expose the kernels
+ * behind individual runlist ops so a caller (this library's tests and benchmark,
+ * or an integrator that keeps its own memory) can run one op on device buffers
+ * without building a blob. Each names the reference routine whose result it
+ * reproduces.
+ *
+ * Conventions: every pointer is a DEVICE pointer; `stream` is a hipStream_t
+ * (NULL = the legacy default stream); the call only enqueues work. Return 0 on
+ * success, GEHTP_EINVAL for a rejected shape/alignment, or a positive hipError_t.
+ */
+#ifndef GEHTP_KERNELS_H
+#define GEHTP_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GEHTP_EINVAL (-22)
+
+/* y[M, ldy] = x[M, ldx] . dequant(W)^T, W4G int4 group-64 (OP_MATMUL_W4G_F16):
+ * M <= 4 runs the GEMV, larger M the MFMA GEMM. Mirrors exec_matmul_f16's scalar
+ * arithmetic (oplist_exec.c:1802-1811) on dequant(W) = fp16(q*s).
+ * K % 64 == 0, ldx % 8 == 0, x and wq 16-byte aligned. */
+int gehtp_w4g_matmul(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y,
+                     uint32_t ldy, uint32_t M, uint32_t N, uint32_t K, void* stream);
+/* Force one implementation (for measurement): GEMV needs M <= 4. */
+int gehtp_w4g_gemv(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y,
+                   uint32_t ldy, uint32_t M, uint32_t N, uint32_t K, void* stream);
+int gehtp_w4g_gemm(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y,
+                   uint32_t ldy, uint32_t M, uint32_t N, uint32_t K, void* stream);
+/* w[N, K] fp16 = fp16(q * s): the dequant, bit-exact. */
+int gehtp_w4g_dequant(const void* wq, const void* ws, void* w, uint32_t N, uint32_t K, void* stream);
+
+/* OP_MATMUL_F16 / _SPLIT semantics (oplist_exec.c:1709-1813), flags as in the op. */
+int gehtp_matmul_f16(const void* a, const void* w, void* y, uint32_t M, uint32_t K,
+                     uint32_t N_full, uint32_t n0, uint32_t N, uint32_t flags, void* stream);
+
+/* OP_RMSNORM2_F16 (oplist_exec.c:1817-1872): rows x rw, b may be NULL. */
+int gehtp_rmsnorm2(const void* x, const void* gamma, const void* beta, void* y, uint32_t rows,
+                   uint32_t rw, void* stream);
+/* OP_SOFTMAX_F16 (oplist_exec.c:1163-1194). */
+int gehtp_softmax(const void* x, void* y, uint32_t rows, uint32_t n, void* stream);
+
+/* Fused causal GQA attention (OP_ATTN_F16): q [S,H,128], k/v [S,KVH,128] -> out [S,H,128]. */
+int gehtp_attn_prefill(const void* q, const void* k, const void* v, void* out, uint32_t S,
+                       uint32_t H, uint32_t KVH, uint32_t hd, float scale, int causal, void* stream);
+/* Decode attention (OP_ATTN_DECODE_F16) over positions [0, n_kv) of a KV ring of
+ * state_bytes (slot = [K | V], each KVH*hd fp16): q [H,128] -> out [H,128].
+ * work: device float buffer of gehtp_attn_decode_work_floats(n_kv, H, hd). */
+int gehtp_attn_decode(const void* q, const void* ring, uint32_t state_bytes, void* out,
+                      uint32_t n_kv, uint32_t H, uint32_t KVH, uint32_t hd, float scale,
+                      void* work, uint32_t work_floats, void* stream);
+uint32_t gehtp_attn_decode_work_floats(uint32_t n_kv, uint32_t H, uint32_t hd);
+/* Append n_tok tokens (k/v [n_tok, KVH*hd]) at positions pos..pos+n_tok-1 of the ring. */
+int gehtp_kv_append(void* ring, uint32_t state_bytes, const void* k, const void* v,
+                    uint32_t kv_elems, uint32_t n_tok, uint32_t pos, void* stream);
+/* OP_ROPE_F16 with an explicit start position. */
+int gehtp_rope(const void* x, void* y, uint32_t n_tok, uint32_t n_heads, uint32_t hd,
+               uint32_t pos0, float theta, uint32_t row_stride, void* stream);
+/* OP_ARGMAX_F16: out (device int32) = first index of the maximum. */
+int gehtp_argmax(const void* x, uint32_t n, void* out, void* stream);
+
+/* Library identification: "gehtp-gfx950 <version>". */
+const char* gehtp_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

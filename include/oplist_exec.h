@@ -1,0 +1,96 @@
+/* oplist_exec.h — runlist engine ABI (HIP/gfx950 implementation).
+ *
+ * Drop-in for GEHTP's engine header (reference: kernels/include/oplist_exec.h).
+ * Same functions, same struct layouts, same return conventions:
+ *   run*  -> 0 on success, the 1-based index of the failing op, or -1 on a
+ *            setup failure; a human-readable reason is written to err.
+ *
+ * Differences a caller can observe, all forced by the device being a GPU:
+ *   - Every op runs as HIP kernels on one stream of the current device; the run
+ *     functions return after that stream has drained.
+ *   - wt_exec_temp() returns a host mirror of the temp's device buffer, copied
+ *     back at the time of the call (valid until the next run or shutdown).
+ *   - An opcode without a gfx950 kernel fails the run with "no HIP kernel"; there
+ *     is no silent CPU fallback.
+ */
+#ifndef GEHTP_OPLIST_EXEC_H
+#define GEHTP_OPLIST_EXEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include "oplist_parse.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WT_EXEC_MAX_TEMPS 4096
+
+/* Run every op of b (reference oplist_exec.c:2573). */
+int wt_exec_run(const struct wt_blob* b, uint32_t* engine_m,
+                int64_t* op_us, char* err, size_t errn);
+
+/* Host view of temp id (reference oplist_exec.h:34-38). */
+uint8_t*  wt_exec_temp(uint32_t id);
+uint32_t  wt_exec_temp_bytes(uint32_t id);
+uint32_t  wt_exec_temp_last_bytes(uint32_t id);
+
+/* Free temps and pools; persistent states survive (reference oplist_exec.c:531). */
+void wt_exec_shutdown(void);
+
+/* Zero every persistent state and its KV counters (reference oplist_exec.c:2104). */
+void wt_exec_state_reset(void);
+
+/* Caller-provided temp pool (reference oplist_exec.c:351-359). base is a DEVICE
+ * pointer in this implementation; base=NULL && offsets=NULL restores bump mode. */
+void wt_exec_pool_init(uint8_t* base, uint32_t total_cap, uint32_t static_cap,
+                       const uint32_t* offsets);
+
+struct wt_exec_stats {
+    uint32_t ops, nop, matmul, rmsnorm, silu, pin, pin_skipped;
+    uint32_t im2col, conv2d, add, spill, fill, transpose;
+};
+
+/* Run ops[first, first+count) (reference oplist_exec.c:2499-2565). */
+int  wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count,
+                       uint32_t* engine_m, int64_t* op_us, char* err, size_t errn);
+void wt_exec_get_stats(struct wt_exec_stats* st);
+
+/* Run with injected input and copied-back output (reference oplist_exec.c:2587-2602).
+ * in_ptr/out_ptr are HOST pointers; out receives wt_exec_temp_last_bytes(out_temp). */
+int  wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr,
+                    uint32_t out_temp,
+                    uint32_t* engine_m, int64_t* op_us, char* err, size_t errn);
+
+/* External weight image for WT_SLOT_EXT_WGT slots (host pointer; uploaded to
+ * HBM on the next run, once per (pointer, blob)). NULL disables. */
+void wt_exec_set_ext_weights(const void* wgt_ptr);
+
+enum wt_engine { WT_ENG_SCALAR = 0, WT_ENG_HVX = 1, WT_ENG_HMX = 2 };
+/* In this implementation every op's engine is reported as WT_ENG_HMX (= "matrix
+ * device") and dma_us/dma_bytes carry host->device copy time/bytes of the op. */
+struct wt_op_ts {
+    uint32_t start_us;
+    uint32_t dur_us;
+    uint32_t dma_us;
+    uint32_t dma_bytes;
+    uint32_t engine;
+};
+void wt_exec_set_ts(struct wt_op_ts* buf, uint32_t cap);
+
+/* Per-op trace lines to stderr when on (default off here: no device log path). */
+void wt_exec_set_trace(int on);
+
+/* Tensor dump hook "opidx:temp,..." -> /tmp/hook_<idx>_<temp>.f16.raw
+ * (reference oplist_exec.c:108-166); falls back to env GEHTP_HOOK. */
+void wt_exec_set_hook(const char* spec);
+
+/* W3 inspect report: one JSON line per call of emit (reference wt_w3.c). */
+void wt_w3_report(const char* blob_name, const uint8_t* buf, size_t size,
+                  const struct wt_blob* w,
+                  void (*emit)(const char* line, void* ud), void* ud);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GEHTP_OPLIST_EXEC_H */

@@ -1,0 +1,84 @@
+/* gehtp_oracle.h — CPU restatement of GEHTP's scalar golden path (TEST INFRASTRUCTURE).
+ *
+ * This library is the checker for the HIP engine. Only tests/, the smoke check
+ * and bench.py's cpu_baseline leg may load it; the product never does.
+ *
+ * Each function restates one reference routine (file:line in the .c file) with
+ * the same arithmetic order, so results are bit-identical to the reference's
+ * scalar path when compiled with -O2 -ffp-contract=off and no fast-math.
+ */
+#ifndef GEHTP_ORACLE_H
+#define GEHTP_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- IEEE binary16 conversion ---- */
+float go_f16_to_f32(uint16_t h);
+uint16_t go_f32_to_f16(float f);
+void go_f16_to_f32_n(const uint16_t* in, float* out, size_t n);
+void go_f32_to_f16_n(const float* in, uint16_t* out, size_t n);
+
+/* ---- int4 group-quantized weights (the W4G format of OP_MATMUL_W4G_F16) ---- */
+void go_w4g_pack(const int8_t* q, uint32_t N, uint32_t K, uint8_t* wq);
+void go_w4g_unpack(const uint8_t* wq, uint32_t N, uint32_t K, int8_t* q);
+int  go_w4g_dequant(const uint8_t* wq, const uint16_t* ws, uint32_t N, uint32_t K,
+                    uint32_t group, uint16_t* w /* [N,K] fp16 */);
+
+/* ---- linears ---- */
+int go_matmul_f16(const uint16_t* a, const uint16_t* w, uint16_t* y,
+                  uint32_t M, uint32_t K, uint32_t N_full, uint32_t n0, uint32_t N,
+                  uint32_t flags);
+/* y[M,N] = a[M,K] . dequant(W)^T with the OP_MATMUL_F16 scalar arithmetic.
+ * n_threads > 1 splits the N outputs over OpenMP threads; every output keeps
+ * the sequential k order, so the result is identical for any thread count. */
+int go_matmul_w4g(const uint16_t* a, const uint8_t* wq, const uint16_t* ws, uint16_t* y,
+                  uint32_t M, uint32_t K, uint32_t N, uint32_t group, int n_threads);
+/* Same for fp16 weights stored [N,K] (the lm_head). */
+int go_matmul_f16_nk_mt(const uint16_t* a, const uint16_t* w, uint16_t* y,
+                        uint32_t M, uint32_t K, uint32_t N, int n_threads);
+
+/* ---- row ops ---- */
+int  go_rmsnorm2(const uint16_t* x, const uint16_t* gamma, const uint16_t* beta,
+                 uint16_t* y, uint32_t n, uint32_t rw);
+void go_softmax_scalar(const uint16_t* x, uint16_t* y, uint32_t rows, uint32_t n);
+void go_softmax_host(const uint16_t* x, uint16_t* y, uint32_t rows, uint32_t n);
+void go_softmax(const uint16_t* x, uint16_t* y, uint32_t rows, uint32_t n);
+int  go_binary(const uint16_t* a, const uint16_t* b, uint16_t* y, uint32_t n, uint32_t subtype);
+int  go_unary(const uint16_t* x, uint16_t* y, uint32_t n, uint32_t subtype);
+int32_t go_argmax(const uint16_t* x, uint32_t n);
+
+/* ---- KV ring state (OP_KV_APPEND_F16 / OP_KV_GATHER_F16) ---- */
+struct go_kv {
+    uint8_t* buf;         /* nslots * slot_bytes, slot = [K face | V face] */
+    uint32_t slot_bytes;  /* 2 * kv_elems * 2 */
+    uint32_t nslots;
+    uint32_t count;       /* auto-position counter */
+    uint32_t* posmap;     /* nslots entries, 0xFFFFFFFF = empty */
+};
+int go_kv_init(struct go_kv* c, uint8_t* buf, uint32_t state_bytes, uint32_t kv_elems,
+               uint32_t* posmap);
+int go_kv_append(struct go_kv* c, const uint16_t* k, const uint16_t* v, uint32_t pos);
+int go_kv_gather(struct go_kv* c, uint16_t* kT, uint16_t* vo, uint32_t n_kv,
+                 uint32_t n_heads, uint32_t kv_heads, uint32_t hd);
+
+/* ---- attention as the reference runlist composes it (f16 at every op) ----
+ * q [S,H,hd], k/v [S,KVH,hd] -> out [S,H,hd]. scale is applied as the fp16
+ * value f16(scale) (it arrives as an f16 constant slot in reference blobs). */
+int go_attn_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                    uint32_t S, uint32_t H, uint32_t KVH, uint32_t hd, float scale, int causal);
+/* One query token against the ring: q [H,hd] -> out [H,hd]. */
+int go_attn_decode(struct go_kv* c, const uint16_t* q, uint16_t* out, uint32_t n_kv,
+                   uint32_t H, uint32_t KVH, uint32_t hd, float scale);
+/* Rotary embedding as the runlist's mul/slice/neg/concat/add chain computes it. */
+int go_rope(const uint16_t* x, uint16_t* y, uint32_t n_tok, uint32_t n_heads, uint32_t hd,
+            uint32_t pos0, float theta, uint32_t row_stride);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

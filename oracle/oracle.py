@@ -1,0 +1,259 @@
+"""numpy front end of the C oracle (TEST INFRASTRUCTURE — the checker, never the product).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this.
+Arrays in and out are numpy float16 (bit-identical to the C uint16 buffers).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+REF = HERE / "_ref"
+
+_lib = None
+
+
+def build() -> None:
+    """Compile liboracle.so (and oracle/_ref when the reference tree is present)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        _lib = C.CDLL(str(LIB))
+        _p = C.c_void_p
+        u = C.c_uint32
+        sig = {
+            "go_f16_to_f32": (C.c_float, [C.c_uint16]),
+            "go_f32_to_f16": (C.c_uint16, [C.c_float]),
+            "go_f16_to_f32_n": (None, [_p, _p, C.c_size_t]),
+            "go_f32_to_f16_n": (None, [_p, _p, C.c_size_t]),
+            "go_w4g_pack": (None, [_p, u, u, _p]),
+            "go_w4g_unpack": (None, [_p, u, u, _p]),
+            "go_w4g_dequant": (C.c_int, [_p, _p, u, u, u, _p]),
+            "go_matmul_f16": (C.c_int, [_p, _p, _p, u, u, u, u, u, u]),
+            "go_matmul_w4g": (C.c_int, [_p, _p, _p, _p, u, u, u, u, C.c_int]),
+            "go_matmul_f16_nk_mt": (C.c_int, [_p, _p, _p, u, u, u, C.c_int]),
+            "go_rmsnorm2": (C.c_int, [_p, _p, _p, _p, u, u]),
+            "go_softmax_scalar": (None, [_p, _p, u, u]),
+            "go_softmax_host": (None, [_p, _p, u, u]),
+            "go_softmax": (None, [_p, _p, u, u]),
+            "go_binary": (C.c_int, [_p, _p, _p, u, u]),
+            "go_unary": (C.c_int, [_p, _p, u, u]),
+            "go_argmax": (C.c_int32, [_p, u]),
+            "go_attn_prefill": (C.c_int, [_p, _p, _p, _p, u, u, u, u, C.c_float, C.c_int]),
+            "go_rope": (C.c_int, [_p, _p, u, u, u, u, C.c_float, u]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(_lib, name)
+            f.restype, f.argtypes = res, args
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle buffers must be C-contiguous"
+    return a.ctypes.data
+
+
+def _h(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float16)
+
+
+# ---- conversions ----
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().go_f16_to_f32_n(_p(bits), _p(out), bits.size)
+    return out
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().go_f32_to_f16_n(_p(x), _p(out), x.size)
+    return out
+
+
+# ---- W4G ----
+def w4g_pack(q: np.ndarray) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    N, K = q.shape
+    out = np.empty((N, K // 2), np.uint8)
+    lib().go_w4g_pack(_p(q), N, K, _p(out))
+    return out
+
+
+def w4g_unpack(wq: np.ndarray, K: int) -> np.ndarray:
+    wq = np.ascontiguousarray(wq, dtype=np.uint8)
+    N = wq.shape[0]
+    out = np.empty((N, K), np.int8)
+    lib().go_w4g_unpack(_p(wq), N, K, _p(out))
+    return out
+
+
+def w4g_dequant(wq: np.ndarray, ws: np.ndarray, K: int, group: int = 64) -> np.ndarray:
+    wq = np.ascontiguousarray(wq, dtype=np.uint8)
+    ws = _h(ws)
+    N = wq.shape[0]
+    out = np.empty((N, K), np.float16)
+    if lib().go_w4g_dequant(_p(wq), _p(ws), N, K, group, _p(out)):
+        raise ValueError("bad w4g shape")
+    return out
+
+
+# ---- linears ----
+def matmul_f16(a, w, M, K, N_full, n0=0, N=None, flags=0, out=None) -> np.ndarray:
+    a, w = _h(a), _h(w)
+    N = N_full if N is None else N
+    Bn = max(flags >> 16, 1) if flags & 4 else 1
+    y = _h(out) if out is not None else np.zeros(Bn * M * N_full, np.float16)
+    lib().go_matmul_f16(_p(a), _p(w), _p(y), M, K, N_full, n0, N, flags)
+    return y
+
+
+def matmul_w4g(a, wq, ws, threads: int = 1) -> np.ndarray:
+    a = _h(a)
+    wq = np.ascontiguousarray(wq, dtype=np.uint8)
+    ws = _h(ws)
+    M, K = a.shape
+    N = wq.shape[0]
+    y = np.empty((M, N), np.float16)
+    if lib().go_matmul_w4g(_p(a), _p(wq), _p(ws), _p(y), M, K, N, 64, threads):
+        raise ValueError("bad w4g shape")
+    return y
+
+
+def matmul_f16_nk(a, w, threads: int = 1) -> np.ndarray:
+    """y = a . w^T with w [N, K] fp16 (the lm_head form), sequential-k arithmetic."""
+    a, w = _h(a), _h(w)
+    M, K = a.shape
+    N = w.shape[0]
+    y = np.empty((M, N), np.float16)
+    lib().go_matmul_f16_nk_mt(_p(a), _p(w), _p(y), M, K, N, threads)
+    return y
+
+
+# ---- rows ----
+def rmsnorm2(x, gamma, beta=None) -> np.ndarray:
+    x, gamma = _h(x), _h(gamma)
+    rw = gamma.size
+    y = np.empty(x.shape, np.float16)
+    b = _h(beta) if beta is not None else None
+    if lib().go_rmsnorm2(_p(x), _p(gamma), _p(b) if b is not None else None, _p(y), x.size, rw):
+        raise ValueError("bad rmsnorm shape")
+    return y
+
+
+def softmax(x, rows, n, form: str = "dispatch") -> np.ndarray:
+    x = _h(x)
+    y = np.empty(x.shape, np.float16)
+    fn = {"dispatch": lib().go_softmax, "scalar": lib().go_softmax_scalar,
+          "host": lib().go_softmax_host}[form]
+    fn(_p(x), _p(y), rows, n)
+    return y
+
+
+def binary(a, b, subtype: int) -> np.ndarray:
+    a, b = _h(a), _h(b)
+    y = np.empty(a.shape, np.float16)
+    lib().go_binary(_p(a), _p(b), _p(y), a.size, subtype)
+    return y
+
+
+def unary(x, subtype: int) -> np.ndarray:
+    x = _h(x)
+    y = np.empty(x.shape, np.float16)
+    lib().go_unary(_p(x), _p(y), x.size, subtype)
+    return y
+
+
+def argmax(x) -> int:
+    x = _h(x)
+    return int(lib().go_argmax(_p(x), x.size))
+
+
+def attn_prefill(q, k, v, scale: float, causal: bool = True) -> np.ndarray:
+    """q [S,H,hd], k/v [S,KVH,hd] -> [S,H,hd], reference runlist composition."""
+    q, k, v = _h(q), _h(k), _h(v)
+    S, H, hd = q.shape
+    KVH = k.shape[1]
+    out = np.empty_like(q)
+    if lib().go_attn_prefill(_p(q), _p(k), _p(v), _p(out), S, H, KVH, hd, scale, int(causal)):
+        raise ValueError("bad attention shape")
+    return out
+
+
+def rope(x, n_heads: int, hd: int, pos0: int, theta: float, row_stride: int | None = None) -> np.ndarray:
+    x = _h(x)
+    n_tok = x.shape[0]
+    row_stride = row_stride or n_heads * hd
+    y = x.copy()
+    lib().go_rope(_p(x), _p(y), n_tok, n_heads, hd, pos0, theta, row_stride)
+    return y
+
+
+class KVRing:
+    """The reference KV ring (kvcache.c) restated: slot = pos % nslots, [K | V] faces."""
+
+    def __init__(self, state_bytes: int, kv_elems: int):
+        self.slot_bytes = kv_elems * 4
+        if self.slot_bytes < 256 or self.slot_bytes % 128 or state_bytes % self.slot_bytes:
+            raise ValueError("kv geometry bad")
+        self.kv_elems = kv_elems
+        self.nslots = state_bytes // self.slot_bytes
+        self.buf = np.zeros(state_bytes, np.uint8)
+        self.posmap = np.full(self.nslots, 0xFFFFFFFF, np.uint32)
+        self.count = 0
+
+    def append(self, k, v, pos: int | None = None) -> int:
+        if pos is None:
+            if self.count >= self.nslots:
+                raise OverflowError("kv ring full")
+            pos = self.count
+            self.count += 1
+        slot = pos % self.nslots
+        half = self.slot_bytes // 2
+        base = slot * self.slot_bytes
+        self.buf[base:base + half] = _h(k).view(np.uint8).ravel()
+        self.buf[base + half:base + 2 * half] = _h(v).view(np.uint8).ravel()
+        self.posmap[slot] = pos
+        return slot
+
+    def gather(self, n_kv: int, H: int, KVH: int, hd: int, pstride: int | None = None):
+        """(kT [H, hd, pstride], v [H, pstride, hd]) with GQA expansion kv = h // (H/KVH)."""
+        pstride = pstride or n_kv
+        kT = np.zeros((H, hd, pstride), np.float16)
+        vo = np.zeros((H, pstride, hd), np.float16)
+        rep = H // KVH
+        for p in range(n_kv):
+            slot = p % self.nslots
+            if self.posmap[slot] != p:
+                raise KeyError(f"kv gather miss pos {p}")
+            face = self.buf[slot * self.slot_bytes:(slot + 1) * self.slot_bytes].view(np.float16)
+            kf = face[:KVH * hd].reshape(KVH, hd)
+            vf = face[KVH * hd:].reshape(KVH, hd)
+            for h in range(H):
+                kT[h, :, p] = kf[h // rep]
+                vo[h, p, :] = vf[h // rep]
+        return kT, vo
+
+    def attn_decode(self, q, n_kv: int, H: int, KVH: int, hd: int, scale: float) -> np.ndarray:
+        """One-token attention as the reference decode chain computes it (f16 at each op)."""
+        kT, vo = self.gather(n_kv, H, KVH, hd)
+        q = _h(q).reshape(H, hd)
+        out = np.empty((H, hd), np.float16)
+        sc = np.float16(scale)
+        for h in range(H):
+            s = matmul_f16(q[h], kT[h], 1, hd, n_kv)
+            s = binary(s, np.full(n_kv, sc, np.float16), 2)
+            p = softmax(s, 1, n_kv)
+            out[h] = matmul_f16(p, vo[h], 1, n_kv, hd)
+        return out

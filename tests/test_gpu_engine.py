@@ -1,0 +1,216 @@
+"""The runlist engine through the reference ABI (wt_parse / wt_exec_run_io / temps /
+states) on hand-built WTOP blobs, checked against the CPU oracle."""
+from __future__ import annotations
+
+import math
+import struct
+
+import numpy as np
+import pytest
+
+from helpers import assert_close, normal_f16, w4g_weights
+
+from gehtp_amd import WtExecError
+from gehtp_amd.abi import WT_KV_POS_AUTO, opcodes as OP
+from gehtp_amd.runlist import BlobBuilder, f32_bits
+
+pytestmark = pytest.mark.gpu
+
+SCALE = float(np.float16(1.0 / math.sqrt(128)))
+
+
+@pytest.fixture(autouse=True)
+def fresh_engine(engine, torch_dev):
+    engine.shutdown()
+    engine.state_reset()
+    yield
+    engine.shutdown()
+
+
+def _h(b: bytes, shape=None):
+    a = np.frombuffer(b, np.float16)
+    return a.reshape(shape) if shape else a
+
+
+def test_w4g_op_via_run_io(engine, oracle):
+    rng = np.random.default_rng(1)
+    M, N, K = 1, 3072, 1024
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, M, K)
+    bb = BlobBuilder()
+    xs = bb.add_input_slot(M * K * 2)
+    sq = bb.add_slot(wq, count=N * K)
+    ss = bb.add_slot(ws)
+    t = bb.temp()
+    bb.op(OP.MATMUL_W4G_F16, bb.slot_ref(xs), bb.slot_ref(sq), bb.slot_ref(ss), t, M, K, N, 64, 2)
+    pb = engine.parse(bb.build())
+    out, us = engine.run_io(pb, x.tobytes(), t, timing=True)
+    assert_close(_h(out, (M, N)), oracle.matmul_w4g(x, wq, ws), what="run_io w4g")
+    assert len(us) == 1 and us[0] >= 0
+    assert engine.stats().matmul == 1 and engine.stats().ops == 1
+    # second call with a different input re-uses the resident weights
+    x2 = normal_f16(rng, M, K)
+    out2, _ = engine.run_io(pb, x2.tobytes(), t)
+    assert_close(_h(out2, (M, N)), oracle.matmul_w4g(x2, wq, ws), what="run_io w4g #2")
+
+
+def test_rmsnorm_then_w4g_gemm_runlist(engine, oracle):
+    """Config 2 as a two-op runlist: RMSNORM2_F16 -> MATMUL_W4G_F16 (M=512)."""
+    rng = np.random.default_rng(2)
+    M, N, K = 512, 3072, 1024
+    x = normal_f16(rng, M, K)
+    gamma = rng.uniform(0.8, 1.2, K).astype(np.float16)
+    _, wq, ws = w4g_weights(rng, N, K)
+    bb = BlobBuilder()
+    xs = bb.add_input_slot(M * K * 2)
+    gs = bb.add_slot(gamma)
+    zs = bb.add_slot(np.zeros(K, np.float16))
+    sq, ss = bb.add_slot(wq, count=N * K), bb.add_slot(ws)
+    h, y = bb.temp(), bb.temp()
+    bb.op(OP.RMSNORM2_F16, bb.slot_ref(xs), bb.slot_ref(gs), bb.slot_ref(zs), h, M * K)
+    bb.op(OP.MATMUL_W4G_F16, h, bb.slot_ref(sq), bb.slot_ref(ss), y, M, K, N, 64, 2)
+    pb = engine.parse(bb.build())
+    out, _ = engine.run_io(pb, x.tobytes(), y, out_bytes=M * N * 2)
+    h_ref = oracle.rmsnorm2(x, gamma, np.zeros(K, np.float16))
+    h_got = _h(engine.temp(h), (M, K))
+    assert np.abs(h_got.astype(np.float32) - h_ref.astype(np.float32)).max() <= 2e-3
+    assert_close(_h(out, (M, N)), oracle.matmul_w4g(h_ref, wq, ws, threads=8), what="rms+gemm")
+
+
+def _attention_chain_blob(S, H, KVH, hd, q, k, v):
+    """Reference-style prefill attention: per kv-group batched MATMUL_F16 (q . k^T),
+    BINARY mul (scale), BINARY add (causal mask), SOFTMAX, batched MATMUL_F16 (p . v).
+    Heads are laid out [H, S, hd] (the reference chain's batched layout)."""
+    rep = H // KVH
+    bb = BlobBuilder()
+    qh = np.ascontiguousarray(q.transpose(1, 0, 2))                       # [H,S,hd]
+    kx = np.ascontiguousarray(np.repeat(k.transpose(1, 0, 2), rep, 0))     # [H,S,hd] (GQA expanded)
+    vx = np.ascontiguousarray(np.repeat(v.transpose(1, 0, 2), rep, 0))
+    sq, sk, sv = bb.add_slot(qh), bb.add_slot(kx), bb.add_slot(vx)
+    scale = bb.add_slot(np.full(H * S * S, np.float16(SCALE), np.float16))
+    mask = np.where(np.tril(np.ones((S, S), bool)), 0.0, -np.inf).astype(np.float16)
+    smask = bb.add_slot(np.ascontiguousarray(np.broadcast_to(mask, (H, S, S))))
+    t_s, t_sc, t_m, t_p, t_o = (bb.temp() for _ in range(5))
+    bb.op(OP.MATMUL_F16, bb.slot_ref(sq), bb.slot_ref(sk), t_s, S, hd, S, (H << 16) | 4 | 2)
+    bb.op(OP.BINARY_F16, t_s, bb.slot_ref(scale), t_sc, H * S * S, 2)
+    bb.op(OP.BINARY_F16, t_sc, bb.slot_ref(smask), t_m, H * S * S, 0)
+    bb.op(OP.SOFTMAX_F16, t_m, t_p, H * S, S)
+    bb.op(OP.MATMUL_F16, t_p, bb.slot_ref(sv), t_o, S, S, hd, (H << 16) | 4)
+    # fused op on the same data, token-major
+    sq2, sk2, sv2 = bb.add_slot(q), bb.add_slot(k), bb.add_slot(v)
+    t_f = bb.temp()
+    bb.op(OP.ATTN_F16, bb.slot_ref(sq2), bb.slot_ref(sk2), bb.slot_ref(sv2), t_f, S, H, KVH, hd,
+          f32_bits(SCALE), 1)
+    return bb, t_o, t_f
+
+
+def test_attention_chain_vs_fused_vs_oracle(engine, oracle):
+    rng = np.random.default_rng(4)
+    S, H, KVH, hd = 160, 4, 2, 128
+    q, k, v = normal_f16(rng, S, H, hd), normal_f16(rng, S, KVH, hd), normal_f16(rng, S, KVH, hd)
+    bb, t_chain, t_fused = _attention_chain_blob(S, H, KVH, hd, q, k, v)
+    pb = engine.parse(bb.build())
+    engine.run(pb)
+    chain = _h(engine.temp(t_chain), (H, S, hd)).transpose(1, 0, 2)
+    fused = _h(engine.temp(t_fused), (S, H, hd))
+    ref = oracle.attn_prefill(q, k, v, SCALE, True)
+    assert_close(chain, ref, what="runlist chain vs oracle")
+    assert_close(fused, ref, what="fused vs oracle")
+
+
+def _decode_blob(H, KVH, hd, max_pos):
+    bb = BlobBuilder()
+    kv_elems = KVH * hd
+    st = bb.add_state(max_pos * kv_elems * 4)
+    qs = bb.add_input_slot((H * hd + 2 * kv_elems) * 2)
+    # the input face is [q | k | v]; three slices split it (STRIDED_SLICE, rank 1)
+    tq, tk, tv, to = bb.temp(), bb.temp(), bb.temp(), bb.temp()
+    n_in = H * hd + 2 * kv_elems
+    for t, b0, n in ((tq, 0, H * hd), (tk, H * hd, kv_elems), (tv, H * hd + kv_elems, kv_elems)):
+        bb.op(OP.STRIDED_SLICE_F16, bb.slot_ref(qs), t, n, 1, b0, 0, 0, b0 + n, 1, 1, 1, 1, 1, n_in, 1, 1)
+    bb.op(OP.KV_APPEND_F16, tk, tv, st, WT_KV_POS_AUTO)
+    bb.op(OP.ATTN_DECODE_F16, tq, st, to, WT_KV_POS_AUTO, H, KVH, hd, f32_bits(SCALE))
+    return bb, to
+
+
+def test_decode_loop_auto_positions(engine, oracle):
+    """KV_APPEND (auto position) + ATTN_DECODE over 40 steps vs the reference ring + chain."""
+    rng = np.random.default_rng(5)
+    H, KVH, hd, max_pos = 16, 8, 128, 64
+    bb, to = _decode_blob(H, KVH, hd, max_pos)
+    pb = engine.parse(bb.build())
+    ring = oracle.KVRing(max_pos * KVH * hd * 4, KVH * hd)
+    for step in range(40):
+        q, k, v = normal_f16(rng, H * hd), normal_f16(rng, KVH * hd), normal_f16(rng, KVH * hd)
+        out, _ = engine.run_io(pb, np.concatenate([q, k, v]).tobytes(), to)
+        ring.append(k, v)
+        ref = ring.attn_decode(q, step + 1, H, KVH, hd, SCALE)
+        assert_close(_h(out, (H, hd)), ref, what=f"decode step {step}")
+
+
+def test_kv_gather_and_overflow(engine, oracle):
+    """KV_GATHER output layout (kT [H,hd,nslots] zero tail, v [H,nslots,hd]) is byte-exact;
+    appending past nslots is the reference's hard error."""
+    rng = np.random.default_rng(6)
+    H, KVH, hd, max_pos = 4, 2, 128, 8
+    kv = KVH * hd
+    bb = BlobBuilder()
+    st = bb.add_state(max_pos * kv * 4)
+    ks, vs = bb.add_input_slot(kv * 2), bb.add_slot(np.zeros(kv, np.float16))
+    tkT, tvo = bb.temp(), bb.temp()
+    bb.op(OP.KV_APPEND_F16, bb.slot_ref(ks), bb.slot_ref(vs), st, WT_KV_POS_AUTO)
+    bb.op(OP.KV_GATHER_F16, st, tkT, tvo, WT_KV_POS_AUTO, H, KVH, hd)
+    pb = engine.parse(bb.build())
+    ring = oracle.KVRing(max_pos * kv * 4, kv)
+    for step in range(max_pos):
+        k = normal_f16(rng, kv)
+        engine.run_io(pb, k.tobytes(), tkT)
+        ring.append(k, np.zeros(kv, np.float16))
+        kT_ref, v_ref = ring.gather(step + 1, H, KVH, hd, pstride=max_pos)
+        assert np.array_equal(_h(engine.temp(tkT)), kT_ref.ravel())
+        assert np.array_equal(_h(engine.temp(tvo)), v_ref.ravel())
+    with pytest.raises(WtExecError) as ei:
+        engine.run_io(pb, normal_f16(rng, kv).tobytes(), tkT)
+    assert ei.value.rc == 1 and "nslots" in str(ei.value)
+    engine.state_reset()
+    engine.run_io(pb, normal_f16(rng, kv).tobytes(), tkT)   # fresh sequence works again
+
+
+def test_unported_opcode_fails_loudly(engine):
+    bb = BlobBuilder()
+    s = bb.add_slot(np.zeros(64, np.float16))
+    t = bb.temp()
+    bb.op(OP.NOP)
+    bb.op(OP.CUMSUM_F32, bb.slot_ref(s), t, 1, 64, 0, 0, 0)
+    pb = engine.parse(bb.build())
+    with pytest.raises(WtExecError) as ei:
+        engine.run(pb)
+    assert ei.value.rc == 2 and "no HIP kernel" in str(ei.value)
+
+
+def test_tempoff_static_plan_matches_bump(engine, oracle):
+    """The same two-op blob with and without a TEMPOFF plan gives identical bytes."""
+    rng = np.random.default_rng(8)
+    M, N, K = 4, 640, 256
+    x = normal_f16(rng, M, K)
+    gamma = rng.uniform(0.8, 1.2, K).astype(np.float16)
+    _, wq, ws = w4g_weights(rng, N, K)
+
+    def blob(static):
+        bb = BlobBuilder()
+        xs = bb.add_input_slot(M * K * 2)
+        gs, zs = bb.add_slot(gamma), bb.add_slot(np.zeros(K, np.float16))
+        sq, ss = bb.add_slot(wq, count=N * K), bb.add_slot(ws)
+        bb.op(OP.RMSNORM2_F16, bb.slot_ref(xs), bb.slot_ref(gs), bb.slot_ref(zs), 0, M * K)
+        bb.op(OP.MATMUL_W4G_F16, 0, bb.slot_ref(sq), bb.slot_ref(ss), 1, M, K, N, 64, 2)
+        if static:
+            bb.set_tempoff(1 << 20, [(0, 0, M * K * 2), (1, 65536, M * N * 2)], bump_kb=64)
+        return bb.build()
+
+    outs = []
+    for static in (False, True):
+        engine.shutdown()
+        pb = engine.parse(blob(static))
+        out, _ = engine.run_io(pb, x.tobytes(), 1)
+        outs.append(out)
+    assert outs[0] == outs[1]

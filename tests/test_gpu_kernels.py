@@ -1,0 +1,293 @@
+"""Parity of the gfx950 kernels with the CPU oracle, called through the C ABI
+(include/gehtp_kernels.h) on device buffers. Inputs are the seeded BASELINE shapes."""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+from helpers import (assert_close, from_dev, normal_f16, ptr, stream_ptr, to_dev, w4g_weights)
+
+pytestmark = pytest.mark.gpu
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def _w4g(lib, dev, x, wq, ws, M, N, K, which="auto"):
+    import torch
+    xd, qd, sd = to_dev(x, dev), to_dev(wq, dev), to_dev(ws, dev)
+    yd = torch.empty((M, N), dtype=torch.float16, device=dev)
+    fn = {"auto": lib.gehtp_w4g_matmul, "gemv": lib.gehtp_w4g_gemv, "gemm": lib.gehtp_w4g_gemm}[which]
+    rc = fn(ptr(xd), K, ptr(qd), ptr(sd), ptr(yd), N, M, N, K, stream_ptr())
+    assert rc == 0, rc
+    _sync()
+    return from_dev(yd)
+
+
+# ---------------------------------------------------------------- W4A16 ------
+def test_w4g_dequant_bit_exact(lib, oracle, torch_dev):
+    import torch
+    rng = np.random.default_rng(7)
+    N, K = 384, 1024
+    q, wq, ws = w4g_weights(rng, N, K)
+    # include extreme scales: subnormal products, large values
+    ws[0, :] = np.float16(6e-5)
+    ws[1, :] = np.float16(1000.0)
+    ws[2, :] = np.float16(-0.0137)
+    wd = torch.empty((N, K), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_w4g_dequant(ptr(to_dev(wq, torch_dev)), ptr(to_dev(ws, torch_dev)), ptr(wd), N, K,
+                                 stream_ptr()) == 0
+    _sync()
+    got = from_dev(wd).view(np.uint16)
+    ref = oracle.w4g_dequant(wq, ws, K).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_w4g_gemv_config1(lib, oracle, torch_dev, M):
+    """Config 1: x [M,1024] ~N(0,1), W int4 [3072,1024] g64, scales U[0.005,0.02]."""
+    rng = np.random.default_rng(100 + M)
+    N, K = 3072, 1024
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, M, K)
+    got = _w4g(lib, torch_dev, x, wq, ws, M, N, K, "gemv")
+    ref = oracle.matmul_w4g(x, wq, ws, threads=8)
+    assert_close(got, ref, what=f"gemv M={M}")
+
+
+@pytest.mark.parametrize("N,K", [(2560, 2560), (4096, 2560), (9728, 2560), (2560, 9728), (1000, 192), (7, 64)])
+def test_w4g_gemv_shapes(lib, oracle, torch_dev, N, K):
+    rng = np.random.default_rng(N * 7 + K)
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, 1, K)
+    got = _w4g(lib, torch_dev, x, wq, ws, 1, N, K, "gemv")
+    ref = oracle.matmul_w4g(x, wq, ws, threads=8)
+    assert_close(got, ref, what=f"gemv {N}x{K}")
+
+
+def test_w4g_gemm_config2(lib, oracle, torch_dev):
+    """Config 2: RMSNorm(eps 1e-6, gamma U(0.8,1.2)) then W4A16 GEMM [512,1024] x [3072,1024]^T."""
+    import torch
+    rng = np.random.default_rng(2)
+    M, N, K = 512, 3072, 1024
+    x = normal_f16(rng, M, K)
+    gamma = rng.uniform(0.8, 1.2, K).astype(np.float16)
+    _, wq, ws = w4g_weights(rng, N, K)
+    xd, gd = to_dev(x, torch_dev), to_dev(gamma, torch_dev)
+    hd = torch.empty((M, K), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_rmsnorm2(ptr(xd), ptr(gd), None, ptr(hd), M, K, stream_ptr()) == 0
+    _sync()
+    h_ref = oracle.rmsnorm2(x, gamma)
+    h_got = from_dev(hd)
+    ulps = np.abs(h_got.view(np.int16).astype(np.int32) - h_ref.view(np.int16).astype(np.int32))
+    assert ulps.max() <= 1, f"rmsnorm differs by {ulps.max()} ulp"
+    got = _w4g(lib, torch_dev, h_ref, wq, ws, M, N, K, "gemm")
+    ref = oracle.matmul_w4g(h_ref, wq, ws, threads=8)
+    assert_close(got, ref, what="gemm config2")
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 384, 128), (200, 130, 192), (129, 257, 64), (2048, 256, 2560)])
+def test_w4g_gemm_ragged(lib, oracle, torch_dev, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, M, K)
+    got = _w4g(lib, torch_dev, x, wq, ws, M, N, K, "gemm")
+    ref = oracle.matmul_w4g(x, wq, ws, threads=8)
+    assert_close(got, ref, what=f"gemm {M}x{N}x{K}")
+
+
+def test_w4g_gemv_equals_gemm_small_m(lib, torch_dev):
+    """The two implementations agree with each other (same dequant, different order)."""
+    rng = np.random.default_rng(11)
+    N, K = 1536, 2560
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, 4, K)
+    a = _w4g(lib, torch_dev, x, wq, ws, 4, N, K, "gemv")
+    b = _w4g(lib, torch_dev, x, wq, ws, 4, N, K, "gemm")
+    assert_close(a, b, max_abs=4e-3, min_cos=0.99999, what="gemv vs gemm")
+
+
+# ---------------------------------------------------------------- rows -------
+@pytest.mark.parametrize("rows,rw", [(512, 1024), (1, 2560), (4096, 128), (3, 100)])
+def test_rmsnorm2(lib, oracle, torch_dev, rows, rw):
+    import torch
+    rng = np.random.default_rng(rows + rw)
+    x = normal_f16(rng, rows, rw)
+    x[0, :] = 0   # zero row
+    gamma = rng.uniform(0.8, 1.2, rw).astype(np.float16)
+    beta = (rng.standard_normal(rw) * 0.1).astype(np.float16)
+    for b in (None, beta):
+        y = torch.empty((rows, rw), dtype=torch.float16, device=torch_dev)
+        assert lib.gehtp_rmsnorm2(ptr(to_dev(x, torch_dev)), ptr(to_dev(gamma, torch_dev)),
+                                  ptr(to_dev(b, torch_dev)) if b is not None else None, ptr(y),
+                                  rows, rw, stream_ptr()) == 0
+        _sync()
+        ref = oracle.rmsnorm2(x, gamma, b)
+        got = from_dev(y)
+        d = np.abs(got.view(np.int16).astype(np.int32) - ref.view(np.int16).astype(np.int32))
+        assert d.max() <= 1, f"rmsnorm max ulp diff {d.max()}"
+        assert (d == 0).mean() > 0.999
+
+
+@pytest.mark.parametrize("rows,n", [(64, 1024), (16, 100), (3, 4096)])
+def test_softmax(lib, oracle, torch_dev, rows, n):
+    import torch
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((rows, n)) * 3).astype(np.float16)
+    y = torch.empty((rows, n), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_softmax(ptr(to_dev(x, torch_dev)), ptr(y), rows, n, stream_ptr()) == 0
+    _sync()
+    ref = oracle.softmax(x, rows, n)
+    assert_close(from_dev(y), ref, max_abs=1e-3, what="softmax")
+
+
+def test_argmax_first_max(lib, oracle, torch_dev):
+    import torch
+    rng = np.random.default_rng(5)
+    n = 151936
+    x = normal_f16(rng, n)
+    x[[1000, 77777, 150000]] = np.float16(9.0)   # ties: first index wins
+    x[5] = np.float16(-np.inf)
+    out = torch.zeros(1, dtype=torch.int32, device=torch_dev)
+    assert lib.gehtp_argmax(ptr(to_dev(x, torch_dev)), n, ptr(out), stream_ptr()) == 0
+    _sync()
+    assert int(out.item()) == oracle.argmax(x) == 1000
+    allneg = np.full(300, -np.inf, np.float16)
+    assert lib.gehtp_argmax(ptr(to_dev(allneg, torch_dev)), 300, ptr(out), stream_ptr()) == 0
+    _sync()
+    assert int(out.item()) == oracle.argmax(allneg) == 0
+
+
+def test_rope_bit_exact(lib, oracle, torch_dev):
+    import torch
+    rng = np.random.default_rng(9)
+    n_tok, H, hd = 37, 4, 128
+    x = normal_f16(rng, n_tok, H * hd)
+    for pos0 in (0, 1000):
+        y = torch.empty_like(to_dev(x, torch_dev))
+        assert lib.gehtp_rope(ptr(to_dev(x, torch_dev)), ptr(y), n_tok, H, hd, pos0, 1e6, H * hd,
+                              stream_ptr()) == 0
+        _sync()
+        ref = oracle.rope(x, H, hd, pos0, 1e6)
+        got = from_dev(y)
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+def test_matmul_f16_flags(lib, oracle, torch_dev):
+    """OP_MATMUL_F16 layouts: plain, t0, t1, batched, SPLIT window; GEMV and GEMM sizes."""
+    import torch
+    rng = np.random.default_rng(21)
+    for (M, K, N) in [(1, 256, 300), (3, 64, 130), (40, 96, 72), (128, 128, 128)]:
+        for flags in (0, 1, 2, 3):
+            a = normal_f16(rng, M * K)
+            w = normal_f16(rng, K * N)
+            y = torch.zeros(M * N, dtype=torch.float16, device=torch_dev)
+            assert lib.gehtp_matmul_f16(ptr(to_dev(a, torch_dev)), ptr(to_dev(w, torch_dev)), ptr(y),
+                                        M, K, N, 0, N, flags, stream_ptr()) == 0
+            _sync()
+            ref = oracle.matmul_f16(a, w, M, K, N, flags=flags)
+            assert_close(from_dev(y), ref, max_abs=3e-2, what=f"mm {M}x{K}x{N} f{flags}")
+    # batched (Bn=4), t1 (q . k^T form)
+    Bn, M, K, N = 4, 33, 128, 70
+    a = normal_f16(rng, Bn * M * K)
+    w = normal_f16(rng, Bn * N * K)
+    flags = (Bn << 16) | 4 | 2
+    y = torch.zeros(Bn * M * N, dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_matmul_f16(ptr(to_dev(a, torch_dev)), ptr(to_dev(w, torch_dev)), ptr(y), M, K, N, 0, N,
+                                flags, stream_ptr()) == 0
+    _sync()
+    assert_close(from_dev(y), oracle.matmul_f16(a, w, M, K, N, flags=flags), max_abs=3e-2, what="batched")
+    # SPLIT window: columns [64, 128) of N_full = 192 only
+    M, K, Nf = 8, 64, 192
+    a = normal_f16(rng, M * K)
+    w = normal_f16(rng, Nf * K)
+    y = torch.zeros(M * Nf, dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_matmul_f16(ptr(to_dev(a, torch_dev)), ptr(to_dev(w, torch_dev)), ptr(y), M, K, Nf, 64, 64,
+                                2, stream_ptr()) == 0
+    _sync()
+    got = from_dev(y).reshape(M, Nf)
+    ref = oracle.matmul_f16(a, w, M, K, Nf, 64, 64, 2).reshape(M, Nf)
+    assert np.all(got[:, :64] == 0) and np.all(got[:, 128:] == 0)
+    assert_close(got[:, 64:128], ref[:, 64:128], max_abs=3e-2, what="split")
+
+
+# ---------------------------------------------------------------- attention --
+SCALE = float(np.float16(1.0 / math.sqrt(128)))
+
+
+@pytest.mark.parametrize("S,H,KVH,causal", [(1024, 16, 8, True), (200, 4, 2, True), (130, 8, 8, False),
+                                            (1, 2, 1, True)])
+def test_attn_prefill(lib, oracle, torch_dev, S, H, KVH, causal):
+    """Config 3 prefill: Q/K/V ~N(0,1), 16 Q / 8 KV heads, hd 128, scale 1/sqrt(128)."""
+    import torch
+    rng = np.random.default_rng(S + H)
+    hd = 128
+    q, k, v = normal_f16(rng, S, H, hd), normal_f16(rng, S, KVH, hd), normal_f16(rng, S, KVH, hd)
+    out = torch.empty((S, H, hd), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_attn_prefill(ptr(to_dev(q, torch_dev)), ptr(to_dev(k, torch_dev)), ptr(to_dev(v, torch_dev)),
+                                  ptr(out), S, H, KVH, hd, SCALE, int(causal), stream_ptr()) == 0
+    _sync()
+    ref = oracle.attn_prefill(q, k, v, SCALE, causal)
+    got = from_dev(out)
+    assert_close(got, ref, what=f"attn S={S}")
+    if causal:   # query 0 sees only key 0: the output is V[0] exactly
+        rep = H // KVH
+        for h in range(H):
+            assert np.array_equal(got[0, h], v[0, h // rep])
+
+
+@pytest.mark.parametrize("n_kv,H,KVH", [(4096, 16, 8), (77, 32, 8), (1, 16, 8)])
+def test_attn_decode(lib, oracle, torch_dev, n_kv, H, KVH):
+    """Config 3 decode: batch 1 over a KV cache of n_kv tokens in the reference ring layout."""
+    import torch
+    rng = np.random.default_rng(n_kv + H)
+    hd = 128
+    kv_elems = KVH * hd
+    state_bytes = 4096 * kv_elems * 4
+    ring = oracle.KVRing(state_bytes, kv_elems)
+    ks, vs = normal_f16(rng, n_kv, kv_elems), normal_f16(rng, n_kv, kv_elems)
+    for t in range(n_kv):
+        ring.append(ks[t], vs[t])
+    q = normal_f16(rng, H, hd)
+    ring_d = torch.zeros(state_bytes, dtype=torch.uint8, device=torch_dev)
+    assert lib.gehtp_kv_append(ptr(ring_d), state_bytes, ptr(to_dev(ks, torch_dev)), ptr(to_dev(vs, torch_dev)),
+                               kv_elems, n_kv, 0, stream_ptr()) == 0
+    _sync()
+    assert np.array_equal(ring_d.cpu().numpy(), ring.buf), "device ring differs from the reference ring"
+    wf = lib.gehtp_attn_decode_work_floats(n_kv, H, hd)
+    work = torch.empty(wf, dtype=torch.float32, device=torch_dev)
+    out = torch.empty((H, hd), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_attn_decode(ptr(to_dev(q, torch_dev)), ptr(ring_d), state_bytes, ptr(out), n_kv, H, KVH, hd,
+                                 SCALE, ptr(work), wf, stream_ptr()) == 0
+    _sync()
+    ref = ring.attn_decode(q, n_kv, H, KVH, hd, SCALE)
+    assert_close(from_dev(out), ref, what=f"decode n_kv={n_kv}")
+
+
+def test_decode_matches_prefill_last_row(lib, torch_dev):
+    """Decode of token t over keys [0, t] equals row t of the causal prefill (reference's
+    decode==prefill gate, scripts/judge_logits.py: cos >= 0.9999)."""
+    import torch
+    rng = np.random.default_rng(3)
+    S, H, KVH, hd = 300, 16, 8, 128
+    q, k, v = normal_f16(rng, S, H, hd), normal_f16(rng, S, KVH, hd), normal_f16(rng, S, KVH, hd)
+    out = torch.empty((S, H, hd), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_attn_prefill(ptr(to_dev(q, torch_dev)), ptr(to_dev(k, torch_dev)), ptr(to_dev(v, torch_dev)),
+                                  ptr(out), S, H, KVH, hd, SCALE, 1, stream_ptr()) == 0
+    state_bytes = 512 * KVH * hd * 4
+    ring_d = torch.zeros(state_bytes, dtype=torch.uint8, device=torch_dev)
+    assert lib.gehtp_kv_append(ptr(ring_d), state_bytes, ptr(to_dev(k.reshape(S, -1), torch_dev)),
+                               ptr(to_dev(v.reshape(S, -1), torch_dev)), KVH * hd, S, 0, stream_ptr()) == 0
+    wf = lib.gehtp_attn_decode_work_floats(S, H, hd)
+    work = torch.empty(wf, dtype=torch.float32, device=torch_dev)
+    dec = torch.empty((H, hd), dtype=torch.float16, device=torch_dev)
+    qd = to_dev(q, torch_dev)
+    assert lib.gehtp_attn_decode(ptr(qd[S - 1]), ptr(ring_d), state_bytes, ptr(dec), S, H, KVH, hd, SCALE,
+                                 ptr(work), wf, stream_ptr()) == 0
+    _sync()
+    assert_close(from_dev(dec), from_dev(out)[S - 1], max_abs=4e-3, min_cos=0.99999, what="decode vs prefill")
