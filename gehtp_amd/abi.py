@@ -172,6 +172,15 @@ def load_library(path: str | Path):
     if not path.exists():
         raise FileNotFoundError(
             f"{path} is not built: run `python -m gehtp_amd.build` (there is no CPU fallback)")
+    # One HIP runtime per process: PyTorch-ROCm bundles its own libamdhip64.so.7. When
+    # torch is present, load it first so libgehtp's libamdhip64.so.7 dependency binds to
+    # that already-loaded copy (same SONAME) and device pointers from torch tensors are
+    # valid in the runtime our kernels launch through. Without torch the system ROCm
+    # runtime is used.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(str(path))
     for name, (res, args) in EXPORTS.items():
         fn = getattr(lib, name)

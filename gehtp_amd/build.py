@@ -26,6 +26,9 @@ ARCH = "gfx950"
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # No FP contraction: ops the reference rounds through f16 must not be fused
+    # (clang otherwise narrows f32 mul/add of f16 values to f16 and fuses them).
+    "-ffp-contract=off",
     "-Wall", "-Wno-unused-result", "-Wno-unused-variable",
 ]
 SOURCES = ["wt_parse.cpp", "engine.cpp", "capi.cpp",

@@ -338,8 +338,11 @@ int load_tempoff(const wt_blob* b, char* err, size_t errn) {
 }
 
 // STATE slot (oplist_exec.c:2071-2102): [n][n x bytes], zeroed, process lifetime.
+// The reference loads the table once per process. Here a blob whose STATE table
+// differs from the loaded one (another model in the same process) replaces it with
+// fresh zeroed states; a blob with the same table, or with none, keeps the states,
+// so a prefill blob and a decode blob of one model share their KV rings.
 int load_states(const wt_blob* b, char* err, size_t errn) {
-    if (g.states_loaded) return 0;
     for (uint32_t s = 0; s < b->n_slots; ++s) {
         if (b->slots[s].addr != WT_SLOT_STATE) continue;
         const uint8_t* p = b->weight_base + b->slots[s].offset;
@@ -349,6 +352,20 @@ int load_states(const wt_blob* b, char* err, size_t errn) {
         std::memcpy(&n, p, 4);
         if (n == 0 || n > WT_MAX_STATES || len < 4u + n * 4u)
             return ERR("state slot table bad (n=%u len=%u)", n, len);
+        bool same = g.states_loaded && g.n_states == n;
+        for (uint32_t i = 0; same && i < n; ++i) {
+            uint32_t bytes;
+            std::memcpy(&bytes, p + 4 + 4 * i, 4);
+            same = g.st[i].bytes == bytes;
+        }
+        if (same) return 0;
+        for (uint32_t i = 0; i < g.n_states; ++i) {
+            if (g.st[i].dev) hipFree(g.st[i].dev);
+            g.st[i] = State{};
+        }
+        g.n_states = 0;
+        if (g.counters_dev && hipMemset(g.counters_dev, 0, WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
+            return ERR("counter clear failed");
         for (uint32_t i = 0; i < n; ++i) {
             uint32_t bytes;
             std::memcpy(&bytes, p + 4 + 4 * i, 4);

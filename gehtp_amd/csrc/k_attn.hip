@@ -21,6 +21,10 @@ typedef float f16x_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Reinterpret a 32-bit word as two halves. Takes the word BY VALUE: a bit cast applied
+// directly to an ext_vector element (v[e]) miscompiles to always reading element 0.
+__device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+
 constexpr int HD = 128;          // head dim this kernel is built for
 constexpr int QT = 128;          // queries per workgroup (4 waves x 32)
 constexpr int KT = 64;           // keys per LDS stage
@@ -198,8 +202,8 @@ __global__ __launch_bounds__(256) void attn_decode_chunk_kernel(
             for (int r = 0; r < REP; ++r)
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, kv4[e]),
-                                                    __builtin_bit_cast(h2_t, qv[r][e]), acc[r], false);
+                    acc[r] = __builtin_amdgcn_fdot2(as_h2(kv4[e]),
+                                                    as_h2(qv[r][e]), acc[r], false);
         }
 #pragma unroll
         for (int r = 0; r < REP; ++r) {

@@ -17,6 +17,10 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f16x_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Reinterpret a 32-bit word as two halves. Takes the word BY VALUE: a bit cast applied
+// directly to an ext_vector element (v[e]) miscompiles to always reading element 0.
+__device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -55,8 +59,8 @@ __global__ __launch_bounds__(256) void gemv_nk_kernel(const __half* __restrict__
                 const u32x4 xv = xs[m * kc + c];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    acc[m] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, wv[e]),
-                                                    __builtin_bit_cast(h2_t, xv[e]), acc[m], false);
+                    acc[m] = __builtin_amdgcn_fdot2(as_h2(wv[e]),
+                                                    as_h2(xv[e]), acc[m], false);
             }
         }
 #pragma unroll

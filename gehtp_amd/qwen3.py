@@ -1,0 +1,232 @@
+"""Runlist emitter for Qwen3-style decoder models with W4A16 (int4 g64) linears.
+
+Writes WTOP blobs for prefill and for one decode step, in the reference engine's
+terms: weights as EXT_WGT slots of one external image (so a multi-GB model is not
+inlined into the blob), one persistent KV-ring STATE per layer, activations in
+temps, the token embeddings arriving through the EXT_IN slot.
+
+Per layer (pre-norm, eps 1e-6):
+    h  = RMSNORM2(x, g_attn)
+    q, k, v = MATMUL_W4G(h, Wq | Wk | Wv)
+    q, k = RMSNORM2 per head (q_norm, k_norm; Qwen3's QK-norm), ROPE (theta)
+    KV append (prefill: KV_APPEND_N, decode: KV_APPEND) into the layer's ring
+    a  = ATTN (prefill, causal) | ATTN_DECODE (one token over the ring)
+    x  = x + MATMUL_W4G(a, Wo)
+    h  = RMSNORM2(x, g_ffn)
+    x  = x + MATMUL_W4G(silu(h Wg^T) * (h Wu^T), Wd)
+then RMSNORM2(x, g_final), the fp16 lm_head (MATMUL_F16, w stored [V, D]) on the
+last token and ARGMAX. RoPE positions come from the layer state's counter, so the
+decode blob is identical for every step.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from .abi import WT_KV_POS_AUTO, opcodes as OP
+from .runlist import BlobBuilder, f32_bits
+
+
+@dataclass(frozen=True)
+class Qwen3Config:
+    layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    ffn: int
+    vocab: int
+    head_dim: int = 128
+    theta: float = 1e6
+    group: int = 64
+
+    @property
+    def q_dim(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.kv_heads * self.head_dim
+
+    @property
+    def scale(self) -> float:
+        # the attention scale as an fp16 constant, as reference runlists carry it
+        return float(np.float16(1.0 / math.sqrt(self.head_dim)))
+
+    def linears(self):
+        """(name, N, K) of the per-layer W4A16 linears."""
+        D, F = self.hidden, self.ffn
+        return [("wq", self.q_dim, D), ("wk", self.kv_dim, D), ("wv", self.kv_dim, D),
+                ("wo", D, self.q_dim), ("wg", F, D), ("wu", F, D), ("wd", D, F)]
+
+    def decode_weight_bytes(self) -> int:
+        """Algorithmic HBM bytes of one decode token: int4 weights + fp16 scales of every
+        linear, plus the fp16 lm_head."""
+        per_layer = sum(n * k // 2 + n * (k // self.group) * 2 for _, n, k in self.linears())
+        return self.layers * per_layer + self.vocab * self.hidden * 2
+
+    def prefill_flops(self, S: int) -> float:
+        lin = sum(2.0 * S * n * k for _, n, k in self.linears()) * self.layers
+        attn = 2 * 2.0 * self.heads * (S * (S + 1) / 2) * self.head_dim * self.layers
+        return lin + attn + 2.0 * self.vocab * self.hidden   # lm_head on the last token
+
+
+# BASELINE configs 4 and 5.
+CONFIG_08B_LAYER = Qwen3Config(layers=1, hidden=1024, heads=16, kv_heads=8, ffn=3072, vocab=151936)
+CONFIG_4B = Qwen3Config(layers=36, hidden=2560, heads=32, kv_heads=8, ffn=9728, vocab=151936)
+
+
+class Weights:
+    """Random-init weights laid out in ONE external image (numpy uint8), plus views.
+
+    int4 values are uniform in [-8, 7] (random bytes = two uniform nibbles), scales
+    U[0.005, 0.02], norm gammas U(0.8, 1.2), embeddings ~N(0, 1) (tied lm_head)."""
+
+    def __init__(self, cfg: Qwen3Config, seed: int = 0, embed_std: float = 1.0):
+        self.cfg = cfg
+        rng = np.random.default_rng(seed)
+        layout, off = {}, 0
+
+        def reserve(name, nbytes):
+            nonlocal off
+            off = (off + 127) // 128 * 128
+            layout[name] = (off, nbytes)
+            off += nbytes
+
+        for l in range(cfg.layers):
+            for nm, n, k in cfg.linears():
+                reserve(f"{l}.{nm}.q", n * k // 2)
+                reserve(f"{l}.{nm}.s", n * (k // cfg.group) * 2)
+            for nm, n in (("g_attn", cfg.hidden), ("g_ffn", cfg.hidden), ("q_norm", cfg.head_dim),
+                          ("k_norm", cfg.head_dim)):
+                reserve(f"{l}.{nm}", n * 2)
+        reserve("g_final", cfg.hidden * 2)
+        reserve("embed", cfg.vocab * cfg.hidden * 2)
+        self.layout = layout
+        self.image = np.zeros((off + 127) // 128 * 128, np.uint8)
+        for name, (o, nb) in layout.items():
+            view = self.image[o:o + nb]
+            if name.endswith(".q"):
+                view[:] = np.frombuffer(rng.bytes(nb), np.uint8)
+            elif name.endswith(".s"):
+                view.view(np.float16)[:] = rng.uniform(0.005, 0.02, nb // 2).astype(np.float16)
+            elif name == "embed":
+                e = view.view(np.float16).reshape(cfg.vocab, cfg.hidden)
+                for r0 in range(0, cfg.vocab, 8192):
+                    r1 = min(cfg.vocab, r0 + 8192)
+                    e[r0:r1] = (rng.standard_normal((r1 - r0, cfg.hidden), np.float32) * embed_std).astype(np.float16)
+            else:
+                view.view(np.float16)[:] = rng.uniform(0.8, 1.2, nb // 2).astype(np.float16)
+
+    def get(self, name: str) -> np.ndarray:
+        o, nb = self.layout[name]
+        return self.image[o:o + nb]
+
+    def f16(self, name: str) -> np.ndarray:
+        return self.get(name).view(np.float16)
+
+    def linear(self, layer: int, nm: str):
+        """(wq packed uint8 [N, K/2], scales fp16 [N, K/64])."""
+        n, k = {x[0]: (x[1], x[2]) for x in self.cfg.linears()}[nm]
+        return (self.get(f"{layer}.{nm}.q").reshape(n, k // 2),
+                self.f16(f"{layer}.{nm}.s").reshape(n, k // self.cfg.group))
+
+    def embed(self) -> np.ndarray:
+        return self.f16("embed").reshape(self.cfg.vocab, self.cfg.hidden)
+
+
+class _Emitter:
+    def __init__(self, cfg: Qwen3Config, w: Weights, max_pos: int):
+        self.cfg, self.w, self.max_pos = cfg, w, max_pos
+        self.bb = BlobBuilder()
+        self.slot = {}
+        # EXT_WGT slots pointing into the external image (descriptors only).
+        for name, (off, nb) in w.layout.items():
+            count = nb * 2 if name.endswith(".q") else nb // 2
+            self.slot[name] = self._ext_slot(off, nb, count)
+        self.zero_bias = self.bb.add_slot(np.zeros(max(cfg.hidden, cfg.head_dim), np.float16))
+        self.states = [self.bb.add_state(max_pos * cfg.kv_dim * 4) for _ in range(cfg.layers)]
+        self.t = {n: self.bb.temp() for n in
+                  ("x", "x1", "h", "q", "k", "v", "qn", "kn", "qr", "kr", "a", "o", "g", "u", "sg", "m", "d",
+                   "last", "logits", "tok")}
+
+    def _ext_slot(self, off, nb, count):
+        from .abi import WT_SLOT_EXT_WGT
+        from .runlist import _Slot
+        self.bb.slots.append(_Slot(None, nb, count, WT_SLOT_EXT_WGT, off))
+        return len(self.bb.slots) - 1
+
+    def ref(self, name):
+        return self.bb.slot_ref(self.slot[name])
+
+    def norm(self, x, gamma, y, n):
+        bb = self.bb
+        bb.op(OP.RMSNORM2_F16, x, self.ref(gamma), bb.slot_ref(self.zero_bias), y, n)
+
+    def w4g(self, a, l, nm, y, M):
+        n, k = {x[0]: (x[1], x[2]) for x in self.cfg.linears()}[nm]
+        self.bb.op(OP.MATMUL_W4G_F16, a, self.ref(f"{l}.{nm}.q"), self.ref(f"{l}.{nm}.s"), y, M, k, n,
+                   self.cfg.group, 2)
+
+    def layer(self, l: int, S: int, x_in: int, decode: bool):
+        c, bb, t = self.cfg, self.bb, self.t
+        st = self.states[l]
+        self.norm(x_in, f"{l}.g_attn", t["h"], S * c.hidden)
+        self.w4g(t["h"], l, "wq", t["q"], S)
+        self.w4g(t["h"], l, "wk", t["k"], S)
+        self.w4g(t["h"], l, "wv", t["v"], S)
+        # Qwen3 QK-norm: RMSNorm over each head's 128 dims (row width = gamma length)
+        self.norm(t["q"], f"{l}.q_norm", t["qn"], S * c.q_dim)
+        self.norm(t["k"], f"{l}.k_norm", t["kn"], S * c.kv_dim)
+        bb.op(OP.ROPE_F16, t["qn"], t["qr"], S, c.heads, c.head_dim, st, f32_bits(c.theta), c.q_dim)
+        bb.op(OP.ROPE_F16, t["kn"], t["kr"], S, c.kv_heads, c.head_dim, st, f32_bits(c.theta), c.kv_dim)
+        if decode:
+            bb.op(OP.KV_APPEND_F16, t["kr"], t["v"], st, WT_KV_POS_AUTO)
+            bb.op(OP.ATTN_DECODE_F16, t["qr"], st, t["a"], WT_KV_POS_AUTO, c.heads, c.kv_heads, c.head_dim,
+                  f32_bits(c.scale))
+        else:
+            bb.op(OP.KV_APPEND_N_F16, t["kr"], t["v"], st, WT_KV_POS_AUTO, S, c.kv_dim)
+            bb.op(OP.ATTN_F16, t["qr"], t["kr"], t["v"], t["a"], S, c.heads, c.kv_heads, c.head_dim,
+                  f32_bits(c.scale), 1)
+        self.w4g(t["a"], l, "wo", t["o"], S)
+        bb.op(OP.ADD_F16, x_in, t["o"], t["x1"], S * c.hidden)
+        self.norm(t["x1"], f"{l}.g_ffn", t["h"], S * c.hidden)
+        self.w4g(t["h"], l, "wg", t["g"], S)
+        self.w4g(t["h"], l, "wu", t["u"], S)
+        bb.op(OP.UNARY_F16, t["g"], t["sg"], S * c.ffn, 12)          # SiLU
+        bb.op(OP.BINARY_F16, t["sg"], t["u"], t["m"], S * c.ffn, 2)  # * up
+        self.w4g(t["m"], l, "wd", t["d"], S)
+        bb.op(OP.ADD_F16, t["x1"], t["d"], t["x"], S * c.hidden)
+
+    def head(self, S: int):
+        c, bb, t = self.cfg, self.bb, self.t
+        self.norm(t["x"], "g_final", t["h"], S * c.hidden)
+        src = t["h"]
+        if S > 1:   # lm_head on the last token only
+            n = S * c.hidden
+            bb.op(OP.STRIDED_SLICE_F16, t["h"], t["last"], c.hidden, 1, n - c.hidden, 0, 0, n, 1, 1,
+                  1, 1, 1, n, 1, 1)
+            src = t["last"]
+        bb.op(OP.MATMUL_F16, src, self.ref("embed"), t["logits"], 1, c.hidden, c.vocab, 2)
+        bb.op(OP.ARGMAX_F16, t["logits"], t["tok"], c.vocab)
+
+    def emit(self, S: int, decode: bool) -> bytes:
+        c = self.cfg
+        xin = self.bb.add_input_slot(S * c.hidden * 2)
+        for l in range(c.layers):
+            self.layer(l, S, self.bb.slot_ref(xin) if l == 0 else self.t["x"], decode)
+        self.head(S)
+        return self.bb.build()
+
+
+def emit_prefill(cfg: Qwen3Config, w: Weights, S: int, max_pos: int):
+    """(blob bytes, temp ids): a prefill of S tokens; input = embeddings [S, hidden] fp16."""
+    e = _Emitter(cfg, w, max_pos)
+    return e.emit(S, decode=False), dict(e.t)
+
+
+def emit_decode(cfg: Qwen3Config, w: Weights, max_pos: int):
+    """(blob bytes, temp ids): one decode step; input = the token's embedding [hidden]."""
+    e = _Emitter(cfg, w, max_pos)
+    return e.emit(1, decode=True), dict(e.t)

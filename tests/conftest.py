@@ -45,3 +45,10 @@ def torch_dev():
 @pytest.fixture
 def rng():
     return np.random.default_rng(1234)
+
+
+@pytest.fixture(autouse=True)
+def _release_device_operands():
+    yield
+    import helpers
+    helpers.KEEP_ALIVE.clear()

@@ -41,12 +41,21 @@ def normal_f16(rng, *shape):
 
 
 # ---- torch plumbing (GPU tests only) ----
+# Device tensors made by to_dev stay referenced until the test ends (conftest clears
+# this list), so `ptr(to_dev(x))` inside a call cannot hand a kernel freed memory that
+# the caching allocator gives to the next operand.
+KEEP_ALIVE: list = []
+
+
 def to_dev(a, dev):
     import torch
     a = np.ascontiguousarray(a)
     if a.dtype == np.float16:
-        return torch.from_numpy(a.view(np.int16)).to(dev).view(torch.float16)
-    return torch.from_numpy(a).to(dev)
+        t = torch.from_numpy(a.view(np.int16)).to(dev).view(torch.float16)
+    else:
+        t = torch.from_numpy(a).to(dev)
+    KEEP_ALIVE.append(t)
+    return t
 
 
 def from_dev(t) -> np.ndarray:

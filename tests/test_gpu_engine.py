@@ -157,6 +157,7 @@ def test_kv_gather_and_overflow(engine, oracle):
     bb = BlobBuilder()
     st = bb.add_state(max_pos * kv * 4)
     ks, vs = bb.add_input_slot(kv * 2), bb.add_slot(np.zeros(kv, np.float16))
+    bb.temp()                     # temp id 0 means "skip this face" in KV_GATHER
     tkT, tvo = bb.temp(), bb.temp()
     bb.op(OP.KV_APPEND_F16, bb.slot_ref(ks), bb.slot_ref(vs), st, WT_KV_POS_AUTO)
     bb.op(OP.KV_GATHER_F16, st, tkT, tvo, WT_KV_POS_AUTO, H, KVH, hd)
