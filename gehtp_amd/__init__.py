@@ -59,6 +59,7 @@ class Engine:
 
     def __init__(self, path: str | Path | None = None):
         self.lib = load_library(path or lib_path)
+        self._obuf = None
 
     def parse(self, data: bytes) -> ParsedBlob:
         return ParsedBlob(self.lib, data)
@@ -86,15 +87,18 @@ class Engine:
         err = C.create_string_buffer(512)
         m = C.c_uint32(0)
         us = (C.c_int64 * max(pb.n_ops, 1))() if timing else None
-        ibuf = C.create_string_buffer(bytes(inp), len(inp)) if inp is not None else None
-        cap = out_bytes if out_bytes is not None else 64 << 20
-        obuf = C.create_string_buffer(cap)
-        rc = self.lib.wt_exec_run_io(C.byref(pb.blob), ibuf, obuf, out_temp, C.byref(m), us, err, 512)
+        ibuf = C.c_char_p(bytes(inp)) if inp is not None else None
+        # run_io copies the output temp's last-written bytes into out_ptr, so the buffer
+        # must hold the largest output the caller expects (out_bytes, default 64 MiB).
+        # One buffer per engine, allocated once: a fresh 64 MiB buffer per decode step
+        # would cost more than the step.
+        cap = max(out_bytes or 0, 64 << 20)
+        if self._obuf is None or len(self._obuf) < cap:
+            self._obuf = C.create_string_buffer(cap)
+        rc = self.lib.wt_exec_run_io(C.byref(pb.blob), ibuf, self._obuf, out_temp, C.byref(m), us, err, 512)
         self._check(rc, err)
         n = self.lib.wt_exec_temp_last_bytes(out_temp)
-        if n > cap:
-            raise WtExecError(-1, f"output temp {out_temp} has {n} bytes > buffer {cap}")
-        return obuf.raw[:n], (list(us) if timing else None)
+        return C.string_at(self._obuf, n), (list(us) if timing else None)
 
     def temp(self, tid: int) -> bytes:
         """Bytes last written to temp tid (host copy)."""

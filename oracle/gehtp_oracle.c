@@ -209,6 +209,24 @@ static void matmul_nk_core(const uint16_t* a, const float* wT /* [K][N] f32 */,
 
 static int matmul_nk_mt(const uint16_t* a, const uint16_t* w_nk, uint16_t* y,
                         uint32_t M, uint32_t K, uint32_t N, int n_threads) {
+    if (n_threads < 1) n_threads = 1;
+    if (M <= 4) {
+        /* decode sizes: the reference's own loop order (row n of w streamed once per m) */
+        float* af = (float*)malloc((size_t)M * K * sizeof(float));
+        if (!af) return -1;
+        for (size_t i = 0; i < (size_t)M * K; i++) af[i] = F(a[i]);
+#pragma omp parallel for num_threads(n_threads) schedule(static)
+        for (uint32_t n = 0; n < N; n++) {
+            const uint16_t* wr = w_nk + (size_t)n * K;
+            for (uint32_t m = 0; m < M; m++) {
+                float acc = 0.0f;
+                for (uint32_t k = 0; k < K; k++) acc += af[(size_t)m * K + k] * F(wr[k]);
+                y[(size_t)m * N + n] = H(acc);
+            }
+        }
+        free(af);
+        return 0;
+    }
     float* wT = (float*)malloc((size_t)K * N * sizeof(float));
     if (!wT) return -1;
     for (uint32_t n = 0; n < N; n++)

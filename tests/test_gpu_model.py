@@ -1,0 +1,64 @@
+"""End-to-end: Qwen3-style W4A16 runlists (gehtp_amd.qwen3) on the engine vs the oracle
+model, teacher-forced: per step logits within tolerance and top-1 identical (the
+reference's decode gate, scripts/judge_logits.py: cos >= 0.9999, exact top-1)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import cosine
+
+from gehtp_amd.qwen3 import CONFIG_08B_LAYER, Qwen3Config, Weights, emit_decode, emit_prefill
+
+pytestmark = pytest.mark.gpu
+
+SMALL = Qwen3Config(layers=2, hidden=512, heads=4, kv_heads=2, ffn=1024, vocab=3000)
+
+
+def _run(engine, cfg, S, n_dec, seed, max_pos=256):
+    from oracle.qwen3_ref import RefModel
+    w = Weights(cfg, seed=seed)
+    engine.shutdown()
+    engine.set_ext_weights(w.image.ctypes.data)
+    pre, tp = emit_prefill(cfg, w, S, max_pos)
+    dec, td = emit_decode(cfg, w, max_pos)
+    pp, pd = engine.parse(pre), engine.parse(dec)
+    engine.state_reset()
+    rng = np.random.default_rng(seed + 1)
+    ids = rng.integers(0, cfg.vocab, S + n_dec)
+    emb = w.embed()
+    ref = RefModel(cfg, w, max_pos)
+    out, _ = engine.run_io(pp, np.ascontiguousarray(emb[ids[:S]]).tobytes(), tp["tok"])
+    got = [np.frombuffer(engine.temp(tp["logits"]), np.float16)[:cfg.vocab].copy()]
+    refl = [ref.prefill(np.ascontiguousarray(emb[ids[:S]]))]
+    assert int(np.frombuffer(out, np.int32)[0]) == int(np.argmax(got[0].astype(np.float32)))
+    for t in range(n_dec):   # teacher forced: both sides consume ids[S + t]
+        engine.run_io(pd, emb[ids[S + t]].tobytes(), td["tok"])
+        got.append(np.frombuffer(engine.temp(td["logits"]), np.float16)[:cfg.vocab].copy())
+        refl.append(ref.decode(emb[ids[S + t]]))
+    engine.shutdown()
+    return got, refl
+
+
+def _check(got, refl, min_cos):
+    for step, (g, r) in enumerate(zip(got, refl)):
+        gf, rf = g.astype(np.float32), r.astype(np.float32)
+        assert np.isfinite(gf).all()
+        c = cosine(gf, rf)
+        top = np.sort(rf)[-2:]
+        margin = float(top[1] - top[0])
+        assert c >= min_cos, f"step {step}: cos {c:.6f}"
+        assert int(np.argmax(gf)) == int(np.argmax(rf)), f"step {step}: top-1 differs (ref margin {margin:.3g})"
+
+
+def test_small_model_prefill_and_decode(engine):
+    got, refl = _run(engine, SMALL, S=40, n_dec=6, seed=3)
+    _check(got, refl, 0.9999)
+
+
+def test_config4_layer_prefill_then_decode(engine):
+    """BASELINE config 4 geometry (one 0.8B-class layer: hidden 1024, 16Q/8KV hd128, FFN 3072,
+    vocab 151936), prefill then greedy-position decode steps, teacher forced. The prefill is
+    shortened to 128 tokens and 4 decode steps to keep the CPU oracle within seconds."""
+    got, refl = _run(engine, CONFIG_08B_LAYER, S=128, n_dec=4, seed=5)
+    _check(got, refl, 0.9999)
