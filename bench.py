@@ -44,11 +44,26 @@ def parse_args():
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the GEMV roofline replay + a 256 MiB copy (for PMC counter runs)")
     return ap.parse_args()
 
 
 def w4g_bytes(n: int, k: int) -> int:
     return n * k // 2 + n * (k // 64) * 2 + k * 2 + n * 2
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed PMC summary (FETCH_SIZE + WRITE_SIZE
+    runs, calibrated with a copy kernel), or None when absent."""
+    p = ROOT / "profiles" / "w4g_gemv_4b_decode_pmc.md"
+    try:
+        for line in p.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def main() -> int:
@@ -57,6 +72,8 @@ def main() -> int:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         return 2
+    if args.roofline_only:
+        return roofline_only(args)
     import numpy as np
     import torch
 
@@ -123,41 +140,7 @@ def main() -> int:
     _, op_us = eng.run_io(pd, emb[tok].tobytes(), td["tok"], timing=True)
     gpu_us_step = float(sum(op_us))
 
-    # Roofline of the dominant decode kernel: the W4A16 GEMV over one token's linears
-    # (36 layers x 7 shapes, the model's own weights), replayed on torch's stream.
-    img = torch.from_numpy(w.image).to(dev)
-    base = img.data_ptr()
-    lin = [(l, nm, n, k) for l in range(cfg.layers) for nm, n, k in cfg.linears()]
-    xs = {k: torch.randn(k, device=dev, dtype=torch.float16) for k in {k for *_, k in lin}}
-    ys = {n: torch.empty(n, device=dev, dtype=torch.float16) for n in {n for _, _, n, _ in lin}}
-    calls = []
-    for l, nm, n, k in lin:
-        qo, _ = w.layout[f"{l}.{nm}.q"]
-        so, _ = w.layout[f"{l}.{nm}.s"]
-        calls.append((xs[k].data_ptr(), base + qo, base + so, ys[n].data_ptr(), n, k))
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
-
-    def replay():
-        for xp, qp, spp, yp, n, k in calls:
-            rc = lib.gehtp_w4g_gemv(xp, k, qp, spp, yp, n, 1, n, k, sp)
-            assert rc == 0, rc
-
-    replay()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(args.roofline_reps):
-        replay()
-    ev1.record(stream)
-    ev1.synchronize()
-    n_launch = len(calls) * args.roofline_reps
-    avg_s = ev0.elapsed_time(ev1) / 1e3 / n_launch
-    bytes_per_launch = sum(w4g_bytes(n, k) for *_, n, k in calls) / len(calls)
-    gemv_gbs = bytes_per_launch / avg_s / 1e9
-    log(f"w4g gemv: {avg_s * 1e6:.2f} us avg over {n_launch} launches, "
-        f"{bytes_per_launch / 1e6:.2f} MB/launch -> {gemv_gbs:.0f} GB/s")
-    del img
+    avg_s, bytes_per_launch, gemv_gbs = gemv_roofline(cfg, w, lib, args.roofline_reps)
 
     # CPU baseline: the oracle on a bounded sample of one decode token.
     cpu = None
@@ -190,11 +173,72 @@ def main() -> int:
         "decode_ideal_tok_s_at_hbm_peak": round(HBM_PEAK_GBS * 1e9 / cfg.decode_weight_bytes(), 1),
         "roofline": {"bound": "hbm", "kernel": "w4g_gemv_kernel<1> (decode W4A16 GEMV)",
                      "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": round(bytes_per_launch), "avg_launch_us": round(avg_s * 1e6, 3)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+    return 0
+
+
+def gemv_roofline(cfg, w, lib, reps):
+    """Roofline of the dominant decode kernel: the W4A16 GEMV over one token's linears
+    (layers x 7 shapes, the model's own weights), replayed back to back on torch's
+    stream and timed with HIP events on that stream. Returns (mean seconds per launch,
+    mean algorithmic bytes per launch, GB/s)."""
+    import torch
+    dev = torch.device("cuda:0")
+    img = torch.from_numpy(w.image).to(dev)
+    base = img.data_ptr()
+    lin = [(l, nm, n, k) for l in range(cfg.layers) for nm, n, k in cfg.linears()]
+    xs = {k: torch.randn(k, device=dev, dtype=torch.float16) for k in {k for *_, k in lin}}
+    ys = {n: torch.empty(n, device=dev, dtype=torch.float16) for n in {n for _, _, n, _ in lin}}
+    calls = []
+    for l, nm, n, k in lin:
+        qo, _ = w.layout[f"{l}.{nm}.q"]
+        so, _ = w.layout[f"{l}.{nm}.s"]
+        calls.append((xs[k].data_ptr(), base + qo, base + so, ys[n].data_ptr(), n, k))
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def replay():
+        for xp, qp, spp, yp, n, k in calls:
+            rc = lib.gehtp_w4g_gemv(xp, k, qp, spp, yp, n, 1, n, k, sp)
+            assert rc == 0, rc
+
+    replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(reps):
+        replay()
+    ev1.record(stream)
+    ev1.synchronize()
+    n_launch = len(calls) * reps
+    avg_s = ev0.elapsed_time(ev1) / 1e3 / n_launch
+    bytes_per_launch = sum(w4g_bytes(n, k) for *_, n, k in calls) / len(calls)
+    gbs = bytes_per_launch / avg_s / 1e9
+    log(f"w4g gemv: {avg_s * 1e6:.2f} us avg over {n_launch} launches, "
+        f"{bytes_per_launch / 1e6:.2f} MB/launch -> {gbs:.0f} GB/s")
+    return avg_s, bytes_per_launch, gbs
+
+
+def roofline_only(args) -> int:
+    """The GEMV replay alone plus a 256 MiB device-to-device copy (the calibration kernel
+    for FETCH_SIZE / WRITE_SIZE counter runs): short enough to run under --pmc."""
+    import torch
+
+    from gehtp_amd import load_library, lib_path
+    from gehtp_amd.qwen3 import CONFIG_4B, Weights
+    w = Weights(CONFIG_4B, seed=args.seed)
+    lib = load_library(lib_path)
+    avg_s, bpl, gbs = gemv_roofline(CONFIG_4B, w, lib, args.roofline_reps)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"roofline_only": True, "avg_launch_us": avg_s * 1e6, "bytes_per_launch": bpl,
+                      "achieved_gbs": gbs, "copy_bytes": 256 << 20}), flush=True)
     return 0
 
 
