@@ -182,28 +182,42 @@ def main() -> int:
 
 
 def gemv_roofline(cfg, w, lib, reps):
-    """Roofline of the dominant decode kernel: the W4A16 GEMV over one token's linears
-    (layers x 7 shapes, the model's own weights), replayed back to back on torch's
-    stream and timed with HIP events on that stream. Returns (mean seconds per launch,
-    mean algorithmic bytes per launch, GB/s)."""
+    """Roofline of the dominant decode kernel: the fused W4A16 GEMV exactly as one decode
+    token runs it (per layer: norm+qkv, o+residual, norm+gate/up+SwiGLU, down+residual;
+    the model's own weights), replayed back to back on torch's stream and timed with HIP
+    events on that stream. Returns (mean seconds per launch, mean algorithmic bytes per
+    launch, GB/s). Algorithmic bytes: int4 weights + fp16 scales + activation in + out
+    (+ gamma, + residual read)."""
     import torch
     dev = torch.device("cuda:0")
     img = torch.from_numpy(w.image).to(dev)
     base = img.data_ptr()
-    lin = [(l, nm, n, k) for l in range(cfg.layers) for nm, n, k in cfg.linears()]
-    xs = {k: torch.randn(k, device=dev, dtype=torch.float16) for k in {k for *_, k in lin}}
-    ys = {n: torch.empty(n, device=dev, dtype=torch.float16) for n in {n for _, _, n, _ in lin}}
-    calls = []
-    for l, nm, n, k in lin:
-        qo, _ = w.layout[f"{l}.{nm}.q"]
-        so, _ = w.layout[f"{l}.{nm}.s"]
-        calls.append((xs[k].data_ptr(), base + qo, base + so, ys[n].data_ptr(), n, k))
+    D, F = cfg.hidden, cfg.ffn
+    nq = cfg.q_dim + 2 * cfg.kv_dim
+    buf = {n: torch.randn(n, device=dev, dtype=torch.float16) for n in {D, cfg.q_dim, nq, F}}
+    out = {n: torch.empty(n, device=dev, dtype=torch.float16) for n in {D, nq, F}}
+    calls, total_bytes = [], 0
+    for l in range(cfg.layers):
+        # (matrix, rows N, K, input, output, gamma name, residual, mode)
+        for nm, n, k, x, y, gname, res, mode in (
+                ("wqkv", nq, D, buf[D], out[nq], f"{l}.g_attn", None, 0),
+                ("wo", D, cfg.q_dim, buf[cfg.q_dim], out[D], None, buf[D], 0),
+                ("wgu", 2 * F, D, buf[D], out[F], f"{l}.g_ffn", None, 1),
+                ("wd", D, F, buf[F], out[D], None, buf[D], 0)):
+            n_out = n // 2 if mode else n
+            qo, _ = w.layout[f"{l}.{nm}.q"]
+            so, _ = w.layout[f"{l}.{nm}.s"]
+            gp = base + w.layout[gname][0] if gname else None
+            calls.append((x.data_ptr(), base + qo, base + so, y.data_ptr(), n, k, gp,
+                          res.data_ptr() if res is not None else None, n_out, mode))
+            total_bytes += w4g_bytes(n, k) - n * 2 + n_out * 2 + (k * 2 if gname else 0) + \
+                (n_out * 2 if res is not None else 0)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
 
     def replay():
-        for xp, qp, spp, yp, n, k in calls:
-            rc = lib.gehtp_w4g_gemv(xp, k, qp, spp, yp, n, 1, n, k, sp)
+        for xp, qp, spp, yp, n, k, gp, rp, n_out, mode in calls:
+            rc = lib.gehtp_w4g_fused(xp, k, qp, spp, yp, n_out, 1, n, k, gp, rp, n_out, mode, sp)
             assert rc == 0, rc
 
     replay()
@@ -216,7 +230,7 @@ def gemv_roofline(cfg, w, lib, reps):
     ev1.synchronize()
     n_launch = len(calls) * reps
     avg_s = ev0.elapsed_time(ev1) / 1e3 / n_launch
-    bytes_per_launch = sum(w4g_bytes(n, k) for *_, n, k in calls) / len(calls)
+    bytes_per_launch = total_bytes / len(calls)
     gbs = bytes_per_launch / avg_s / 1e9
     log(f"w4g gemv: {avg_s * 1e6:.2f} us avg over {n_launch} launches, "
         f"{bytes_per_launch / 1e6:.2f} MB/launch -> {gbs:.0f} GB/s")

@@ -75,6 +75,11 @@ class opcodes:
     ATTN_DECODE_F16 = 42
     ROPE_F16 = 43
     KV_APPEND_N_F16 = 44
+    W4G_FUSED_F16 = 45
+    QK_ROPE_KV_F16 = 46
+
+
+WT_REF_NONE = 0xFFFFFFFF
 
 
 # Arity table (include/oplist_parse.h); opcodes absent here are unknown to wt_parse.
@@ -82,7 +87,7 @@ ARITY = {
     0: 0, 1: 6, 2: 4, 3: 1, 4: 3, 5: 15, 6: 13, 7: 4, 8: 4, 9: 4, 10: 6, 11: 4, 12: 5, 13: 4,
     14: 16, 15: 16, 16: 16, 17: 9, 18: 7, 19: 6, 20: 15, 21: 3, 22: 4, 23: 7, 24: 7, 25: 5,
     26: 12, 27: 8, 28: 14, 29: 6, 30: 12, 33: 8, 34: 7, 35: 9,
-    40: 9, 41: 10, 42: 8, 43: 8, 44: 6,
+    40: 9, 41: 10, 42: 8, 43: 8, 44: 6, 45: 11, 46: 12,
 }
 
 
@@ -148,6 +153,8 @@ EXPORTS = {
     "gehtp_w4g_gemv": (_i, [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "gehtp_w4g_gemm": (_i, [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "gehtp_w4g_dequant": (_i, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "gehtp_w4g_fused": (_i, [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _u32, _vp]),
+    "gehtp_qk_rope_kv": (_i, [_vp, _u32, _u32, _u32, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp, _u32, _vp, _vp]),
     "gehtp_matmul_f16": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp]),
     "gehtp_rmsnorm2": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _vp]),
     "gehtp_softmax": (_i, [_vp, _vp, _u32, _u32, _vp]),

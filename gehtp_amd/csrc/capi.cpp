@@ -45,6 +45,37 @@ int gehtp_w4g_matmul(const void* x, uint32_t ldx, const void* wq, const void* ws
                              : gehtp_w4g_gemm(x, ldx, wq, ws, y, ldy, M, N, K, stream);
 }
 
+int gehtp_w4g_fused(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y, uint32_t ldy,
+                    uint32_t M, uint32_t N, uint32_t K, const void* gamma, const void* res, uint32_t ldr,
+                    uint32_t mode, void* stream) {
+    const uint32_t n_out = mode == 1 ? N / 2 : N;
+    if (mode > 1 || (mode == 1 && (N & 1)) || !w4g_args_ok(x, ldx, wq, ws, y, ldy, n_out, K) ||
+        (gamma && !al16(gamma)) || (res && ldr < n_out))
+        return GEHTP_EINVAL;
+    W4gEpilogue epi;
+    epi.gamma = H(gamma);
+    epi.res = H(res);
+    epi.ldr = ldr;
+    epi.swiglu = mode == 1;
+    if (M <= kW4gGemvMaxM && (size_t)M * K * 2 + (size_t)M * 4096 * 4 <= 65536)
+        return rc(launch_w4g_gemv(H(x), ldx, static_cast<const uint8_t*>(wq), H(ws), Hm(y), ldy, M, N, K,
+                                  S(stream), epi));
+    if (gamma) return GEHTP_EINVAL;   // GEMM path: normalize with gehtp_rmsnorm2 first
+    return rc(launch_w4g_gemm(H(x), ldx, static_cast<const uint8_t*>(wq), H(ws), Hm(y), ldy, M, N, K, S(stream), epi));
+}
+
+int gehtp_qk_rope_kv(const void* qkv, uint32_t n_tok, uint32_t Hh, uint32_t KVH, const void* q_gamma,
+                     const void* k_gamma, float theta, void* q_out, void* k_out, void* v_out, void* ring,
+                     uint32_t state_bytes, void* count_dev, void* stream) {
+    const uint32_t slot_bytes = KVH * 128u * 4u;
+    if (!qkv || !q_gamma || !k_gamma || !q_out || !ring || !count_dev || !Hh || !KVH ||
+        state_bytes % slot_bytes)
+        return GEHTP_EINVAL;
+    return rc(launch_qk_rope_kv(H(qkv), n_tok, Hh, KVH, H(q_gamma), H(k_gamma), theta, Hm(q_out), Hm(k_out),
+                                Hm(v_out), static_cast<uint8_t*>(ring), slot_bytes, state_bytes / slot_bytes,
+                                static_cast<uint32_t*>(count_dev), S(stream)));
+}
+
 int gehtp_w4g_dequant(const void* wq, const void* ws, void* w, uint32_t N, uint32_t K, void* stream) {
     if (!wq || !ws || !w || K % 64 || !al16(wq) || !al16(w)) return GEHTP_EINVAL;
     return rc(launch_w4g_dequant(static_cast<const uint8_t*>(wq), H(ws), Hm(w), N, K, S(stream)));

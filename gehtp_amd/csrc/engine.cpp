@@ -96,6 +96,8 @@ struct Engine {
 
     float* attn_work = nullptr;
     uint32_t attn_work_floats = 0;
+    uint8_t* norm_buf = nullptr;   // normalized rows for OP_W4G_FUSED_F16 on the GEMM path
+    size_t norm_cap = 0;
 
     wt_exec_stats stats{};
     wt_op_ts* ts = nullptr;
@@ -783,11 +785,112 @@ int op_attn_decode(Ctx& cx) {
         g.attn_work = nullptr;
         g.attn_work_floats = 0;
         if (hipMalloc(&g.attn_work, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace alloc");
+        // the leading completion counters must start at zero (kernels leave them zero)
+        if (hipMemset(g.attn_work, 0, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace clear");
         g.attn_work_floats = need;
     }
     CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o, n_kv,
                                     autopos ? g.counters_dev + (A(1) & 0x1FFFu) : nullptr, H, KVH, hd,
                                     scale, g.attn_work, g.attn_work_floats, g.stream));
+    return 0;
+}
+
+// Engine-private device scratch (grown on demand, freed at shutdown).
+int scratch(uint8_t** p, size_t* cap, size_t bytes, char* err, size_t errn) {
+    if (bytes <= *cap) return 0;
+    if (*p) hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    if (hipMalloc(reinterpret_cast<void**>(p), bytes) != hipSuccess) return ERR("scratch alloc %zu", bytes);
+    *cap = bytes;
+    return 0;
+}
+
+int op_w4g_fused(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t M = A(4), K = A(5), N = A(6), mode = A(9), flags = A(10);
+    const bool swiglu = mode == 1;
+    if (mode > 1) return ERR("w4g_fused mode %u unknown", mode);
+    if (!(flags & 2u) || (flags & 0xFFFDu)) return ERR("w4g_fused flags 0x%X unsupported (need t1)", flags);
+    if (K == 0 || K % 64) return ERR("w4g_fused K=%u not a multiple of 64", K);
+    if (swiglu && (N & 1)) return ERR("w4g_fused SwiGLU needs an even row count, got %u", N);
+    const uint32_t n_out = swiglu ? N / 2 : N;
+    const uint32_t ldy = (flags >> 16) ? (flags >> 16) : n_out;
+    if (ldy < n_out) return ERR("w4g_fused output stride %u < %u", ldy, n_out);
+    const __half* a = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const uint8_t* wq = ref_ptr(cx.b, A(1));
+    const __half* ws = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(2)));
+    const __half* gamma = A(7) == WT_REF_NONE ? nullptr : reinterpret_cast<const __half*>(ref_ptr(cx.b, A(7)));
+    const __half* res = A(8) == WT_REF_NONE ? nullptr : reinterpret_cast<const __half*>(ref_ptr(cx.b, A(8)));
+    if (!a || !wq || !ws || (A(7) != WT_REF_NONE && !gamma) || (A(8) != WT_REF_NONE && !res))
+        return ERR("w4g_fused ref fail");
+    const size_t ab = ref_bytes(cx.b, A(0)), qb = ref_bytes(cx.b, A(1)), sb = ref_bytes(cx.b, A(2));
+    if (ab && ab < (uint64_t)M * K * 2u) return ERR("w4g_fused activation smaller than M*K");
+    if (qb && qb < (uint64_t)N * K / 2u) return ERR("w4g_fused weight slot %zu < N*K/2", qb);
+    if (sb && sb < (uint64_t)N * (K / 64) * 2u) return ERR("w4g_fused scale slot %zu < N*K/64*2", sb);
+    if (gamma) {
+        const size_t gb = ref_bytes(cx.b, A(7));
+        if (gb && gb < (uint64_t)K * 2u) return ERR("w4g_fused gamma shorter than K");
+    }
+    if (res) {
+        const size_t rb = ref_bytes(cx.b, A(8));
+        if (rb && rb < (uint64_t)M * n_out * 2u) return ERR("w4g_fused residual smaller than M*N_out");
+    }
+    if (((uintptr_t)a | (uintptr_t)wq | (uintptr_t)gamma) % 16) return ERR("w4g_fused operands not 16-byte aligned");
+    const uint64_t ybytes = ((uint64_t)(M ? M - 1 : 0) * ldy + n_out) * 2u;
+    __half* y = reinterpret_cast<__half*>(temp_get(A(3), (uint32_t)ybytes));
+    if (!y) return ERR("w4g_fused out alloc");
+    g.stats.matmul++;
+    *cx.engine_m = M;
+    W4gEpilogue epi;
+    epi.res = res;
+    epi.ldr = n_out;
+    epi.swiglu = swiglu;
+    const bool gemv_fits = M <= kW4gGemvMaxM && (size_t)M * K * 2 + (size_t)M * 4096 * 4 <= 65536;
+    if (gemv_fits) {
+        epi.gamma = gamma;
+        CHECK_LAUNCH(launch_w4g_gemv(a, K, wq, ws, y, ldy, M, N, K, g.stream, epi));
+        return 0;
+    }
+    const __half* src = a;
+    if (gamma) {   // normalize the rows into scratch, then the GEMM
+        if (scratch(&g.norm_buf, &g.norm_cap, (size_t)M * K * 2, err, errn)) return -1;
+        CHECK_LAUNCH(launch_rmsnorm2(a, gamma, nullptr, reinterpret_cast<__half*>(g.norm_buf), M, K, g.stream));
+        src = reinterpret_cast<const __half*>(g.norm_buf);
+    }
+    CHECK_LAUNCH(launch_w4g_gemm(src, K, wq, ws, y, ldy, M, N, K, g.stream, epi));
+    return 0;
+}
+
+int op_qk_rope_kv(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n_tok = A(5), H = A(6), KVH = A(7), hd = A(8);
+    const float theta = f32_from_bits(A(11));
+    if (hd != 128) return ERR("qk_rope_kv head_dim %u unsupported (128 only)", hd);
+    if (!n_tok || !H || !KVH) return ERR("qk_rope_kv empty shape");
+    const __half* qkv = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const __half* qg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(9)));
+    const __half* kg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(10)));
+    if (!qkv || !qg || !kg) return ERR("qk_rope_kv ref fail");
+    const uint64_t row = (uint64_t)(H + 2 * KVH) * hd;
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < n_tok * row * 2u) return ERR("qk_rope_kv input smaller than n_tok rows");
+    const size_t qgb = ref_bytes(cx.b, A(9)), kgb = ref_bytes(cx.b, A(10));
+    if ((qgb && qgb < hd * 2u) || (kgb && kgb < hd * 2u)) return ERR("qk_rope_kv gamma shorter than head_dim");
+    State* s = state_kv(A(4), KVH * hd, err, errn);
+    if (!s) return -1;
+    const uint32_t si = A(4) & 0x1FFFu;
+    if ((uint64_t)s->count + n_tok > s->nslots)
+        return ERR("qk_rope_kv state %u count=%u + %u > nslots=%u", si, s->count, n_tok, s->nslots);
+    __half* q_out = reinterpret_cast<__half*>(temp_get(A(1), n_tok * H * hd * 2u));
+    __half* k_out = A(2) == WT_REF_NONE ? nullptr : reinterpret_cast<__half*>(temp_get(A(2), n_tok * KVH * hd * 2u));
+    __half* v_out = A(3) == WT_REF_NONE ? nullptr : reinterpret_cast<__half*>(temp_get(A(3), n_tok * KVH * hd * 2u));
+    if (!q_out || (A(2) != WT_REF_NONE && !k_out) || (A(3) != WT_REF_NONE && !v_out)) return ERR("qk_rope_kv out alloc");
+    const uint32_t pos = s->count;
+    s->count += n_tok;
+    for (uint32_t t = 0; t < n_tok; ++t) s->posmap[(pos + t) % s->nslots] = pos + t;
+    CHECK_LAUNCH(launch_qk_rope_kv(qkv, n_tok, H, KVH, qg, kg, theta, q_out, k_out, v_out, s->dev, s->slot_bytes,
+                                   s->nslots, g.counters_dev + si, g.stream));
     return 0;
 }
 
@@ -847,6 +950,8 @@ struct Table {
         fn[OP_ATTN_DECODE_F16] = op_attn_decode;
         fn[OP_ROPE_F16] = op_rope;
         fn[OP_KV_APPEND_N_F16] = op_kv_append_n;
+        fn[OP_W4G_FUSED_F16] = op_w4g_fused;
+        fn[OP_QK_ROPE_KV_F16] = op_qk_rope_kv;
     }
 };
 const Table kTable;
@@ -1032,6 +1137,9 @@ void wt_exec_shutdown(void) {
     if (g.attn_work) hipFree(g.attn_work);
     g.attn_work = nullptr;
     g.attn_work_floats = 0;
+    if (g.norm_buf) hipFree(g.norm_buf);
+    g.norm_buf = nullptr;
+    g.norm_cap = 0;
     // Weights stay resident (keyed by content); states persist until state_reset.
 }
 

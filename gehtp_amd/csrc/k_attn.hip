@@ -169,12 +169,15 @@ constexpr int DC = 64;          // keys per chunk
 constexpr int MAX_REP = 8;
 
 template <int REP>
-__global__ __launch_bounds__(256) void attn_decode_chunk_kernel(
+__global__ __launch_bounds__(256) void attn_decode_kernel(
     const __half* __restrict__ q, const uint8_t* __restrict__ ring, uint32_t slot_bytes,
     uint32_t nslots, uint32_t n_kv_host, const uint32_t* __restrict__ count_dev, uint32_t KVH,
-    float scale_log2, float* __restrict__ work, uint32_t max_chunks) {
+    float scale_log2, float* __restrict__ work, uint32_t* __restrict__ done, uint32_t max_chunks,
+    __half* __restrict__ out) {
     __shared__ float sc[REP][DC];
     __shared__ float red[4][REP][HD];
+    __shared__ float s_M[REP], s_L[REP];
+    __shared__ uint32_t s_last;
     const uint32_t n_kv = count_dev ? *count_dev : n_kv_host;
     const uint32_t c = blockIdx.x, g = blockIdx.y;
     if (c * DC >= n_kv) return;
@@ -278,26 +281,43 @@ __global__ __launch_bounds__(256) void attn_decode_chunk_kernel(
         const uint32_t r = i / HD, d = i % HD;
         wchunk[r * (HD + 2) + 2 + d] = red[0][r][d] + red[1][r][d] + red[2][r][d] + red[3][r][d];
     }
-}
 
-__global__ __launch_bounds__(128) void attn_decode_combine_kernel(
-    const float* __restrict__ work, __half* __restrict__ out, uint32_t n_kv_host,
-    const uint32_t* __restrict__ count_dev, uint32_t rep, uint32_t max_chunks) {
-    const uint32_t n_kv = count_dev ? *count_dev : n_kv_host;
-    const uint32_t h = blockIdx.x, d = threadIdx.x;
-    const uint32_t g = h / rep, r = h % rep;
+    // The last workgroup of this kv head to finish merges the chunks (log-sum-exp) and
+    // resets the completion counter for the next call.
     const uint32_t nc = (n_kv + DC - 1) / DC;
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < nc; ++c)
-        M = fmaxf(M, work[((size_t)g * max_chunks + c) * rep * (HD + 2) + r * (HD + 2)]);
-    float L = 0.0f, O = 0.0f;
-    for (uint32_t c = 0; c < nc; ++c) {
-        const float* wc = work + ((size_t)g * max_chunks + c) * rep * (HD + 2) + r * (HD + 2);
-        const float f = exp2f(wc[0] - M);
-        L += wc[1] * f;
-        O += wc[2 + d] * f;
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = (atomicAdd(&done[g], 1u) == nc - 1) ? 1u : 0u;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    const float* wg = work + (size_t)g * max_chunks * REP * (HD + 2);
+    for (uint32_t r = wave; r < REP; r += 4) {
+        float M = -INFINITY;
+        for (uint32_t cc = lane; cc < nc; cc += 64) M = fmaxf(M, wg[(size_t)cc * REP * (HD + 2) + r * (HD + 2)]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        float L = 0.0f;
+        for (uint32_t cc = lane; cc < nc; cc += 64) {
+            const float* w = wg + (size_t)cc * REP * (HD + 2) + r * (HD + 2);
+            L += w[1] * exp2f(w[0] - M);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+        if (lane == 0) { s_M[r] = M; s_L[r] = L; }
     }
-    out[(size_t)h * HD + d] = __float2half(L > 0.0f ? O / L : 0.0f);
+    __syncthreads();
+    for (uint32_t i = tid; i < REP * HD; i += 256) {
+        const uint32_t r = i / HD, d = i % HD;
+        const float M = s_M[r];
+        float O = 0.0f;
+        for (uint32_t cc = 0; cc < nc; ++cc) {
+            const float* w = wg + (size_t)cc * REP * (HD + 2) + r * (HD + 2);
+            O += w[2 + d] * exp2f(w[0] - M);
+        }
+        out[(size_t)(g * REP + r) * HD + d] = __float2half(s_L[r] > 0.0f ? O / s_L[r] : 0.0f);
+    }
+    if (tid == 0) done[g] = 0;
 }
 
 }  // namespace
@@ -319,15 +339,19 @@ hipError_t launch_attn_prefill(const __half* q, uint32_t ldq, const __half* k, c
     return hipGetLastError();
 }
 
+// Workspace: KVH completion counters (64 floats reserved, zero before the first call;
+// every call leaves them zero) followed by the per-chunk partials.
+constexpr uint32_t kDoneSlots = 64;
+
 uint32_t attn_decode_work_floats(uint32_t max_kv, uint32_t H, uint32_t hd) {
-    return ((max_kv + DC - 1) / DC) * H * (hd + 2);
+    return kDoneSlots + ((max_kv + DC - 1) / DC) * H * (hd + 2);
 }
 
 hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slot_bytes,
                               uint32_t nslots, __half* out, uint32_t n_kv_host,
                               const uint32_t* count_dev, uint32_t H, uint32_t KVH, uint32_t hd,
                               float scale, float* work, uint32_t work_floats, hipStream_t st) {
-    if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
+    if (hd != HD || !KVH || H % KVH || KVH > kDoneSlots) return hipErrorInvalidValue;
     const uint32_t rep = H / KVH;
     if (rep > MAX_REP || slot_bytes != KVH * HD * 4) return hipErrorInvalidValue;
     // Chunks cover every position the ring can hold, so a device-side count never
@@ -337,18 +361,16 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
     if (attn_decode_work_floats(max_kv, H, hd) > work_floats) return hipErrorInvalidValue;
     if (!max_chunks) return hipSuccess;
     const float sl2 = scale * kLog2e;
+    uint32_t* done = reinterpret_cast<uint32_t*>(work);
+    float* part = work + kDoneSlots;
     dim3 grid(max_chunks, KVH);
     switch (rep) {
-    case 1: hipLaunchKernelGGL(attn_decode_chunk_kernel<1>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, work, max_chunks); break;
-    case 2: hipLaunchKernelGGL(attn_decode_chunk_kernel<2>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, work, max_chunks); break;
-    case 4: hipLaunchKernelGGL(attn_decode_chunk_kernel<4>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, work, max_chunks); break;
-    case 8: hipLaunchKernelGGL(attn_decode_chunk_kernel<8>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, work, max_chunks); break;
+    case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, part, done, max_chunks, out); break;
+    case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, part, done, max_chunks, out); break;
+    case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, part, done, max_chunks, out); break;
+    case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, part, done, max_chunks, out); break;
     default: return hipErrorInvalidValue;
     }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_decode_combine_kernel, dim3(H), dim3(HD), 0, st, work, out, n_kv_host,
-                       count_dev, rep, max_chunks);
     return hipGetLastError();
 }
 

@@ -354,6 +354,78 @@ __global__ __launch_bounds__(256) void kv_append_kernel(uint8_t* __restrict__ ri
 
 __global__ void counter_add_kernel(uint32_t* count, uint32_t n) { *count += n; }
 
+// Fused per-token QK-norm + RoPE + KV append (OP_QK_ROPE_KV_F16). Workgroup t handles
+// token t of a [q | k | v] row; each wavefront takes whole 128-dim heads, lane l owning
+// the RoPE pair (l, l+64). Arithmetic = RMSNORM2_F16 (rw 128, zero bias) then the RoPE
+// chain of rope_kernel, so results equal the separate ops bit for bit.
+struct QkRopeKvArgs {
+    const __half* qkv;
+    uint32_t ld, H, KVH;
+    const __half* qg;
+    const __half* kg;
+    float theta;
+    __half* q_out;
+    __half* k_out;
+    __half* v_out;
+    uint8_t* ring;
+    uint32_t slot_bytes, nslots;
+    uint32_t* count;
+    int advance;    // single-workgroup launch: advance the counter in-kernel
+};
+
+__global__ __launch_bounds__(256) void qk_rope_kv_kernel(QkRopeKvArgs A) {
+    constexpr uint32_t HD = 128;
+    __shared__ uint32_t s_pos;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (tid == 0) s_pos = *A.count;
+    __syncthreads();
+    const uint32_t pos = s_pos + t;
+    const uint32_t slot = pos % A.nslots;
+    const double inv = 1.0 / pow((double)A.theta, (double)(2 * lane) / (double)HD);
+    const float c = __half2float(__ushort_as_half(f64_to_f16_bits(cos((double)pos * inv))));
+    const float s = __half2float(__ushort_as_half(f64_to_f16_bits(sin((double)pos * inv))));
+    const __half* row = A.qkv + (size_t)t * A.ld;
+    __half* kface = reinterpret_cast<__half*>(A.ring + (size_t)slot * A.slot_bytes);
+    __half* vface = kface + A.KVH * HD;
+    for (uint32_t r = wave; r < A.H + A.KVH; r += 4) {
+        const bool is_q = r < A.H;
+        const __half* src = row + (size_t)r * HD;   // k heads follow the q heads
+        const __half* gm = is_q ? A.qg : A.kg;
+        const float x1 = h2f(src[lane]), x2 = h2f(src[lane + 64]);
+        double ss = (double)x1 * (double)x1 + (double)x2 * (double)x2;
+        ss = wave_sum_d(ss);
+        const float rms = (float)sqrt(ss / (double)HD + 1e-6);
+        const float h1 = h2f(f2h(__fadd_rn(__fmul_rn(__fdiv_rn(x1, rms), h2f(gm[lane])), 0.0f)));
+        const float h2 = h2f(f2h(__fadd_rn(__fmul_rn(__fdiv_rn(x2, rms), h2f(gm[lane + 64])), 0.0f)));
+        const float a1 = h2f(f2h(__fmul_rn(h1, c))), b1 = h2f(f2h(__fmul_rn(-h2, s)));
+        const float a2 = h2f(f2h(__fmul_rn(h2, c))), b2 = h2f(f2h(__fmul_rn(h1, s)));
+        const __half y1 = f2h(__fadd_rn(a1, b1)), y2 = f2h(__fadd_rn(a2, b2));
+        if (is_q) {
+            __half* qo = A.q_out + (size_t)t * A.H * HD + (size_t)r * HD;
+            qo[lane] = y1;
+            qo[lane + 64] = y2;
+        } else {
+            const uint32_t kh = r - A.H;
+            kface[kh * HD + lane] = y1;
+            kface[kh * HD + lane + 64] = y2;
+            if (A.k_out) {
+                __half* ko = A.k_out + (size_t)t * A.KVH * HD + (size_t)kh * HD;
+                ko[lane] = y1;
+                ko[lane + 64] = y2;
+            }
+        }
+    }
+    const __half* v = row + (size_t)(A.H + A.KVH) * HD;
+    for (uint32_t i = tid; i < A.KVH * HD; i += 256) {
+        vface[i] = v[i];
+        if (A.v_out) A.v_out[(size_t)t * A.KVH * HD + i] = v[i];
+    }
+    if (A.advance) {
+        __syncthreads();
+        if (tid == 0) *A.count = s_pos + 1;
+    }
+}
+
 // KV gather with GQA expansion (oplist_exec.c:2183-2231): kT[h][d][p], v[h][p][d].
 __global__ void kv_gather_kernel(const uint8_t* __restrict__ ring, uint32_t slot_bytes,
                                  uint32_t nslots, __half* __restrict__ kT, __half* __restrict__ vo,
@@ -514,6 +586,20 @@ hipError_t launch_kv_append(uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
                             const __half* v, uint32_t kv_elems, uint32_t pos, uint32_t* count_dev,
                             hipStream_t st) {
     return launch_kv_append_n(ring, slot_bytes, nslots, k, v, kv_elems, 1, pos, count_dev, st);
+}
+
+hipError_t launch_qk_rope_kv(const __half* qkv, uint32_t n_tok, uint32_t H, uint32_t KVH,
+                             const __half* q_gamma, const __half* k_gamma, float theta, __half* q_out,
+                             __half* k_out, __half* v_out, uint8_t* ring, uint32_t slot_bytes,
+                             uint32_t nslots, uint32_t* count_dev, hipStream_t st) {
+    if (!n_tok) return hipSuccess;
+    QkRopeKvArgs A{qkv, (H + 2 * KVH) * 128u, H, KVH, q_gamma, k_gamma, theta, q_out, k_out, v_out,
+                   ring, slot_bytes, nslots, count_dev, n_tok == 1 ? 1 : 0};
+    hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(n_tok), dim3(256), 0, st, A);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || n_tok == 1) return e;
+    hipLaunchKernelGGL(counter_add_kernel, dim3(1), dim3(1), 0, st, count_dev, n_tok);
+    return hipGetLastError();
 }
 
 hipError_t launch_kv_gather(const uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,

@@ -45,21 +45,45 @@ __device__ __forceinline__ float wave_sum(float v) {
 // consecutive 32-byte pieces regardless of K. Activations sit in LDS as
 // xs[m][c][g] (16 bytes each, pair order) so that threads working on consecutive
 // groups read consecutive 16-byte LDS words. Group partial sums land in LDS and
-// one wavefront per row adds them up.
+// one wavefront per row (or row pair, for SwiGLU) adds them up and applies the
+// epilogue.
+struct GemvArgs {
+    const __half* x;
+    uint32_t ldx;
+    const u32x4* wq;
+    const __half* ws;
+    __half* y;
+    uint32_t ldy;
+    uint32_t N, G, rows_per_wg;
+    const __half* gamma;
+    const __half* res;
+    uint32_t ldr;
+    int swiglu;
+};
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ uint16_t f2hb(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
 template <int MR>
-__global__ __launch_bounds__(256) void w4g_gemv_kernel(
-    const __half* __restrict__ x, uint32_t ldx, const u32x4* __restrict__ wq,
-    const __half* __restrict__ ws, __half* __restrict__ y, uint32_t ldy, uint32_t N, uint32_t G,
-    uint32_t rows_per_wg) {
+__global__ __launch_bounds__(256) void w4g_gemv_kernel(GemvArgs A) {
     extern __shared__ uint4 smem[];
+    const uint32_t G = A.G;
     uint4* xs = smem;                                   // [MR][8][G]
     float* red = reinterpret_cast<float*>(smem + MR * 8 * G);   // [MR][RB*G]
-    const uint32_t tid = threadIdx.x;
-    const uint32_t r0 = blockIdx.x * rows_per_wg;
-    const uint32_t RB = min(rows_per_wg, N - r0);
+    __shared__ double s_ss[4][MR];
+    __shared__ float s_rms[MR];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t r0 = blockIdx.x * A.rows_per_wg;
+    const uint32_t RB = min(A.rows_per_wg, A.N - r0);
     const uint32_t T = RB * G;
-    const u32x4* wrow = wq + (size_t)r0 * G * 2;
-    const __half* srow = ws + (size_t)r0 * G;
+    const u32x4* wrow = A.wq + (size_t)r0 * G * 2;
+    const __half* srow = A.ws + (size_t)r0 * G;
 
     constexpr int U = 4;
     // Issue the first batch of weight loads before staging activations.
@@ -75,11 +99,60 @@ __global__ __launch_bounds__(256) void w4g_gemv_kernel(
         }
     }
 
+    // Optional RMSNorm prologue: every workgroup computes the rows' sums of squares
+    // (in double, as RMSNORM2_F16 does) from its own reads of x.
+    if (A.gamma) {
+        double ss[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) ss[m] = 0.0;
+        for (uint32_t i = tid; i < 8 * G; i += 256) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const uint4 v = *reinterpret_cast<const uint4*>(A.x + (size_t)m * A.ldx + i * 8);
+                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const double lo = (double)h2f((uint16_t)(w4[e] & 0xFFFFu));
+                    const double hi = (double)h2f((uint16_t)(w4[e] >> 16));
+                    ss[m] += lo * lo;
+                    ss[m] += hi * hi;
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const double t = wave_sum_d(ss[m]);
+            if (lane == 0) s_ss[wave][m] = t;
+        }
+        __syncthreads();
+        if (tid < MR) {
+            const double t = s_ss[0][tid] + s_ss[1][tid] + s_ss[2][tid] + s_ss[3][tid];
+            s_rms[tid] = (float)sqrt(t / (double)(G * 64) + 1e-6);
+        }
+        __syncthreads();
+    }
+
     for (uint32_t i = tid; i < MR * 8 * G; i += 256) {
         const uint32_t m = i / (8 * G);
         const uint32_t rem = i - m * 8 * G;
         const uint32_t g = rem >> 3, c = rem & 7;
-        const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)m * ldx + g * 64 + c * 8);
+        uint4 v = *reinterpret_cast<const uint4*>(A.x + (size_t)m * A.ldx + g * 64 + c * 8);
+        if (A.gamma) {
+            // h = f16(f16-exact x / rms * gamma + 0), the RMSNORM2_F16 arithmetic
+            const uint4 gv = *reinterpret_cast<const uint4*>(A.gamma + g * 64 + c * 8);
+            const float rms = s_rms[m];
+            uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t g4[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float lo = __fdiv_rn(h2f((uint16_t)(w4[e] & 0xFFFFu)), rms);
+                float hi = __fdiv_rn(h2f((uint16_t)(w4[e] >> 16)), rms);
+                lo = __fadd_rn(__fmul_rn(lo, h2f((uint16_t)(g4[e] & 0xFFFFu))), 0.0f);
+                hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(g4[e] >> 16))), 0.0f);
+                w4[e] = (uint32_t)f2hb(lo) | ((uint32_t)f2hb(hi) << 16);
+            }
+            v = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
         uint4 p;
         p.x = (v.x & 0xFFFFu) | (v.z << 16);
         p.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
@@ -89,8 +162,7 @@ __global__ __launch_bounds__(256) void w4g_gemv_kernel(
     }
     __syncthreads();
 
-    const uint32_t step = 256u % G, gstep = 256u / G;
-    (void)gstep;
+    const uint32_t step = 256u % G;
     uint32_t g0 = tid % G;
     for (uint32_t jb = tid; jb < T; jb += 256u * U) {
         uint32_t g = g0;
@@ -138,14 +210,41 @@ __global__ __launch_bounds__(256) void w4g_gemv_kernel(
     }
     __syncthreads();
 
-    const uint32_t wave = tid >> 6, lane = tid & 63;
-    for (uint32_t r = wave; r < RB; r += 4) {
+    if (!A.swiglu) {
+        for (uint32_t r = wave; r < RB; r += 4) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            float s = 0.0f;
-            for (uint32_t i = lane; i < G; i += 64) s += red[m * T + r * G + i];
-            s = wave_sum(s);
-            if (lane == 0) y[(size_t)m * ldy + r0 + r] = __float2half(s);
+            for (int m = 0; m < MR; ++m) {
+                float s = 0.0f;
+                for (uint32_t i = lane; i < G; i += 64) s += red[m * T + r * G + i];
+                s = wave_sum(s);
+                if (lane == 0) {
+                    uint16_t v = f2hb(s);
+                    if (A.res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + r0 + r]))));
+                    reinterpret_cast<uint16_t*>(A.y)[(size_t)m * A.ldy + r0 + r] = v;
+                }
+            }
+        }
+    } else {
+        // rows (2p, 2p+1) = (gate, up) of output column (r0 + 2p) / 2; r0 and RB are even
+        for (uint32_t p = wave; 2 * p < RB; p += 4) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                float sg = 0.0f, su = 0.0f;
+                for (uint32_t i = lane; i < G; i += 64) {
+                    sg += red[m * T + (2 * p) * G + i];
+                    su += red[m * T + (2 * p + 1) * G + i];
+                }
+                sg = wave_sum(sg);
+                su = wave_sum(su);
+                if (lane == 0) {
+                    const float gv = h2f(f2hb(sg)), uv = h2f(f2hb(su));
+                    const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
+                    uint16_t v = f2hb(__fmul_rn(act, uv));
+                    const uint32_t col = (r0 >> 1) + p;
+                    if (A.res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + col]))));
+                    reinterpret_cast<uint16_t*>(A.y)[(size_t)m * A.ldy + col] = v;
+                }
+            }
         }
     }
 }
@@ -187,7 +286,7 @@ constexpr int BM = 128, BN = 128, BK = 64, LDS_STRIDE = BK + 8;   // halves
 __global__ __launch_bounds__(256) void w4g_gemm_kernel(
     const __half* __restrict__ a, uint32_t lda, const uint4* __restrict__ wq,
     const __half* __restrict__ ws, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
-    uint32_t K) {
+    uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu) {
     __shared__ __align__(16) _Float16 As[BM * LDS_STRIDE];
     __shared__ __align__(16) _Float16 Bs[BN * LDS_STRIDE];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -269,16 +368,30 @@ __global__ __launch_bounds__(256) void w4g_gemm_kernel(
     }
 
     // Accumulator layout (32x32): lane l, reg r -> col l%32, row 8*(r/4) + 4*(l/32) + r%4.
+    // With SwiGLU, columns 2c / 2c+1 (gate / up of output c) sit in lanes l, l^1.
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const uint32_t col = n0 + wn * 64 + j * 32 + (lane & 31);
-            if (col >= N) continue;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < M) y[(size_t)row * ldy + col] = __float2half(acc[i][j][r]);
+                const float partner = __shfl_xor(acc[i][j][r], 1, 64);
+                if (col >= N || row >= M) continue;
+                uint16_t v;
+                uint32_t oc = col;
+                if (swiglu) {
+                    if (lane & 1) continue;
+                    const float gv = h2f(f2hb(acc[i][j][r])), uv = h2f(f2hb(partner));
+                    const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
+                    v = f2hb(__fmul_rn(act, uv));
+                    oc = col >> 1;
+                } else {
+                    v = f2hb(acc[i][j][r]);
+                }
+                if (res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, res[(size_t)row * ldr + oc]))));
+                reinterpret_cast<uint16_t*>(y)[(size_t)row * ldy + oc] = v;
             }
         }
 }
@@ -287,8 +400,9 @@ __global__ __launch_bounds__(256) void w4g_gemm_kernel(
 
 hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
-                           hipStream_t st) {
+                           hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
+    if (epi.swiglu && (N & 1)) return hipErrorInvalidValue;
     const uint32_t G = K / 64;
     const uint32_t target_wgs = 2u * (uint32_t)device_cu_count();
     const uint32_t t_max = M == 1 ? 2048u : 1024u;
@@ -296,16 +410,21 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
     const uint32_t rb_cap = t_max / G > 0 ? t_max / G : 1;
     if (rb > rb_cap) rb = rb_cap;
     if (rb < 1) rb = 1;
+    if (epi.swiglu) rb = (rb + 1) & ~1u;   // gate/up pairs never straddle workgroups
     const uint32_t grid = (N + rb - 1) / rb;
     const size_t lds = (size_t)M * K * 2 + (size_t)M * rb * G * 4;
     // Activations live in LDS: beyond the 64 KiB dynamic-LDS budget use the GEMM.
-    if (lds > 65536) return launch_w4g_gemm(x, ldx, wq, ws, y, ldy, M, N, K, st);
-    const u32x4* w4 = reinterpret_cast<const u32x4*>(wq);
+    if (lds > 65536) {
+        if (epi.gamma) return hipErrorInvalidValue;   // the engine normalizes before a GEMM
+        return launch_w4g_gemm(x, ldx, wq, ws, y, ldy, M, N, K, st, epi);
+    }
+    GemvArgs A{x, ldx, reinterpret_cast<const u32x4*>(wq), ws, y, ldy, N, G, rb,
+               epi.gamma, epi.res, epi.ldr, epi.swiglu ? 1 : 0};
     switch (M) {
-    case 1: hipLaunchKernelGGL(w4g_gemv_kernel<1>, dim3(grid), dim3(256), lds, st, x, ldx, w4, ws, y, ldy, N, G, rb); break;
-    case 2: hipLaunchKernelGGL(w4g_gemv_kernel<2>, dim3(grid), dim3(256), lds, st, x, ldx, w4, ws, y, ldy, N, G, rb); break;
-    case 3: hipLaunchKernelGGL(w4g_gemv_kernel<3>, dim3(grid), dim3(256), lds, st, x, ldx, w4, ws, y, ldy, N, G, rb); break;
-    case 4: hipLaunchKernelGGL(w4g_gemv_kernel<4>, dim3(grid), dim3(256), lds, st, x, ldx, w4, ws, y, ldy, N, G, rb); break;
+    case 1: hipLaunchKernelGGL(w4g_gemv_kernel<1>, dim3(grid), dim3(256), lds, st, A); break;
+    case 2: hipLaunchKernelGGL(w4g_gemv_kernel<2>, dim3(grid), dim3(256), lds, st, A); break;
+    case 3: hipLaunchKernelGGL(w4g_gemv_kernel<3>, dim3(grid), dim3(256), lds, st, A); break;
+    case 4: hipLaunchKernelGGL(w4g_gemv_kernel<4>, dim3(grid), dim3(256), lds, st, A); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -313,11 +432,13 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
 
 hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
-                           hipStream_t st) {
+                           hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
+    if (epi.gamma || (epi.swiglu && (N & 1))) return hipErrorInvalidValue;
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
     hipLaunchKernelGGL(w4g_gemm_kernel, grid, dim3(256), 0, st, a, lda,
-                       reinterpret_cast<const uint4*>(wq), ws, y, ldy, M, N, K);
+                       reinterpret_cast<const uint4*>(wq), ws, y, ldy, M, N, K, epi.res, epi.ldr,
+                       epi.swiglu ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -14,13 +14,27 @@ namespace gehtp {
 int device_cu_count();
 
 // ---- W4G (int4, group 64, fp16 scales) ----
-// y[m*ldy + n] = f16( sum_k x[m*ldx + k] * fp16(q[n,k] * s[n, k/64]) ), m < M.
+// Optional fused parts of a W4A16 linear (OP_W4G_FUSED_F16), each reproducing the
+// runlist op it replaces with that op's roundings:
+//   gamma  RMSNorm of the input rows first (RMSNORM2_F16 with a zero bias; GEMV only —
+//          callers of the GEMM normalize into a buffer first)
+//   res    y = f16(f16(acc) + res[m*ldr + n])                  (ADD_F16 after the matmul)
+//   swiglu weight rows interleaved (2j = gate j, 2j+1 = up j); output column j =
+//          f16(f16(silu(f16(acc_g))) * f16(acc_u))            (UNARY silu, BINARY mul)
+struct W4gEpilogue {
+    const __half* gamma = nullptr;
+    const __half* res = nullptr;
+    uint32_t ldr = 0;
+    bool swiglu = false;
+};
+// y[m*ldy + n] = f16( sum_k x[m*ldx + k] * fp16(q[n,k] * s[n, k/64]) ), m < M, n < N
+// (N = weight rows; with swiglu the output has N/2 columns).
 hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
-                           hipStream_t st);
+                           hipStream_t st, const W4gEpilogue& epi = W4gEpilogue());
 hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
-                           hipStream_t st);
+                           hipStream_t st, const W4gEpilogue& epi = W4gEpilogue());
 // w[n*K + k] = fp16(q * s) (bit-exact dequant; used by tests and the fp16 fallback).
 hipError_t launch_w4g_dequant(const uint8_t* wq, const __half* ws, __half* w,
                               uint32_t N, uint32_t K, hipStream_t st);
@@ -73,6 +87,14 @@ hipError_t launch_kv_append(uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
 hipError_t launch_kv_append_n(uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
                               const __half* k, const __half* v, uint32_t kv_elems, uint32_t n_tok,
                               uint32_t pos, uint32_t* count_dev, hipStream_t st);
+// OP_QK_ROPE_KV_F16: per token t of qkv [n_tok][(H+2KVH)*128] (= [q | k | v]):
+// q_out[t] = rope(rmsnorm_128(q, q_gamma)), k = rope(rmsnorm_128(k, k_gamma)) and v go to
+// ring slot (*count_dev + t) % nslots (and to k_out / v_out when non-null); then
+// *count_dev += n_tok. Positions for RoPE are *count_dev + t. head_dim is 128.
+hipError_t launch_qk_rope_kv(const __half* qkv, uint32_t n_tok, uint32_t H, uint32_t KVH,
+                             const __half* q_gamma, const __half* k_gamma, float theta, __half* q_out,
+                             __half* k_out, __half* v_out, uint8_t* ring, uint32_t slot_bytes,
+                             uint32_t nslots, uint32_t* count_dev, hipStream_t st);
 // kT [H][hd][pstride], v [H][pstride][hd]; positions >= n_kv of the pstride are zero.
 hipError_t launch_kv_gather(const uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
                             __half* kT, __half* vo, uint32_t n_kv, uint32_t pstride, uint32_t H,

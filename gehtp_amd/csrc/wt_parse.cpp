@@ -68,6 +68,8 @@ struct OpTable {
         info[OP_ATTN_DECODE_F16] = {WT_ARITY_ATTN_DECODE_F16, bits({0})};
         info[OP_ROPE_F16] = {WT_ARITY_ROPE_F16, bits({0})};
         info[OP_KV_APPEND_N_F16] = {WT_ARITY_KV_APPEND_N_F16, bits({0, 1})};
+        info[OP_W4G_FUSED_F16] = {WT_ARITY_W4G_FUSED_F16, bits({0, 1, 2, 7, 8})};
+        info[OP_QK_ROPE_KV_F16] = {WT_ARITY_QK_ROPE_KV_F16, bits({0, 9, 10})};
     }
 };
 
@@ -150,6 +152,8 @@ extern "C" int wt_parse(const uint8_t* buf, size_t size, struct wt_blob* out) {
             const uint32_t v = op.args[a];
             // OP_DMA may name an engine surface (0xC000|id) instead of a slot.
             if (op.opcode == OP_DMA && (v & 0xC000u) == 0xC000u) continue;
+            // Optional references of the added fused opcodes.
+            if (v == WT_REF_NONE && op.opcode >= OP_W4G_FUSED_F16) continue;
             // Only 0x8000-tagged values address slot space; bare ids are temps.
             if ((v & 0x8000u) && (v & 0x7FFFu) >= out->n_slots) return WT_ERR_BAD_REF;
         }

@@ -5,18 +5,18 @@ terms: weights as EXT_WGT slots of one external image (so a multi-GB model is no
 inlined into the blob), one persistent KV-ring STATE per layer, activations in
 temps, the token embeddings arriving through the EXT_IN slot.
 
-Per layer (pre-norm, eps 1e-6):
-    h  = RMSNORM2(x, g_attn)
-    q, k, v = MATMUL_W4G(h, Wq | Wk | Wv)
-    q, k = RMSNORM2 per head (q_norm, k_norm; Qwen3's QK-norm), ROPE (theta)
-    KV append (prefill: KV_APPEND_N, decode: KV_APPEND) into the layer's ring
-    a  = ATTN (prefill, causal) | ATTN_DECODE (one token over the ring)
-    x  = x + MATMUL_W4G(a, Wo)
-    h  = RMSNORM2(x, g_ffn)
-    x  = x + MATMUL_W4G(silu(h Wg^T) * (h Wu^T), Wd)
+Per layer (pre-norm, eps 1e-6), four fused linears and two attention ops:
+    qkv = W4G_FUSED(x, Wqkv, norm=g_attn)            RMSNORM2 + q|k|v linears
+    q   = QK_ROPE_KV(qkv)                            Qwen3 QK-norm, RoPE, KV append
+    a   = ATTN (prefill, causal) | ATTN_DECODE (one token over the layer's ring)
+    x1  = W4G_FUSED(a, Wo, residual=x)               o-proj + ADD
+    m   = W4G_FUSED(x1, Wgu, norm=g_ffn, SwiGLU)     RMSNORM2 + gate|up + silu * up
+    x   = W4G_FUSED(m, Wd, residual=x1)              down-proj + ADD
 then RMSNORM2(x, g_final), the fp16 lm_head (MATMUL_F16, w stored [V, D]) on the
-last token and ARGMAX. RoPE positions come from the layer state's counter, so the
-decode blob is identical for every step.
+last token and ARGMAX. Each fused op rounds where the separate runlist ops it replaces
+round, so the oracle composition of the separate ops (oracle/qwen3_ref.py) is the
+checker. RoPE positions come from the layer state's counter, so the decode blob is
+identical for every step.
 """
 from __future__ import annotations
 
@@ -25,7 +25,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from .abi import WT_KV_POS_AUTO, opcodes as OP
+from .abi import WT_KV_POS_AUTO, WT_REF_NONE, opcodes as OP
 from .runlist import BlobBuilder, f32_bits
 
 
@@ -59,6 +59,13 @@ class Qwen3Config:
         D, F = self.hidden, self.ffn
         return [("wq", self.q_dim, D), ("wk", self.kv_dim, D), ("wv", self.kv_dim, D),
                 ("wo", D, self.q_dim), ("wg", F, D), ("wu", F, D), ("wd", D, F)]
+
+    def fused_linears(self):
+        """(name, rows, K) of the stored (fused) matrices: q|k|v rows, o, gate/up rows
+        interleaved, down."""
+        D, F = self.hidden, self.ffn
+        return [("wqkv", self.q_dim + 2 * self.kv_dim, D), ("wo", D, self.q_dim),
+                ("wgu", 2 * F, D), ("wd", D, F)]
 
     def decode_weight_bytes(self) -> int:
         """Algorithmic HBM bytes of one decode token: int4 weights + fp16 scales of every
@@ -104,7 +111,7 @@ class Weights:
             off += nbytes
 
         for l in range(cfg.layers):
-            for nm, n, k in cfg.linears():
+            for nm, n, k in cfg.fused_linears():
                 reserve(f"{l}.{nm}.q", n * k // 2)
                 reserve(f"{l}.{nm}.s", n * (k // cfg.group) * 2)
             for nm, n in (("g_attn", cfg.hidden), ("g_ffn", cfg.hidden), ("q_norm", cfg.head_dim),
@@ -135,11 +142,26 @@ class Weights:
     def f16(self, name: str) -> np.ndarray:
         return self.get(name).view(np.float16)
 
-    def linear(self, layer: int, nm: str):
-        """(wq packed uint8 [N, K/2], scales fp16 [N, K/64])."""
-        n, k = {x[0]: (x[1], x[2]) for x in self.cfg.linears()}[nm]
+    def fused(self, layer: int, nm: str):
+        """(wq uint8 [rows, K/2], scales fp16 [rows, K/64]) of a stored fused matrix."""
+        n, k = {x[0]: (x[1], x[2]) for x in self.cfg.fused_linears()}[nm]
         return (self.get(f"{layer}.{nm}.q").reshape(n, k // 2),
                 self.f16(f"{layer}.{nm}.s").reshape(n, k // self.cfg.group))
+
+    def linear(self, layer: int, nm: str):
+        """(wq packed uint8 [N, K/2], scales fp16 [N, K/64]) of a logical linear
+        (wq, wk, wv, wo, wg, wu, wd), cut out of the fused storage."""
+        c = self.cfg
+        if nm in ("wq", "wk", "wv"):
+            q, s = self.fused(layer, "wqkv")
+            lo = {"wq": 0, "wk": c.q_dim, "wv": c.q_dim + c.kv_dim}[nm]
+            hi = lo + (c.q_dim if nm == "wq" else c.kv_dim)
+            return q[lo:hi], s[lo:hi]
+        if nm in ("wg", "wu"):
+            q, s = self.fused(layer, "wgu")
+            r = 0 if nm == "wg" else 1
+            return np.ascontiguousarray(q[r::2]), np.ascontiguousarray(s[r::2])
+        return self.fused(layer, nm)
 
     def embed(self) -> np.ndarray:
         return self.f16("embed").reshape(self.cfg.vocab, self.cfg.hidden)
@@ -157,8 +179,7 @@ class _Emitter:
         self.zero_bias = self.bb.add_slot(np.zeros(max(cfg.hidden, cfg.head_dim), np.float16))
         self.states = [self.bb.add_state(max_pos * cfg.kv_dim * 4) for _ in range(cfg.layers)]
         self.t = {n: self.bb.temp() for n in
-                  ("x", "x1", "h", "q", "k", "v", "qn", "kn", "qr", "kr", "a", "o", "g", "u", "sg", "m", "d",
-                   "last", "logits", "tok")}
+                  ("x", "x1", "h", "qkv", "qr", "kr", "v", "a", "m", "last", "logits", "tok")}
 
     def _ext_slot(self, off, nb, count):
         from .abi import WT_SLOT_EXT_WGT
@@ -173,40 +194,28 @@ class _Emitter:
         bb = self.bb
         bb.op(OP.RMSNORM2_F16, x, self.ref(gamma), bb.slot_ref(self.zero_bias), y, n)
 
-    def w4g(self, a, l, nm, y, M):
-        n, k = {x[0]: (x[1], x[2]) for x in self.cfg.linears()}[nm]
-        self.bb.op(OP.MATMUL_W4G_F16, a, self.ref(f"{l}.{nm}.q"), self.ref(f"{l}.{nm}.s"), y, M, k, n,
-                   self.cfg.group, 2)
+    def w4g(self, a, l, nm, y, M, norm=None, res=None, swiglu=False):
+        n, k = {x[0]: (x[1], x[2]) for x in self.cfg.fused_linears()}[nm]
+        self.bb.op(OP.W4G_FUSED_F16, a, self.ref(f"{l}.{nm}.q"), self.ref(f"{l}.{nm}.s"), y, M, k, n,
+                   self.ref(norm) if norm else WT_REF_NONE, res if res is not None else WT_REF_NONE,
+                   1 if swiglu else 0, 2)
 
     def layer(self, l: int, S: int, x_in: int, decode: bool):
         c, bb, t = self.cfg, self.bb, self.t
         st = self.states[l]
-        self.norm(x_in, f"{l}.g_attn", t["h"], S * c.hidden)
-        self.w4g(t["h"], l, "wq", t["q"], S)
-        self.w4g(t["h"], l, "wk", t["k"], S)
-        self.w4g(t["h"], l, "wv", t["v"], S)
-        # Qwen3 QK-norm: RMSNorm over each head's 128 dims (row width = gamma length)
-        self.norm(t["q"], f"{l}.q_norm", t["qn"], S * c.q_dim)
-        self.norm(t["k"], f"{l}.k_norm", t["kn"], S * c.kv_dim)
-        bb.op(OP.ROPE_F16, t["qn"], t["qr"], S, c.heads, c.head_dim, st, f32_bits(c.theta), c.q_dim)
-        bb.op(OP.ROPE_F16, t["kn"], t["kr"], S, c.kv_heads, c.head_dim, st, f32_bits(c.theta), c.kv_dim)
+        self.w4g(x_in, l, "wqkv", t["qkv"], S, norm=f"{l}.g_attn")
+        bb.op(OP.QK_ROPE_KV_F16, t["qkv"], t["qr"], WT_REF_NONE if decode else t["kr"],
+              WT_REF_NONE if decode else t["v"], st, S, c.heads, c.kv_heads, c.head_dim,
+              self.ref(f"{l}.q_norm"), self.ref(f"{l}.k_norm"), f32_bits(c.theta))
         if decode:
-            bb.op(OP.KV_APPEND_F16, t["kr"], t["v"], st, WT_KV_POS_AUTO)
             bb.op(OP.ATTN_DECODE_F16, t["qr"], st, t["a"], WT_KV_POS_AUTO, c.heads, c.kv_heads, c.head_dim,
                   f32_bits(c.scale))
         else:
-            bb.op(OP.KV_APPEND_N_F16, t["kr"], t["v"], st, WT_KV_POS_AUTO, S, c.kv_dim)
             bb.op(OP.ATTN_F16, t["qr"], t["kr"], t["v"], t["a"], S, c.heads, c.kv_heads, c.head_dim,
                   f32_bits(c.scale), 1)
-        self.w4g(t["a"], l, "wo", t["o"], S)
-        bb.op(OP.ADD_F16, x_in, t["o"], t["x1"], S * c.hidden)
-        self.norm(t["x1"], f"{l}.g_ffn", t["h"], S * c.hidden)
-        self.w4g(t["h"], l, "wg", t["g"], S)
-        self.w4g(t["h"], l, "wu", t["u"], S)
-        bb.op(OP.UNARY_F16, t["g"], t["sg"], S * c.ffn, 12)          # SiLU
-        bb.op(OP.BINARY_F16, t["sg"], t["u"], t["m"], S * c.ffn, 2)  # * up
-        self.w4g(t["m"], l, "wd", t["d"], S)
-        bb.op(OP.ADD_F16, t["x1"], t["d"], t["x"], S * c.hidden)
+        self.w4g(t["a"], l, "wo", t["x1"], S, res=x_in)
+        self.w4g(t["x1"], l, "wgu", t["m"], S, norm=f"{l}.g_ffn", swiglu=True)
+        self.w4g(t["m"], l, "wd", t["x"], S, res=t["x1"])
 
     def head(self, S: int):
         c, bb, t = self.cfg, self.bb, self.t

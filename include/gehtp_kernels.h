@@ -33,6 +33,19 @@ int gehtp_w4g_gemv(const void* x, uint32_t ldx, const void* wq, const void* ws, 
                    uint32_t ldy, uint32_t M, uint32_t N, uint32_t K, void* stream);
 int gehtp_w4g_gemm(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y,
                    uint32_t ldy, uint32_t M, uint32_t N, uint32_t K, void* stream);
+/* OP_W4G_FUSED_F16 on device buffers: gamma (NULL = none) RMSNorm of x first (GEMV
+ * sizes only), mode 1 = SwiGLU over interleaved gate/up rows (N/2 outputs), res (NULL =
+ * none) added with row stride ldr. Same roundings as the separate runlist ops. */
+int gehtp_w4g_fused(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y,
+                    uint32_t ldy, uint32_t M, uint32_t N, uint32_t K, const void* gamma,
+                    const void* res, uint32_t ldr, uint32_t mode, void* stream);
+/* OP_QK_ROPE_KV_F16 on device buffers: qkv [n_tok, (H+2KVH)*128]; ring of state_bytes;
+ * count_dev = device uint32 auto-position counter (read, then advanced by n_tok);
+ * k_out / v_out may be NULL. */
+int gehtp_qk_rope_kv(const void* qkv, uint32_t n_tok, uint32_t H, uint32_t KVH,
+                     const void* q_gamma, const void* k_gamma, float theta, void* q_out,
+                     void* k_out, void* v_out, void* ring, uint32_t state_bytes,
+                     void* count_dev, void* stream);
 /* w[N, K] fp16 = fp16(q * s): the dequant, bit-exact. */
 int gehtp_w4g_dequant(const void* wq, const void* ws, void* w, uint32_t N, uint32_t K, void* stream);
 

@@ -135,7 +135,30 @@ enum {
      *   WT_KV_POS_AUTO: the state's counter, advanced by n_tok). Same ring as
      *   OP_KV_APPEND_F16, which appends exactly one token. */
     OP_KV_APPEND_N_F16 = 44,
+    /* OP_W4G_FUSED_F16: OP_MATMUL_W4G_F16 with the ops around a decoder linear folded in.
+     *   args [a_ref, wq_ref, ws_ref, out_t, M, K, N, gamma_ref, res_ref, mode, flags]
+     *   gamma_ref != WT_REF_NONE: a := RMSNORM2_F16(a, gamma, zero bias) first.
+     *   mode 0: y = a.dequant(W)^T (N output columns).
+     *   mode 1 (SwiGLU): weight rows interleaved, row 2j = gate j, row 2j+1 = up j;
+     *          y[:, j] = f16(f16(silu(f16(gate))) * f16(up)), N/2 output columns
+     *          (= UNARY_F16 silu then BINARY_F16 mul).
+     *   res_ref != WT_REF_NONE: y = f16(y + res) (= ADD_F16), res [M, N_out].
+     *   flags: bit1 must be set; bits 16..31 = output row stride (0 = N_out).
+     *   Each fused step rounds exactly where the op it replaces does. */
+    OP_W4G_FUSED_F16 = 45,
+    /* OP_QK_ROPE_KV_F16: per-head QK RMSNorm + RoPE + KV append for a fused QKV row.
+     *   args [qkv_ref, q_out_t, k_out_t, v_out_t, state_ref, n_tok, H, KVH, hd,
+     *         q_gamma_ref, k_gamma_ref, theta_f32_bits]
+     *   qkv [n_tok, (H + 2*KVH)*hd] rows [q | k | v]; hd == 128.
+     *   q_out[t] = ROPE(RMSNORM2(q_t, q_gamma)), k_t = ROPE(RMSNORM2(k_t, k_gamma)) and
+     *   v_t are appended to the ring at the state's counter (advanced by n_tok);
+     *   k_out_t / v_out_t (WT_REF_NONE to skip) receive k_t / v_t token-major.
+     *   RoPE positions = counter + t. Replaces RMSNORM2 x2, ROPE x2, KV_APPEND_N. */
+    OP_QK_ROPE_KV_F16 = 46,
 };
+
+/* "No reference" argument value of the added opcodes. */
+#define WT_REF_NONE 0xFFFFFFFFu
 
 /* Arities (reference oplist_parse.h:218-251). */
 #define WT_ARITY_NOP 0
@@ -177,6 +200,8 @@ enum {
 #define WT_ARITY_ATTN_DECODE_F16 8
 #define WT_ARITY_ROPE_F16 8
 #define WT_ARITY_KV_APPEND_N_F16 6
+#define WT_ARITY_W4G_FUSED_F16 11
+#define WT_ARITY_QK_ROPE_KV_F16 12
 
 /* In-memory records (reference oplist_parse.h:253-275); layouts are ABI. */
 struct wt_slot {

@@ -260,7 +260,7 @@ def test_attn_decode(lib, oracle, torch_dev, n_kv, H, KVH):
     _sync()
     assert np.array_equal(ring_d.cpu().numpy(), ring.buf), "device ring differs from the reference ring"
     wf = lib.gehtp_attn_decode_work_floats(n_kv, H, hd)
-    work = torch.empty(wf, dtype=torch.float32, device=torch_dev)
+    work = torch.zeros(wf, dtype=torch.float32, device=torch_dev)
     out = torch.empty((H, hd), dtype=torch.float16, device=torch_dev)
     assert lib.gehtp_attn_decode(ptr(to_dev(q, torch_dev)), ptr(ring_d), state_bytes, ptr(out), n_kv, H, KVH, hd,
                                  SCALE, ptr(work), wf, stream_ptr()) == 0
@@ -284,10 +284,92 @@ def test_decode_matches_prefill_last_row(lib, torch_dev):
     assert lib.gehtp_kv_append(ptr(ring_d), state_bytes, ptr(to_dev(k.reshape(S, -1), torch_dev)),
                                ptr(to_dev(v.reshape(S, -1), torch_dev)), KVH * hd, S, 0, stream_ptr()) == 0
     wf = lib.gehtp_attn_decode_work_floats(S, H, hd)
-    work = torch.empty(wf, dtype=torch.float32, device=torch_dev)
+    work = torch.zeros(wf, dtype=torch.float32, device=torch_dev)
     dec = torch.empty((H, hd), dtype=torch.float16, device=torch_dev)
     qd = to_dev(q, torch_dev)
     assert lib.gehtp_attn_decode(ptr(qd[S - 1]), ptr(ring_d), state_bytes, ptr(dec), S, H, KVH, hd, SCALE,
                                  ptr(work), wf, stream_ptr()) == 0
     _sync()
     assert_close(from_dev(dec), from_dev(out)[S - 1], max_abs=4e-3, min_cos=0.99999, what="decode vs prefill")
+
+
+# ---------------------------------------------------------------- fused ops --
+@pytest.mark.parametrize("mode,use_norm,use_res", [(0, True, False), (0, False, True), (1, True, False),
+                                                    (1, False, True)])
+def test_w4g_fused_gemv(lib, oracle, torch_dev, mode, use_norm, use_res):
+    """OP_W4G_FUSED_F16 GEMV = RMSNORM2 -> MATMUL_W4G (-> silu*up) (-> ADD), same roundings."""
+    import torch
+    rng = np.random.default_rng(31 + mode * 2 + use_norm)
+    N, K = (2 * 1536 if mode else 2048), 2560
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, 1, K)
+    gamma = rng.uniform(0.8, 1.2, K).astype(np.float16)
+    n_out = N // 2 if mode else N
+    res = normal_f16(rng, 1, n_out)
+    y = torch.empty((1, n_out), dtype=torch.float16, device=torch_dev)
+    rc = lib.gehtp_w4g_fused(ptr(to_dev(x, torch_dev)), K, ptr(to_dev(wq, torch_dev)), ptr(to_dev(ws, torch_dev)),
+                             ptr(y), n_out, 1, N, K, ptr(to_dev(gamma, torch_dev)) if use_norm else None,
+                             ptr(to_dev(res, torch_dev)) if use_res else None, n_out, mode, stream_ptr())
+    assert rc == 0
+    _sync()
+    h = oracle.rmsnorm2(x, gamma, np.zeros(K, np.float16)) if use_norm else x
+    acc = oracle.matmul_w4g(h, wq, ws, threads=8)
+    ref = oracle.binary(oracle.unary(acc[:, 0::2], 12), acc[:, 1::2].copy(), 2) if mode else acc
+    if use_res:
+        ref = oracle.binary(ref, res, 0)
+    assert_close(from_dev(y), ref, what=f"w4g_fused mode={mode} norm={use_norm} res={use_res}")
+
+
+def test_w4g_fused_gemm_epilogues(lib, oracle, torch_dev):
+    """The GEMM path (M > 4) applies the same SwiGLU and residual epilogues."""
+    import torch
+    rng = np.random.default_rng(41)
+    M, N, K = 96, 2 * 320, 512
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, M, K)
+    res = normal_f16(rng, M, N // 2)
+    y = torch.empty((M, N // 2), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_w4g_fused(ptr(to_dev(x, torch_dev)), K, ptr(to_dev(wq, torch_dev)), ptr(to_dev(ws, torch_dev)),
+                               ptr(y), N // 2, M, N, K, None, ptr(to_dev(res, torch_dev)), N // 2, 1,
+                               stream_ptr()) == 0
+    _sync()
+    acc = oracle.matmul_w4g(x, wq, ws, threads=8)
+    ref = oracle.binary(oracle.binary(oracle.unary(acc[:, 0::2].copy(), 12), acc[:, 1::2].copy(), 2), res, 0)
+    assert_close(from_dev(y), ref, what="gemm swiglu+res")
+
+
+@pytest.mark.parametrize("n_tok", [1, 37])
+def test_qk_rope_kv(lib, oracle, torch_dev, n_tok):
+    """OP_QK_ROPE_KV_F16 = per-head RMSNORM2 (q_norm / k_norm), ROPE at the counter
+    position, KV append into the reference ring layout; counter advances by n_tok."""
+    import torch
+    rng = np.random.default_rng(50 + n_tok)
+    H, KVH, hd, nslots, pos0 = 8, 2, 128, 64, 5
+    qkv = normal_f16(rng, n_tok, (H + 2 * KVH) * hd) * np.float16(3)
+    qg = rng.uniform(0.8, 1.2, hd).astype(np.float16)
+    kg = rng.uniform(0.8, 1.2, hd).astype(np.float16)
+    state_bytes = nslots * KVH * hd * 4
+    ring = torch.zeros(state_bytes, dtype=torch.uint8, device=torch_dev)
+    count = torch.tensor([pos0], dtype=torch.int32, device=torch_dev)
+    q_out = torch.empty((n_tok, H * hd), dtype=torch.float16, device=torch_dev)
+    k_out = torch.empty((n_tok, KVH * hd), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_qk_rope_kv(ptr(to_dev(qkv, torch_dev)), n_tok, H, KVH, ptr(to_dev(qg, torch_dev)),
+                                ptr(to_dev(kg, torch_dev)), 1e6, ptr(q_out), ptr(k_out), None, ptr(ring),
+                                state_bytes, ptr(count), stream_ptr()) == 0
+    _sync()
+    assert int(count.item()) == pos0 + n_tok
+    q = qkv[:, :H * hd]
+    k = qkv[:, H * hd:(H + KVH) * hd]
+    v = qkv[:, (H + KVH) * hd:]
+    qn = oracle.rmsnorm2(q.reshape(-1, hd), qg, np.zeros(hd, np.float16)).reshape(n_tok, -1)
+    kn = oracle.rmsnorm2(k.reshape(-1, hd), kg, np.zeros(hd, np.float16)).reshape(n_tok, -1)
+    q_ref = oracle.rope(qn, H, hd, pos0, 1e6)
+    k_ref = oracle.rope(kn, KVH, hd, pos0, 1e6)
+    rq = np.abs(from_dev(q_out).view(np.int16).astype(np.int32) - q_ref.view(np.int16).astype(np.int32))
+    assert rq.max() <= 1 and (rq == 0).mean() > 0.999     # RMSNorm's double sum order may flip 1 ulp
+    ring_ref = oracle.KVRing(state_bytes, KVH * hd)
+    for t in range(n_tok):
+        ring_ref.append(from_dev(k_out)[t], v[t], pos0 + t)
+    assert np.array_equal(ring.cpu().numpy(), ring_ref.buf)
+    rk = np.abs(from_dev(k_out).view(np.int16).astype(np.int32) - k_ref.view(np.int16).astype(np.int32))
+    assert rk.max() <= 1 and (rk == 0).mean() > 0.999
