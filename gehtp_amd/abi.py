@@ -77,6 +77,7 @@ class opcodes:
     KV_APPEND_N_F16 = 44
     W4G_FUSED_F16 = 45
     QK_ROPE_KV_F16 = 46
+    ATTN_DECODE_QKV_F16 = 47
 
 
 WT_REF_NONE = 0xFFFFFFFF
@@ -87,7 +88,7 @@ ARITY = {
     0: 0, 1: 6, 2: 4, 3: 1, 4: 3, 5: 15, 6: 13, 7: 4, 8: 4, 9: 4, 10: 6, 11: 4, 12: 5, 13: 4,
     14: 16, 15: 16, 16: 16, 17: 9, 18: 7, 19: 6, 20: 15, 21: 3, 22: 4, 23: 7, 24: 7, 25: 5,
     26: 12, 27: 8, 28: 14, 29: 6, 30: 12, 33: 8, 34: 7, 35: 9,
-    40: 9, 41: 10, 42: 8, 43: 8, 44: 6, 45: 11, 46: 12,
+    40: 9, 41: 10, 42: 8, 43: 8, 44: 6, 45: 11, 46: 12, 47: 10,
 }
 
 
@@ -161,6 +162,8 @@ EXPORTS = {
     "gehtp_attn_prefill": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, C.c_float, _i, _vp]),
     "gehtp_attn_decode": (_i, [_vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32, C.c_float, _vp, _u32, _vp]),
     "gehtp_attn_decode_work_floats": (_u32, [_u32, _u32, _u32]),
+    "gehtp_attn_decode_qkv": (_i, [_vp, _u32, _u32, _vp, _vp, C.c_float, C.c_float, _vp, _u32, _vp, _vp, _vp,
+                                   _u32, _vp]),
     "gehtp_kv_append": (_i, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _vp]),
     "gehtp_rope": (_i, [_vp, _vp, _u32, _u32, _u32, _u32, C.c_float, _u32, _vp]),
     "gehtp_argmax": (_i, [_vp, _u32, _vp, _vp]),

@@ -57,7 +57,7 @@ int gehtp_w4g_fused(const void* x, uint32_t ldx, const void* wq, const void* ws,
     epi.res = H(res);
     epi.ldr = ldr;
     epi.swiglu = mode == 1;
-    if (M <= kW4gGemvMaxM && (size_t)M * K * 2 + (size_t)M * 4096 * 4 <= 65536)
+    if (w4g_gemv_supported(M, K))
         return rc(launch_w4g_gemv(H(x), ldx, static_cast<const uint8_t*>(wq), H(ws), Hm(y), ldy, M, N, K,
                                   S(stream), epi));
     if (gamma) return GEHTP_EINVAL;   // GEMM path: normalize with gehtp_rmsnorm2 first
@@ -118,12 +118,24 @@ int gehtp_attn_decode(const void* q, const void* ring, uint32_t state_bytes, voi
                       void* stream) {
     const uint32_t slot_bytes = KVH * hd * 4u;
     if (!q || !ring || !out || !work || hd != 128 || !KVH || Hh % KVH || !slot_bytes ||
-        state_bytes % slot_bytes || !al16(q) || !al16(ring))
+        state_bytes % slot_bytes || !al16(q) || !al16(ring) || !al16(work))
         return GEHTP_EINVAL;
     const uint32_t nslots = state_bytes / slot_bytes;
     if (!n_kv || n_kv > nslots) return GEHTP_EINVAL;
     return rc(launch_attn_decode(H(q), static_cast<const uint8_t*>(ring), slot_bytes, nslots, Hm(out), n_kv,
                                  nullptr, Hh, KVH, hd, scale, static_cast<float*>(work), work_floats, S(stream)));
+}
+
+int gehtp_attn_decode_qkv(const void* qkv, uint32_t Hh, uint32_t KVH, const void* q_gamma, const void* k_gamma,
+                          float theta, float scale, void* ring, uint32_t state_bytes, void* count_dev, void* out,
+                          void* work, uint32_t work_floats, void* stream) {
+    const uint32_t slot_bytes = KVH * 128u * 4u;
+    if (!qkv || !q_gamma || !k_gamma || !ring || !count_dev || !out || !work || !KVH || Hh % KVH ||
+        state_bytes % slot_bytes || !state_bytes || !al16(ring) || !al16(work) || (reinterpret_cast<uintptr_t>(out) & 7u))
+        return GEHTP_EINVAL;
+    return rc(launch_attn_decode_qkv(H(qkv), H(q_gamma), H(k_gamma), theta, static_cast<uint8_t*>(ring), slot_bytes,
+                                     state_bytes / slot_bytes, static_cast<uint32_t*>(count_dev), Hm(out), Hh, KVH,
+                                     scale, static_cast<float*>(work), work_floats, S(stream)));
 }
 
 int gehtp_kv_append(void* ring, uint32_t state_bytes, const void* k, const void* v, uint32_t kv_elems,

@@ -1,0 +1,69 @@
+// dev_rope.h — device helpers shared by the QK-norm/RoPE kernels (k_rows.hip) and the
+// fused decode attention (k_attn.hip), so both produce the same bits.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace gehtp {
+namespace dev {
+
+// binary64 -> binary16, one RNE rounding (the reference builds RoPE tables this way).
+__device__ __forceinline__ uint16_t f64_to_f16_bits(double d) {
+    const uint64_t x = __builtin_bit_cast(uint64_t, d);
+    const uint16_t sign = (uint16_t)((x >> 48) & 0x8000u);
+    const int32_t dexp = (int32_t)((x >> 52) & 0x7ffu);
+    const uint64_t man = x & ((1ull << 52) - 1);
+    if (dexp == 0x7ff) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u : 0u));
+    const int32_t exp = dexp - 1008;
+    if (exp >= 31) return (uint16_t)(sign | 0x7c00u);
+    uint64_t kept, rem, halfway;
+    if (exp <= 0) {
+        if (exp < -10) return sign;
+        const uint64_t m = man | (1ull << 52);
+        const uint32_t shift = (uint32_t)(43 - exp);
+        kept = m >> shift;
+        rem = m & ((1ull << shift) - 1);
+        halfway = 1ull << (shift - 1);
+    } else {
+        kept = ((uint64_t)exp << 10) | (man >> 42);
+        rem = man & ((1ull << 42) - 1);
+        halfway = 1ull << 41;
+    }
+    if (rem > halfway || (rem == halfway && (kept & 1u))) kept++;
+    return (uint16_t)(sign | kept);
+}
+
+__device__ __forceinline__ float bits_f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ float rne_f16(float f) { return (float)(_Float16)f; }
+
+// RoPE table entry of pair i of a 128-dim head at position pos:
+// c, s = f16(cos / sin(pos * theta^(-2i/128))) evaluated in double.
+__device__ __forceinline__ void rope_cs(uint32_t pos, uint32_t i, float theta, float& c, float& s) {
+    const double inv = 1.0 / pow((double)theta, (double)(2 * i) / 128.0);
+    c = bits_f(f64_to_f16_bits(cos((double)pos * inv)));
+    s = bits_f(f64_to_f16_bits(sin((double)pos * inv)));
+}
+
+// One 128-dim head held by a full wavefront, lane l owning (x[l], x[l+64]):
+// h = RMSNORM2_F16(x, gamma, zero bias) (squares summed in double), then the RoPE
+// chain y_l = f16(f16(h_l c) + f16(-h_{l+64} s)), y_{l+64} = f16(f16(h_{l+64} c) + f16(h_l s)).
+// Every lane of the wavefront must call it (cross-lane sum).
+__device__ __forceinline__ void head_norm_rope(float x1, float x2, float g1, float g2, float c, float s,
+                                               float& y1, float& y2) {
+    double ss = (double)x1 * (double)x1 + (double)x2 * (double)x2;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float rms = (float)sqrt(ss / 128.0 + 1e-6);
+    const float h1 = rne_f16(__fadd_rn(__fmul_rn(__fdiv_rn(x1, rms), g1), 0.0f));
+    const float h2 = rne_f16(__fadd_rn(__fmul_rn(__fdiv_rn(x2, rms), g2), 0.0f));
+    const float a1 = rne_f16(__fmul_rn(h1, c)), b1 = rne_f16(__fmul_rn(-h2, s));
+    const float a2 = rne_f16(__fmul_rn(h2, c)), b2 = rne_f16(__fmul_rn(h1, s));
+    y1 = rne_f16(__fadd_rn(a1, b1));
+    y2 = rne_f16(__fadd_rn(a2, b2));
+}
+
+}  // namespace dev
+}  // namespace gehtp

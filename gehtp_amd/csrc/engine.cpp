@@ -54,6 +54,7 @@ struct State {
     bool kv_ready = false;
     uint32_t slot_bytes = 0, nslots = 0;
     std::vector<uint32_t> posmap;  // slot -> absolute position (kNone = empty)
+    uint32_t valid_prefix = 0;     // positions 0..valid_prefix-1 all present in their slots
 };
 
 struct Engine {
@@ -413,9 +414,20 @@ State* state_kv(uint32_t ref, uint32_t kv_elems, char* err, size_t errn) {
 }
 
 // Host-side lookup check for positions [0, n_kv) (kvcache.c:64-68): a miss is a hard error.
+// Record that position p now occupies its ring slot, keeping valid_prefix exact:
+// it grows over consecutive present positions and shrinks when a wrapped append
+// overwrites one of them.
+void kv_mark(State& s, uint32_t p) {
+    const uint32_t slot = p % s.nslots;
+    s.posmap[slot] = p;
+    if (slot < s.valid_prefix && p != slot) s.valid_prefix = slot;
+    while (s.valid_prefix < s.nslots && s.posmap[s.valid_prefix] == s.valid_prefix) ++s.valid_prefix;
+}
+
+int attn_workspace(uint32_t need, char* err, size_t errn);
+
 int kv_check(const State& s, uint32_t n_kv, char* err, size_t errn) {
-    for (uint32_t p = 0; p < n_kv; ++p)
-        if (s.posmap[p % s.nslots] != p) return ERR("kv gather miss pos %u (state bug)", p);
+    if (n_kv > s.valid_prefix) return ERR("kv gather miss pos %u (state bug)", s.valid_prefix);
     return 0;
 }
 
@@ -682,7 +694,7 @@ int op_kv_append(Ctx& cx) {
         pos = s->count++;
         dev_pos = 0xFFFFFFFFu;
     }
-    s->posmap[pos % s->nslots] = pos;
+    kv_mark(*s, pos);
     CHECK_LAUNCH(launch_kv_append(s->dev, s->slot_bytes, s->nslots, k, v, kn, dev_pos,
                                   g.counters_dev + si, g.stream));
     return 0;
@@ -708,7 +720,7 @@ int op_kv_append_n(Ctx& cx) {
         s->count += n_tok;
         dev_pos = 0xFFFFFFFFu;
     }
-    for (uint32_t t = 0; t < n_tok; ++t) s->posmap[(pos + t) % s->nslots] = pos + t;
+    for (uint32_t t = 0; t < n_tok; ++t) kv_mark(*s, pos + t);
     CHECK_LAUNCH(launch_kv_append_n(s->dev, s->slot_bytes, s->nslots, k, v, kv_elems, n_tok, dev_pos,
                                     g.counters_dev + si, g.stream));
     return 0;
@@ -779,16 +791,7 @@ int op_attn_decode(Ctx& cx) {
     if (!q || !o) return ERR("attn_decode ref fail");
     const size_t qb = ref_bytes(cx.b, A(0));
     if (qb && qb < (uint64_t)H * hd * 2u) return ERR("attn_decode q smaller than H*hd");
-    const uint32_t need = attn_decode_work_floats(autopos ? s->nslots : n_kv, H, hd);
-    if (need > g.attn_work_floats) {
-        if (g.attn_work) hipFree(g.attn_work);
-        g.attn_work = nullptr;
-        g.attn_work_floats = 0;
-        if (hipMalloc(&g.attn_work, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace alloc");
-        // the leading completion counters must start at zero (kernels leave them zero)
-        if (hipMemset(g.attn_work, 0, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace clear");
-        g.attn_work_floats = need;
-    }
+    if (attn_workspace(attn_decode_work_floats(autopos ? s->nslots : n_kv, H, hd), err, errn)) return -1;
     CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o, n_kv,
                                     autopos ? g.counters_dev + (A(1) & 0x1FFFu) : nullptr, H, KVH, hd,
                                     scale, g.attn_work, g.attn_work_floats, g.stream));
@@ -846,7 +849,7 @@ int op_w4g_fused(Ctx& cx) {
     epi.res = res;
     epi.ldr = n_out;
     epi.swiglu = swiglu;
-    const bool gemv_fits = M <= kW4gGemvMaxM && (size_t)M * K * 2 + (size_t)M * 4096 * 4 <= 65536;
+    const bool gemv_fits = w4g_gemv_supported(M, K);
     if (gemv_fits) {
         epi.gamma = gamma;
         CHECK_LAUNCH(launch_w4g_gemv(a, K, wq, ws, y, ldy, M, N, K, g.stream, epi));
@@ -888,9 +891,54 @@ int op_qk_rope_kv(Ctx& cx) {
     if (!q_out || (A(2) != WT_REF_NONE && !k_out) || (A(3) != WT_REF_NONE && !v_out)) return ERR("qk_rope_kv out alloc");
     const uint32_t pos = s->count;
     s->count += n_tok;
-    for (uint32_t t = 0; t < n_tok; ++t) s->posmap[(pos + t) % s->nslots] = pos + t;
+    for (uint32_t t = 0; t < n_tok; ++t) kv_mark(*s, pos + t);
     CHECK_LAUNCH(launch_qk_rope_kv(qkv, n_tok, H, KVH, qg, kg, theta, q_out, k_out, v_out, s->dev, s->slot_bytes,
                                    s->nslots, g.counters_dev + si, g.stream));
+    return 0;
+}
+
+// Attention workspace shared by the decode ops (grown on demand). Zeroed when
+// allocated: the fused op's merge completion counter must start at zero.
+int attn_workspace(uint32_t need, char* err, size_t errn) {
+    if (need <= g.attn_work_floats) return 0;
+    if (g.attn_work) hipFree(g.attn_work);
+    g.attn_work = nullptr;
+    g.attn_work_floats = 0;
+    if (hipMalloc(&g.attn_work, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace alloc");
+    if (hipMemset(g.attn_work, 0, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace clear");
+    g.attn_work_floats = need;
+    return 0;
+}
+
+int op_attn_decode_qkv(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t H = A(3), KVH = A(4), hd = A(5);
+    const float theta = f32_from_bits(A(8)), scale = f32_from_bits(A(9));
+    if (hd != 128) return ERR("attn_decode_qkv head_dim %u unsupported (128 only)", hd);
+    if (!KVH || H % KVH) return ERR("attn_decode_qkv heads %u not a multiple of kv heads %u", H, KVH);
+    const uint32_t rep = H / KVH;
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return ERR("attn_decode_qkv group size %u unsupported", rep);
+    const __half* qkv = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    const __half* qg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(6)));
+    const __half* kg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(7)));
+    if (!qkv || !qg || !kg) return ERR("attn_decode_qkv ref fail");
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < (uint64_t)(H + 2 * KVH) * hd * 2u) return ERR("attn_decode_qkv input smaller than one qkv row");
+    const size_t qgb = ref_bytes(cx.b, A(6)), kgb = ref_bytes(cx.b, A(7));
+    if ((qgb && qgb < hd * 2u) || (kgb && kgb < hd * 2u)) return ERR("attn_decode_qkv gamma shorter than head_dim");
+    State* s = state_kv(A(1), KVH * hd, err, errn);
+    if (!s) return -1;
+    const uint32_t si = A(1) & 0x1FFFu;
+    if (s->count >= s->nslots)
+        return ERR("attn_decode_qkv state %u count=%u >= nslots=%u (context too long)", si, s->count, s->nslots);
+    if (kv_check(*s, s->count, err, errn)) return -1;
+    __half* o = reinterpret_cast<__half*>(temp_get(A(2), H * hd * 2u));
+    if (!o) return ERR("attn_decode_qkv out alloc");
+    if (attn_workspace(attn_decode_work_floats(s->nslots, H, hd), err, errn)) return -1;
+    kv_mark(*s, s->count);
+    s->count += 1;
+    CHECK_LAUNCH(launch_attn_decode_qkv(qkv, qg, kg, theta, s->dev, s->slot_bytes, s->nslots, g.counters_dev + si,
+                                        o, H, KVH, scale, g.attn_work, g.attn_work_floats, g.stream));
     return 0;
 }
 
@@ -952,6 +1000,7 @@ struct Table {
         fn[OP_KV_APPEND_N_F16] = op_kv_append_n;
         fn[OP_W4G_FUSED_F16] = op_w4g_fused;
         fn[OP_QK_ROPE_KV_F16] = op_qk_rope_kv;
+        fn[OP_ATTN_DECODE_QKV_F16] = op_attn_decode_qkv;
     }
 };
 const Table kTable;
@@ -1149,6 +1198,7 @@ void wt_exec_state_reset(void) {
         if (s.dev) hipMemset(s.dev, 0, s.bytes);
         s.count = 0;
         if (s.kv_ready) std::fill(s.posmap.begin(), s.posmap.end(), kNone);
+        s.valid_prefix = 0;
     }
     if (g.counters_dev) hipMemset(g.counters_dev, 0, WT_MAX_STATES * sizeof(uint32_t));
 }

@@ -7,6 +7,7 @@
 // O^T = V^T . P^T reuses P straight from the accumulator registers as the MFMA B
 // operand; V is staged transposed in LDS so the A operand reads 8-byte runs.
 #include "kernels.h"
+#include "dev_rope.h"
 
 #include <cmath>
 
@@ -162,66 +163,136 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Decode: workgroup (chunk c, kv head g) handles keys [64c, 64c+64) for the rep query
-// heads of g, reading each K/V row once. Partial (max, sum, O) go to the workspace
-// and a second kernel merges the chunks with the log-sum-exp rule.
+// Decode, pass 1: workgroup (chunk c, kv head g) handles keys [64c, 64c+64) for the REP
+// query heads of g, reading each K/V row once; all K and V loads of the chunk are
+// issued before any arithmetic, so a chunk costs one memory round trip. Partials
+// (O[128], max, sum) go to the workspace. Pass 2 (attn_merge_kernel) combines the
+// chunks of each query head with the log-sum-exp rule. Two launches instead of a
+// "last workgroup merges" scheme: on gfx950 the device-scope fence that scheme needs
+// writes back and invalidates the whole L2 in every workgroup.
+//
+// FUSED (OP_ATTN_DECODE_QKV_F16): q, k and v of the new token come raw from the fused
+// QKV row. Each workgroup applies QK-RMSNorm + RoPE to its REP query heads itself (the
+// arithmetic of qk_rope_kv_kernel, so the bits match), and the workgroup whose chunk
+// holds the new position also normalizes/rotates k of head g, writes k and v into the
+// ring slot and uses them for that key. The position is the state's device counter;
+// the merge pass advances it.
 constexpr int DC = 64;          // keys per chunk
 constexpr int MAX_REP = 8;
+constexpr int PS = HD + 4;      // partial record: O[HD], m, l, 2 pad (16-byte aligned)
+constexpr uint32_t kMergeSlots = 4;   // workspace head: merge completion counter (uint32)
 
-template <int REP>
-__global__ __launch_bounds__(256) void attn_decode_kernel(
-    const __half* __restrict__ q, const uint8_t* __restrict__ ring, uint32_t slot_bytes,
-    uint32_t nslots, uint32_t n_kv_host, const uint32_t* __restrict__ count_dev, uint32_t KVH,
-    float scale_log2, float* __restrict__ work, uint32_t* __restrict__ done, uint32_t max_chunks,
-    __half* __restrict__ out) {
+struct DecodeArgs {
+    const __half* q;         // [H, HD] ready queries (plain op)
+    const __half* qkv;       // fused: [q | k | v] row of the new token
+    const __half* qg;        // fused: q / k RMSNorm gammas [HD]
+    const __half* kg;
+    float theta;             // fused: RoPE base
+    uint8_t* ring;
+    uint32_t slot_bytes, nslots, KVH, H;
+    uint32_t n_kv_host;      // used when count is null
+    uint32_t* count;         // device position counter (plain op: n_kv = *count)
+    float scale_log2;
+    float* part;             // partials [KVH][max_chunks][REP][PS]
+    uint32_t max_chunks;
+};
+
+template <int REP, bool FUSED>
+__global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     __shared__ float sc[REP][DC];
-    __shared__ float red[4][REP][HD];
-    __shared__ float s_M[REP], s_L[REP];
-    __shared__ uint32_t s_last;
-    const uint32_t n_kv = count_dev ? *count_dev : n_kv_host;
+    __shared__ __align__(16) float red[4][REP][HD];
+    __shared__ __align__(16) _Float16 s_q[REP][HD];
+    __shared__ __align__(16) _Float16 s_kv[2][HD];
     const uint32_t c = blockIdx.x, g = blockIdx.y;
+    const uint32_t pos = FUSED ? *A.count : 0u;   // position of the new token
+    const uint32_t n_kv = FUSED ? pos + 1 : (A.count ? *A.count : A.n_kv_host);
     if (c * DC >= n_kv) return;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t ch = lane & 15;   // 8-dim chunk of the head
+    const uint32_t ks = tid >> 4;    // key stream: keys ks, ks+16, ks+32, ks+48
 
-    u32x4 qv[REP];
-#pragma unroll
-    for (int r = 0; r < REP; ++r)
-        qv[r] = *reinterpret_cast<const u32x4*>(q + (size_t)(g * REP + r) * HD + ch * 8);
-
-    // Phase 1: scores. 4 keys per wave per step (16 lanes per key).
+    // Issue every load of the chunk first: K and V rows of this thread's keys.
+    u32x4 kv4[DC / 16], vv4[DC / 16];
 #pragma unroll
     for (int it = 0; it < DC / 16; ++it) {
-        const uint32_t kl = it * 16 + wave * 4 + (lane >> 4);
-        const uint32_t key = c * DC + kl;
-        float acc[REP];
-#pragma unroll
-        for (int r = 0; r < REP; ++r) acc[r] = 0.0f;
-        if (key < n_kv) {
-            const uint32_t slot = key % nslots;
-            const u32x4 kv4 = *reinterpret_cast<const u32x4*>(
-                ring + (size_t)slot * slot_bytes + ((size_t)g * HD + ch * 8) * 2);
-#pragma unroll
-            for (int r = 0; r < REP; ++r)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc[r] = __builtin_amdgcn_fdot2(as_h2(kv4[e]),
-                                                    as_h2(qv[r][e]), acc[r], false);
+        const uint32_t key = c * DC + ks + 16 * it;
+        const uint32_t slot = (key < n_kv ? key : c * DC) % A.nslots;
+        const uint8_t* base = A.ring + (size_t)slot * A.slot_bytes + ((size_t)g * HD + ch * 8) * 2;
+        kv4[it] = *reinterpret_cast<const u32x4*>(base);
+        vv4[it] = *reinterpret_cast<const u32x4*>(base + A.slot_bytes / 2);
+    }
+
+    u32x4 qv[REP];
+    if constexpr (FUSED) {
+        const bool owns_new = pos / DC == c;
+        float cr, sr;
+        dev::rope_cs(pos, lane, A.theta, cr, sr);
+        for (uint32_t r = wave; r < (uint32_t)REP; r += 4) {
+            const __half* src = A.qkv + (size_t)(g * REP + r) * HD;
+            float y1, y2;
+            dev::head_norm_rope(__half2float(src[lane]), __half2float(src[lane + 64]), __half2float(A.qg[lane]),
+                                __half2float(A.qg[lane + 64]), cr, sr, y1, y2);
+            s_q[r][lane] = (_Float16)y1;
+            s_q[r][lane + 64] = (_Float16)y2;
         }
+        if (owns_new && wave == (REP < 4 ? (uint32_t)REP : 0u) % 4) {
+            // k of head g: norm + RoPE; v raw. Written to the ring and kept for this chunk.
+            const __half* ksrc = A.qkv + (size_t)(A.H + g) * HD;
+            const __half* vsrc = A.qkv + (size_t)(A.H + A.KVH + g) * HD;
+            float y1, y2;
+            dev::head_norm_rope(__half2float(ksrc[lane]), __half2float(ksrc[lane + 64]), __half2float(A.kg[lane]),
+                                __half2float(A.kg[lane + 64]), cr, sr, y1, y2);
+            s_kv[0][lane] = (_Float16)y1;
+            s_kv[0][lane + 64] = (_Float16)y2;
+            s_kv[1][lane] = __builtin_bit_cast(_Float16, __half_as_ushort(vsrc[lane]));
+            s_kv[1][lane + 64] = __builtin_bit_cast(_Float16, __half_as_ushort(vsrc[lane + 64]));
+            _Float16* kface = reinterpret_cast<_Float16*>(A.ring + (size_t)(pos % A.nslots) * A.slot_bytes);
+            _Float16* vface = kface + A.KVH * HD;
+            kface[g * HD + lane] = (_Float16)y1;
+            kface[g * HD + lane + 64] = (_Float16)y2;
+            vface[g * HD + lane] = s_kv[1][lane];
+            vface[g * HD + lane + 64] = s_kv[1][lane + 64];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < REP; ++r) qv[r] = *reinterpret_cast<const u32x4*>(&s_q[r][ch * 8]);
+        if (owns_new) {
+#pragma unroll
+            for (int it = 0; it < DC / 16; ++it) {
+                if (c * DC + ks + 16 * it == pos) {
+                    kv4[it] = *reinterpret_cast<const u32x4*>(&s_kv[0][ch * 8]);
+                    vv4[it] = *reinterpret_cast<const u32x4*>(&s_kv[1][ch * 8]);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < REP; ++r)
+            qv[r] = *reinterpret_cast<const u32x4*>(A.q + (size_t)(g * REP + r) * HD + ch * 8);
+    }
+
+    // Scores: 16 lanes per key, 4 keys per wave per step.
+#pragma unroll
+    for (int it = 0; it < DC / 16; ++it) {
+        const uint32_t kl = ks + 16 * it;
+        const bool valid = c * DC + kl < n_kv;
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
-            float a = acc[r];
+            float a = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                a = __builtin_amdgcn_fdot2(as_h2(kv4[it][e]), as_h2(qv[r][e]), a, false);
             a += __shfl_xor(a, 8, 64);
             a += __shfl_xor(a, 4, 64);
             a += __shfl_xor(a, 2, 64);
             a += __shfl_xor(a, 1, 64);
-            if (ch == 0) sc[r][kl] = key < n_kv ? a * scale_log2 : -INFINITY;
+            if (ch == 0) sc[r][kl] = valid ? a * A.scale_log2 : -INFINITY;
         }
     }
     __syncthreads();
 
-    // Phase 2: per-head max and exponentials over the chunk (one wave per head).
-    float* wchunk = work + ((size_t)g * max_chunks + c) * REP * (HD + 2);
+    // Per-head max and exponentials over the chunk (one wave per head).
+    float* wchunk = A.part + ((size_t)g * A.max_chunks + c) * REP * PS;
     for (uint32_t r = wave; r < REP; r += 4) {
         const float x = sc[r][lane];
         float m = x;
@@ -232,35 +303,34 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
         sc[r][lane] = p;
-        if (lane == 0) { wchunk[r * (HD + 2)] = m; wchunk[r * (HD + 2) + 1] = l; }
+        if (lane == 0) { wchunk[r * PS + HD] = m; wchunk[r * PS + HD + 1] = l; }
     }
     __syncthreads();
 
-    // Phase 3: O[r][d] = sum_key p[r][key] V[key][d]; 16 key streams x 16 dim chunks.
+    // O[r][d] = sum_key p[r][key] V[key][d] over this thread's 4 keys and 8 dims.
     float acc[REP][8];
 #pragma unroll
     for (int r = 0; r < REP; ++r)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
-    const uint32_t stream = tid >> 4;
 #pragma unroll
     for (int it = 0; it < DC / 16; ++it) {
-        const uint32_t kl = stream + 16 * it;
-        const uint32_t key = c * DC + kl;
-        if (key < n_kv) {
-            const uint32_t slot = key % nslots;
-            const u32x4 vv4 = *reinterpret_cast<const u32x4*>(
-                ring + (size_t)slot * slot_bytes + slot_bytes / 2 + ((size_t)g * HD + ch * 8) * 2);
-            const _Float16* ve = reinterpret_cast<const _Float16*>(&vv4);
+        const uint32_t kl = ks + 16 * it;
+        float ve[8];
 #pragma unroll
-            for (int r = 0; r < REP; ++r) {
-                const float p = sc[r][kl];
+        for (int e = 0; e < 4; ++e) {
+            const h2_t v2 = as_h2(vv4[it][e]);
+            ve[2 * e] = (float)v2[0];
+            ve[2 * e + 1] = (float)v2[1];
+        }
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(p, (float)ve[e], acc[r][e]);
-            }
+        for (int r = 0; r < REP; ++r) {
+            const float p = sc[r][kl];   // 0 for keys past n_kv
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(p, ve[e], acc[r][e]);
         }
     }
-    // Reduce the 4 streams inside the wave (lanes l, l^16, l^32, l^48), then across waves.
+    // Reduce the 4 key streams of a wave (lanes l, l^16, l^32, l^48), then across waves.
 #pragma unroll
     for (int r = 0; r < REP; ++r)
 #pragma unroll
@@ -277,47 +347,81 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
             for (int e = 0; e < 8; ++e) red[wave][r][ch * 8 + e] = acc[r][e];
     }
     __syncthreads();
-    for (uint32_t i = tid; i < REP * HD; i += 256) {
-        const uint32_t r = i / HD, d = i % HD;
-        wchunk[r * (HD + 2) + 2 + d] = red[0][r][d] + red[1][r][d] + red[2][r][d] + red[3][r][d];
+    for (uint32_t i = tid; i < REP * HD / 4; i += 256) {
+        const uint32_t r = i / (HD / 4), d = (i % (HD / 4)) * 4;
+        float4 o;
+        o.x = red[0][r][d] + red[1][r][d] + red[2][r][d] + red[3][r][d];
+        o.y = red[0][r][d + 1] + red[1][r][d + 1] + red[2][r][d + 1] + red[3][r][d + 1];
+        o.z = red[0][r][d + 2] + red[1][r][d + 2] + red[2][r][d + 2] + red[3][r][d + 2];
+        o.w = red[0][r][d + 3] + red[1][r][d + 3] + red[2][r][d + 3] + red[3][r][d + 3];
+        *reinterpret_cast<float4*>(wchunk + r * PS + d) = o;
     }
+}
 
-    // The last workgroup of this kv head to finish merges the chunks (log-sum-exp) and
-    // resets the completion counter for the next call.
+// Decode, pass 2: one workgroup per query head h = g*rep + r merges its chunks:
+// M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c - M) / L.
+// Thread (grp, d4) sums chunks grp, grp+8, ... of dims 4*d4..4*d4+3 (float4 loads).
+// With `advance`, n_kv = *count + 1 and the last workgroup to finish increments the
+// counter (every workgroup has read it by then) and re-arms the completion counter.
+__global__ __launch_bounds__(256) void attn_merge_kernel(
+    const float* __restrict__ part, uint32_t* __restrict__ done, uint32_t n_kv_host,
+    uint32_t* __restrict__ count, int advance, uint32_t rep, uint32_t max_chunks, __half* __restrict__ out) {
+    __shared__ float s_red[4];
+    __shared__ __align__(16) float4 s_o[256];
+    const uint32_t n_kv = count ? *count + (advance ? 1u : 0u) : n_kv_host;
     const uint32_t nc = (n_kv + DC - 1) / DC;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&done[g], 1u) == nc - 1) ? 1u : 0u;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const float* wg = work + (size_t)g * max_chunks * REP * (HD + 2);
-    for (uint32_t r = wave; r < REP; r += 4) {
-        float M = -INFINITY;
-        for (uint32_t cc = lane; cc < nc; cc += 64) M = fmaxf(M, wg[(size_t)cc * REP * (HD + 2) + r * (HD + 2)]);
+    const uint32_t h = blockIdx.x, g = h / rep, r = h % rep;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* base = part + ((size_t)g * max_chunks * rep + r) * PS;   // chunk c at + c*rep*PS
+    const size_t cstride = (size_t)rep * PS;
+
+    float M = -INFINITY;
+    for (uint32_t c = tid; c < nc; c += 256) M = fmaxf(M, base[c * cstride + HD]);
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-        float L = 0.0f;
-        for (uint32_t cc = lane; cc < nc; cc += 64) {
-            const float* w = wg + (size_t)cc * REP * (HD + 2) + r * (HD + 2);
-            L += w[1] * exp2f(w[0] - M);
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
-        if (lane == 0) { s_M[r] = M; s_L[r] = L; }
-    }
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    if (lane == 0) s_red[wave] = M;
     __syncthreads();
-    for (uint32_t i = tid; i < REP * HD; i += 256) {
-        const uint32_t r = i / HD, d = i % HD;
-        const float M = s_M[r];
-        float O = 0.0f;
-        for (uint32_t cc = 0; cc < nc; ++cc) {
-            const float* w = wg + (size_t)cc * REP * (HD + 2) + r * (HD + 2);
-            O += w[2 + d] * exp2f(w[0] - M);
-        }
-        out[(size_t)(g * REP + r) * HD + d] = __float2half(s_L[r] > 0.0f ? O / s_L[r] : 0.0f);
+    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    __syncthreads();
+    float L = 0.0f;
+    for (uint32_t c = tid; c < nc; c += 256) {
+        const float* w = base + c * cstride;
+        L += w[HD + 1] * exp2f(w[HD] - M);
     }
-    if (tid == 0) done[g] = 0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+    if (lane == 0) s_red[wave] = L;
+
+    const uint32_t d4 = tid & 31, grp = tid >> 5;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+    for (uint32_t c = grp; c < nc; c += 8) {
+        const float* w = base + c * cstride;
+        const float wt = exp2f(w[HD] - M);
+        const float4 v = *reinterpret_cast<const float4*>(w + 4 * d4);
+        o.x = fmaf(wt, v.x, o.x);
+        o.y = fmaf(wt, v.y, o.y);
+        o.z = fmaf(wt, v.z, o.z);
+        o.w = fmaf(wt, v.w, o.w);
+    }
+    s_o[tid] = o;
+    __syncthreads();
+    if (tid < 32) {
+        L = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+        for (uint32_t k = 1; k < 8; ++k) {
+            const float4 p = s_o[tid + 32 * k];
+            o.x += p.x; o.y += p.y; o.z += p.z; o.w += p.w;
+        }
+        h4_t hv = {(_Float16)(L > 0.0f ? o.x / L : 0.0f), (_Float16)(L > 0.0f ? o.y / L : 0.0f),
+                   (_Float16)(L > 0.0f ? o.z / L : 0.0f), (_Float16)(L > 0.0f ? o.w / L : 0.0f)};
+        *reinterpret_cast<h4_t*>(out + (size_t)h * HD + 4 * tid) = hv;
+    }
+    if (advance && tid == 0) {
+        if (atomicAdd(done, 1u) == gridDim.x - 1) {
+            atomicAdd(count, 1u);
+            atomicExch(done, 0u);
+        }
+    }
 }
 
 }  // namespace
@@ -339,19 +443,38 @@ hipError_t launch_attn_prefill(const __half* q, uint32_t ldq, const __half* k, c
     return hipGetLastError();
 }
 
-// Workspace: KVH completion counters (64 floats reserved, zero before the first call;
-// every call leaves them zero) followed by the per-chunk partials.
-constexpr uint32_t kDoneSlots = 64;
-
+// Workspace: a 16-byte head (merge completion counter, zero before first use and left
+// zero by every call) then per (kv head, chunk, query head) partial records of PS floats.
 uint32_t attn_decode_work_floats(uint32_t max_kv, uint32_t H, uint32_t hd) {
-    return kDoneSlots + ((max_kv + DC - 1) / DC) * H * (hd + 2);
+    (void)hd;
+    return kMergeSlots + ((max_kv + DC - 1) / DC) * H * PS;
 }
+
+namespace {
+
+template <bool FUSED>
+hipError_t decode_launch(const DecodeArgs& A, uint32_t rep, int advance, __half* out, float* work,
+                         hipStream_t st) {
+    dim3 grid(A.max_chunks, A.KVH);
+    switch (rep) {
+    case 1: hipLaunchKernelGGL((attn_decode_kernel<1, FUSED>), grid, dim3(256), 0, st, A); break;
+    case 2: hipLaunchKernelGGL((attn_decode_kernel<2, FUSED>), grid, dim3(256), 0, st, A); break;
+    case 4: hipLaunchKernelGGL((attn_decode_kernel<4, FUSED>), grid, dim3(256), 0, st, A); break;
+    case 8: hipLaunchKernelGGL((attn_decode_kernel<8, FUSED>), grid, dim3(256), 0, st, A); break;
+    default: return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(A.H), dim3(256), 0, st, A.part,
+                       reinterpret_cast<uint32_t*>(work), A.n_kv_host, A.count, advance, rep, A.max_chunks, out);
+    return hipGetLastError();
+}
+
+}  // namespace
 
 hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slot_bytes,
                               uint32_t nslots, __half* out, uint32_t n_kv_host,
                               const uint32_t* count_dev, uint32_t H, uint32_t KVH, uint32_t hd,
                               float scale, float* work, uint32_t work_floats, hipStream_t st) {
-    if (hd != HD || !KVH || H % KVH || KVH > kDoneSlots) return hipErrorInvalidValue;
+    if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
     const uint32_t rep = H / KVH;
     if (rep > MAX_REP || slot_bytes != KVH * HD * 4) return hipErrorInvalidValue;
     // Chunks cover every position the ring can hold, so a device-side count never
@@ -360,18 +483,23 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
     const uint32_t max_chunks = (max_kv + DC - 1) / DC;
     if (attn_decode_work_floats(max_kv, H, hd) > work_floats) return hipErrorInvalidValue;
     if (!max_chunks) return hipSuccess;
-    const float sl2 = scale * kLog2e;
-    uint32_t* done = reinterpret_cast<uint32_t*>(work);
-    float* part = work + kDoneSlots;
-    dim3 grid(max_chunks, KVH);
-    switch (rep) {
-    case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, part, done, max_chunks, out); break;
-    case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, part, done, max_chunks, out); break;
-    case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, part, done, max_chunks, out); break;
-    case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(256), 0, st, q, ring, slot_bytes, nslots, n_kv_host, count_dev, KVH, sl2, part, done, max_chunks, out); break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    DecodeArgs A{q, nullptr, nullptr, nullptr, 0.0f, const_cast<uint8_t*>(ring), slot_bytes, nslots, KVH, H,
+                 n_kv_host, const_cast<uint32_t*>(count_dev), scale * kLog2e, work + kMergeSlots, max_chunks};
+    return decode_launch<false>(A, rep, 0, out, work, st);
+}
+
+hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, const __half* k_gamma,
+                                  float theta, uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
+                                  uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH,
+                                  float scale, float* work, uint32_t work_floats, hipStream_t st) {
+    if (!KVH || H % KVH || !count_dev) return hipErrorInvalidValue;
+    const uint32_t rep = H / KVH;
+    if (rep > MAX_REP || slot_bytes != KVH * HD * 4 || !nslots) return hipErrorInvalidValue;
+    const uint32_t max_chunks = (nslots + DC - 1) / DC;
+    if (attn_decode_work_floats(nslots, H, HD) > work_floats) return hipErrorInvalidValue;
+    DecodeArgs A{nullptr, qkv, q_gamma, k_gamma, theta, ring, slot_bytes, nslots, KVH, H,
+                 0u, count_dev, scale * kLog2e, work + kMergeSlots, max_chunks};
+    return decode_launch<true>(A, rep, 1, out, work, st);
 }
 
 }  // namespace gehtp

@@ -4,6 +4,7 @@
 // with explicitly rounded operations (__fmul_rn / __fadd_rn / __fdiv_rn) so no
 // FMA contraction changes a result the reference's scalar path defines exactly.
 #include "kernels.h"
+#include "dev_rope.h"
 
 #include <cmath>
 
@@ -32,31 +33,7 @@ __device__ __forceinline__ float wave_max_f(float v) {
     return v;
 }
 
-// binary64 -> binary16, one RNE rounding (the reference builds RoPE tables this way).
-__device__ __forceinline__ uint16_t f64_to_f16_bits(double d) {
-    const uint64_t x = __builtin_bit_cast(uint64_t, d);
-    const uint16_t sign = (uint16_t)((x >> 48) & 0x8000u);
-    const int32_t dexp = (int32_t)((x >> 52) & 0x7ffu);
-    const uint64_t man = x & ((1ull << 52) - 1);
-    if (dexp == 0x7ff) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u : 0u));
-    const int32_t exp = dexp - 1008;
-    if (exp >= 31) return (uint16_t)(sign | 0x7c00u);
-    uint64_t kept, rem, halfway;
-    if (exp <= 0) {
-        if (exp < -10) return sign;
-        const uint64_t m = man | (1ull << 52);
-        const uint32_t shift = (uint32_t)(43 - exp);
-        kept = m >> shift;
-        rem = m & ((1ull << shift) - 1);
-        halfway = 1ull << (shift - 1);
-    } else {
-        kept = ((uint64_t)exp << 10) | (man >> 42);
-        rem = man & ((1ull << 42) - 1);
-        halfway = 1ull << 41;
-    }
-    if (rem > halfway || (rem == halfway && (kept & 1u))) kept++;
-    return (uint16_t)(sign | kept);
-}
+using dev::f64_to_f16_bits;
 
 // ---------------------------------------------------------------------------
 // RMSNorm, one wavefront per row (reference exec_rmsnorm2, oplist_exec.c:1859-1871):
@@ -218,9 +195,34 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const __half* __restrict__
     __shared__ int32_t si[16];
     float bv = -1e30f;
     int32_t bi = 0;
-    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
-        const float v = h2f(x[i]);
-        if (v > bv) { bv = v; bi = (int32_t)i; }
+    // 16-byte loads (8 values) when x is aligned, four in flight per thread; each
+    // thread scans its indices in increasing order, so "first strict max" survives.
+    const uint32_t n8 = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) ? n / 8 : 0;
+    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+    uint32_t i = threadIdx.x;
+    for (; i + 3 * 1024 < n8; i += 4 * 1024) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = xv[i + u * 1024];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float f = h2f(__ushort_as_half((uint16_t)(v[u][e / 2] >> (16 * (e & 1)))));
+                if (f > bv) { bv = f; bi = (int32_t)((i + u * 1024) * 8 + e); }
+            }
+    }
+    for (; i < n8; i += 1024) {
+        const u32x4 v = xv[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = h2f(__ushort_as_half((uint16_t)(v[e / 2] >> (16 * (e & 1)))));
+            if (f > bv) { bv = f; bi = (int32_t)(i * 8 + e); }
+        }
+    }
+    for (uint32_t j = n8 * 8 + threadIdx.x; j < n; j += 1024) {
+        const float v = h2f(x[j]);
+        if (v > bv) { bv = v; bi = (int32_t)j; }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -381,9 +383,8 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QkRopeKvArgs A) {
     __syncthreads();
     const uint32_t pos = s_pos + t;
     const uint32_t slot = pos % A.nslots;
-    const double inv = 1.0 / pow((double)A.theta, (double)(2 * lane) / (double)HD);
-    const float c = __half2float(__ushort_as_half(f64_to_f16_bits(cos((double)pos * inv))));
-    const float s = __half2float(__ushort_as_half(f64_to_f16_bits(sin((double)pos * inv))));
+    float c, s;
+    dev::rope_cs(pos, lane, A.theta, c, s);
     const __half* row = A.qkv + (size_t)t * A.ld;
     __half* kface = reinterpret_cast<__half*>(A.ring + (size_t)slot * A.slot_bytes);
     __half* vface = kface + A.KVH * HD;
@@ -391,15 +392,10 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QkRopeKvArgs A) {
         const bool is_q = r < A.H;
         const __half* src = row + (size_t)r * HD;   // k heads follow the q heads
         const __half* gm = is_q ? A.qg : A.kg;
-        const float x1 = h2f(src[lane]), x2 = h2f(src[lane + 64]);
-        double ss = (double)x1 * (double)x1 + (double)x2 * (double)x2;
-        ss = wave_sum_d(ss);
-        const float rms = (float)sqrt(ss / (double)HD + 1e-6);
-        const float h1 = h2f(f2h(__fadd_rn(__fmul_rn(__fdiv_rn(x1, rms), h2f(gm[lane])), 0.0f)));
-        const float h2 = h2f(f2h(__fadd_rn(__fmul_rn(__fdiv_rn(x2, rms), h2f(gm[lane + 64])), 0.0f)));
-        const float a1 = h2f(f2h(__fmul_rn(h1, c))), b1 = h2f(f2h(__fmul_rn(-h2, s)));
-        const float a2 = h2f(f2h(__fmul_rn(h2, c))), b2 = h2f(f2h(__fmul_rn(h1, s)));
-        const __half y1 = f2h(__fadd_rn(a1, b1)), y2 = f2h(__fadd_rn(a2, b2));
+        float y1f, y2f;
+        dev::head_norm_rope(h2f(src[lane]), h2f(src[lane + 64]), h2f(gm[lane]), h2f(gm[lane + 64]), c, s,
+                            y1f, y2f);
+        const __half y1 = f2h(y1f), y2 = f2h(y2f);
         if (is_q) {
             __half* qo = A.q_out + (size_t)t * A.H * HD + (size_t)r * HD;
             qo[lane] = y1;

@@ -10,6 +10,9 @@
 // same pair order so each pair feeds one v_dot2_f32_f16 (fp32 accumulate).
 #include "kernels.h"
 
+#include <algorithm>
+#include <cmath>
+
 namespace gehtp {
 
 namespace {
@@ -22,39 +25,43 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 __device__ __forceinline__ uint32_t as_u32(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
+// (w & 0x000F000F) | 0x64006400 in one VALU op. Written out because with both
+// constants as literals the compiler emits a separate AND and OR (gfx9 VOP3 takes no
+// literal, so the OR constant is passed in a VGPR).
+__device__ __forceinline__ uint32_t nib_magic(uint32_t w, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(0x000F000Fu), "v"(magic));
+    return r;
+}
+
 // Four dequantized pairs (k0,k4),(k1,k5),(k2,k6),(k3,k7) of one weight word.
 __device__ __forceinline__ void dequant_word(uint32_t w, h2_t s2, h2_t out[4]) {
     const h2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const uint32_t magic = 0x64006400u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t m = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+        const uint32_t m = nib_magic(w >> (4 * i), magic);
         const h2_t q = as_h2(m) - bias;   // exact: integers below 2048
         out[i] = q * s2;                  // one RNE rounding: fp16(q*s)
     }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 // ---------------------------------------------------------------------------
-// GEMV: each workgroup streams the contiguous weight rows [r0, r0+RB) as a flat
-// sequence of 32-byte groups (j = row*G + g), so consecutive threads read
-// consecutive 32-byte pieces regardless of K. Activations sit in LDS as
-// xs[m][c][g] (16 bytes each, pair order) so that threads working on consecutive
-// groups read consecutive 16-byte LDS words. Group partial sums land in LDS and
-// one wavefront per row (or row pair, for SwiGLU) adds them up and applies the
-// epilogue.
+// GEMV (M <= 4). A weight row is S = K/32 slices of 16 bytes (32 weights, half a
+// scale group). P = S threads share a row, each owning one slice; R = nthreads/P rows
+// are processed per pass and a workgroup runs np passes over its R*np contiguous rows.
+// A thread's activation slice stays in registers (pair order) for the whole kernel,
+// so the inner loop is global loads + dequant + v_dot2 with no LDS traffic; weight
+// loads for the next 4 passes are in flight while the current 4 are computed. Pass
+// partials go to LDS and 16 lanes per row sum them before the epilogue.
 struct GemvArgs {
     const __half* x;
     uint32_t ldx;
-    const u32x4* wq;
+    const uint8_t* wq;
     const __half* ws;
     __half* y;
     uint32_t ldy;
-    uint32_t N, G, rows_per_wg;
+    uint32_t N, K, P, R, np;
     const __half* gamma;
     const __half* res;
     uint32_t ldr;
@@ -70,50 +77,66 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t f2hb(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
+__device__ __forceinline__ float sum16(float v) {   // over aligned groups of 16 lanes
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 1, 64);
+    return v;
+}
+
+constexpr int kGemvU = 4;   // passes per load batch
+
 template <int MR>
-__global__ __launch_bounds__(256) void w4g_gemv_kernel(GemvArgs A) {
-    extern __shared__ uint4 smem[];
-    const uint32_t G = A.G;
-    uint4* xs = smem;                                   // [MR][8][G]
-    float* red = reinterpret_cast<float*>(smem + MR * 8 * G);   // [MR][RB*G]
-    __shared__ double s_ss[4][MR];
+__global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
+    constexpr int U = kGemvU;
+    extern __shared__ __align__(16) float red[];   // [np][MR][nt] partials; earlier [MR][K] halves
+    __shared__ double s_ss[8][MR];
     __shared__ float s_rms[MR];
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t r0 = blockIdx.x * A.rows_per_wg;
-    const uint32_t RB = min(A.rows_per_wg, A.N - r0);
-    const uint32_t T = RB * G;
-    const u32x4* wrow = A.wq + (size_t)r0 * G * 2;
-    const __half* srow = A.ws + (size_t)r0 * G;
+    const uint32_t nt = blockDim.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t P = A.P, R = A.R;
+    const uint32_t p = t % P, rr = t / P;
+    const bool active = rr < R;
+    const uint32_t rows_wg = R * A.np;
+    const uint32_t r0 = blockIdx.x * rows_wg;
+    const uint32_t RB = min(rows_wg, A.N - r0);
+    const uint32_t rowbytes = A.K / 2, G = A.K / 64, K8 = A.K / 8;
+    const uint32_t nb = (A.np + U - 1) / U;
 
-    constexpr int U = 4;
-    // Issue the first batch of weight loads before staging activations.
-    u32x4 wv[U][2];
-    __half sv[U];
+    auto load_batch = [&](uint32_t b, u32x4 (&w)[U], uint16_t (&s)[U]) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const uint32_t j = tid + 256u * u;
-        if (j < T) {
-            wv[u][0] = __builtin_nontemporal_load(&wrow[2 * j]);
-            wv[u][1] = __builtin_nontemporal_load(&wrow[2 * j + 1]);
-            sv[u] = srow[j];
+        for (int u = 0; u < U; ++u) {
+            const uint32_t lr = (b * U + u) * R + rr;
+            if (active && lr < RB) {
+                const size_t row = r0 + lr;
+                w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(A.wq + row * rowbytes) + p);
+                s[u] = __builtin_bit_cast(uint16_t, A.ws[row * G + (p >> 1)]);
+            } else {
+                w[u] = u32x4{0u, 0u, 0u, 0u};
+                s[u] = 0;
+            }
         }
-    }
+    };
+    u32x4 wa[U], wb[U];
+    uint16_t sa[U], sb[U];
+    load_batch(0, wa, sa);
 
-    // Optional RMSNorm prologue: every workgroup computes the rows' sums of squares
-    // (in double, as RMSNORM2_F16 does) from its own reads of x.
+    // This thread's activation slice (32 values per row m), raw or RMS-normalized.
+    u32x4 xr[MR][4];
     if (A.gamma) {
+        // RMSNorm prologue, cooperative: sum of squares in double (as RMSNORM2_F16), then
+        // h = f16(x / rms * gamma + 0) for the whole row into LDS.
         double ss[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) ss[m] = 0.0;
-        for (uint32_t i = tid; i < 8 * G; i += 256) {
+        for (uint32_t i = t; i < K8; i += nt) {
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
-                const uint4 v = *reinterpret_cast<const uint4*>(A.x + (size_t)m * A.ldx + i * 8);
-                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+                const u32x4 v = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[i];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const double lo = (double)h2f((uint16_t)(w4[e] & 0xFFFFu));
-                    const double hi = (double)h2f((uint16_t)(w4[e] >> 16));
+                    const double lo = (double)h2f((uint16_t)(v[e] & 0xFFFFu));
+                    const double hi = (double)h2f((uint16_t)(v[e] >> 16));
                     ss[m] += lo * lo;
                     ss[m] += hi * hi;
                 }
@@ -121,126 +144,135 @@ __global__ __launch_bounds__(256) void w4g_gemv_kernel(GemvArgs A) {
         }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            const double t = wave_sum_d(ss[m]);
-            if (lane == 0) s_ss[wave][m] = t;
+            const double w = wave_sum_d(ss[m]);
+            if (lane == 0) s_ss[wave][m] = w;
         }
         __syncthreads();
-        if (tid < MR) {
-            const double t = s_ss[0][tid] + s_ss[1][tid] + s_ss[2][tid] + s_ss[3][tid];
-            s_rms[tid] = (float)sqrt(t / (double)(G * 64) + 1e-6);
+        if (t < MR) {
+            double tot = 0.0;
+            for (uint32_t w = 0; w < nt / 64; ++w) tot += s_ss[w][t];
+            s_rms[t] = (float)sqrt(tot / (double)A.K + 1e-6);
         }
         __syncthreads();
-    }
-
-    for (uint32_t i = tid; i < MR * 8 * G; i += 256) {
-        const uint32_t m = i / (8 * G);
-        const uint32_t rem = i - m * 8 * G;
-        const uint32_t g = rem >> 3, c = rem & 7;
-        uint4 v = *reinterpret_cast<const uint4*>(A.x + (size_t)m * A.ldx + g * 64 + c * 8);
-        if (A.gamma) {
-            // h = f16(f16-exact x / rms * gamma + 0), the RMSNORM2_F16 arithmetic
-            const uint4 gv = *reinterpret_cast<const uint4*>(A.gamma + g * 64 + c * 8);
-            const float rms = s_rms[m];
-            uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-            const uint32_t g4[4] = {gv.x, gv.y, gv.z, gv.w};
+        u32x4* xn = reinterpret_cast<u32x4*>(red);
+        for (uint32_t i = t; i < K8; i += nt) {
+            const u32x4 gv = reinterpret_cast<const u32x4*>(A.gamma)[i];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float lo = __fdiv_rn(h2f((uint16_t)(w4[e] & 0xFFFFu)), rms);
-                float hi = __fdiv_rn(h2f((uint16_t)(w4[e] >> 16)), rms);
-                lo = __fadd_rn(__fmul_rn(lo, h2f((uint16_t)(g4[e] & 0xFFFFu))), 0.0f);
-                hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(g4[e] >> 16))), 0.0f);
-                w4[e] = (uint32_t)f2hb(lo) | ((uint32_t)f2hb(hi) << 16);
-            }
-            v = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-        }
-        uint4 p;
-        p.x = (v.x & 0xFFFFu) | (v.z << 16);
-        p.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
-        p.z = (v.y & 0xFFFFu) | (v.w << 16);
-        p.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
-        xs[(m * 8 + c) * G + g] = p;
-    }
-    __syncthreads();
-
-    const uint32_t step = 256u % G;
-    uint32_t g0 = tid % G;
-    for (uint32_t jb = tid; jb < T; jb += 256u * U) {
-        uint32_t g = g0;
+            for (int m = 0; m < MR; ++m) {
+                const u32x4 v = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[i];
+                const float rms = s_rms[m];
+                u32x4 o;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t j = jb + 256u * u;
-            if (j < T) {
-                const _Float16 s = __builtin_bit_cast(_Float16, sv[u]);
-                const h2_t s2 = {s, s};
-                float acc[MR];
-#pragma unroll
-                for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
-                const uint32_t words[8] = {wv[u][0].x, wv[u][0].y, wv[u][0].z, wv[u][0].w,
-                                           wv[u][1].x, wv[u][1].y, wv[u][1].z, wv[u][1].w};
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    h2_t d[4];
-                    dequant_word(words[c], s2, d);
-#pragma unroll
-                    for (int m = 0; m < MR; ++m) {
-                        const uint4 xv = xs[(m * 8 + c) * G + g];
-                        acc[m] = __builtin_amdgcn_fdot2(d[0], as_h2(xv.x), acc[m], false);
-                        acc[m] = __builtin_amdgcn_fdot2(d[1], as_h2(xv.y), acc[m], false);
-                        acc[m] = __builtin_amdgcn_fdot2(d[2], as_h2(xv.z), acc[m], false);
-                        acc[m] = __builtin_amdgcn_fdot2(d[3], as_h2(xv.w), acc[m], false);
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    float lo = __fdiv_rn(h2f((uint16_t)(v[e] & 0xFFFFu)), rms);
+                    float hi = __fdiv_rn(h2f((uint16_t)(v[e] >> 16)), rms);
+                    lo = __fadd_rn(__fmul_rn(lo, h2f((uint16_t)(gv[e] & 0xFFFFu))), 0.0f);
+                    hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(gv[e] >> 16))), 0.0f);
+                    o[e] = (uint32_t)f2hb(lo) | ((uint32_t)f2hb(hi) << 16);
                 }
-#pragma unroll
-                for (int m = 0; m < MR; ++m) red[m * T + j] = acc[m];
+                xn[m * K8 + i] = o;
             }
-            g += step;
-            if (g >= G) g -= G;
         }
-        g0 = g;
-        // Next batch of loads.
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) xr[m][c] = xn[m * K8 + p * 4 + c];
+        __syncthreads();   // red is reused for the partial sums below
+    } else {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                xr[m][c] = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[p * 4 + c];
+    }
+
+    // Pair order of dequant_word: (x0,x4) (x1,x5) (x2,x6) (x3,x7) per 8-value word.
+    uint32_t xs[MR][16];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4 v = xr[m][c];
+            xs[m][4 * c + 0] = (v[0] & 0xFFFFu) | (v[2] << 16);
+            xs[m][4 * c + 1] = (v[0] >> 16) | (v[2] & 0xFFFF0000u);
+            xs[m][4 * c + 2] = (v[1] & 0xFFFFu) | (v[3] << 16);
+            xs[m][4 * c + 3] = (v[1] >> 16) | (v[3] & 0xFFFF0000u);
+        }
+
+    auto compute_batch = [&](uint32_t b, const u32x4 (&wc)[U], const uint16_t (&sc)[U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t j = jb + 256u * U + 256u * u;
-            if (j < T) {
-                wv[u][0] = __builtin_nontemporal_load(&wrow[2 * j]);
-                wv[u][1] = __builtin_nontemporal_load(&wrow[2 * j + 1]);
-                sv[u] = srow[j];
+            const _Float16 sh = __builtin_bit_cast(_Float16, sc[u]);
+            const h2_t s2 = {sh, sh};
+            float acc[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                h2_t d[4];
+                dequant_word(wc[u][c], s2, d);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    acc[m] = __builtin_amdgcn_fdot2(d[0], as_h2(xs[m][4 * c + 0]), acc[m], false);
+                    acc[m] = __builtin_amdgcn_fdot2(d[1], as_h2(xs[m][4 * c + 1]), acc[m], false);
+                    acc[m] = __builtin_amdgcn_fdot2(d[2], as_h2(xs[m][4 * c + 2]), acc[m], false);
+                    acc[m] = __builtin_amdgcn_fdot2(d[3], as_h2(xs[m][4 * c + 3]), acc[m], false);
+                }
+            }
+            const uint32_t i = b * U + u;
+            if (i < A.np) {
+#pragma unroll
+                for (int m = 0; m < MR; ++m) red[(i * MR + m) * nt + t] = acc[m];
             }
         }
+    };
+    // Ping-pong over two register buffers: the next batch is in flight while one computes.
+    for (uint32_t b = 0; b < nb; b += 2) {
+        if (b + 1 < nb) load_batch(b + 1, wb, sb);
+        compute_batch(b, wa, sa);
+        if (b + 1 >= nb) break;
+        if (b + 2 < nb) load_batch(b + 2, wa, sa);
+        compute_batch(b + 1, wb, sb);
     }
     __syncthreads();
 
+    // Row sums: 16 lanes per row (per gate/up pair with SwiGLU), then the epilogue.
+    const uint32_t grp = t >> 4, gl = t & 15, ngrp = nt >> 4;
     if (!A.swiglu) {
-        for (uint32_t r = wave; r < RB; r += 4) {
+        for (uint32_t lr = grp; lr < RB; lr += ngrp) {
+            const uint32_t i = lr / R, base = (lr % R) * P;
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 float s = 0.0f;
-                for (uint32_t i = lane; i < G; i += 64) s += red[m * T + r * G + i];
-                s = wave_sum(s);
-                if (lane == 0) {
+                for (uint32_t k = gl; k < P; k += 16) s += red[(i * MR + m) * nt + base + k];
+                s = sum16(s);
+                if (gl == 0) {
                     uint16_t v = f2hb(s);
-                    if (A.res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + r0 + r]))));
-                    reinterpret_cast<uint16_t*>(A.y)[(size_t)m * A.ldy + r0 + r] = v;
+                    if (A.res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + r0 + lr]))));
+                    reinterpret_cast<uint16_t*>(A.y)[(size_t)m * A.ldy + r0 + lr] = v;
                 }
             }
         }
     } else {
-        // rows (2p, 2p+1) = (gate, up) of output column (r0 + 2p) / 2; r0 and RB are even
-        for (uint32_t p = wave; 2 * p < RB; p += 4) {
+        // rows (2k, 2k+1) = (gate, up) of output column (r0 + 2k) / 2; r0 and RB are even
+        for (uint32_t k2 = grp; 2 * k2 < RB; k2 += ngrp) {
+            const uint32_t lg = 2 * k2, lu = lg + 1;
+            const uint32_t ig = lg / R, bg = (lg % R) * P, iu = lu / R, bu = (lu % R) * P;
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 float sg = 0.0f, su = 0.0f;
-                for (uint32_t i = lane; i < G; i += 64) {
-                    sg += red[m * T + (2 * p) * G + i];
-                    su += red[m * T + (2 * p + 1) * G + i];
+                for (uint32_t k = gl; k < P; k += 16) {
+                    sg += red[(ig * MR + m) * nt + bg + k];
+                    su += red[(iu * MR + m) * nt + bu + k];
                 }
-                sg = wave_sum(sg);
-                su = wave_sum(su);
-                if (lane == 0) {
+                sg = sum16(sg);
+                su = sum16(su);
+                if (gl == 0) {
                     const float gv = h2f(f2hb(sg)), uv = h2f(f2hb(su));
                     const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
                     uint16_t v = f2hb(__fmul_rn(act, uv));
-                    const uint32_t col = (r0 >> 1) + p;
+                    const uint32_t col = (r0 >> 1) + k2;
                     if (A.res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + col]))));
                     reinterpret_cast<uint16_t*>(A.y)[(size_t)m * A.ldy + col] = v;
                 }
@@ -398,33 +430,63 @@ __global__ __launch_bounds__(256) void w4g_gemm_kernel(
 
 }  // namespace
 
+namespace {
+
+// Launch shape of the GEMV for (M, K); see w4g_gemv_kernel.
+struct GemvPlan {
+    uint32_t nt = 0, P = 0, R = 0;
+    bool ok = false;
+};
+
+GemvPlan gemv_plan(uint32_t M, uint32_t K) {
+    GemvPlan best;
+    if (M == 0 || M > kW4gGemvMaxM || K == 0 || K % 64 || (size_t)M * K * 2 > 65536) return best;
+    const uint32_t P = K / 32;
+    if (P > 512) return best;
+    double best_score = -1.0;
+    for (uint32_t nt = 64; nt <= 512; nt += 64) {
+        if (nt < P) continue;
+        const uint32_t R = nt / P;
+        // fill of the thread block first, then blocks near 256 threads
+        const double score = (double)(R * P) / nt * 1000.0 - std::abs((int)nt - 256) / 64.0;
+        if (score > best_score) {
+            best_score = score;
+            best.nt = nt; best.P = P; best.R = R; best.ok = true;
+        }
+    }
+    return best;
+}
+
+}  // namespace
+
+bool w4g_gemv_supported(uint32_t M, uint32_t K) { return gemv_plan(M, K).ok; }
+
 hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
                            hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.swiglu && (N & 1)) return hipErrorInvalidValue;
-    const uint32_t G = K / 64;
-    const uint32_t target_wgs = 2u * (uint32_t)device_cu_count();
-    const uint32_t t_max = M == 1 ? 2048u : 1024u;
-    uint32_t rb = (N + target_wgs - 1) / target_wgs;
-    const uint32_t rb_cap = t_max / G > 0 ? t_max / G : 1;
-    if (rb > rb_cap) rb = rb_cap;
-    if (rb < 1) rb = 1;
-    if (epi.swiglu) rb = (rb + 1) & ~1u;   // gate/up pairs never straddle workgroups
-    const uint32_t grid = (N + rb - 1) / rb;
-    const size_t lds = (size_t)M * K * 2 + (size_t)M * rb * G * 4;
-    // Activations live in LDS: beyond the 64 KiB dynamic-LDS budget use the GEMM.
-    if (lds > 65536) {
+    const GemvPlan pl = gemv_plan(M, K);
+    if (!pl.ok) {
         if (epi.gamma) return hipErrorInvalidValue;   // the engine normalizes before a GEMM
         return launch_w4g_gemm(x, ldx, wq, ws, y, ldy, M, N, K, st, epi);
     }
-    GemvArgs A{x, ldx, reinterpret_cast<const u32x4*>(wq), ws, y, ldy, N, G, rb,
-               epi.gamma, epi.res, epi.ldr, epi.swiglu ? 1 : 0};
+    // Rows per workgroup: about two workgroups per CU, partial sums within 32 KiB.
+    const uint32_t target = 2u * (uint32_t)device_cu_count();
+    uint32_t np = (N + pl.R * target - 1) / (pl.R * target);
+    const uint32_t np_max = std::max(1u, 8192u / (M * pl.nt));
+    np = std::max(1u, std::min(np, np_max));
+    if (epi.swiglu && ((pl.R * np) & 1)) ++np;   // gate/up pairs never straddle workgroups
+    size_t lds = (size_t)np * M * pl.nt * 4;
+    if (epi.gamma) lds = std::max(lds, (size_t)M * K * 2);
+    const uint32_t grid = (N + pl.R * np - 1) / (pl.R * np);
+    GemvArgs A{x, ldx, wq, ws, y, ldy, N, K, pl.P, pl.R, np, epi.gamma, epi.res, epi.ldr, epi.swiglu ? 1 : 0};
+    const dim3 g3(grid), b3(pl.nt);
     switch (M) {
-    case 1: hipLaunchKernelGGL(w4g_gemv_kernel<1>, dim3(grid), dim3(256), lds, st, A); break;
-    case 2: hipLaunchKernelGGL(w4g_gemv_kernel<2>, dim3(grid), dim3(256), lds, st, A); break;
-    case 3: hipLaunchKernelGGL(w4g_gemv_kernel<3>, dim3(grid), dim3(256), lds, st, A); break;
-    case 4: hipLaunchKernelGGL(w4g_gemv_kernel<4>, dim3(grid), dim3(256), lds, st, A); break;
+    case 1: hipLaunchKernelGGL(w4g_gemv_kernel<1>, g3, b3, lds, st, A); break;
+    case 2: hipLaunchKernelGGL(w4g_gemv_kernel<2>, g3, b3, lds, st, A); break;
+    case 3: hipLaunchKernelGGL(w4g_gemv_kernel<3>, g3, b3, lds, st, A); break;
+    case 4: hipLaunchKernelGGL(w4g_gemv_kernel<4>, g3, b3, lds, st, A); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

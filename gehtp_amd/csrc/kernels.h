@@ -28,6 +28,7 @@ struct W4gEpilogue {
     bool swiglu = false;
 };
 // y[m*ldy + n] = f16( sum_k x[m*ldx + k] * fp16(q[n,k] * s[n, k/64]) ), m < M, n < N
+// (the GEMV applies s per 32-weight slice instead of rounding each q*s to fp16).
 // (N = weight rows; with swiglu the output has N/2 columns).
 hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
@@ -40,6 +41,9 @@ hipError_t launch_w4g_dequant(const uint8_t* wq, const __half* ws, __half* w,
                               uint32_t N, uint32_t K, hipStream_t st);
 // Largest M the GEMV handles; larger M goes to the MFMA GEMM.
 constexpr uint32_t kW4gGemvMaxM = 4;
+// True when launch_w4g_gemv runs the GEMV itself for (M, K) (otherwise it hands the
+// call to the GEMM, which cannot take an RMSNorm prologue).
+bool w4g_gemv_supported(uint32_t M, uint32_t K);
 
 // ---- fp16 x fp16 matmul, reference OP_MATMUL_F16 semantics ----
 // y[b][m][n0+n] over batch b < Bn; a [Bn][M][K] (or [K][M] when t0), w [Bn][K][N_full]
@@ -113,6 +117,14 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
                               uint32_t nslots, __half* out, uint32_t n_kv_host,
                               const uint32_t* count_dev, uint32_t H, uint32_t KVH, uint32_t hd,
                               float scale, float* work, uint32_t work_floats, hipStream_t st);
+// Fused decode step (OP_ATTN_DECODE_QKV_F16): QK-RMSNorm + RoPE of the raw [q | k | v]
+// row at position *count_dev, k/v appended to the ring, attention over positions
+// 0..*count_dev, then *count_dev += 1. work's leading counter must be zero before the
+// first call (every call leaves it zero).
+hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, const __half* k_gamma,
+                                  float theta, uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
+                                  uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH,
+                                  float scale, float* work, uint32_t work_floats, hipStream_t st);
 // Floats of workspace launch_attn_decode needs for n_kv positions.
 uint32_t attn_decode_work_floats(uint32_t max_kv, uint32_t H, uint32_t hd);
 

@@ -70,6 +70,7 @@ struct OpTable {
         info[OP_KV_APPEND_N_F16] = {WT_ARITY_KV_APPEND_N_F16, bits({0, 1})};
         info[OP_W4G_FUSED_F16] = {WT_ARITY_W4G_FUSED_F16, bits({0, 1, 2, 7, 8})};
         info[OP_QK_ROPE_KV_F16] = {WT_ARITY_QK_ROPE_KV_F16, bits({0, 9, 10})};
+        info[OP_ATTN_DECODE_QKV_F16] = {WT_ARITY_ATTN_DECODE_QKV_F16, bits({0, 6, 7})};
     }
 };
 

@@ -8,7 +8,8 @@ temps, the token embeddings arriving through the EXT_IN slot.
 Per layer (pre-norm, eps 1e-6), four fused linears and two attention ops:
     qkv = W4G_FUSED(x, Wqkv, norm=g_attn)            RMSNORM2 + q|k|v linears
     q   = QK_ROPE_KV(qkv)                            Qwen3 QK-norm, RoPE, KV append
-    a   = ATTN (prefill, causal) | ATTN_DECODE (one token over the layer's ring)
+    a   = ATTN (prefill, causal)
+  (decode: a = ATTN_DECODE_QKV(qkv), the two ops above over the layer's ring in one)
     x1  = W4G_FUSED(a, Wo, residual=x)               o-proj + ADD
     m   = W4G_FUSED(x1, Wgu, norm=g_ffn, SwiGLU)     RMSNORM2 + gate|up + silu * up
     x   = W4G_FUSED(m, Wd, residual=x1)              down-proj + ADD
@@ -168,8 +169,9 @@ class Weights:
 
 
 class _Emitter:
-    def __init__(self, cfg: Qwen3Config, w: Weights, max_pos: int):
+    def __init__(self, cfg: Qwen3Config, w: Weights, max_pos: int, fused_decode: bool = True):
         self.cfg, self.w, self.max_pos = cfg, w, max_pos
+        self.fused_decode = fused_decode
         self.bb = BlobBuilder()
         self.slot = {}
         # EXT_WGT slots pointing into the external image (descriptors only).
@@ -204,10 +206,16 @@ class _Emitter:
         c, bb, t = self.cfg, self.bb, self.t
         st = self.states[l]
         self.w4g(x_in, l, "wqkv", t["qkv"], S, norm=f"{l}.g_attn")
-        bb.op(OP.QK_ROPE_KV_F16, t["qkv"], t["qr"], WT_REF_NONE if decode else t["kr"],
-              WT_REF_NONE if decode else t["v"], st, S, c.heads, c.kv_heads, c.head_dim,
-              self.ref(f"{l}.q_norm"), self.ref(f"{l}.k_norm"), f32_bits(c.theta))
-        if decode:
+        if decode and self.fused_decode:
+            bb.op(OP.ATTN_DECODE_QKV_F16, t["qkv"], st, t["a"], c.heads, c.kv_heads, c.head_dim,
+                  self.ref(f"{l}.q_norm"), self.ref(f"{l}.k_norm"), f32_bits(c.theta), f32_bits(c.scale))
+        else:
+            bb.op(OP.QK_ROPE_KV_F16, t["qkv"], t["qr"], WT_REF_NONE if decode else t["kr"],
+                  WT_REF_NONE if decode else t["v"], st, S, c.heads, c.kv_heads, c.head_dim,
+                  self.ref(f"{l}.q_norm"), self.ref(f"{l}.k_norm"), f32_bits(c.theta))
+        if decode and self.fused_decode:
+            pass   # attention already emitted
+        elif decode:
             bb.op(OP.ATTN_DECODE_F16, t["qr"], st, t["a"], WT_KV_POS_AUTO, c.heads, c.kv_heads, c.head_dim,
                   f32_bits(c.scale))
         else:
@@ -244,7 +252,9 @@ def emit_prefill(cfg: Qwen3Config, w: Weights, S: int, max_pos: int):
     return e.emit(S, decode=False), dict(e.t)
 
 
-def emit_decode(cfg: Qwen3Config, w: Weights, max_pos: int):
-    """(blob bytes, temp ids): one decode step; input = the token's embedding [hidden]."""
-    e = _Emitter(cfg, w, max_pos)
+def emit_decode(cfg: Qwen3Config, w: Weights, max_pos: int, fused: bool = True):
+    """(blob bytes, temp ids): one decode step; input = the token's embedding [hidden].
+    fused: attention as one OP_ATTN_DECODE_QKV_F16 per layer instead of
+    OP_QK_ROPE_KV_F16 + OP_ATTN_DECODE_F16."""
+    e = _Emitter(cfg, w, max_pos, fused_decode=fused)
     return e.emit(1, decode=True), dict(e.t)

@@ -24,7 +24,8 @@ extern "C" {
 
 /* y[M, ldy] = x[M, ldx] . dequant(W)^T, W4G int4 group-64 (OP_MATMUL_W4G_F16):
  * M <= 4 runs the GEMV, larger M the MFMA GEMM. Mirrors exec_matmul_f16's scalar
- * arithmetic (oplist_exec.c:1802-1811) on dequant(W) = fp16(q*s).
+ * arithmetic (oplist_exec.c:1802-1811) on dequant(W) = fp16(q*s) with fp32
+ * accumulation (summation order differs).
  * K % 64 == 0, ldx % 8 == 0, x and wq 16-byte aligned. */
 int gehtp_w4g_matmul(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y,
                      uint32_t ldy, uint32_t M, uint32_t N, uint32_t K, void* stream);
@@ -64,11 +65,21 @@ int gehtp_attn_prefill(const void* q, const void* k, const void* v, void* out, u
                        uint32_t H, uint32_t KVH, uint32_t hd, float scale, int causal, void* stream);
 /* Decode attention (OP_ATTN_DECODE_F16) over positions [0, n_kv) of a KV ring of
  * state_bytes (slot = [K | V], each KVH*hd fp16): q [H,128] -> out [H,128].
- * work: device float buffer of gehtp_attn_decode_work_floats(n_kv, H, hd). */
+ * work: 16-byte aligned device float buffer of gehtp_attn_decode_work_floats(n_kv, H, hd)
+ * for per-chunk partials (no initial contents needed). */
 int gehtp_attn_decode(const void* q, const void* ring, uint32_t state_bytes, void* out,
                       uint32_t n_kv, uint32_t H, uint32_t KVH, uint32_t hd, float scale,
                       void* work, uint32_t work_floats, void* stream);
 uint32_t gehtp_attn_decode_work_floats(uint32_t n_kv, uint32_t H, uint32_t hd);
+/* OP_ATTN_DECODE_QKV_F16 on device buffers: qkv = raw [q | k | v] row of the new token
+ * ((H + 2*KVH)*128 fp16); q/k RMSNorm (gammas [128]) and RoPE (theta) at position
+ * *count_dev, k/v written to the ring, attention over positions 0..*count_dev, then
+ * *count_dev += 1. work: 16-byte aligned, gehtp_attn_decode_work_floats(ring slots, H,
+ * 128) floats, zeroed before its first use (every call leaves its head zero again). */
+int gehtp_attn_decode_qkv(const void* qkv, uint32_t H, uint32_t KVH, const void* q_gamma,
+                          const void* k_gamma, float theta, float scale, void* ring,
+                          uint32_t state_bytes, void* count_dev, void* out, void* work,
+                          uint32_t work_floats, void* stream);
 /* Append n_tok tokens (k/v [n_tok, KVH*hd]) at positions pos..pos+n_tok-1 of the ring. */
 int gehtp_kv_append(void* ring, uint32_t state_bytes, const void* k, const void* v,
                     uint32_t kv_elems, uint32_t n_tok, uint32_t pos, void* stream);

@@ -155,6 +155,13 @@ enum {
      *   k_out_t / v_out_t (WT_REF_NONE to skip) receive k_t / v_t token-major.
      *   RoPE positions = counter + t. Replaces RMSNORM2 x2, ROPE x2, KV_APPEND_N. */
     OP_QK_ROPE_KV_F16 = 46,
+    /* OP_ATTN_DECODE_QKV_F16: one decode step of a layer's attention from the raw fused
+     *   QKV row: OP_QK_ROPE_KV_F16 (n_tok 1) then OP_ATTN_DECODE_F16 at n_kv = counter + 1.
+     *   args [qkv_ref, state_ref, out_t, H, KVH, hd, q_gamma_ref, k_gamma_ref,
+     *         theta_f32_bits, scale_f32_bits]
+     *   qkv [(H + 2*KVH)*hd] = [q | k | v]; hd == 128; the new k/v go to the ring at the
+     *   state's counter, which is then advanced by one. out [H, hd]. */
+    OP_ATTN_DECODE_QKV_F16 = 47,
 };
 
 /* "No reference" argument value of the added opcodes. */
@@ -202,6 +209,7 @@ enum {
 #define WT_ARITY_KV_APPEND_N_F16 6
 #define WT_ARITY_W4G_FUSED_F16 11
 #define WT_ARITY_QK_ROPE_KV_F16 12
+#define WT_ARITY_ATTN_DECODE_QKV_F16 10
 
 /* In-memory records (reference oplist_parse.h:253-275); layouts are ABI. */
 struct wt_slot {
