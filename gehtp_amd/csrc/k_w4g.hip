@@ -121,18 +121,43 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
     uint16_t sa[U], sb[U];
     load_batch(0, wa, sa);
 
+    // Residual of this thread's first epilogue row, fetched now (behind the weights) so
+    // the epilogue does not wait on a fresh global load.
+    const uint32_t grp = t >> 4, gl = t & 15, ngrp = nt >> 4;
+    const uint32_t n_out_wg = A.swiglu ? RB / 2 : RB, out0 = A.swiglu ? r0 / 2 : r0;
+    uint16_t res0[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+        res0[m] = (A.res && gl == 0 && grp < n_out_wg)
+                      ? __builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + out0 + grp]) : (uint16_t)0;
+
     // This thread's activation slice (32 values per row m), raw or RMS-normalized.
     u32x4 xr[MR][4];
     if (A.gamma) {
         // RMSNorm prologue, cooperative: sum of squares in double (as RMSNORM2_F16), then
-        // h = f16(x / rms * gamma + 0) for the whole row into LDS.
+        // h = f16(x / rms * gamma + 0) for the whole row into LDS. The first two chunks
+        // of x and gamma per thread are loaded before any wait.
+        constexpr int PRE = 2;
+        u32x4 xv[PRE][MR], gv[PRE];
+#pragma unroll
+        for (int k = 0; k < PRE; ++k) {
+            const uint32_t i = t + k * nt;
+            if (i < K8) {
+#pragma unroll
+                for (int m = 0; m < MR; ++m) xv[k][m] = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[i];
+                gv[k] = reinterpret_cast<const u32x4*>(A.gamma)[i];
+            }
+        }
+        auto chunk_x = [&](int k, uint32_t i, int m) -> u32x4 {
+            return k < PRE ? xv[k][m] : reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[i];
+        };
         double ss[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) ss[m] = 0.0;
-        for (uint32_t i = t; i < K8; i += nt) {
+        for (uint32_t k = 0, i = t; i < K8; ++k, i += nt) {
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
-                const u32x4 v = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[i];
+                const u32x4 v = chunk_x((int)min(k, (uint32_t)PRE), i, m);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const double lo = (double)h2f((uint16_t)(v[e] & 0xFFFFu));
@@ -155,19 +180,19 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
         }
         __syncthreads();
         u32x4* xn = reinterpret_cast<u32x4*>(red);
-        for (uint32_t i = t; i < K8; i += nt) {
-            const u32x4 gv = reinterpret_cast<const u32x4*>(A.gamma)[i];
+        for (uint32_t k = 0, i = t; i < K8; ++k, i += nt) {
+            const u32x4 g4 = k < PRE ? gv[k] : reinterpret_cast<const u32x4*>(A.gamma)[i];
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
-                const u32x4 v = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[i];
+                const u32x4 v = chunk_x((int)min(k, (uint32_t)PRE), i, m);
                 const float rms = s_rms[m];
                 u32x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float lo = __fdiv_rn(h2f((uint16_t)(v[e] & 0xFFFFu)), rms);
                     float hi = __fdiv_rn(h2f((uint16_t)(v[e] >> 16)), rms);
-                    lo = __fadd_rn(__fmul_rn(lo, h2f((uint16_t)(gv[e] & 0xFFFFu))), 0.0f);
-                    hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(gv[e] >> 16))), 0.0f);
+                    lo = __fadd_rn(__fmul_rn(lo, h2f((uint16_t)(g4[e] & 0xFFFFu))), 0.0f);
+                    hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(g4[e] >> 16))), 0.0f);
                     o[e] = (uint32_t)f2hb(lo) | ((uint32_t)f2hb(hi) << 16);
                 }
                 xn[m * K8 + i] = o;
@@ -238,7 +263,9 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
     __syncthreads();
 
     // Row sums: 16 lanes per row (per gate/up pair with SwiGLU), then the epilogue.
-    const uint32_t grp = t >> 4, gl = t & 15, ngrp = nt >> 4;
+    auto res_at = [&](int m, uint32_t j) -> float {   // residual of output j of this workgroup
+        return h2f(j == grp ? res0[m] : __builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + out0 + j]));
+    };
     if (!A.swiglu) {
         for (uint32_t lr = grp; lr < RB; lr += ngrp) {
             const uint32_t i = lr / R, base = (lr % R) * P;
@@ -249,7 +276,7 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                 s = sum16(s);
                 if (gl == 0) {
                     uint16_t v = f2hb(s);
-                    if (A.res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + r0 + lr]))));
+                    if (A.res) v = f2hb(__fadd_rn(h2f(v), res_at(m, lr)));
                     reinterpret_cast<uint16_t*>(A.y)[(size_t)m * A.ldy + r0 + lr] = v;
                 }
             }
@@ -273,7 +300,7 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                     const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
                     uint16_t v = f2hb(__fmul_rn(act, uv));
                     const uint32_t col = (r0 >> 1) + k2;
-                    if (A.res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + col]))));
+                    if (A.res) v = f2hb(__fadd_rn(h2f(v), res_at(m, k2)));
                     reinterpret_cast<uint16_t*>(A.y)[(size_t)m * A.ldy + col] = v;
                 }
             }
@@ -498,9 +525,8 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.gamma || (epi.swiglu && (N & 1))) return hipErrorInvalidValue;
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    hipLaunchKernelGGL(w4g_gemm_kernel, grid, dim3(256), 0, st, a, lda,
-                       reinterpret_cast<const uint4*>(wq), ws, y, ldy, M, N, K, epi.res, epi.ldr,
-                       epi.swiglu ? 1 : 0);
+    hipLaunchKernelGGL(w4g_gemm_kernel, grid, dim3(256), 0, st, a, lda, reinterpret_cast<const uint4*>(wq), ws, y, ldy,
+                       M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0);
     return hipGetLastError();
 }
 
