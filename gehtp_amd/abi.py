@@ -167,6 +167,10 @@ EXPORTS = {
     "gehtp_kv_append": (_i, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _vp]),
     "gehtp_rope": (_i, [_vp, _vp, _u32, _u32, _u32, _u32, C.c_float, _u32, _vp]),
     "gehtp_argmax": (_i, [_vp, _u32, _vp, _vp]),
+    "gehtp_crouton_encode": (_i, [_vp, _vp, _u32, _u32, _vp]),
+    "gehtp_crouton_decode": (_i, [_vp, _vp, _u32, _u32, _vp]),
+    "gehtp_matmul_w4a16": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "gehtp_rmsnorm_crouton": (_i, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "gehtp_version": (C.c_char_p, []),
 }
 

@@ -32,7 +32,7 @@ DEVICE_FLAGS = [
     "-Wall", "-Wno-unused-result", "-Wno-unused-variable",
 ]
 SOURCES = ["wt_parse.cpp", "engine.cpp", "capi.cpp",
-           "k_w4g.hip", "k_rows.hip", "k_f16mm.hip", "k_attn.hip"]
+           "k_w4g.hip", "k_rows.hip", "k_f16mm.hip", "k_attn.hip", "k_data.hip"]
 
 
 def _compile(src: Path, verbose: bool) -> Path:

@@ -157,6 +157,32 @@ int gehtp_argmax(const void* x, uint32_t n, void* out, void* stream) {
     return rc(launch_argmax(H(x), n, static_cast<int32_t*>(out), S(stream)));
 }
 
+int gehtp_crouton_encode(const void* lin, void* surf, uint32_t rows, uint32_t cols, void* stream) {
+    if (!lin || !surf || rows % 32 || cols % 32 || (reinterpret_cast<uintptr_t>(surf) & 3u)) return GEHTP_EINVAL;
+    return rc(launch_crouton_encode(static_cast<const uint16_t*>(lin), static_cast<uint16_t*>(surf), rows, cols,
+                                    S(stream)));
+}
+
+int gehtp_crouton_decode(const void* surf, void* lin, uint32_t rows, uint32_t cols, void* stream) {
+    if (!lin || !surf || rows % 32 || cols % 32 || (reinterpret_cast<uintptr_t>(surf) & 3u)) return GEHTP_EINVAL;
+    return rc(launch_crouton_decode(static_cast<const uint16_t*>(surf), static_cast<uint16_t*>(lin), rows, cols,
+                                    S(stream)));
+}
+
+int gehtp_matmul_w4a16(const void* act_surf, const void* w, void* out_surf, uint32_t M, uint32_t K, uint32_t N,
+                       void* stream) {
+    if (!act_surf || !w || !out_surf || !M || !K || !N || M % 32 || K % 32 || N % 32 || !al16(act_surf) ||
+        !al16(w) || (reinterpret_cast<uintptr_t>(out_surf) & 1u))
+        return GEHTP_EINVAL;
+    return rc(launch_matmul_w4a16(static_cast<const uint16_t*>(act_surf), static_cast<const uint8_t*>(w),
+                                  static_cast<uint16_t*>(out_surf), M, K, N, S(stream)));
+}
+
+int gehtp_rmsnorm_crouton(const void* x_surf, const void* w, void* y, uint32_t m, uint32_t n, void* stream) {
+    if (!x_surf || !w || !y || !m || m % 32 || n % 32) return GEHTP_EINVAL;
+    return rc(launch_rmsnorm_crouton(static_cast<const uint16_t*>(x_surf), H(w), Hm(y), m, n, S(stream)));
+}
+
 const char* gehtp_version(void) { return "gehtp-gfx950 0.1"; }
 
 }  // extern "C"

@@ -100,6 +100,16 @@ struct Engine {
     uint8_t* norm_buf = nullptr;   // normalized rows for OP_W4G_FUSED_F16 on the GEMM path
     size_t norm_cap = 0;
 
+    // OP_MATMUL_W4A16 engine surfaces (the reference's HMX engine: shape, act, out,
+    // weights, bias), read by OP_DMA's 0xC000 references; engine_m reports w4_m.
+    bool w4_ready = false;
+    uint32_t w4_m = 0, w4_k = 0, w4_n = 0;
+    uint8_t* w4_out = nullptr;
+    size_t w4_out_cap = 0;
+    uint8_t* w4_act = nullptr;
+    const uint8_t* w4_wt = nullptr;
+    const uint8_t* w4_bias = nullptr;
+
     wt_exec_stats stats{};
     wt_op_ts* ts = nullptr;
     uint32_t ts_cap = 0;
@@ -510,7 +520,6 @@ int op_matmul_w4g(Ctx& cx) {
     if (sb && sb < (uint64_t)N * (K / 64) * 2u) return ERR("w4g scale slot %zu < N*K/64*2", sb);
     if (((uintptr_t)a | (uintptr_t)wq) % 16) return ERR("w4g operands not 16-byte aligned");
     g.stats.matmul++;
-    *cx.engine_m = M;
     if (M <= kW4gGemvMaxM)
         CHECK_LAUNCH(launch_w4g_gemv(a, K, wq, ws, y, ldy, M, N, K, g.stream));
     else
@@ -844,7 +853,6 @@ int op_w4g_fused(Ctx& cx) {
     __half* y = reinterpret_cast<__half*>(temp_get(A(3), (uint32_t)ybytes));
     if (!y) return ERR("w4g_fused out alloc");
     g.stats.matmul++;
-    *cx.engine_m = M;
     W4gEpilogue epi;
     epi.res = res;
     epi.ldr = n_out;
@@ -942,6 +950,288 @@ int op_attn_decode_qkv(Ctx& cx) {
     return 0;
 }
 
+// ---- OP_MATMUL_W4A16 (opcode 1, oplist_exec.c:438-529) ----
+// Supply slots (folded bias, act/out tables) are located by length in slot order as
+// the reference does; the math is the closed form of kernels/docs/api_v22_w4a16.md:11.
+// The result always lands in the engine's out surface (OP_DMA's ENG_OUT); with a slot
+// activation it is also copied to the out temp, with a VTCM-staged activation
+// (0x4000|temp) it stays in the engine surface, as in the reference.
+int op_matmul_w4a16(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const wt_blob* b = cx.b;
+    const uint32_t act_s = A(0), w_s = A(1), out_t = A(2), M = A(3), K = A(4), N = A(5);
+    const uint64_t act_b = (uint64_t)M * K * 2u, wt_b = (uint64_t)K * N / 2u, out_b = (uint64_t)M * N * 2u;
+    const uint64_t bias_b = (uint64_t)(N / 32u) * 512u, tbl_b = 8ull * (K / 32u) * 4u;
+    g.stats.matmul++;
+    const uint8_t *bias = nullptr, *atbl = nullptr, *otbl = nullptr;
+    for (uint32_t i = 0; i < b->n_slots; ++i) {
+        const uint8_t* p = slot_ptr(b, i);
+        const uint32_t L = b->slots[i].len;
+        if (!bias && L == bias_b) bias = p;
+        else if (!atbl && L == tbl_b) atbl = p;
+        else if (!otbl && L == tbl_b) otbl = p;
+    }
+    if (!bias || !atbl || !otbl) return ERR("supply slots missing (bias/atbl/otbl)");
+    if (!M || M % 32u || K % 32u || N % 32u || !K || !N)
+        return ERR("w4a16 shape m%u k%u n%u (multiples of 32 needed)", M, K, N);
+    if (out_b > 0xFFFFFFFFull) return ERR("w4a16 output too large");
+    const uint8_t* act = nullptr;
+    if (act_s & WT_REF_VTCM_FLAG) {
+        act = ref_ptr(b, act_s);
+        if (!act) return ERR("dma-prestaged act bad (temp %u not in the VTCM pool)", act_s & 0x3FFFu);
+        if (g.vtcm_off_arr[act_s & 0x3FFFu] + act_b > g.vtcm_pool_size) return ERR("dma-prestaged act beyond the pool");
+    } else {
+        if (act_s >= b->n_slots || b->slots[act_s].len != act_b) return ERR("act slot size mismatch");
+        act = slot_ptr(b, act_s);
+    }
+    if (w_s >= b->n_slots || b->slots[w_s].len != wt_b) return ERR("w slot size mismatch");
+    const uint8_t* w = slot_ptr(b, w_s);
+    if (!act || !w) return ERR("w4a16 ref fail");
+    uint8_t* out = temp_get(out_t, (uint32_t)out_b);
+    if (!out) return ERR("temp %u alloc", out_t);
+    if (scratch(&g.w4_out, &g.w4_out_cap, out_b, err, errn)) return -1;
+    CHECK_LAUNCH(launch_matmul_w4a16(reinterpret_cast<const uint16_t*>(act), w, reinterpret_cast<uint16_t*>(g.w4_out),
+                                     M, K, N, g.stream));
+    if (!(act_s & WT_REF_VTCM_FLAG) && hipMemcpyAsync(out, g.w4_out, out_b, hipMemcpyDeviceToDevice, g.stream) != hipSuccess)
+        return ERR("w4a16 out copy");
+    g.w4_ready = true;
+    g.w4_m = M; g.w4_k = K; g.w4_n = N;
+    g.w4_act = const_cast<uint8_t*>(act);
+    g.w4_wt = w;
+    g.w4_bias = bias;
+    *cx.engine_m = M;
+    return 0;
+}
+
+// ---- OP_RMSNORM_F16 (opcode 2, oplist_exec.c:559-591): rows = the W4A16 engine's M ----
+int op_rmsnorm_crouton(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t x_t = A(0), w_s = A(1), y_t = A(2), n = A(3), m = *cx.engine_m;
+    g.stats.rmsnorm++;
+    if (x_t >= kMaxTemps || !g.temps[x_t]) return ERR("rmsnorm src temp %u empty", x_t);
+    if (w_s >= cx.b->n_slots || cx.b->slots[w_s].len != n * 2u) return ERR("rms w slot len mismatch");
+    if (!m || m % 32u || n % 32u) return ERR("rms shape m%u n%u", m, n);
+    if ((uint64_t)m * n * 2u > g.temp_bytes[x_t]) return ERR("rmsnorm src temp %u smaller than m*n", x_t);
+    __half* y = reinterpret_cast<__half*>(temp_get(y_t, m * n * 2u));
+    const __half* w = reinterpret_cast<const __half*>(slot_ptr(cx.b, w_s));
+    if (!y || !w) return ERR("rms alloc");
+    CHECK_LAUNCH(launch_rmsnorm_crouton(reinterpret_cast<const uint16_t*>(g.temps[x_t]), w, y, m, n, g.stream));
+    return 0;
+}
+
+// ---- OP_FILL (opcode 9, oplist_exec.c:864-885): n f16 from a pool slot at byte offset ----
+int op_fill(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t pool_s = A(0), off = A(1), dst = A(2), n = A(3);
+    const uint64_t bytes = (uint64_t)n * 2u;
+    g.stats.fill++;
+    if (pool_s >= cx.b->n_slots || cx.b->slots[pool_s].len < (uint64_t)off + bytes) return ERR("fill pool oob");
+    const uint8_t* src = slot_ptr(cx.b, pool_s) + off;
+    uint8_t* d = nullptr;
+    if (dst & 0x8000u) {
+        const uint32_t s2 = dst & 0x7FFFu;
+        if (s2 >= cx.b->n_slots || cx.b->slots[s2].len < bytes) return ERR("fill dst empty");
+        d = slot_ptr(cx.b, s2);
+    } else {
+        d = temp_get(dst, (uint32_t)bytes);
+    }
+    if (!d) return ERR("fill dst empty");
+    if (bytes && hipMemcpyAsync(d, src, bytes, hipMemcpyDeviceToDevice, g.stream) != hipSuccess) return ERR("fill copy");
+    return 0;
+}
+
+// ---- OP_TRANSPOSE_F16 (opcode 10, oplist_exec.c:983-1011): (1, H, W, C), perm per byte ----
+int op_transpose4(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t Hh = A(2), W = A(3), Cc = A(4), perm = A(5);
+    g.stats.transpose++;
+    const uint64_t n = (uint64_t)Hh * W * Cc;
+    const uint8_t* src = ref_ptr(cx.b, A(0));
+    if (!src) return ERR("transpose src ref empty");
+    const size_t sb = ref_bytes(cx.b, A(0));
+    if (sb && sb < n * 2u) return ERR("transpose source smaller than H*W*C");
+    for (int i = 0; i < 32; i += 8)
+        if (((perm >> i) & 0xFFu) > 3u) return ERR("transpose perm 0x%08X bad", perm);
+    uint8_t* dst = temp_get(A(1), (uint32_t)(n * 2u));
+    if (!dst) return ERR("transpose temp alloc");
+    CHECK_LAUNCH(launch_transpose4(reinterpret_cast<const uint16_t*>(src), reinterpret_cast<uint16_t*>(dst), Hh, W, Cc,
+                                   perm, g.stream));
+    return 0;
+}
+
+// ---- OP_CONCAT_F16 (opcode 14, oplist_exec.c:1196-1220) ----
+int op_concat(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t out_t = A(8), n_seg = std::min<uint32_t>(A(10), 4u), n_elems = A(11);
+    uint32_t sizes[4] = {A(12), A(13), A(14), A(15)}, total = 0;
+    for (uint32_t i = 0; i < n_seg; ++i) total += sizes[i];
+    if (total == 0 || n_elems % total != 0) return ERR("concat shape");
+    const uint32_t outer = n_elems / total;
+    uint16_t* y = reinterpret_cast<uint16_t*>(temp_get(out_t, n_elems * 2u));
+    if (!y) return ERR("concat out fail");
+    const uint16_t* xs[4] = {nullptr, nullptr, nullptr, nullptr};
+    for (uint32_t k = 0; k < n_seg; ++k) {
+        xs[k] = reinterpret_cast<const uint16_t*>(ref_ptr(cx.b, A(k)));
+        if (!xs[k]) return ERR("concat in fail");
+        const size_t xb = ref_bytes(cx.b, A(k));
+        if (xb && xb < (uint64_t)outer * sizes[k] * 2u) return ERR("concat segment %u smaller than its span", k);
+    }
+    CHECK_LAUNCH(launch_concat(xs, sizes, n_seg, y, n_elems, g.stream));
+    return 0;
+}
+
+// ---- OP_SPLIT_F16 (opcode 16, oplist_exec.c:1222-1256): writes segment split_index ----
+int op_split(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t x_t = A(0), n_seg = std::min<uint32_t>(A(10), 4u), idx = A(15);
+    uint32_t sizes[4] = {A(11), A(12), A(13), A(14)}, total = 0;
+    const uint16_t* x = reinterpret_cast<const uint16_t*>(ref_ptr(cx.b, x_t));
+    if (!x) return ERR("split in fail");
+    for (uint32_t i = 0; i < n_seg; ++i) total += sizes[i];
+    if (total == 0) return ERR("split shape");
+    uint32_t x_elems = 0;
+    if ((x_t & 0x8000u) == 0 && x_t < kMaxTemps) x_elems = g.temp_bytes[x_t] / 2u;
+    if (x_elems == 0) return ERR("split x size");
+    const uint32_t outer = x_elems / total;
+    uint32_t off = 0;
+    for (uint32_t k = 0; k < n_seg; ++k) {
+        if (k == idx) {
+            uint16_t* y = reinterpret_cast<uint16_t*>(temp_get(A(1), outer * sizes[k] * 2u));
+            if (!y) return ERR("split out fail");
+            CHECK_LAUNCH(launch_split(x, y, outer, total, off, sizes[k], g.stream));
+        }
+        off += sizes[k];
+    }
+    return 0;
+}
+
+// ---- OP_REDUCE_F16 (opcode 17, oplist_exec.c:1258-1299) ----
+int op_reduce(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n = A(2), axis = A(3), subtype = A(4);
+    const uint32_t d[4] = {A(5), A(6), A(7), A(8)};
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    if (!x) return ERR("reduce in fail");
+    if (axis >= 4 || subtype > 3) return ERR("reduce axis/subtype bad (axis=%u sub=%u)", axis, subtype);
+    const uint32_t L = d[axis] ? d[axis] : 1u;
+    uint64_t inner = 1;
+    for (uint32_t a = axis + 1; a < 4; ++a) inner *= d[a];
+    if (inner * L == 0 || inner * L > 0xFFFFFFFFull || n % (uint32_t)(inner * L) != 0)
+        return ERR("reduce geom (n=%u L=%u inner=%llu)", n, L, (unsigned long long)inner);
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < (uint64_t)n * 2u) return ERR("reduce input smaller than n");
+    const uint32_t outer = n / (uint32_t)(inner * L);
+    __half* y = reinterpret_cast<__half*>(temp_get(A(1), (uint32_t)(outer * inner * 2u)));
+    if (!y) return ERR("reduce out fail");
+    CHECK_LAUNCH(launch_reduce(x, y, outer, L, (uint32_t)inner, subtype, g.stream));
+    return 0;
+}
+
+// ---- OP_CUMSUM_F32 (opcode 18, oplist_exec.c:1320-1347) ----
+int op_cumsum(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t rows = A(2), n = A(3), excl = A(5), rev = A(6);
+    const uint64_t bytes = (uint64_t)rows * n * 2u;
+    const __half* x = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
+    __half* y = reinterpret_cast<__half*>(temp_get(A(1), (uint32_t)bytes));
+    if (!x || !y || bytes > 0xFFFFFFFFull) return ERR("cumsum ref fail");
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < bytes) return ERR("cumsum input smaller than rows*n");
+    CHECK_LAUNCH(launch_cumsum(x, y, rows, n, excl, rev, g.stream));
+    return 0;
+}
+
+// ---- OP_GATHER_F16 (opcode 20, oplist_exec.c:1378-1436) ----
+int op_gather(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t n = A(3), packed = A(4);
+    const uint32_t axis = packed & 0xFFu, xrank = (packed >> 8) & 0xFFu, irank = (packed >> 16) & 0xFFu;
+    const uint32_t td[5] = {A(5), A(6), A(7), A(8), A(9)}, xd[5] = {A(10), A(11), A(12), A(13), A(14)};
+    const uint16_t* tbl = reinterpret_cast<const uint16_t*>(ref_ptr(cx.b, A(0)));
+    const int32_t* idx = reinterpret_cast<const int32_t*>(ref_ptr(cx.b, A(1)));
+    uint16_t* y = reinterpret_cast<uint16_t*>(temp_get(A(2), n * 2u));
+    if (!tbl || !idx || !y) return ERR("gather ref fail");
+    if (axis >= irank || irank > 5 || xrank > 5 || xrank == 0)
+        return ERR("gather axis/rank bad (a=%u x=%u i=%u)", axis, xrank, irank);
+    uint64_t tn = 1, xn = 1;
+    for (int i = 0; i < 5; ++i) {
+        if (!td[i] || !xd[i]) return ERR("gather zero dimension");
+        tn *= td[i];
+        xn *= xd[i];
+    }
+    const size_t tb = ref_bytes(cx.b, A(0)), ib = ref_bytes(cx.b, A(1));
+    if ((tb && tb < tn * 2u) || (ib && ib < xn * 4u)) return ERR("gather table or index smaller than its dims");
+    CHECK_LAUNCH(launch_gather(tbl, idx, y, n, axis, xrank, irank, td, xd, g.stream));
+    return 0;
+}
+
+// ---- OP_DMA (opcode 33, oplist_exec.c:887-981): a device copy between references ----
+uint8_t* dma_resolve(const wt_blob* b, uint32_t ref, uint32_t off, uint32_t bytes, bool is_dst) {
+    if ((ref & 0xC000u) == WT_REF_ENG_FLAG) {
+        if (!g.w4_ready) return nullptr;
+        uint8_t* p = nullptr;
+        uint64_t cap = 0;
+        switch (ref & 0xFFu) {
+        case WT_ENG_ACT: p = g.w4_act; cap = (uint64_t)g.w4_m * g.w4_k * 2u; break;
+        case WT_ENG_OUT: p = g.w4_out; cap = (uint64_t)g.w4_m * g.w4_n * 2u; break;
+        case WT_ENG_WT: p = const_cast<uint8_t*>(g.w4_wt); cap = (uint64_t)g.w4_k * g.w4_n / 2u; break;
+        case WT_ENG_BIAS: p = const_cast<uint8_t*>(g.w4_bias); cap = (uint64_t)(g.w4_n / 32u) * 512u; break;
+        default: return nullptr;
+        }
+        if (!p || (uint64_t)off + bytes > cap) return nullptr;
+        return p + off;
+    }
+    if (ref & 0x8000u) {
+        const uint32_t s = ref & 0x7FFFu;
+        if (s >= b->n_slots || (uint64_t)off + bytes > b->slots[s].len) return nullptr;
+        uint8_t* p = slot_ptr(b, s);
+        return p ? p + off : nullptr;
+    }
+    if (ref & 0x4000u) {
+        const uint32_t t = ref & 0x3FFFu;
+        if (t >= kMaxTemps || g.vtcm_off_arr[t] == kNone || !g.vtcm_pool) return nullptr;
+        if ((uint64_t)g.vtcm_off_arr[t] + off + bytes > g.vtcm_pool_size) return nullptr;
+        return g.vtcm_pool + g.vtcm_off_arr[t] + off;
+    }
+    if (ref >= kMaxTemps) return nullptr;
+    if (is_dst) {
+        uint8_t* p = temp_get(ref, off + bytes);
+        return p ? p + off : nullptr;
+    }
+    if (!g.temps[ref] || (uint64_t)off + bytes > g.temp_bytes[ref]) return nullptr;
+    return g.temps[ref] + off;
+}
+
+int op_dma(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t bytes = A(2), f_src = A(6), f_dst = A(7);
+    if (bytes == 0) return 0;
+    if ((f_src > 3u && f_src != WT_DMA_FENCE_NONE) || (f_dst > 3u && f_dst != WT_DMA_FENCE_NONE))
+        return ERR("dma fence arg bad");
+    if ((uint64_t)A(4) + bytes > 0xFFFFFFFFull) return ERR("dma ref fail");
+    const uint8_t* src = dma_resolve(cx.b, A(0), A(3), bytes, false);
+    uint8_t* dst = dma_resolve(cx.b, A(1), A(4), bytes, true);
+    if (!src || !dst) return ERR("dma ref fail");
+    if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g.stream) != hipSuccess) return ERR("dma copy");
+    return 0;
+}
+
+// ---- OP_PAD_F16 (opcode 34, oplist_exec.c:1301-1318) ----
+int op_pad(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    const uint32_t outer = A(2), in_inner = A(3), out_inner = A(4), before = A(5);
+    const uint16_t pv = (uint16_t)A(6);
+    const uint64_t ob = (uint64_t)outer * out_inner * 2u;
+    const uint16_t* x = reinterpret_cast<const uint16_t*>(ref_ptr(cx.b, A(0)));
+    uint16_t* y = ob <= 0xFFFFFFFFull ? reinterpret_cast<uint16_t*>(temp_get(A(1), (uint32_t)ob)) : nullptr;
+    if (!x || !y) return ERR("pad ref fail");
+    if ((uint64_t)before + in_inner > out_inner) return ERR("pad geom");
+    const size_t xb = ref_bytes(cx.b, A(0));
+    if (xb && xb < (uint64_t)outer * in_inner * 2u) return ERR("pad input smaller than outer*in_inner");
+    CHECK_LAUNCH(launch_pad(x, y, outer, in_inner, out_inner, before, pv, g.stream));
+    return 0;
+}
+
 int op_rope(Ctx& cx) {
     char* err = cx.err; size_t errn = cx.errn;
     const uint32_t n_tok = A(2), H = A(3), hd = A(4), pos0 = A(5), row_stride = A(7);
@@ -978,6 +1268,17 @@ struct Table {
     Table() {
         for (auto& f : fn) f = op_unsupported;
         fn[OP_NOP] = op_nop;
+        fn[OP_MATMUL_W4A16] = op_matmul_w4a16;
+        fn[OP_RMSNORM_F16] = op_rmsnorm_crouton;
+        fn[OP_FILL] = op_fill;
+        fn[OP_TRANSPOSE_F16] = op_transpose4;
+        fn[OP_CONCAT_F16] = op_concat;
+        fn[OP_SPLIT_F16] = op_split;
+        fn[OP_REDUCE_F16] = op_reduce;
+        fn[OP_CUMSUM_F32] = op_cumsum;
+        fn[OP_GATHER_F16] = op_gather;
+        fn[OP_DMA] = op_dma;
+        fn[OP_PAD_F16] = op_pad;
         fn[OP_PIN] = op_pin;
         fn[OP_SILU_F16] = op_silu;
         fn[OP_ADD_F16] = op_add;
@@ -1052,6 +1353,7 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
     if (!err || !errn) { err = dummy_err; errn = sizeof dummy_err; }
     uint32_t dummy_m = 0;
     if (!engine_m) engine_m = &dummy_m;
+    *engine_m = g.w4_ready ? g.w4_m : 0;   // oplist_exec.c:2503
     if (!b) return ERR("null blob");
     if ((uint64_t)first + count > b->n_ops) return ERR("range oob");
     if (ensure_ready(err, errn)) return -1;
@@ -1189,6 +1491,13 @@ void wt_exec_shutdown(void) {
     if (g.norm_buf) hipFree(g.norm_buf);
     g.norm_buf = nullptr;
     g.norm_cap = 0;
+    if (g.w4_out) hipFree(g.w4_out);
+    g.w4_out = nullptr;
+    g.w4_out_cap = 0;
+    g.w4_ready = false;
+    g.w4_m = g.w4_k = g.w4_n = 0;
+    g.w4_act = nullptr;
+    g.w4_wt = g.w4_bias = nullptr;
     // Weights stay resident (keyed by content); states persist until state_reset.
 }
 

@@ -128,4 +128,30 @@ hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, cons
 // Floats of workspace launch_attn_decode needs for n_kv positions.
 uint32_t attn_decode_work_floats(uint32_t max_kv, uint32_t H, uint32_t hd);
 
+// ---- crouton16_row4 surfaces, opcode 1 / 2, data ops (k_data.hip) ----
+hipError_t launch_crouton_encode(const uint16_t* lin, uint16_t* surf, uint32_t rows, uint32_t cols,
+                                 hipStream_t st);
+hipError_t launch_crouton_decode(const uint16_t* surf, uint16_t* lin, uint32_t rows, uint32_t cols,
+                                 hipStream_t st);
+// OP_MATMUL_W4A16: act / out are crouton16_row4 u16 surfaces, w = [N][K/2] +8 nibbles.
+hipError_t launch_matmul_w4a16(const uint16_t* act, const uint8_t* w, uint16_t* out, uint32_t M, uint32_t K,
+                               uint32_t N, hipStream_t st);
+hipError_t launch_rmsnorm_crouton(const uint16_t* x, const __half* w, __half* y, uint32_t m, uint32_t n,
+                                  hipStream_t st);
+hipError_t launch_concat(const uint16_t* const* xs, const uint32_t* sizes, uint32_t n_seg, uint16_t* y,
+                         uint32_t n_elems, hipStream_t st);
+hipError_t launch_split(const uint16_t* x, uint16_t* y, uint32_t outer, uint32_t total, uint32_t off,
+                        uint32_t size, hipStream_t st);
+hipError_t launch_pad(const uint16_t* x, uint16_t* y, uint32_t outer, uint32_t in_inner, uint32_t out_inner,
+                      uint32_t before, uint16_t pv, hipStream_t st);
+hipError_t launch_reduce(const __half* x, __half* y, uint32_t outer, uint32_t L, uint32_t inner,
+                         uint32_t subtype, hipStream_t st);
+hipError_t launch_cumsum(const __half* x, __half* y, uint32_t rows, uint32_t n, uint32_t exclusive,
+                         uint32_t reverse, hipStream_t st);
+hipError_t launch_gather(const uint16_t* tbl, const int32_t* idx, uint16_t* y, uint32_t n, uint32_t axis,
+                         uint32_t xrank, uint32_t irank, const uint32_t* td, const uint32_t* xd,
+                         hipStream_t st);
+hipError_t launch_transpose4(const uint16_t* x, uint16_t* y, uint32_t Hh, uint32_t W, uint32_t Cc,
+                             uint32_t perm, hipStream_t st);
+
 }  // namespace gehtp

@@ -89,6 +89,21 @@ int gehtp_rope(const void* x, void* y, uint32_t n_tok, uint32_t n_heads, uint32_
 /* OP_ARGMAX_F16: out (device int32) = first index of the maximum. */
 int gehtp_argmax(const void* x, uint32_t n, void* out, void* stream);
 
+/* crouton16_row4 surfaces (kernels/src/runtime/gemm_dispatch.c:38-72): rows, cols
+ * multiples of 32; surf 4-byte aligned. Bit copies of u16 elements. */
+int gehtp_crouton_encode(const void* lin, void* surf, uint32_t rows, uint32_t cols, void* stream);
+int gehtp_crouton_decode(const void* surf, void* lin, uint32_t rows, uint32_t cols, void* stream);
+/* OP_MATMUL_W4A16 (opcode 1, exec_matmul oplist_exec.c:438-529; formula
+ * kernels/docs/api_v22_w4a16.md:11): out_surf[M,N] (crouton u16) =
+ * clip(nearest(sum_k (A[m,k] - 32768) * W[k,n] / 7) + 32768), act_surf [M,K] crouton u16,
+ * w = [N][K/2] bytes, low nibble = even k, value = nibble - 8. M, K, N multiples of 32. */
+int gehtp_matmul_w4a16(const void* act_surf, const void* w, void* out_surf, uint32_t M, uint32_t K,
+                       uint32_t N, void* stream);
+/* OP_RMSNORM_F16 (opcode 2, exec_rmsnorm oplist_exec.c:559-591): y [m,n] fp16 row-major
+ * from a crouton u16 surface (value - 32768) and weights w [n] fp16. */
+int gehtp_rmsnorm_crouton(const void* x_surf, const void* w, void* y, uint32_t m, uint32_t n,
+                          void* stream);
+
 /* Library identification: "gehtp-gfx950 <version>". */
 const char* gehtp_version(void);
 

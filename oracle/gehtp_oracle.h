@@ -78,6 +78,26 @@ int go_attn_decode(struct go_kv* c, const uint16_t* q, uint16_t* out, uint32_t n
 int go_rope(const uint16_t* x, uint16_t* y, uint32_t n_tok, uint32_t n_heads, uint32_t hd,
             uint32_t pos0, float theta, uint32_t row_stride);
 
+/* ---- remaining runlist ops (gehtp_oracle_ops.c) ---- */
+int go_crouton_encode(const uint16_t* lin, uint16_t* surf, uint32_t rows, uint32_t cols);
+int go_crouton_decode(const uint16_t* surf, uint16_t* lin, uint32_t rows, uint32_t cols);
+int go_matmul_w4a16(const uint16_t* act_surf, const uint8_t* w, uint16_t* out_surf,
+                    uint32_t M, uint32_t K, uint32_t N);
+int go_rmsnorm_crouton(const uint16_t* x_surf, const uint16_t* w16, uint16_t* y, uint32_t m, uint32_t n);
+int go_concat(const uint16_t* const* xs, uint16_t* y, uint32_t n_seg, uint32_t n_elems,
+              const uint32_t* sizes);
+int go_split(const uint16_t* x, uint32_t x_elems, uint16_t* y, uint32_t n_seg, const uint32_t* sizes,
+             uint32_t split_index);
+int go_reduce(const uint16_t* x, uint16_t* y, uint32_t n, uint32_t axis, uint32_t subtype,
+              const uint32_t* d);
+int go_pad(const uint16_t* x, uint16_t* y, uint32_t outer, uint32_t in_inner, uint32_t out_inner,
+           uint32_t pad_before, uint16_t pv);
+int go_cumsum(const uint16_t* x, uint16_t* y, uint32_t rows, uint32_t n, uint32_t exclusive,
+              uint32_t reverse);
+int go_gather(const uint16_t* tbl, const int32_t* idx, uint16_t* y, uint32_t n, uint32_t packed,
+              const uint32_t* td, const uint32_t* xd);
+int go_transpose4(const uint16_t* x, uint16_t* y, uint32_t Hh, uint32_t W, uint32_t Cc, uint32_t perm);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,17 @@ def lib():
             "go_argmax": (C.c_int32, [_p, u]),
             "go_attn_prefill": (C.c_int, [_p, _p, _p, _p, u, u, u, u, C.c_float, C.c_int]),
             "go_rope": (C.c_int, [_p, _p, u, u, u, u, C.c_float, u]),
+            "go_crouton_encode": (C.c_int, [_p, _p, u, u]),
+            "go_crouton_decode": (C.c_int, [_p, _p, u, u]),
+            "go_matmul_w4a16": (C.c_int, [_p, _p, _p, u, u, u]),
+            "go_rmsnorm_crouton": (C.c_int, [_p, _p, _p, u, u]),
+            "go_concat": (C.c_int, [_p, _p, u, u, _p]),
+            "go_split": (C.c_int, [_p, u, _p, u, _p, u]),
+            "go_reduce": (C.c_int, [_p, _p, u, u, u, _p]),
+            "go_pad": (C.c_int, [_p, _p, u, u, u, u, C.c_uint16]),
+            "go_cumsum": (C.c_int, [_p, _p, u, u, u, u]),
+            "go_gather": (C.c_int, [_p, _p, _p, u, u, _p, _p]),
+            "go_transpose4": (C.c_int, [_p, _p, u, u, u, u]),
         }
         for name, (res, args) in sig.items():
             f = getattr(_lib, name)
@@ -257,3 +268,126 @@ class KVRing:
             p = softmax(s, 1, n_kv)
             out[h] = matmul_f16(p, vo[h], 1, n_kv, hd)
         return out
+
+
+# ---- remaining runlist ops (gehtp_oracle_ops.c) ----
+def _u16(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint16)
+
+
+def crouton_encode(lin) -> np.ndarray:
+    """crouton16_row4 surface (flat u16) of a row-major [rows, cols] u16 array."""
+    lin = _u16(lin)
+    rows, cols = lin.shape
+    out = np.empty(rows * cols, np.uint16)
+    if lib().go_crouton_encode(_p(lin), _p(out), rows, cols):
+        raise ValueError("crouton shape must be multiples of 32")
+    return out
+
+
+def crouton_decode(surf, rows: int, cols: int) -> np.ndarray:
+    surf = _u16(surf).ravel()
+    out = np.empty((rows, cols), np.uint16)
+    if lib().go_crouton_decode(_p(surf), _p(out), rows, cols):
+        raise ValueError("crouton shape must be multiples of 32")
+    return out
+
+
+def w4a16_pack(w_nk) -> np.ndarray:
+    """W [N, K] int values in [-8, 7] -> the K*N/2-byte slot ([N][K/2], +8 nibbles)."""
+    return w4g_pack(np.asarray(w_nk, np.int8)).ravel()
+
+
+def matmul_w4a16(act_surf, w_slot, M: int, K: int, N: int) -> np.ndarray:
+    """OP_MATMUL_W4A16: crouton u16 surface [M,N] from crouton act [M,K] and the W slot."""
+    a = _u16(act_surf).ravel()
+    w = np.ascontiguousarray(w_slot, np.uint8).ravel()
+    out = np.empty(M * N, np.uint16)
+    if lib().go_matmul_w4a16(_p(a), _p(w), _p(out), M, K, N):
+        raise ValueError("matmul_w4a16 shape")
+    return out
+
+
+def rmsnorm_crouton(x_surf, w, m: int, n: int) -> np.ndarray:
+    """OP_RMSNORM_F16 on a crouton u16 surface: row-major f16 [m, n]."""
+    x = _u16(x_surf).ravel()
+    wv = _h(w)
+    y = np.empty((m, n), np.float16)
+    if lib().go_rmsnorm_crouton(_p(x), _p(wv), _p(y), m, n):
+        raise ValueError("rmsnorm shape")
+    return y
+
+
+def concat(segs, outer: int) -> np.ndarray:
+    segs = [_h(s) for s in segs]
+    sizes = (C.c_uint32 * 4)(*([s.size // outer for s in segs] + [0] * (4 - len(segs))))
+    ptrs = (C.c_void_p * 4)(*([_p(s) for s in segs] + [None] * (4 - len(segs))))
+    n = sum(s.size for s in segs)
+    y = np.empty(n, np.float16)
+    if lib().go_concat(C.cast(ptrs, C.c_void_p), _p(y), len(segs), n, C.cast(sizes, C.c_void_p)):
+        raise ValueError("concat shape")
+    return y
+
+
+def split(x, sizes, index: int) -> np.ndarray:
+    x = _h(x).ravel()
+    sz = (C.c_uint32 * 4)(*(list(sizes) + [0] * (4 - len(sizes))))
+    outer = x.size // sum(sizes)
+    y = np.empty(outer * sizes[index], np.float16)
+    if lib().go_split(_p(x), x.size, _p(y), len(sizes), C.cast(sz, C.c_void_p), index):
+        raise ValueError("split shape")
+    return y
+
+
+def reduce(x, dims, axis: int, subtype: int) -> np.ndarray:
+    x = _h(x).ravel()
+    d = (C.c_uint32 * 4)(*dims)
+    if not 0 <= axis < 4:
+        raise ValueError("reduce axis")
+    L = dims[axis] or 1
+    inner = int(np.prod(dims[axis + 1:])) if axis < 3 else 1
+    y = np.empty(x.size // (L * inner) * inner, np.float16)
+    if lib().go_reduce(_p(x), _p(y), x.size, axis, subtype, C.cast(d, C.c_void_p)):
+        raise ValueError("reduce geometry")
+    return y
+
+
+def pad(x, outer: int, in_inner: int, out_inner: int, before: int, value) -> np.ndarray:
+    x = _h(x).ravel()
+    y = np.empty(outer * out_inner, np.float16)
+    pv = int(np.float16(value).view(np.uint16))
+    if lib().go_pad(_p(x), _p(y), outer, in_inner, out_inner, before, pv):
+        raise ValueError("pad geometry")
+    return y
+
+
+def cumsum(x, rows: int, n: int, exclusive: bool = False, reverse: bool = False) -> np.ndarray:
+    x = _h(x).ravel()
+    y = np.empty(rows * n, np.float16)
+    lib().go_cumsum(_p(x), _p(y), rows, n, int(exclusive), int(reverse))
+    return y
+
+
+def gather(tbl, idx, td, xd, axis: int) -> np.ndarray:
+    """OP_GATHER_F16 with tbl dims td (irank = len(td)) and index dims xd."""
+    tbl = _h(tbl).ravel()
+    idx = np.ascontiguousarray(idx, np.int32).ravel()
+    irank, xrank = len(td), len(xd)
+    tdv = (C.c_uint32 * 5)(*(list(td) + [1] * (5 - irank)))
+    xdv = (C.c_uint32 * 5)(*(list(xd) + [1] * (5 - xrank)))
+    od = list(td[:axis]) + list(xd) + list(td[axis + 1:])
+    n = int(np.prod(od))
+    y = np.empty(n, np.float16)
+    packed = axis | (xrank << 8) | (irank << 16)
+    if lib().go_gather(_p(tbl), _p(idx), _p(y), n, packed, C.cast(tdv, C.c_void_p), C.cast(xdv, C.c_void_p)):
+        raise ValueError("gather rank/axis")
+    return y
+
+
+def transpose4(x, Hh: int, W: int, Cc: int, perm) -> np.ndarray:
+    x = _h(x).ravel()
+    y = np.empty(x.size, np.float16)
+    pv = perm[0] | (perm[1] << 8) | (perm[2] << 16) | (perm[3] << 24)
+    if lib().go_transpose4(_p(x), _p(y), Hh, W, Cc, pv):
+        raise ValueError("transpose perm")
+    return y

@@ -182,7 +182,7 @@ def test_unported_opcode_fails_loudly(engine):
     s = bb.add_slot(np.zeros(64, np.float16))
     t = bb.temp()
     bb.op(OP.NOP)
-    bb.op(OP.CUMSUM_F32, bb.slot_ref(s), t, 1, 64, 0, 0, 0)
+    bb.op(OP.SCATTER_ND_F16, bb.slot_ref(s), bb.slot_ref(s), bb.slot_ref(s), t, *([1] * 10))
     pb = engine.parse(bb.build())
     with pytest.raises(WtExecError) as ei:
         engine.run(pb)
