@@ -222,6 +222,10 @@ def gemv_roofline(cfg, w, lib, reps):
 
     replay()
     torch.cuda.synchronize()
+    # Back-to-back launches between two events: the GPU runs ahead of this loop (a
+    # launch costs less host time than a kernel takes), so the mean is the kernels'
+    # duration plus the dispatch gap between them. Events around each launch would add
+    # their own marker overhead; under a profiler the host loop itself slows down.
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
     for _ in range(reps):
