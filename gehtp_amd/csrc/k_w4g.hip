@@ -337,41 +337,48 @@ __global__ __launch_bounds__(256) void w4g_dequant_kernel(const uint4* __restric
 
 // ---------------------------------------------------------------------------
 // Prefill GEMM: C[M,N] = A[M,K] . dequant(W)^T on v_mfma_f32_32x32x16_f16.
-// Workgroup tile 128x128, BK = 64 (one scale group), 4 waves in a 2x2 layout, each
-// wave 64x64 = 2x2 MFMA tiles. A and the dequantized W tile are staged in LDS with
+// Workgroup tile (64*WM)x128, K step BKT (64 = one scale group), WM x 2 waves, each
+// wave 64x64 = 2x2 MFMA tiles; the launcher uses WM = 2 (larger M tiles, which cut
+// the dequant work per MFMA, measured no faster at the 4B-class shapes). A and the dequantized W tile are staged in LDS with
 // a 16-byte row pad; the next K step's global loads are issued before the MFMAs.
-constexpr int BM = 128, BN = 128, BK = 64, LDS_STRIDE = BK + 8;   // halves
+constexpr int BN = 128;
 
-__global__ __launch_bounds__(256) void w4g_gemm_kernel(
+template <int BKT, int WM>
+__global__ __launch_bounds__(128 * WM) void w4g_gemm_kernel(
     const __half* __restrict__ a, uint32_t lda, const uint4* __restrict__ wq,
     const __half* __restrict__ ws, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
     uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu) {
+    constexpr int NT = 128 * WM, BM = 64 * WM;     // waves: WM along M x 2 along N
+    constexpr int LDS_STRIDE = BKT + 8;            // halves; 16-byte pad per row
+    constexpr int AP = BKT / 8;                    // 16-byte A pieces per row
+    constexpr int CA = BM * AP / NT;               // A pieces per thread
+    constexpr int WP = BKT / 32;                   // 16-byte W pieces (32 weights) per row
+    constexpr int CW = (BN * WP + NT - 1) / NT;    // W pieces per thread (some threads idle)
     __shared__ __align__(16) _Float16 As[BM * LDS_STRIDE];
     __shared__ __align__(16) _Float16 Bs[BN * LDS_STRIDE];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const uint32_t G = K / 64;
+    const uint32_t G = K / 64, nsteps = K / BKT;
 
-    // Global load assignment. A: 4 x 16 bytes per thread (rows tid/8 + 32i, chunk tid%8).
-    // W: row n0 + tid/2, half tid%2 (32 weights = 16 bytes) plus its scale.
-    const uint32_t a_chunk = tid & 7, a_row = tid >> 3;
-    const uint32_t w_row = tid >> 1, w_half = tid & 1;
-    const bool w_ok = n0 + w_row < N;
-
-    uint4 ra[4];
-    uint4 rw = make_uint4(0, 0, 0, 0);
-    __half rs = __float2half(0.0f);
-
+    uint4 ra[CA], rw[CW];
+    __half rs[CW];
     auto load_k = [&](uint32_t kb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t r = m0 + a_row + 32u * i;
-            ra[i] = r < M ? *reinterpret_cast<const uint4*>(a + (size_t)r * lda + kb * 64 + a_chunk * 8)
+        for (int i = 0; i < CA; ++i) {
+            const uint32_t c = tid + NT * i, r = m0 + c / AP;
+            ra[i] = r < M ? *reinterpret_cast<const uint4*>(a + (size_t)r * lda + kb * BKT + (c % AP) * 8)
                           : make_uint4(0, 0, 0, 0);
         }
-        if (w_ok) {
-            rw = wq[((size_t)(n0 + w_row) * G + kb) * 2 + w_half];
-            rs = ws[(size_t)(n0 + w_row) * G + kb];
+#pragma unroll
+        for (int i = 0; i < CW; ++i) {
+            const uint32_t c = tid + NT * i, n = n0 + c / WP, q = c % WP;
+            if (c < BN * WP && n < N) {
+                rw[i] = wq[(size_t)n * (K / 32) + kb * WP + q];
+                rs[i] = ws[(size_t)n * G + kb * (BKT / 64) + q / 2];
+            } else {
+                rw[i] = make_uint4(0, 0, 0, 0);
+                rs[i] = __float2half(0.0f);
+            }
         }
     };
 
@@ -385,30 +392,35 @@ __global__ __launch_bounds__(256) void w4g_gemm_kernel(
 
     const uint32_t wm = wave >> 1, wn = wave & 1;
     load_k(0);
-    for (uint32_t kb = 0; kb < G; ++kb) {
+    for (uint32_t kb = 0; kb < nsteps; ++kb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<uint4*>(&As[(a_row + 32 * i) * LDS_STRIDE + a_chunk * 8]) = ra[i];
-        {
-            const _Float16 s = __builtin_bit_cast(_Float16, rs);
+        for (int i = 0; i < CA; ++i) {
+            const uint32_t c = tid + NT * i;
+            *reinterpret_cast<uint4*>(&As[(c / AP) * LDS_STRIDE + (c % AP) * 8]) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < CW; ++i) {
+            const uint32_t c = tid + NT * i;
+            if (c >= BN * WP) continue;
+            const _Float16 s = __builtin_bit_cast(_Float16, rs[i]);
             const h2_t s2 = {s, s};
-            const uint32_t words[4] = {rw.x, rw.y, rw.z, rw.w};
+            const uint32_t words[4] = {rw[i].x, rw[i].y, rw[i].z, rw[i].w};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
+            for (int q = 0; q < 4; ++q) {
                 h2_t d[4];
-                dequant_word(words[c], s2, d);
-                uint4 o;
-                o.x = (as_u32(d[0]) & 0xFFFFu) | (as_u32(d[1]) << 16);
-                o.y = (as_u32(d[2]) & 0xFFFFu) | (as_u32(d[3]) << 16);
-                o.z = (as_u32(d[0]) >> 16) | (as_u32(d[1]) & 0xFFFF0000u);
-                o.w = (as_u32(d[2]) >> 16) | (as_u32(d[3]) & 0xFFFF0000u);
-                *reinterpret_cast<uint4*>(&Bs[w_row * LDS_STRIDE + w_half * 32 + c * 8]) = o;
+                dequant_word(words[q], s2, d);
+                uint4 o;   // pair order (k0,k4)(k1,k5)(k2,k6)(k3,k7) back to k0..k7
+                o.x = __builtin_amdgcn_perm(as_u32(d[1]), as_u32(d[0]), 0x05040100u);
+                o.y = __builtin_amdgcn_perm(as_u32(d[3]), as_u32(d[2]), 0x05040100u);
+                o.z = __builtin_amdgcn_perm(as_u32(d[1]), as_u32(d[0]), 0x07060302u);
+                o.w = __builtin_amdgcn_perm(as_u32(d[3]), as_u32(d[2]), 0x07060302u);
+                *reinterpret_cast<uint4*>(&Bs[(c / WP) * LDS_STRIDE + (c % WP) * 32 + q * 8]) = o;
             }
         }
         __syncthreads();
-        if (kb + 1 < G) load_k(kb + 1);
+        if (kb + 1 < nsteps) load_k(kb + 1);
 #pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
+        for (int kk = 0; kk < BKT / 16; ++kk) {
             h8_t af[2], bf[2];
             const uint32_t kof = kk * 16 + 8 * (lane >> 5);
 #pragma unroll
@@ -524,9 +536,8 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
                            hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.gamma || (epi.swiglu && (N & 1))) return hipErrorInvalidValue;
-    dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    hipLaunchKernelGGL(w4g_gemm_kernel, grid, dim3(256), 0, st, a, lda, reinterpret_cast<const uint4*>(wq), ws, y, ldy,
-                       M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0);
+    hipLaunchKernelGGL((w4g_gemm_kernel<64, 2>), dim3((N + BN - 1) / BN, (M + 127) / 128), dim3(256), 0, st, a, lda,
+                       reinterpret_cast<const uint4*>(wq), ws, y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0);
     return hipGetLastError();
 }
 
