@@ -135,6 +135,8 @@ def main() -> int:
     t_dec = time.perf_counter() - t0
     tok_s = args.steps / t_dec
     log(f"decode: {args.steps} steps in {t_dec * 1e3:.1f} ms -> {tok_s:.1f} tok/s; tokens {toks[:8]}")
+    caps, reps = eng.graph_stats()
+    log(f"decode graphs: {caps} captured, {reps} replays")
 
     # Per-op device time of one decode step (engine's HIP events).
     _, op_us = eng.run_io(pd, emb[tok].tobytes(), td["tok"], timing=True)

@@ -132,5 +132,15 @@ class Engine:
     def set_trace(self, on: bool) -> None:
         self.lib.wt_exec_set_trace(1 if on else 0)
 
+    def set_graphs(self, on: bool) -> bool:
+        """Graph replay of repeated runs on/off; returns the previous setting."""
+        return bool(self.lib.wt_exec_set_graphs(1 if on else 0))
+
+    def graph_stats(self) -> tuple[int, int]:
+        """(graphs captured, graph replays) since the library was loaded."""
+        c, r = C.c_uint32(0), C.c_uint32(0)
+        self.lib.wt_exec_graph_stats(C.byref(c), C.byref(r))
+        return c.value, r.value
+
 
 WT_ERR = WT_ERR

@@ -9,7 +9,9 @@
 //   - each op enqueues gfx950 kernels on the engine stream; a run drains the stream
 //     before returning; there is no CPU compute path for any op;
 //   - KV ring bookkeeping (positions, counters) is mirrored on the host for the
-//     reference's hard-error checks, and on the device so kernels read positions.
+//     reference's hard-error checks, and on the device so kernels read positions;
+//   - a run repeated with the same ops and the same device buffers (a decode step)
+//     is replayed as a HIP graph, which halves the per-kernel launch cost.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -90,8 +92,9 @@ struct Engine {
     uint8_t* ext_dev = nullptr;
     size_t ext_cap = 0;
     uint64_t ext_key = 0;
-    // Injected input for EXT_IN slots.
+    // Injected input for EXT_IN slots (staged through pinned host memory).
     uint8_t* in_dev = nullptr;
+    uint8_t* in_host = nullptr;
     size_t in_cap = 0;
     bool in_active = false;
 
@@ -110,6 +113,15 @@ struct Engine {
     const uint8_t* w4_wt = nullptr;
     const uint8_t* w4_bias = nullptr;
 
+    // Graph replay. `epoch` changes whenever a device pointer that kernels receive may
+    // have changed (any allocation or free, a temp moving, a new pool or weight image).
+    uint64_t epoch = 1;
+    bool replay = false;    // host pass of a graph replay: device work is not enqueued
+    bool variant = false;   // an op of this run passed host-side step state to a kernel
+    int graphs = -1;        // -1: not yet read from the environment; 0 off; 1 on
+    bool graphs_broken = false;
+    uint32_t n_captures = 0, n_replays = 0;
+
     wt_exec_stats stats{};
     wt_op_ts* ts = nullptr;
     uint32_t ts_cap = 0;
@@ -127,13 +139,24 @@ Engine g;
 
 #define ERR(...) (std::snprintf(err, errn, __VA_ARGS__), -1)
 
+// Every device allocation and free of the engine goes through these two, so that a
+// captured graph is never replayed against moved buffers.
+hipError_t dev_malloc(void** p, size_t bytes) {
+    ++g.epoch;
+    return hipMalloc(p, bytes);
+}
+void dev_free(void* p) {
+    ++g.epoch;
+    if (p) hipFree(p);
+}
+
 int ensure_ready(char* err, size_t errn) {
     if (g.ready) return 0;
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return ERR("no HIP device visible");
     if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess)
         return ERR("hipStreamCreate failed");
-    if (hipMalloc(&g.counters_dev, WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
+    if (dev_malloc(reinterpret_cast<void**>(&g.counters_dev), WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
         return ERR("counter alloc failed");
     if (hipMemset(g.counters_dev, 0, WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
         return ERR("counter clear failed");
@@ -148,27 +171,46 @@ uint64_t fnv(uint64_t h, const void* p, size_t n) {
     return h;
 }
 
-// Identity of a host byte image: pointer, size and sampled content (64 evenly spaced
-// 1 KiB windows plus the whole image when it is small), so a new blob that reuses an
-// old buffer address is still recognised as new.
+// Change-detection hash of a byte range: FNV-style multiply-xor on 8-byte words in
+// four independent lanes (a run checks its images every call, so this stays cheap:
+// about 7 GB/s against FNV-1a's 0.7 GB/s).
+uint64_t hash_bytes(uint64_t h, const void* p, size_t n) {
+    const uint8_t* b = static_cast<const uint8_t*>(p);
+    uint64_t l[4] = {h, h ^ 0x9e3779b97f4a7c15ull, h ^ 0xc2b2ae3d27d4eb4full, h ^ 0x165667b19e3779f9ull};
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int k = 0; k < 4; ++k) {
+            uint64_t w;
+            std::memcpy(&w, b + i + 8 * k, 8);
+            l[k] = (l[k] ^ w) * 0x100000001b3ull;
+            l[k] ^= l[k] >> 29;
+        }
+    uint64_t r = l[0];
+    for (int k = 1; k < 4; ++k) r = (r ^ l[k]) * 0x9e3779b97f4a7c15ull;
+    return fnv(r, b + i, n - i);
+}
+
+// Identity of a host byte image: pointer, size and content (all of it up to 64 KiB,
+// else 64 evenly spaced 1 KiB windows), so a new blob that reuses an old buffer
+// address is still recognised as new.
 uint64_t image_key(const uint8_t* p, size_t n) {
     uint64_t h = 0xcbf29ce484222325ull;
     h = fnv(h, &p, sizeof p);
     h = fnv(h, &n, sizeof n);
-    if (n <= (4u << 20)) return fnv(h, p, n);
+    if (n <= (64u << 10)) return hash_bytes(h, p, n);
     for (int i = 0; i < 64; ++i) {
         const size_t off = (n - 1024) / 63 * (size_t)i;
-        h = fnv(h, p + off, 1024);
+        h = hash_bytes(h, p + off, 1024);
     }
     return h;
 }
 
 int upload(uint8_t** dev, size_t* cap, const uint8_t* host, size_t bytes, char* err, size_t errn) {
     if (bytes > *cap) {
-        if (*dev) hipFree(*dev);
+        if (*dev) dev_free(*dev);
         *dev = nullptr;
         *cap = 0;
-        if (hipMalloc(reinterpret_cast<void**>(dev), bytes) != hipSuccess)
+        if (dev_malloc(reinterpret_cast<void**>(dev), bytes) != hipSuccess)
             return ERR("device alloc of %zu bytes failed", bytes);
         *cap = bytes;
     }
@@ -179,7 +221,7 @@ int upload(uint8_t** dev, size_t* cap, const uint8_t* host, size_t bytes, char* 
 
 int ensure_weights(const wt_blob* b, char* err, size_t errn) {
     uint64_t key = image_key(b->weight_base, b->weight_bytes);
-    key = fnv(key, b->slots, sizeof(wt_slot) * b->n_slots);
+    key = hash_bytes(key, b->slots, sizeof(wt_slot) * b->n_slots);
     if (key != g.w_key || !g.w_dev) {
         if (upload(&g.w_dev, &g.w_cap, b->weight_base, std::max<size_t>(b->weight_bytes, 16), err, errn))
             return -1;
@@ -276,7 +318,7 @@ uint8_t* temp_get(uint32_t id, uint32_t bytes) {
             while (ncap < (uint64_t)g.pool_used + aligned) ncap *= 2;
             if (ncap > 0xFFFFFFFFull) return nullptr;
             void* np = nullptr;
-            if (hipMalloc(&np, ncap) != hipSuccess) return nullptr;
+            if (dev_malloc(&np, ncap) != hipSuccess) return nullptr;
             if (g.pool && g.pool_owned) g.retired_pools.push_back(g.pool);
             g.pool = static_cast<uint8_t*>(np);
             g.pool_cap = (uint32_t)ncap;
@@ -286,6 +328,7 @@ uint8_t* temp_get(uint32_t id, uint32_t bytes) {
         g.temps[id] = g.pool + g.pool_used;
         g.pool_used += aligned;
         g.temp_bytes[id] = bytes;
+        ++g.epoch;
     }
     g.last_bytes[id] = bytes;
     return g.temps[id];
@@ -330,7 +373,7 @@ int load_tempoff(const wt_blob* b, char* err, size_t errn) {
             }
         }
         void* pool = nullptr;
-        if (hipMalloc(&pool, (size_t)cap + reserve) != hipSuccess) return ERR("tempoff pool alloc");
+        if (dev_malloc(&pool, (size_t)cap + reserve) != hipSuccess) return ERR("tempoff pool alloc");
         if (g.pool && g.pool_owned) g.retired_pools.push_back(g.pool);
         std::memcpy(g.static_off_arr, tmp_static, sizeof tmp_static);
         std::memcpy(g.vtcm_off_arr, tmp_vtcm, sizeof tmp_vtcm);
@@ -341,7 +384,7 @@ int load_tempoff(const wt_blob* b, char* err, size_t errn) {
         g.static_offsets = g.static_off_arr;
         if (vtcm_cap) {
             void* vp = nullptr;
-            if (hipMalloc(&vp, vtcm_cap) != hipSuccess) return ERR("vtcm pool alloc");
+            if (dev_malloc(&vp, vtcm_cap) != hipSuccess) return ERR("vtcm pool alloc");
             g.vtcm_pool = static_cast<uint8_t*>(vp);
             g.vtcm_pool_size = vtcm_cap;
         }
@@ -373,7 +416,7 @@ int load_states(const wt_blob* b, char* err, size_t errn) {
         }
         if (same) return 0;
         for (uint32_t i = 0; i < g.n_states; ++i) {
-            if (g.st[i].dev) hipFree(g.st[i].dev);
+            if (g.st[i].dev) dev_free(g.st[i].dev);
             g.st[i] = State{};
         }
         g.n_states = 0;
@@ -384,7 +427,7 @@ int load_states(const wt_blob* b, char* err, size_t errn) {
             std::memcpy(&bytes, p + 4 + 4 * i, 4);
             if (bytes == 0 || bytes > (1u << 30)) return ERR("state %u bytes bad %u", i, bytes);
             void* d = nullptr;
-            if (hipMalloc(&d, bytes) != hipSuccess) return ERR("state %u alloc %u", i, bytes);
+            if (dev_malloc(&d, bytes) != hipSuccess) return ERR("state %u alloc %u", i, bytes);
             if (hipMemset(d, 0, bytes) != hipSuccess) return ERR("state %u clear", i);
             g.st[i] = State{};
             g.st[i].dev = static_cast<uint8_t*>(d);
@@ -456,11 +499,20 @@ struct Ctx {
     size_t errn;
 };
 
+// Enqueue device work; skipped in the host pass of a graph replay, whose kernels
+// the graph already carries.
 #define CHECK_LAUNCH(expr)                                                             \
     do {                                                                               \
-        hipError_t e_ = (expr);                                                        \
-        if (e_ != hipSuccess) return ERR("launch failed: %s", hipGetErrorString(e_));  \
+        if (!g.replay) {                                                               \
+            hipError_t e_ = (expr);                                                    \
+            if (e_ != hipSuccess) return ERR("launch failed: %s", hipGetErrorString(e_)); \
+        }                                                                              \
     } while (0)
+
+hipError_t copy_d2d(void* dst, const void* src, size_t bytes) {
+    if (g.replay || !bytes) return hipSuccess;
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g.stream);
+}
 
 #define A(i) (cx.op->args[i])
 
@@ -748,6 +800,7 @@ int op_kv_gather(Ctx& cx) {
             return ERR("kv gather state %u count=%u bad (append first?)", A(0) & 0x1FFFu, s->count);
         n_kv = s->count;
         pstride = s->nslots;
+        g.variant = true;   // the position count is a kernel argument
     }
     if (kv_check(*s, n_kv, err, errn)) return -1;
     const uint64_t bytes = (uint64_t)H * hd * pstride * 2u;
@@ -801,7 +854,7 @@ int op_attn_decode(Ctx& cx) {
     const size_t qb = ref_bytes(cx.b, A(0));
     if (qb && qb < (uint64_t)H * hd * 2u) return ERR("attn_decode q smaller than H*hd");
     if (attn_workspace(attn_decode_work_floats(autopos ? s->nslots : n_kv, H, hd), err, errn)) return -1;
-    CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o, n_kv,
+    CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o, autopos ? 0u : n_kv,
                                     autopos ? g.counters_dev + (A(1) & 0x1FFFu) : nullptr, H, KVH, hd,
                                     scale, g.attn_work, g.attn_work_floats, g.stream));
     return 0;
@@ -810,10 +863,10 @@ int op_attn_decode(Ctx& cx) {
 // Engine-private device scratch (grown on demand, freed at shutdown).
 int scratch(uint8_t** p, size_t* cap, size_t bytes, char* err, size_t errn) {
     if (bytes <= *cap) return 0;
-    if (*p) hipFree(*p);
+    if (*p) dev_free(*p);
     *p = nullptr;
     *cap = 0;
-    if (hipMalloc(reinterpret_cast<void**>(p), bytes) != hipSuccess) return ERR("scratch alloc %zu", bytes);
+    if (dev_malloc(reinterpret_cast<void**>(p), bytes) != hipSuccess) return ERR("scratch alloc %zu", bytes);
     *cap = bytes;
     return 0;
 }
@@ -909,10 +962,11 @@ int op_qk_rope_kv(Ctx& cx) {
 // allocated: the fused op's merge completion counter must start at zero.
 int attn_workspace(uint32_t need, char* err, size_t errn) {
     if (need <= g.attn_work_floats) return 0;
-    if (g.attn_work) hipFree(g.attn_work);
+    if (g.attn_work) dev_free(g.attn_work);
     g.attn_work = nullptr;
     g.attn_work_floats = 0;
-    if (hipMalloc(&g.attn_work, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace alloc");
+    if (dev_malloc(reinterpret_cast<void**>(&g.attn_work), (size_t)need * 4u) != hipSuccess)
+        return ERR("attn_decode workspace alloc");
     if (hipMemset(g.attn_work, 0, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace clear");
     g.attn_work_floats = need;
     return 0;
@@ -992,7 +1046,7 @@ int op_matmul_w4a16(Ctx& cx) {
     if (scratch(&g.w4_out, &g.w4_out_cap, out_b, err, errn)) return -1;
     CHECK_LAUNCH(launch_matmul_w4a16(reinterpret_cast<const uint16_t*>(act), w, reinterpret_cast<uint16_t*>(g.w4_out),
                                      M, K, N, g.stream));
-    if (!(act_s & WT_REF_VTCM_FLAG) && hipMemcpyAsync(out, g.w4_out, out_b, hipMemcpyDeviceToDevice, g.stream) != hipSuccess)
+    if (!(act_s & WT_REF_VTCM_FLAG) && copy_d2d(out, g.w4_out, out_b) != hipSuccess)
         return ERR("w4a16 out copy");
     g.w4_ready = true;
     g.w4_m = M; g.w4_k = K; g.w4_n = N;
@@ -1036,7 +1090,7 @@ int op_fill(Ctx& cx) {
         d = temp_get(dst, (uint32_t)bytes);
     }
     if (!d) return ERR("fill dst empty");
-    if (bytes && hipMemcpyAsync(d, src, bytes, hipMemcpyDeviceToDevice, g.stream) != hipSuccess) return ERR("fill copy");
+    if (copy_d2d(d, src, bytes) != hipSuccess) return ERR("fill copy");
     return 0;
 }
 
@@ -1212,7 +1266,7 @@ int op_dma(Ctx& cx) {
     const uint8_t* src = dma_resolve(cx.b, A(0), A(3), bytes, false);
     uint8_t* dst = dma_resolve(cx.b, A(1), A(4), bytes, true);
     if (!src || !dst) return ERR("dma ref fail");
-    if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g.stream) != hipSuccess) return ERR("dma copy");
+    if (copy_d2d(dst, src, bytes) != hipSuccess) return ERR("dma copy");
     return 0;
 }
 
@@ -1307,14 +1361,16 @@ struct Table {
 const Table kTable;
 
 // Tensor dump hook "opidx:temp,..." (oplist_exec.c:108-166): host files /tmp/hook_<i>_<t>.f16.raw.
-void hook_dump(uint32_t ii) {
+const char* hook_spec() {
     static const char* env_hook = nullptr;
     static bool env_tried = false;
-    const char* hook = g.hook;
-    if (!hook) {
-        if (!env_tried) { env_hook = std::getenv("GEHTP_HOOK"); env_tried = true; }
-        hook = env_hook;
-    }
+    if (g.hook) return g.hook;
+    if (!env_tried) { env_hook = std::getenv("GEHTP_HOOK"); env_tried = true; }
+    return env_hook;
+}
+
+void hook_dump(uint32_t ii) {
+    const char* hook = hook_spec();
     if (!hook || !hook[0]) return;
     const char* tok = hook;
     while (*tok) {
@@ -1343,6 +1399,157 @@ void hook_dump(uint32_t ii) {
     }
 }
 
+
+// ---- graph replay of repeated runs ----
+// A decode step runs the same ops on the same buffers every time, and its kernels
+// read positions from the device counters, so its launches (kernel, grid, arguments)
+// repeat exactly. Once one direct run of a range has shown that (no device buffer
+// moved during it, no op passed host-side step state to a kernel), the next identical
+// run is captured into a HIP graph. Later identical runs launch the graph and then
+// walk the ops on the host with device work suppressed, which keeps the host-side
+// bookkeeping (KV position mirrors, temp sizes, stats) exactly as a direct run
+// leaves it. A preflight of the KV capacity checks comes first, so a run that would
+// fail its host-side checks takes the direct path and fails at the same op.
+// Host state a handler may read that an earlier run left behind: element counts of
+// temps (ref_elem_count) and the opcode-1 engine surfaces (OP_DMA's 0xC000 refs).
+struct HostIn {   // no padding: compared with memcmp
+    uint32_t last_bytes[kMaxTemps];
+    uint32_t w4_ready, w4_m, w4_k, w4_n;
+    const void* w4p[4];
+};
+static_assert(sizeof(HostIn) == kMaxTemps * 4 + 16 + 4 * sizeof(void*), "HostIn has padding");
+void host_in(HostIn& h) {
+    std::memset(&h, 0, sizeof h);
+    std::memcpy(h.last_bytes, g.last_bytes, sizeof h.last_bytes);
+    h.w4_ready = g.w4_ready ? 1u : 0u;
+    h.w4_m = g.w4_m; h.w4_k = g.w4_k; h.w4_n = g.w4_n;
+    h.w4p[0] = g.w4_out; h.w4p[1] = g.w4_act; h.w4p[2] = g.w4_wt; h.w4p[3] = g.w4_bias;
+}
+
+struct RunSig {
+    const wt_blob* b = nullptr;
+    uint32_t first = 0, count = 0;
+    bool in_active = false;
+    uint64_t epoch = 0, w_key = 0, ext_key = 0;
+    std::vector<wt_op> ops;
+    HostIn in{};   // at the start of the run
+
+    bool same(const wt_blob* bb, uint32_t f, uint32_t c, const HostIn& now) const {
+        return b == bb && first == f && count == c && in_active == g.in_active && epoch == g.epoch &&
+               w_key == g.w_key && ext_key == g.ext_key && ops.size() == c &&
+               std::memcmp(ops.data(), bb->ops + f, sizeof(wt_op) * c) == 0 &&
+               std::memcmp(&in, &now, sizeof in) == 0;
+    }
+    void set(const wt_blob* bb, uint32_t f, uint32_t c, const HostIn& start) {
+        b = bb; first = f; count = c;
+        in_active = g.in_active;
+        epoch = g.epoch; w_key = g.w_key; ext_key = g.ext_key;
+        ops.assign(bb->ops + f, bb->ops + f + c);
+        in = start;
+    }
+};
+
+struct RunGraph {
+    RunSig sig;
+    hipGraphExec_t exec = nullptr;
+    std::vector<std::pair<uint32_t, uint32_t>> adv;   // (state, positions the run appends)
+    uint64_t used = 0;
+};
+
+constexpr size_t kMaxGraphs = 4;
+std::vector<RunGraph> g_graphs;
+RunSig g_stable;            // last direct run that qualified for capture
+bool g_stable_ok = false;
+uint64_t g_use_tick = 0;
+
+bool graphs_on() {
+    if (g.graphs < 0) {
+        const char* e = std::getenv("GEHTP_NO_GRAPH");
+        g.graphs = (e && e[0] && e[0] != '0') ? 0 : 1;
+    }
+    return g.graphs == 1 && !g.graphs_broken;
+}
+
+// Callers hold the stream idle (runs drain it before returning).
+void drop_graphs() {
+    if (!g_graphs.empty() && g.stream) hipStreamSynchronize(g.stream);
+    for (RunGraph& r : g_graphs)
+        if (r.exec) hipGraphExecDestroy(r.exec);
+    g_graphs.clear();
+    g_stable_ok = false;
+}
+
+RunGraph* find_graph(const wt_blob* b, uint32_t first, uint32_t count, const HostIn& now) {
+    for (RunGraph& r : g_graphs)
+        if (r.sig.same(b, first, count, now)) return &r;
+    return nullptr;
+}
+
+bool preflight(const RunGraph& r) {
+    for (const auto& a : r.adv) {
+        if (a.first >= g.n_states) return false;
+        const State& s = g.st[a.first];
+        if (!s.kv_ready || (uint64_t)s.count + a.second > s.nslots || s.valid_prefix < s.count) return false;
+    }
+    return true;
+}
+
+void keep_graph(const wt_blob* b, uint32_t first, uint32_t count, hipGraphExec_t exec, const uint32_t* counts0,
+                const HostIn& start) {
+    if (g_graphs.size() >= kMaxGraphs) {
+        auto lru = std::min_element(g_graphs.begin(), g_graphs.end(),
+                                    [](const RunGraph& x, const RunGraph& y) { return x.used < y.used; });
+        hipGraphExecDestroy(lru->exec);
+        g_graphs.erase(lru);
+    }
+    RunGraph r;
+    r.sig.set(b, first, count, start);
+    r.exec = exec;
+    r.used = ++g_use_tick;
+    for (uint32_t i = 0; i < g.n_states; ++i)
+        if (g.st[i].count != counts0[i]) r.adv.emplace_back(i, g.st[i].count - counts0[i]);
+    g_graphs.push_back(std::move(r));
+}
+
+// One op through its handler; returns the handler's status.
+int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* err, size_t errn) {
+    const wt_op* op = &b->ops[i];
+    Ctx cx{b, op, engine_m, err, errn};
+    const int rc = op->opcode < 64 ? kTable.fn[op->opcode](cx) : op_unsupported(cx);
+    if (g.trace)
+        std::fprintf(stderr, "[gehtp] op%u code=%u a=%u,%u,%u,%u rc=%d pool=%u%s\n", ii, (unsigned)op->opcode,
+                     op->args[0], op->args[1], op->args[2], op->args[3], rc, g.pool_used,
+                     g.replay ? " (graph)" : "");
+    g.stats.ops++;
+    return rc;
+}
+
+int replay_graph(RunGraph& r, const wt_blob* b, uint32_t first, uint32_t count, uint32_t* engine_m, char* err,
+                 size_t errn) {
+    const hipError_t le = hipGraphLaunch(r.exec, g.stream);
+    if (le != hipSuccess) return ERR("graph launch failed: %s", hipGetErrorString(le));
+    r.used = ++g_use_tick;
+    const uint64_t ep0 = g.epoch;
+    g.variant = false;
+    g.replay = true;
+    int fail = 0;
+    for (uint32_t ii = 0; ii < count && !fail; ++ii)
+        if (run_op(b, first + ii, ii, engine_m, err, errn)) fail = (int)(first + ii) + 1;
+    g.replay = false;
+    const hipError_t e = hipStreamSynchronize(g.stream);
+    if (e != hipSuccess) return ERR("device error: %s", hipGetErrorString(e));
+    if (fail || g.epoch != ep0 || g.variant) {
+        // The preflight makes this unreachable for the ops this engine implements; if
+        // the host pass ever disagrees with the capture, stop using graphs.
+        g.graphs_broken = true;
+        drop_graphs();
+        if (fail) return fail;
+        return ERR("graph replay diverged from its capture");
+    }
+    g.n_replays++;
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1369,29 +1576,72 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
             if (hipEventCreate(&g.events[i]) != hipSuccess) return ERR("event create failed");
     }
     const bool sync_each = std::getenv("GEHTP_SYNC_EACH_OP") != nullptr;
+    const char* hk = hook_spec();
+    const bool can_graph = count && !timed && !sync_each && !(hk && hk[0]) && graphs_on();
+    static HostIn hin;   // one engine per process; runs are not reentrant
+    if (can_graph) {
+        host_in(hin);
+        RunGraph* r = find_graph(b, first, count, hin);
+        if (r && preflight(*r)) return replay_graph(*r, b, first, count, engine_m, err, errn);
+    }
+    bool capture = can_graph && g_stable_ok && g_stable.same(b, first, count, hin);
+    uint32_t counts0[WT_MAX_STATES];
+    for (uint32_t i = 0; i < g.n_states; ++i) counts0[i] = g.st[i].count;
+    const uint64_t ep0 = g.epoch;
+    g.variant = false;
+    if (capture && hipStreamBeginCapture(g.stream, hipStreamCaptureModeRelaxed) != hipSuccess) {
+        (void)hipGetLastError();
+        capture = false;
+    }
+
     if (timed && hipEventRecord(g.events[2 * (size_t)count], g.stream) != hipSuccess)
         return ERR("event record failed");
-    for (uint32_t ii = 0; ii < count; ++ii) {
+    int fail = 0;
+    for (uint32_t ii = 0; ii < count && !fail; ++ii) {
         const uint32_t i = first + ii;
-        const wt_op* op = &b->ops[i];
         if (timed) hipEventRecord(g.events[2 * ii], g.stream);
-        Ctx cx{b, op, engine_m, err, errn};
-        int rc = op->opcode < 64 ? kTable.fn[op->opcode](cx) : op_unsupported(cx);
+        int rc = run_op(b, i, ii, engine_m, err, errn);
         if (timed) hipEventRecord(g.events[2 * ii + 1], g.stream);
-        if (g.trace)
-            std::fprintf(stderr, "[gehtp] op%u code=%u a=%u,%u,%u,%u rc=%d pool=%u\n", ii,
-                         (unsigned)op->opcode, op->args[0], op->args[1], op->args[2], op->args[3], rc,
-                         g.pool_used);
         if (rc == 0 && sync_each) {
             const hipError_t e = hipStreamSynchronize(g.stream);
             if (e != hipSuccess) { std::snprintf(err, errn, "op %u: %s", i, hipGetErrorString(e)); rc = -1; }
         }
-        g.stats.ops++;
         if (rc == 0) hook_dump(ii);
-        if (rc) {
+        if (rc) fail = (int)i + 1;
+    }
+    if (capture) {
+        // The captured work of this run (all of it, or the ops before a failing one)
+        // is launched once from the graph; it is kept for replay only if this run
+        // matched the direct run that qualified it.
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        hipError_t ce = hipStreamEndCapture(g.stream, &graph);
+        if (ce == hipSuccess) ce = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (graph) hipGraphDestroy(graph);
+        if (ce == hipSuccess) ce = hipGraphLaunch(exec, g.stream);
+        if (ce != hipSuccess) {
+            g.graphs_broken = true;
             hipStreamSynchronize(g.stream);
-            return (int)i + 1;
+            if (exec) hipGraphExecDestroy(exec);
+            drop_graphs();
+            return ERR("graph capture of ops %u..%u failed: %s", first, first + count - 1, hipGetErrorString(ce));
         }
+        const bool keep = !fail && !g.variant && g.epoch == ep0;
+        if (keep) {
+            keep_graph(b, first, count, exec, counts0, hin);
+            g.n_captures++;
+            g_stable_ok = false;
+        } else {
+            hipStreamSynchronize(g.stream);
+            hipGraphExecDestroy(exec);
+        }
+    } else if (can_graph && !fail) {
+        g_stable_ok = !g.variant && g.epoch == ep0;
+        if (g_stable_ok) g_stable.set(b, first, count, hin);
+    }
+    if (fail) {
+        hipStreamSynchronize(g.stream);
+        return fail;
     }
     const hipError_t e = hipStreamSynchronize(g.stream);
     if (e != hipSuccess) return ERR("device error: %s", hipGetErrorString(e));
@@ -1432,13 +1682,18 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
             if (b->slots[i].addr == WT_SLOT_EXT_IN) need = std::max<size_t>(need, b->slots[i].len);
         if (need) {
             if (need > g.in_cap) {
-                if (g.in_dev) hipFree(g.in_dev);
-                g.in_dev = nullptr;
+                if (g.in_dev) dev_free(g.in_dev);
+                if (g.in_host) hipHostFree(g.in_host);
+                g.in_dev = g.in_host = nullptr;
                 g.in_cap = 0;
-                if (hipMalloc(&g.in_dev, need) != hipSuccess) return ERR("input buffer alloc");
+                if (dev_malloc(reinterpret_cast<void**>(&g.in_dev), need) != hipSuccess ||
+                    hipHostMalloc(reinterpret_cast<void**>(&g.in_host), need, hipHostMallocDefault) != hipSuccess)
+                    return ERR("input buffer alloc");
                 g.in_cap = need;
             }
-            if (hipMemcpyAsync(g.in_dev, in_ptr, need, hipMemcpyHostToDevice, g.stream) != hipSuccess)
+            // The previous run drained the stream, so the staging buffer is free.
+            std::memcpy(g.in_host, in_ptr, need);
+            if (hipMemcpyAsync(g.in_dev, g.in_host, need, hipMemcpyHostToDevice, g.stream) != hipSuccess)
                 return ERR("input upload failed");
             g.in_active = true;
         }
@@ -1467,14 +1722,15 @@ uint32_t wt_exec_temp_last_bytes(uint32_t id) { return id < kMaxTemps ? g.last_b
 void wt_exec_shutdown(void) {
     if (g.stream) hipStreamSynchronize(g.stream);
     g.stats = wt_exec_stats{};
-    if (g.pool && g.pool_owned) hipFree(g.pool);
-    for (void* p : g.retired_pools) hipFree(p);
+    drop_graphs();
+    if (g.pool && g.pool_owned) dev_free(g.pool);
+    for (void* p : g.retired_pools) dev_free(p);
     g.retired_pools.clear();
     g.pool = nullptr;
     g.pool_cap = g.pool_used = 0;
     g.pool_owned = false;
     g.static_offsets = nullptr;
-    if (g.vtcm_pool) hipFree(g.vtcm_pool);
+    if (g.vtcm_pool) dev_free(g.vtcm_pool);
     g.vtcm_pool = nullptr;
     g.vtcm_pool_size = 0;
     std::fill(std::begin(g.static_off_arr), std::end(g.static_off_arr), kNone);
@@ -1485,13 +1741,13 @@ void wt_exec_shutdown(void) {
         g.last_bytes[i] = 0;
         std::vector<uint8_t>().swap(g.mirror[i]);
     }
-    if (g.attn_work) hipFree(g.attn_work);
+    if (g.attn_work) dev_free(g.attn_work);
     g.attn_work = nullptr;
     g.attn_work_floats = 0;
-    if (g.norm_buf) hipFree(g.norm_buf);
+    if (g.norm_buf) dev_free(g.norm_buf);
     g.norm_buf = nullptr;
     g.norm_cap = 0;
-    if (g.w4_out) hipFree(g.w4_out);
+    if (g.w4_out) dev_free(g.w4_out);
     g.w4_out = nullptr;
     g.w4_out_cap = 0;
     g.w4_ready = false;
@@ -1513,6 +1769,7 @@ void wt_exec_state_reset(void) {
 }
 
 void wt_exec_pool_init(uint8_t* base, uint32_t total_cap, uint32_t static_cap, const uint32_t* offsets) {
+    ++g.epoch;
     if (base) {
         if (g.pool && g.pool_owned) g.retired_pools.push_back(g.pool);
         g.pool = base;
@@ -1528,6 +1785,7 @@ void wt_exec_get_stats(struct wt_exec_stats* st) {
 }
 
 void wt_exec_set_ext_weights(const void* wgt_ptr) {
+    if (wgt_ptr != g.ext_host) ++g.epoch;
     g.ext_host = static_cast<const uint8_t*>(wgt_ptr);
 }
 
@@ -1537,6 +1795,19 @@ void wt_exec_set_ts(struct wt_op_ts* buf, uint32_t cap) {
 }
 
 void wt_exec_set_trace(int on) { g.trace = on != 0; }
+
+int wt_exec_set_graphs(int on) {
+    const int prev = graphs_on() ? 1 : 0;
+    if (!on) drop_graphs();
+    g.graphs = on ? 1 : 0;
+    if (on) g.graphs_broken = false;
+    return prev;
+}
+
+void wt_exec_graph_stats(uint32_t* captures, uint32_t* replays) {
+    if (captures) *captures = g.n_captures;
+    if (replays) *replays = g.n_replays;
+}
 
 void wt_exec_set_hook(const char* spec) { g.hook = spec; }
 

@@ -85,6 +85,18 @@ void wt_exec_set_trace(int on);
  * (reference oplist_exec.c:108-166); falls back to env GEHTP_HOOK. */
 void wt_exec_set_hook(const char* spec);
 
+/* Graph replay of repeated runs. No counterpart in the reference engine, whose ops
+ * have no kernel-launch cost to amortise. When a run of ops[first, first+count) is
+ * repeated with the same ops and the same device buffers (a decode step: positions
+ * come from device-side counters), the engine captures it into a HIP graph on the
+ * second identical run and replays the graph afterwards; results, return codes and
+ * host-side state are those of a direct run. Runs with per-op timing, a tensor
+ * hook or GEHTP_SYNC_EACH_OP always launch directly. Default on unless the
+ * environment sets GEHTP_NO_GRAPH=1. wt_exec_set_graphs returns the previous
+ * setting; wt_exec_graph_stats reports how many graphs were captured and replayed. */
+int  wt_exec_set_graphs(int on);
+void wt_exec_graph_stats(uint32_t* captures, uint32_t* replays);
+
 /* W3 inspect report: one JSON line per call of emit (reference wt_w3.c). */
 void wt_w3_report(const char* blob_name, const uint8_t* buf, size_t size,
                   const struct wt_blob* w,

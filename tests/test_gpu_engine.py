@@ -148,6 +148,34 @@ def test_decode_loop_auto_positions(engine, oracle):
         assert_close(_h(out, (H, hd)), ref, what=f"decode step {step}")
 
 
+@pytest.mark.parametrize("graphs", [False, True])
+def test_decode_overflow_same_with_graphs(engine, oracle, graphs):
+    """Filling the ring and appending once more fails at the KV_APPEND op with the
+    reference's context error whether the steps ran direct or from a replayed graph;
+    outputs of the steps before match the oracle either way."""
+    rng = np.random.default_rng(8)
+    H, KVH, hd, max_pos = 8, 4, 128, 12
+    bb, to = _decode_blob(H, KVH, hd, max_pos)
+    pb = engine.parse(bb.build())
+    ring = oracle.KVRing(max_pos * KVH * hd * 4, KVH * hd)
+    prev = engine.set_graphs(graphs)
+    try:
+        r0 = engine.graph_stats()[1]
+        for step in range(max_pos):
+            q, k, v = normal_f16(rng, H * hd), normal_f16(rng, KVH * hd), normal_f16(rng, KVH * hd)
+            out, _ = engine.run_io(pb, np.concatenate([q, k, v]).tobytes(), to)
+            ring.append(k, v)
+            assert_close(_h(out, (H, hd)), ring.attn_decode(q, step + 1, H, KVH, hd, SCALE),
+                         what=f"decode step {step}")
+        replays = engine.graph_stats()[1] - r0
+        assert (replays >= max_pos - 4) if graphs else replays == 0
+        with pytest.raises(WtExecError) as ei:
+            engine.run_io(pb, normal_f16(rng, H * hd + 2 * KVH * hd).tobytes(), to)
+        assert ei.value.rc == 4 and "context too long" in str(ei.value)
+    finally:
+        engine.set_graphs(prev)
+
+
 def test_kv_gather_and_overflow(engine, oracle):
     """KV_GATHER output layout (kT [H,hd,nslots] zero tail, v [H,nslots,hd]) is byte-exact;
     appending past nslots is the reference's hard error."""

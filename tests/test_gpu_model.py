@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 SMALL = Qwen3Config(layers=2, hidden=512, heads=4, kv_heads=2, ffn=1024, vocab=3000)
 
 
-def _run(engine, cfg, S, n_dec, seed, max_pos=256):
+def _run(engine, cfg, S, n_dec, seed, max_pos=256, with_ref=True):
     from oracle.qwen3_ref import RefModel
     w = Weights(cfg, seed=seed)
     engine.shutdown()
@@ -27,15 +27,17 @@ def _run(engine, cfg, S, n_dec, seed, max_pos=256):
     rng = np.random.default_rng(seed + 1)
     ids = rng.integers(0, cfg.vocab, S + n_dec)
     emb = w.embed()
-    ref = RefModel(cfg, w, max_pos)
+    ref = RefModel(cfg, w, max_pos) if with_ref else None
     out, _ = engine.run_io(pp, np.ascontiguousarray(emb[ids[:S]]).tobytes(), tp["tok"])
     got = [np.frombuffer(engine.temp(tp["logits"]), np.float16)[:cfg.vocab].copy()]
-    refl = [ref.prefill(np.ascontiguousarray(emb[ids[:S]]))]
+    refl = [ref.prefill(np.ascontiguousarray(emb[ids[:S]]))] if ref else []
     assert int(np.frombuffer(out, np.int32)[0]) == int(np.argmax(got[0].astype(np.float32)))
     for t in range(n_dec):   # teacher forced: both sides consume ids[S + t]
-        engine.run_io(pd, emb[ids[S + t]].tobytes(), td["tok"])
+        out, _ = engine.run_io(pd, emb[ids[S + t]].tobytes(), td["tok"])
         got.append(np.frombuffer(engine.temp(td["logits"]), np.float16)[:cfg.vocab].copy())
-        refl.append(ref.decode(emb[ids[S + t]]))
+        assert int(np.frombuffer(out, np.int32)[0]) == int(np.argmax(got[-1].astype(np.float32)))
+        if ref:
+            refl.append(ref.decode(emb[ids[S + t]]))
     engine.shutdown()
     return got, refl
 
@@ -62,3 +64,22 @@ def test_config4_layer_prefill_then_decode(engine):
     shortened to 128 tokens and 4 decode steps to keep the CPU oracle within seconds."""
     got, refl = _run(engine, CONFIG_08B_LAYER, S=128, n_dec=4, seed=5)
     _check(got, refl, 0.9999)
+
+
+def test_decode_graph_replay_matches_direct(engine):
+    """Decode steps replayed from the engine's HIP graph give the same bits as direct
+    launches: every step's logits and token, with the host's input upload, output copy
+    and temp read-back between replays."""
+    prev = engine.set_graphs(False)
+    try:
+        c0, r0 = engine.graph_stats()
+        direct, _ = _run(engine, SMALL, S=24, n_dec=10, seed=7, with_ref=False)
+        assert engine.graph_stats() == (c0, r0)
+        engine.set_graphs(True)
+        graphed, _ = _run(engine, SMALL, S=24, n_dec=10, seed=7, with_ref=False)
+        c1, r1 = engine.graph_stats()
+    finally:
+        engine.set_graphs(prev)
+    assert c1 - c0 >= 1 and r1 - r0 >= 6, (c1 - c0, r1 - r0)
+    for step, (a, b) in enumerate(zip(direct, graphed)):
+        assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"step {step}"
