@@ -103,51 +103,63 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
     const uint32_t rowbytes = A.K / 2, G = A.K / 64, K8 = A.K / 8;
     const uint32_t nb = (A.np + U - 1) / U;
 
+    // Every global load below is unconditional, with out-of-range indices clamped to
+    // valid ones: a load under a divergent branch with a zeroing else-path makes the
+    // compiler wait for each load before issuing the next. Lanes whose row lies past
+    // the workgroup's rows load the workgroup's first row; the reduction never reads
+    // their partial sums.
     auto load_batch = [&](uint32_t b, u32x4 (&w)[U], uint16_t (&s)[U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t lr = (b * U + u) * R + rr;
-            if (active && lr < RB) {
-                const size_t row = r0 + lr;
-                w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(A.wq + row * rowbytes) + p);
-                s[u] = __builtin_bit_cast(uint16_t, A.ws[row * G + (p >> 1)]);
-            } else {
-                w[u] = u32x4{0u, 0u, 0u, 0u};
-                s[u] = 0;
-            }
+            const size_t row = r0 + ((active && lr < RB) ? lr : 0u);
+            w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(A.wq + row * rowbytes) + p);
+            s[u] = __builtin_bit_cast(uint16_t, A.ws[row * G + (p >> 1)]);
         }
     };
+
+    // Activations first: loads complete in order, so the prologue waits only for these
+    // (L2-resident) and not for the weight loads queued behind them.
+    constexpr int PRE = 2;   // chunks of x and gamma per thread fetched up front
+    u32x4 xr[MR][4];         // this thread's activation slice (32 values per row m)
+    u32x4 xv[PRE][MR], gv[PRE];
+    if (A.gamma) {
+#pragma unroll
+        for (int k = 0; k < PRE; ++k) {
+            const uint32_t i = min(t + k * nt, K8 - 1);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) xv[k][m] = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[i];
+            gv[k] = reinterpret_cast<const u32x4*>(A.gamma)[i];
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                xr[m][c] = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[p * 4 + c];
+    }
+
+    // Residual of this thread's first epilogue row, fetched now so the epilogue does not
+    // wait on a fresh global load (16-lane group grp writes output grp first).
+    const uint32_t grp = t >> 4, gl = t & 15, ngrp = nt >> 4;
+    const uint32_t n_out_wg = A.swiglu ? RB / 2 : RB, out0 = A.swiglu ? r0 / 2 : r0;
+    uint16_t res0[MR];
+    if (A.res) {
+        const uint32_t j = grp < n_out_wg ? grp : 0u;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) res0[m] = __builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + out0 + j]);
+    } else {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) res0[m] = 0;
+    }
+
     u32x4 wa[U], wb[U];
     uint16_t sa[U], sb[U];
     load_batch(0, wa, sa);
 
-    // Residual of this thread's first epilogue row, fetched now (behind the weights) so
-    // the epilogue does not wait on a fresh global load.
-    const uint32_t grp = t >> 4, gl = t & 15, ngrp = nt >> 4;
-    const uint32_t n_out_wg = A.swiglu ? RB / 2 : RB, out0 = A.swiglu ? r0 / 2 : r0;
-    uint16_t res0[MR];
-#pragma unroll
-    for (int m = 0; m < MR; ++m)
-        res0[m] = (A.res && gl == 0 && grp < n_out_wg)
-                      ? __builtin_bit_cast(uint16_t, A.res[(size_t)m * A.ldr + out0 + grp]) : (uint16_t)0;
-
-    // This thread's activation slice (32 values per row m), raw or RMS-normalized.
-    u32x4 xr[MR][4];
     if (A.gamma) {
         // RMSNorm prologue, cooperative: sum of squares in double (as RMSNORM2_F16), then
-        // h = f16(x / rms * gamma + 0) for the whole row into LDS. The first two chunks
-        // of x and gamma per thread are loaded before any wait.
-        constexpr int PRE = 2;
-        u32x4 xv[PRE][MR], gv[PRE];
-#pragma unroll
-        for (int k = 0; k < PRE; ++k) {
-            const uint32_t i = t + k * nt;
-            if (i < K8) {
-#pragma unroll
-                for (int m = 0; m < MR; ++m) xv[k][m] = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[i];
-                gv[k] = reinterpret_cast<const u32x4*>(A.gamma)[i];
-            }
-        }
+        // h = f16(x / rms * gamma + 0) for the whole row into LDS.
         auto chunk_x = [&](int k, uint32_t i, int m) -> u32x4 {
             return k < PRE ? xv[k][m] : reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[i];
         };
@@ -204,12 +216,6 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) xr[m][c] = xn[m * K8 + p * 4 + c];
         __syncthreads();   // red is reused for the partial sums below
-    } else {
-#pragma unroll
-        for (int m = 0; m < MR; ++m)
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-                xr[m][c] = reinterpret_cast<const u32x4*>(A.x + (size_t)m * A.ldx)[p * 4 + c];
     }
 
     // Pair order of dequant_word: (x0,x4) (x1,x5) (x2,x6) (x3,x7) per 8-value word.
