@@ -3,11 +3,15 @@
 // Weight format (OP_MATMUL_W4G_F16): wq row n = K/2 bytes, byte j holds k=2j in the
 // low nibble and k=2j+1 in the high nibble, stored as q+8; ws[n][k/64] fp16.
 // Dequant is fp16(q*s), RNE — computed as two exact packed-fp16 steps:
-//   h = half(0x6400 | nib) = 1024 + nib;  q = h - 1032 (exact);  w = q * s (one RNE).
+//   h = half(magic | nibble bits) = base + nib;  q = h - (base + 8) (exact);  w = q * s
+// (one RNE). A nibble in mantissa bits 0-3 takes magic 0x6400 (base 1024, ulp 1); one
+// in bits 4-7 takes 0x5400 (base 64, ulp 1/16), so it needs no shift.
 //
-// One 32-bit word of weights = 8 consecutive k. Masking (w >> 4i) & 0x000F000F gives
-// the half pairs (k0,k4), (k1,k5), (k2,k6), (k3,k7); activations are staged in the
-// same pair order so each pair feeds one v_dot2_f32_f16 (fp32 accumulate).
+// One 32-bit word of weights = 8 consecutive k. With w8 = w >> 8, masking w and w8
+// with 0x000F000F and 0x00F000F0 gives the half pairs (k0,k4), (k1,k5), (k2,k6),
+// (k3,k7); activations are staged in the same pair order so each pair feeds one
+// v_dot2_f32_f16 (fp32 accumulate).
+#include "dev_reduce.h"
 #include "kernels.h"
 
 #include <algorithm>
@@ -25,25 +29,26 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 __device__ __forceinline__ uint32_t as_u32(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
-// (w & 0x000F000F) | 0x64006400 in one VALU op. Written out because with both
-// constants as literals the compiler emits a separate AND and OR (gfx9 VOP3 takes no
-// literal, so the OR constant is passed in a VGPR).
+// (w & mask) | magic in one VALU op. Written out because with both constants as
+// literals the compiler emits a separate AND and OR (gfx9 VOP3 takes no literal, so
+// the mask goes in an SGPR and the magic in a VGPR).
+template <uint32_t MASK>
 __device__ __forceinline__ uint32_t nib_magic(uint32_t w, uint32_t magic) {
     uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(0x000F000Fu), "v"(magic));
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(MASK), "v"(magic));
     return r;
 }
 
 // Four dequantized pairs (k0,k4),(k1,k5),(k2,k6),(k3,k7) of one weight word.
 __device__ __forceinline__ void dequant_word(uint32_t w, h2_t s2, h2_t out[4]) {
-    const h2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
-    const uint32_t magic = 0x64006400u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t m = nib_magic(w >> (4 * i), magic);
-        const h2_t q = as_h2(m) - bias;   // exact: integers below 2048
-        out[i] = q * s2;                  // one RNE rounding: fp16(q*s)
-    }
+    const h2_t b_lo = {(_Float16)1032.0f, (_Float16)1032.0f};   // 1024 + 8
+    const h2_t b_hi = {(_Float16)72.0f, (_Float16)72.0f};       // 64 + 8
+    const uint32_t w8 = w >> 8;
+    // q = h - bias is exact (small integers); q * s is the one RNE rounding: fp16(q*s)
+    out[0] = (as_h2(nib_magic<0x000F000Fu>(w, 0x64006400u)) - b_lo) * s2;
+    out[1] = (as_h2(nib_magic<0x00F000F0u>(w, 0x54005400u)) - b_hi) * s2;
+    out[2] = (as_h2(nib_magic<0x000F000Fu>(w8, 0x64006400u)) - b_lo) * s2;
+    out[3] = (as_h2(nib_magic<0x00F000F0u>(w8, 0x54005400u)) - b_hi) * s2;
 }
 
 // ---------------------------------------------------------------------------
@@ -62,37 +67,25 @@ struct GemvArgs {
     __half* y;
     uint32_t ldy;
     uint32_t N, K, P, R, np;
+    uint32_t red_floats;   // size of the partials region; normalized rows follow it
     const __half* gamma;
     const __half* res;
     uint32_t ldr;
     int swiglu;
 };
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t f2hb(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
-
-__device__ __forceinline__ float sum16(float v) {   // over aligned groups of 16 lanes
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 4, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 1, 64);
-    return v;
-}
 
 constexpr int kGemvU = 4;   // passes per load batch
 
 template <int MR>
 __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
     constexpr int U = kGemvU;
-    extern __shared__ __align__(16) float red[];   // [np][MR][nt] partials; earlier [MR][K] halves
+    // Dynamic LDS: red = [np][MR][nt] pass partials, then (with gamma) the normalized
+    // rows [MR][K] halves at a 16-byte aligned offset.
+    extern __shared__ __align__(16) float red[];
     __shared__ double s_ss[8][MR];
-    __shared__ float s_rms[MR];
     const uint32_t nt = blockDim.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t P = A.P, R = A.R;
     const uint32_t p = t % P, rr = t / P;
@@ -181,28 +174,39 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
         }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            const double w = wave_sum_d(ss[m]);
+            const double w = dev::wave_sum(ss[m]);
             if (lane == 0) s_ss[wave][m] = w;
         }
         __syncthreads();
-        if (t < MR) {
+        // Every thread adds the wave sums itself (same order everywhere), so no second
+        // barrier is needed. x / rms is computed as Markstein's correction of x * y with
+        // y = RN(1/rms): q = RN(x*y), r = fma(-q, rms, x) (exact), RN(q + r*y) — the
+        // correctly rounded quotient, checked against IEEE division for every finite
+        // fp16 x over thousands of divisors (signed zeros aside, which the + 0 below
+        // maps to +0 either way).
+        float rms[MR], rcp[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
             double tot = 0.0;
-            for (uint32_t w = 0; w < nt / 64; ++w) tot += s_ss[w][t];
-            s_rms[t] = (float)sqrt(tot / (double)A.K + 1e-6);
+            for (uint32_t w = 0; w < nt / 64; ++w) tot += s_ss[w][m];
+            rms[m] = (float)sqrt(tot / (double)A.K + 1e-6);
+            rcp[m] = __fdiv_rn(1.0f, rms[m]);
         }
-        __syncthreads();
-        u32x4* xn = reinterpret_cast<u32x4*>(red);
+        auto div_rms = [&](float a, int m) {
+            const float q = a * rcp[m];
+            return __builtin_fmaf(__builtin_fmaf(-q, rms[m], a), rcp[m], q);
+        };
+        u32x4* xn = reinterpret_cast<u32x4*>(red + A.red_floats);
         for (uint32_t k = 0, i = t; i < K8; ++k, i += nt) {
             const u32x4 g4 = k < PRE ? gv[k] : reinterpret_cast<const u32x4*>(A.gamma)[i];
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 const u32x4 v = chunk_x((int)min(k, (uint32_t)PRE), i, m);
-                const float rms = s_rms[m];
                 u32x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float lo = __fdiv_rn(h2f((uint16_t)(v[e] & 0xFFFFu)), rms);
-                    float hi = __fdiv_rn(h2f((uint16_t)(v[e] >> 16)), rms);
+                    float lo = div_rms(h2f((uint16_t)(v[e] & 0xFFFFu)), m);
+                    float hi = div_rms(h2f((uint16_t)(v[e] >> 16)), m);
                     lo = __fadd_rn(__fmul_rn(lo, h2f((uint16_t)(g4[e] & 0xFFFFu))), 0.0f);
                     hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(g4[e] >> 16))), 0.0f);
                     o[e] = (uint32_t)f2hb(lo) | ((uint32_t)f2hb(hi) << 16);
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
         for (int m = 0; m < MR; ++m)
 #pragma unroll
             for (int c = 0; c < 4; ++c) xr[m][c] = xn[m * K8 + p * 4 + c];
-        __syncthreads();   // red is reused for the partial sums below
+        if (A.red_floats == 0) __syncthreads();   // xn shares LDS with red
     }
 
     // Pair order of dequant_word: (x0,x4) (x1,x5) (x2,x6) (x3,x7) per 8-value word.
@@ -279,7 +283,7 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
             for (int m = 0; m < MR; ++m) {
                 float s = 0.0f;
                 for (uint32_t k = gl; k < P; k += 16) s += red[(i * MR + m) * nt + base + k];
-                s = sum16(s);
+                s = dev::row_sum16(s);
                 if (gl == 0) {
                     uint16_t v = f2hb(s);
                     if (A.res) v = f2hb(__fadd_rn(h2f(v), res_at(m, lr)));
@@ -299,8 +303,8 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                     sg += red[(ig * MR + m) * nt + bg + k];
                     su += red[(iu * MR + m) * nt + bu + k];
                 }
-                sg = sum16(sg);
-                su = sum16(su);
+                sg = dev::row_sum16(sg);
+                su = dev::row_sum16(su);
                 if (gl == 0) {
                     const float gv = h2f(f2hb(sg)), uv = h2f(f2hb(su));
                     const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
@@ -522,10 +526,15 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
     const uint32_t np_max = std::max(1u, 8192u / (M * pl.nt));
     np = std::max(1u, std::min(np, np_max));
     if (epi.swiglu && ((pl.R * np) & 1)) ++np;   // gate/up pairs never straddle workgroups
-    size_t lds = (size_t)np * M * pl.nt * 4;
-    if (epi.gamma) lds = std::max(lds, (size_t)M * K * 2);
+    // Normalized rows after the partials when both fit in 64 KiB; otherwise they share
+    // the start of LDS (red_floats = 0) and the kernel adds a barrier between them.
+    const size_t red_b = ((size_t)np * M * pl.nt * 4 + 15) & ~(size_t)15;
+    const size_t xn_b = epi.gamma ? (size_t)M * K * 2 : 0;
+    const bool split = red_b + xn_b <= 65536;
+    const size_t lds = split ? red_b + xn_b : std::max(red_b, xn_b);
     const uint32_t grid = (N + pl.R * np - 1) / (pl.R * np);
-    GemvArgs A{x, ldx, wq, ws, y, ldy, N, K, pl.P, pl.R, np, epi.gamma, epi.res, epi.ldr, epi.swiglu ? 1 : 0};
+    GemvArgs A{x, ldx, wq, ws, y, ldy, N, K, pl.P, pl.R, np, split ? (uint32_t)(red_b / 4) : 0u,
+               epi.gamma, epi.res, epi.ldr, epi.swiglu ? 1 : 0};
     const dim3 g3(grid), b3(pl.nt);
     switch (M) {
     case 1: hipLaunchKernelGGL(w4g_gemv_kernel<1>, g3, b3, lds, st, A); break;
