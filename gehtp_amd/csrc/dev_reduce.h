@@ -40,6 +40,19 @@ __device__ __forceinline__ T row_sum16(T v) {
     return v;
 }
 
+template <typename T>
+__device__ __forceinline__ T row_max16(T v) {
+    v = fmax(v, dpp<kDppQuadSwap1>(v));
+    v = fmax(v, dpp<kDppQuadSwap2>(v));
+    v = fmax(v, dpp<kDppRowHalfMirror>(v));
+    v = fmax(v, dpp<kDppRowMirror>(v));
+    return v;
+}
+
+__device__ __forceinline__ float read_lane(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
 __device__ __forceinline__ double read_lane(double v, int lane) {
     const uint64_t b = __builtin_bit_cast(uint64_t, v);
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
@@ -47,11 +60,41 @@ __device__ __forceinline__ double read_lane(double v, int lane) {
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
-// Sum of all 64 lanes, the same value in every lane: 16-lane sums, then the four group
-// sums added in lane order.
-__device__ __forceinline__ double wave_sum(double v) {
+// Sum / max of all 64 lanes, the same value in every lane: 16-lane reductions, then
+// the four group results combined in lane order.
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
     v = row_sum16(v);
     return ((read_lane(v, 0) + read_lane(v, 16)) + read_lane(v, 32)) + read_lane(v, 48);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = row_max16(v);
+    return fmaxf(fmaxf(read_lane(v, 0), read_lane(v, 16)), fmaxf(read_lane(v, 32), read_lane(v, 48)));
+}
+
+// v[l] + v[l^16] + v[l^32] + v[l^48] in every lane: the same position in the four
+// 16-lane rows, summed with gfx950's row swaps (v_permlane32_swap: lanes 32-63 of the
+// first operand trade with lanes 0-31 of the second; v_permlane16_swap: odd rows of the
+// first trade with even rows of the second). With two copies of v as the operands,
+// each lane ends up holding its partner's value in one of them. Written as inline asm
+// with both registers read-write: the compiler builtin, given one value for both
+// operands, treats its two results as equal and drops the partner. The s_nop covers
+// the VALU-write -> permlane-read hazard, as the compiler's own lowering does.
+__device__ __forceinline__ void permlane32_swap(uint32_t& a, uint32_t& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane16_swap(uint32_t& a, uint32_t& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float cross_row_sum(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    permlane32_swap(a, b);
+    v = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+    a = __builtin_bit_cast(uint32_t, v);
+    b = a;
+    permlane16_swap(a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
 
 }  // namespace dev

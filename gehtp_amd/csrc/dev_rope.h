@@ -7,6 +7,8 @@
 
 #include <cstdint>
 
+#include "dev_reduce.h"
+
 namespace gehtp {
 namespace dev {
 
@@ -51,14 +53,22 @@ __device__ __forceinline__ void rope_cs(uint32_t pos, uint32_t i, float theta, f
 // h = RMSNORM2_F16(x, gamma, zero bias) (squares summed in double), then the RoPE
 // chain y_l = f16(f16(h_l c) + f16(-h_{l+64} s)), y_{l+64} = f16(f16(h_{l+64} c) + f16(h_l s)).
 // Every lane of the wavefront must call it (cross-lane sum).
+// x / rms is RN(x * y) corrected once with y = RN(1 / rms) (Markstein): q = RN(x * y),
+// r = fma(-q, rms, x) (exact), RN(q + r * y) — the correctly rounded quotient, the same
+// as IEEE division for every finite fp16 x (a signed zero may differ, which the + 0
+// below maps to +0 either way).
+__device__ __forceinline__ float div_markstein(float a, float b, float y) {
+    const float q = a * y;
+    return __builtin_fmaf(__builtin_fmaf(-q, b, a), y, q);
+}
+
 __device__ __forceinline__ void head_norm_rope(float x1, float x2, float g1, float g2, float c, float s,
                                                float& y1, float& y2) {
-    double ss = (double)x1 * (double)x1 + (double)x2 * (double)x2;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const double ss = wave_sum((double)x1 * (double)x1 + (double)x2 * (double)x2);
     const float rms = (float)sqrt(ss / 128.0 + 1e-6);
-    const float h1 = rne_f16(__fadd_rn(__fmul_rn(__fdiv_rn(x1, rms), g1), 0.0f));
-    const float h2 = rne_f16(__fadd_rn(__fmul_rn(__fdiv_rn(x2, rms), g2), 0.0f));
+    const float y = __fdiv_rn(1.0f, rms);
+    const float h1 = rne_f16(__fadd_rn(__fmul_rn(div_markstein(x1, rms, y), g1), 0.0f));
+    const float h2 = rne_f16(__fadd_rn(__fmul_rn(div_markstein(x2, rms, y), g2), 0.0f));
     const float a1 = rne_f16(__fmul_rn(h1, c)), b1 = rne_f16(__fmul_rn(-h2, s));
     const float a2 = rne_f16(__fmul_rn(h2, c)), b2 = rne_f16(__fmul_rn(h1, s));
     y1 = rne_f16(__fadd_rn(a1, b1));

@@ -7,6 +7,7 @@
 // O^T = V^T . P^T reuses P straight from the accumulator registers as the MFMA B
 // operand; V is staged transposed in LDS so the A operand reads 8-byte runs.
 #include "kernels.h"
+#include "dev_reduce.h"
 #include "dev_rope.h"
 
 #include <cmath>
@@ -282,10 +283,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 a = __builtin_amdgcn_fdot2(as_h2(kv4[it][e]), as_h2(qv[r][e]), a, false);
-            a += __shfl_xor(a, 8, 64);
-            a += __shfl_xor(a, 4, 64);
-            a += __shfl_xor(a, 2, 64);
-            a += __shfl_xor(a, 1, 64);
+            a = dev::row_sum16(a);   // the 16 lanes of a key form one DPP row
             if (ch == 0) sc[r][kl] = valid ? a * A.scale_log2 : -INFINITY;
         }
     }
@@ -295,13 +293,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     float* wchunk = A.part + ((size_t)g * A.max_chunks + c) * REP * PS;
     for (uint32_t r = wave; r < REP; r += 4) {
         const float x = sc[r][lane];
-        float m = x;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        const float m = dev::wave_max(x);
         const float p = exp2f(x - m);
-        float l = p;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
+        const float l = dev::wave_sum(p);
         sc[r][lane] = p;
         if (lane == 0) { wchunk[r * PS + HD] = m; wchunk[r * PS + HD + 1] = l; }
     }
@@ -334,12 +328,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
 #pragma unroll
     for (int r = 0; r < REP; ++r)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float a = acc[r][e];
-            a += __shfl_xor(a, 16, 64);
-            a += __shfl_xor(a, 32, 64);
-            acc[r][e] = a;
-        }
+        for (int e = 0; e < 8; ++e) acc[r][e] = dev::cross_row_sum(acc[r][e]);
     if (lane < 16) {
 #pragma unroll
         for (int r = 0; r < REP; ++r)
@@ -359,58 +348,60 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
 }
 
 // Decode, pass 2: one workgroup per query head h = g*rep + r merges its chunks:
-// M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c - M) / L.
-// Thread (grp, d4) sums chunks grp, grp+8, ... of dims 4*d4..4*d4+3 (float4 loads).
+// M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c - M) / L, in one pass:
+// thread (grp, d4) merges chunks grp, grp+8, ... of dims 4*d4..4*d4+3 online (running
+// max, rescaling its sums when the max grows), then the 8 groups are merged in LDS.
 // With `advance`, n_kv = *count + 1 and the last workgroup to finish increments the
 // counter (every workgroup has read it by then) and re-arms the completion counter.
 __global__ __launch_bounds__(256) void attn_merge_kernel(
     const float* __restrict__ part, uint32_t* __restrict__ done, uint32_t n_kv_host,
     uint32_t* __restrict__ count, int advance, uint32_t rep, uint32_t max_chunks, __half* __restrict__ out) {
-    __shared__ float s_red[4];
     __shared__ __align__(16) float4 s_o[256];
+    __shared__ float s_m[8], s_l[8];
     const uint32_t n_kv = count ? *count + (advance ? 1u : 0u) : n_kv_host;
     const uint32_t nc = (n_kv + DC - 1) / DC;
     const uint32_t h = blockIdx.x, g = h / rep, r = h % rep;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x;
     const float* base = part + ((size_t)g * max_chunks * rep + r) * PS;   // chunk c at + c*rep*PS
     const size_t cstride = (size_t)rep * PS;
 
-    float M = -INFINITY;
-    for (uint32_t c = tid; c < nc; c += 256) M = fmaxf(M, base[c * cstride + HD]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    if (lane == 0) s_red[wave] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    __syncthreads();
-    float L = 0.0f;
-    for (uint32_t c = tid; c < nc; c += 256) {
-        const float* w = base + c * cstride;
-        L += w[HD + 1] * exp2f(w[HD] - M);
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
-    if (lane == 0) s_red[wave] = L;
-
     const uint32_t d4 = tid & 31, grp = tid >> 5;
+    float mg = -INFINITY, lg = 0.0f;
     float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 4
     for (uint32_t c = grp; c < nc; c += 8) {
         const float* w = base + c * cstride;
-        const float wt = exp2f(w[HD] - M);
+        const float mc = w[HD], lc = w[HD + 1];
         const float4 v = *reinterpret_cast<const float4*>(w + 4 * d4);
+        if (mc > mg) {   // 2^-inf = 0 on the first chunk
+            const float sc = exp2f(mg - mc);
+            o.x *= sc; o.y *= sc; o.z *= sc; o.w *= sc;
+            lg *= sc;
+            mg = mc;
+        }
+        const float wt = exp2f(mc - mg);
         o.x = fmaf(wt, v.x, o.x);
         o.y = fmaf(wt, v.y, o.y);
         o.z = fmaf(wt, v.z, o.z);
         o.w = fmaf(wt, v.w, o.w);
+        lg = fmaf(wt, lc, lg);
     }
     s_o[tid] = o;
+    if (d4 == 0) { s_m[grp] = mg; s_l[grp] = lg; }
     __syncthreads();
     if (tid < 32) {
-        L = s_red[0] + s_red[1] + s_red[2] + s_red[3];
-        for (uint32_t k = 1; k < 8; ++k) {
+        float M = s_m[0];
+        for (uint32_t k = 1; k < 8; ++k) M = fmaxf(M, s_m[k]);
+        float L = 0.0f;
+        o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (uint32_t k = 0; k < 8; ++k) {
+            const float wk = exp2f(s_m[k] - M);   // 0 for a group without chunks
             const float4 p = s_o[tid + 32 * k];
-            o.x += p.x; o.y += p.y; o.z += p.z; o.w += p.w;
+            o.x = fmaf(wk, p.x, o.x);
+            o.y = fmaf(wk, p.y, o.y);
+            o.z = fmaf(wk, p.z, o.z);
+            o.w = fmaf(wk, p.w, o.w);
+            L = fmaf(wk, s_l[k], L);
         }
         h4_t hv = {(_Float16)(L > 0.0f ? o.x / L : 0.0f), (_Float16)(L > 0.0f ? o.y / L : 0.0f),
                    (_Float16)(L > 0.0f ? o.z / L : 0.0f), (_Float16)(L > 0.0f ? o.w / L : 0.0f)};
