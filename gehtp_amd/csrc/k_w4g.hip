@@ -347,48 +347,65 @@ __global__ __launch_bounds__(256) void w4g_dequant_kernel(const uint4* __restric
 
 // ---------------------------------------------------------------------------
 // Prefill GEMM: C[M,N] = A[M,K] . dequant(W)^T on v_mfma_f32_32x32x16_f16.
-// Workgroup tile (64*WM)x128, K step BKT (64 = one scale group), WM x 2 waves, each
-// wave 64x64 = 2x2 MFMA tiles; the launcher uses WM = 2 (larger M tiles, which cut
-// the dequant work per MFMA, measured no faster at the 4B-class shapes). A and the dequantized W tile are staged in LDS with
-// a 16-byte row pad; the next K step's global loads are issued before the MFMAs.
-constexpr int BN = 128;
+// Workgroup tile 128x128, K step 64 (one scale group), 4 waves in a 2x2 layout, each
+// wave 64x64 = 2x2 MFMA tiles. Software pipeline: global loads run two K steps ahead
+// in two register stages, and A plus the dequantized W tile go to a double-buffered
+// LDS stage (16-byte row pad), so a K step has one barrier: MFMAs on stage k, then
+// stage k+1 from registers into the other LDS buffer, then the barrier.
+// Loads are unconditional with clamped rows (rows past M or N are computed, never
+// stored), which keeps the compiler from waiting on each load in turn.
+constexpr int GB_M = 128, GB_N = 128, GB_K = 64, GB_LDS = GB_K + 8;
 
-template <int BKT, int WM>
-__global__ __launch_bounds__(128 * WM) void w4g_gemm_kernel(
+__global__ __launch_bounds__(256) void w4g_gemm_kernel(
     const __half* __restrict__ a, uint32_t lda, const uint4* __restrict__ wq,
     const __half* __restrict__ ws, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
     uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu) {
-    constexpr int NT = 128 * WM, BM = 64 * WM;     // waves: WM along M x 2 along N
-    constexpr int LDS_STRIDE = BKT + 8;            // halves; 16-byte pad per row
-    constexpr int AP = BKT / 8;                    // 16-byte A pieces per row
-    constexpr int CA = BM * AP / NT;               // A pieces per thread
-    constexpr int WP = BKT / 32;                   // 16-byte W pieces (32 weights) per row
-    constexpr int CW = (BN * WP + NT - 1) / NT;    // W pieces per thread (some threads idle)
-    __shared__ __align__(16) _Float16 As[BM * LDS_STRIDE];
-    __shared__ __align__(16) _Float16 Bs[BN * LDS_STRIDE];
+    constexpr int AP = GB_K / 8;             // 16-byte A pieces per row
+    constexpr int CA = GB_M * AP / 256;      // A pieces per thread
+    __shared__ __align__(16) _Float16 As[2][GB_M * GB_LDS];
+    __shared__ __align__(16) _Float16 Bs[2][GB_N * GB_LDS];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const uint32_t G = K / 64, nsteps = K / BKT;
+    const uint32_t m0 = blockIdx.y * GB_M, n0 = blockIdx.x * GB_N;
+    const uint32_t G = K / 64, nsteps = K / GB_K;
+    const uint32_t wr = tid >> 1, wh = tid & 1;          // W piece: tile row, half
+    const size_t wrow = min(n0 + wr, N - 1);
 
-    uint4 ra[CA], rw[CW];
-    __half rs[CW];
-    auto load_k = [&](uint32_t kb) {
+    // A register stage holds this thread's 16-byte pieces of the A tile, 32 weights
+    // (half a row of the W tile) and their scale.
+    // Stage st in registers (st is a literal at every call, so the arrays stay in VGPRs;
+    // native vectors, not HIP's uint4 struct, whose copies lower to memcpy through
+    // private memory).
+    u32x4 ra[2][CA], rw[2];
+    uint16_t rs[2];
+    auto load = [&](int st, uint32_t kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < CA; ++i) {
-            const uint32_t c = tid + NT * i, r = m0 + c / AP;
-            ra[i] = r < M ? *reinterpret_cast<const uint4*>(a + (size_t)r * lda + kb * BKT + (c % AP) * 8)
-                          : make_uint4(0, 0, 0, 0);
+            const uint32_t c = tid + 256u * i;
+            const size_t r = min(m0 + c / AP, M - 1);
+            ra[st][i] = *reinterpret_cast<const u32x4*>(a + r * lda + kb * GB_K + (c % AP) * 8);
         }
+        rw[st] = reinterpret_cast<const u32x4*>(wq)[wrow * (K / 32) + kb * 2 + wh];
+        rs[st] = __builtin_bit_cast(uint16_t, ws[wrow * G + kb]);
+    };
+    auto store = [&](int st, int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < CW; ++i) {
-            const uint32_t c = tid + NT * i, n = n0 + c / WP, q = c % WP;
-            if (c < BN * WP && n < N) {
-                rw[i] = wq[(size_t)n * (K / 32) + kb * WP + q];
-                rs[i] = ws[(size_t)n * G + kb * (BKT / 64) + q / 2];
-            } else {
-                rw[i] = make_uint4(0, 0, 0, 0);
-                rs[i] = __float2half(0.0f);
-            }
+        for (int i = 0; i < CA; ++i) {
+            const uint32_t c = tid + 256u * i;
+            *reinterpret_cast<u32x4*>(&As[buf][(c / AP) * GB_LDS + (c % AP) * 8]) = ra[st][i];
+        }
+        const _Float16 sh = __builtin_bit_cast(_Float16, rs[st]);
+        const h2_t s2 = {sh, sh};
+        const uint32_t words[4] = {rw[st][0], rw[st][1], rw[st][2], rw[st][3]};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            h2_t d[4];
+            dequant_word(words[q], s2, d);
+            uint4 o;   // pair order (k0,k4)(k1,k5)(k2,k6)(k3,k7) back to k0..k7
+            o.x = __builtin_amdgcn_perm(as_u32(d[1]), as_u32(d[0]), 0x05040100u);
+            o.y = __builtin_amdgcn_perm(as_u32(d[3]), as_u32(d[2]), 0x05040100u);
+            o.z = __builtin_amdgcn_perm(as_u32(d[1]), as_u32(d[0]), 0x07060302u);
+            o.w = __builtin_amdgcn_perm(as_u32(d[3]), as_u32(d[2]), 0x07060302u);
+            *reinterpret_cast<uint4*>(&Bs[buf][wr * GB_LDS + wh * 32 + q * 8]) = o;
         }
     };
 
@@ -401,52 +418,52 @@ __global__ __launch_bounds__(128 * WM) void w4g_gemm_kernel(
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     const uint32_t wm = wave >> 1, wn = wave & 1;
-    load_k(0);
-    for (uint32_t kb = 0; kb < nsteps; ++kb) {
+    auto mfma = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            const uint32_t c = tid + NT * i;
-            *reinterpret_cast<uint4*>(&As[(c / AP) * LDS_STRIDE + (c % AP) * 8]) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < CW; ++i) {
-            const uint32_t c = tid + NT * i;
-            if (c >= BN * WP) continue;
-            const _Float16 s = __builtin_bit_cast(_Float16, rs[i]);
-            const h2_t s2 = {s, s};
-            const uint32_t words[4] = {rw[i].x, rw[i].y, rw[i].z, rw[i].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                h2_t d[4];
-                dequant_word(words[q], s2, d);
-                uint4 o;   // pair order (k0,k4)(k1,k5)(k2,k6)(k3,k7) back to k0..k7
-                o.x = __builtin_amdgcn_perm(as_u32(d[1]), as_u32(d[0]), 0x05040100u);
-                o.y = __builtin_amdgcn_perm(as_u32(d[3]), as_u32(d[2]), 0x05040100u);
-                o.z = __builtin_amdgcn_perm(as_u32(d[1]), as_u32(d[0]), 0x07060302u);
-                o.w = __builtin_amdgcn_perm(as_u32(d[3]), as_u32(d[2]), 0x07060302u);
-                *reinterpret_cast<uint4*>(&Bs[(c / WP) * LDS_STRIDE + (c % WP) * 32 + q * 8]) = o;
-            }
-        }
-        __syncthreads();
-        if (kb + 1 < nsteps) load_k(kb + 1);
-#pragma unroll
-        for (int kk = 0; kk < BKT / 16; ++kk) {
+        for (int kk = 0; kk < GB_K / 16; ++kk) {
             h8_t af[2], bf[2];
             const uint32_t kof = kk * 16 + 8 * (lane >> 5);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                af[i] = *reinterpret_cast<const h8_t*>(&As[(wm * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kof]);
+                af[i] = *reinterpret_cast<const h8_t*>(&As[buf][(wm * 64 + i * 32 + (lane & 31)) * GB_LDS + kof]);
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                bf[j] = *reinterpret_cast<const h8_t*>(&Bs[(wn * 64 + j * 32 + (lane & 31)) * LDS_STRIDE + kof]);
+                bf[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][(wn * 64 + j * 32 + (lane & 31)) * GB_LDS + kof]);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
+    };
+    // K steps in pairs, register stage 0 / LDS buffer 0 alternating with stage 1 / buffer 1:
+    // during the MFMAs on stage k, stage k+1 waits in registers and stage k+2 is being
+    // loaded. Nothing is conditional (past the end, the last stage is loaded and stored
+    // again, unread): a load under a branch makes the compiler wait for every
+    // outstanding load before the LDS stores.
+    const uint32_t last = nsteps - 1;
+    load(0, 0);
+    load(1, min(1u, last));
+    store(0, 0);
+    __syncthreads();
+    uint32_t kb = 0;
+    // sched_barrier keeps the scheduler from sinking the loads below the MFMAs and
+    // stores of the step (which would shorten the prefetch distance to one step).
+    for (; kb + 1 < nsteps; kb += 2) {
+        load(0, min(kb + 2, last));
+        __builtin_amdgcn_sched_barrier(0);
+        mfma(0);
+        __builtin_amdgcn_sched_barrier(0);
+        store(1, 1);
+        __syncthreads();
+        load(1, min(kb + 3, last));
+        __builtin_amdgcn_sched_barrier(0);
+        mfma(1);
+        __builtin_amdgcn_sched_barrier(0);
+        store(0, 0);
         __syncthreads();
     }
+    if (kb < nsteps) mfma(0);   // odd step count: the last stage is in buffer 0
 
     // Accumulator layout (32x32): lane l, reg r -> col l%32, row 8*(r/4) + 4*(l/32) + r%4.
     // With SwiGLU, columns 2c / 2c+1 (gate / up of output c) sit in lanes l, l^1.
@@ -551,7 +568,7 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
                            hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.gamma || (epi.swiglu && (N & 1))) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((w4g_gemm_kernel<64, 2>), dim3((N + BN - 1) / BN, (M + 127) / 128), dim3(256), 0, st, a, lda,
+    hipLaunchKernelGGL(w4g_gemm_kernel, dim3((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M), dim3(256), 0, st, a, lda,
                        reinterpret_cast<const uint4*>(wq), ws, y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0);
     return hipGetLastError();
 }
