@@ -819,6 +819,7 @@ int op_attn(Ctx& cx) {
     const float scale = f32_from_bits(A(8));
     if (hd != 128) return ERR("attn head_dim %u unsupported (128 only)", hd);
     if (!KVH || H % KVH) return ERR("attn heads %u not a multiple of kv heads %u", H, KVH);
+    if (!(scale > 0.0f && scale < INFINITY)) return ERR("attn scale %g must be positive and finite", scale);
     const __half* q = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
     const __half* k = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(1)));
     const __half* v = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(2)));

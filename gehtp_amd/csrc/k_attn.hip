@@ -31,16 +31,34 @@ constexpr int HD = 128;          // head dim this kernel is built for
 constexpr int QT = 128;          // queries per workgroup (4 waves x 32)
 constexpr int KT = 64;           // keys per LDS stage
 constexpr int KS = HD + 8;       // K tile row stride (halves)
-constexpr int VS = KT + 8;       // V^T tile row stride (halves)
+constexpr int VSR = HD + 16;     // V tile row stride (halves): 72 dwords, so the transposed
+                                 // 8-byte reads of one 16-lane group hit 32 distinct banks
 constexpr float kLog2e = 1.4426950408889634f;
 
+typedef short s4_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, output lane l receives
+// element l%4 of the 8-byte chunks addressed by lanes l/4, l/4+4, l/4+8, l/4+12.
+__device__ __forceinline__ u32x2 lds_read_tr16(const _Float16* p) {
+    const s4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s4_t*)(const_cast<_Float16*>(p)));
+    return __builtin_bit_cast(u32x2, r);
+}
+
+// Flash attention forward. A workgroup owns 128 queries of one head (wave w: queries
+// 32w..32w+31); per 64-key stage, K and V are staged row-major in LDS (the next stage's
+// loads are in flight during the compute). Scores are computed transposed,
+// S^T = K Q^T (MFMA A = K rows, B = Q^T held in registers), so each lane owns one query
+// and its 32 scores of a stage; the online-softmax statistics need one exchange with
+// lane l^32. O^T = V^T P^T: the V^T operand comes from the row-major V tile through the
+// transposing LDS read, P^T straight from the score registers.
 template <bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(
     const __half* __restrict__ q, uint32_t ldq, const __half* __restrict__ k,
     const __half* __restrict__ v, uint32_t ldkv, __half* __restrict__ out, uint32_t ldo,
     uint32_t S, uint32_t H, uint32_t KVH, float scale_log2) {
     __shared__ __align__(16) _Float16 Ks[KT * KS];
-    __shared__ __align__(16) _Float16 Vt[HD * VS];
+    __shared__ __align__(16) _Float16 Vs[KT * VSR];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t n_qt = (S + QT - 1) / QT;
     const uint32_t qtile = n_qt - 1 - blockIdx.x;      // heaviest causal tiles first
@@ -51,14 +69,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
     const uint32_t my_q = qw + (lane & 31);
     const uint32_t hl = lane >> 5;
 
-    // Q^T fragments (MFMA B operand): query my_q, dims 16*kk + 8*hl + [0,8).
+    // Q^T fragments (MFMA B operand): query my_q, dims 16*kk + 8*hl + [0,8). Queries past
+    // S read row S-1 (their outputs are not stored).
     h8_t qf[HD / 16];
+    {
+        const size_t qrow = min(my_q, S - 1);
 #pragma unroll
-    for (int kk = 0; kk < HD / 16; ++kk) {
-        if (my_q < S)
-            qf[kk] = *reinterpret_cast<const h8_t*>(q + (size_t)my_q * ldq + h * HD + kk * 16 + hl * 8);
-        else
-            qf[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        for (int kk = 0; kk < HD / 16; ++kk)
+            qf[kk] = *reinterpret_cast<const h8_t*>(q + qrow * ldq + h * HD + kk * 16 + hl * 8);
     }
 
     f16x_t o[HD / 32];
@@ -69,81 +87,120 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
     float m_run = -INFINITY, l_run = 0.0f;
 
     const uint32_t kend = CAUSAL ? min(S, q0 + QT) : S;
-    for (uint32_t kb = 0; kb < kend; kb += KT) {
-        __syncthreads();
-        // Stage K (row-major) and V (transposed) for keys [kb, kb+64).
+    // K and V rows of this thread's 4 keys (stage-local key (tid>>4) + 16i, dims 8*ch..).
+    // Loads are unconditional (keys past S read row S-1; their scores are masked).
+    const uint32_t ch = tid & 15;
+    u32x4 kv4[4], vv4[4];
+    auto load_kv = [&](uint32_t kb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t key = (tid >> 4) + 16 * i, ch = tid & 15;
-            u32x4 kv4 = {0, 0, 0, 0}, vv4 = {0, 0, 0, 0};
-            if (kb + key < S) {
-                const size_t off = (size_t)(kb + key) * ldkv + kvh * HD + ch * 8;
-                kv4 = *reinterpret_cast<const u32x4*>(k + off);
-                vv4 = *reinterpret_cast<const u32x4*>(v + off);
-            }
-            *reinterpret_cast<u32x4*>(&Ks[key * KS + ch * 8]) = kv4;
-            const _Float16* ve = reinterpret_cast<const _Float16*>(&vv4);
+            const uint32_t key = min(kb + (tid >> 4) + 16 * i, S - 1);
+            const size_t off = (size_t)key * ldkv + kvh * HD + ch * 8;
+            kv4[i] = *reinterpret_cast<const u32x4*>(k + off);
+            vv4[i] = *reinterpret_cast<const u32x4*>(v + off);
+        }
+    };
+    // This lane's address pattern for the transposed V reads (see lds_read_tr16): source
+    // row 4*hl + (lane%16)/4 (+ 16j, + 8 for the second half), column
+    // 16*((lane/16)%2) + 4*(lane%4) (+ 32*dt).
+    const uint32_t tr_row = 4 * hl + ((lane & 15) >> 2);
+    const uint32_t tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+    load_kv(0);
+    for (uint32_t kb = 0; kb < kend; kb += KT) {
+        __syncthreads();
 #pragma unroll
-            for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VS + key] = ve[e];
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t key = (tid >> 4) + 16 * i;
+            *reinterpret_cast<u32x4*>(&Ks[key * KS + ch * 8]) = kv4[i];
+            *reinterpret_cast<u32x4*>(&Vs[key * VSR + ch * 8]) = vv4[i];
         }
         __syncthreads();
+        load_kv(min(kb + KT, kend - 1));
+        if (CAUSAL && kb > qw + 31) continue;   // the whole stage is masked for this wave
 
+        // Scores of the stage's two 32-key halves: two independent MFMA chains, all K
+        // fragments read first.
+        f16x_t s0, s1;
 #pragma unroll
-        for (int sub = 0; sub < KT / 32; ++sub) {
-            const uint32_t kt0 = kb + sub * 32;
-            if (CAUSAL && kt0 > qw + 31) continue;   // whole 32x32 block masked for this wave
-            if (kt0 >= S) continue;
-            f16x_t s;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+        for (int r = 0; r < 16; ++r) { s0[r] = 0.0f; s1[r] = 0.0f; }
+        {
+            h8_t kf0[HD / 16], kf1[HD / 16];
 #pragma unroll
             for (int kk = 0; kk < HD / 16; ++kk) {
-                const h8_t kf = *reinterpret_cast<const h8_t*>(&Ks[(sub * 32 + (lane & 31)) * KS + kk * 16 + hl * 8]);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], s, 0, 0, 0);
+                kf0[kk] = *reinterpret_cast<const h8_t*>(&Ks[(lane & 31) * KS + kk * 16 + hl * 8]);
+                kf1[kk] = *reinterpret_cast<const h8_t*>(&Ks[(32 + (lane & 31)) * KS + kk * 16 + hl * 8]);
             }
-            // s[r]: key kt0 + 8*(r/4) + 4*hl + r%4, query my_q.
-            float mloc = -INFINITY;
+#pragma unroll
+            for (int kk = 0; kk < HD / 16; ++kk) {
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf0[kk], qf[kk], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf1[kk], qf[kk], s1, 0, 0, 0);
+            }
+        }
+        // s0[r] / s1[r]: key kb (+32) + 8*(r/4) + 4*hl + r%4, query my_q. Scores stay raw
+        // (the launcher guarantees scale > 0, so max commutes with the scaling); a stage
+        // wholly below the diagonal and inside S skips the mask (a wave-uniform test).
+        const bool full = kb + KT <= S && (!CAUSAL || kb + KT - 1 <= qw);
+        float mloc = -INFINITY;
+        if (full) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
+        } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t key = kt0 + 8 * (r >> 2) + 4 * hl + (r & 3);
-                float x = s[r] * scale_log2;
-                if (key >= S || (CAUSAL && key > my_q)) x = -INFINITY;
-                s[r] = x;
-                mloc = fmaxf(mloc, x);
+                const uint32_t key = kb + 8 * (r >> 2) + 4 * hl + (r & 3);
+                if (key >= S || (CAUSAL && key > my_q)) s0[r] = -INFINITY;
+                if (key + 32 >= S || (CAUSAL && key + 32 > my_q)) s1[r] = -INFINITY;
+                mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
             }
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-            const float m_new = fmaxf(m_run, mloc);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = exp2f(m_run - m_use);
-            float lsum = 0.0f;
-            h8_t pb[2];
+        }
+        {   // the other half of this query's keys sits in lane l ^ 32
+            uint32_t x0 = __builtin_bit_cast(uint32_t, mloc), x1 = x0;
+            dev::permlane32_swap(x0, x1);
+            mloc = fmaxf(__builtin_bit_cast(float, x0), __builtin_bit_cast(float, x1));
+        }
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float neg_ms = -m_use * scale_log2;
+        // v_exp_f32 directly: results below 2^-126 flush to 0, which a softmax weight can
+        // afford. p = 2^((s - m) * scale_log2) with the scaling folded into one fma.
+        const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, scale_log2, neg_ms));
+        float lsum = 0.0f;
+        // P^T operand j (keys 16j .. 16j+15 of the stage): k-slot i of lane-half hl holds
+        // key 16j + 8*(i/4) + 4*hl + i%4, i.e. score register 8*(j%2) + i of s0 / s1.
+        h8_t pb[4];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = exp2f(s[r] - m_use);
-                lsum += p;
-                pb[r >> 3][r & 7] = (_Float16)p;
-            }
-            lsum += __shfl_xor(lsum, 32, 64);
-            l_run = l_run * alpha + lsum;
-            m_run = m_new;
+        for (int r = 0; r < 16; ++r) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale_log2, neg_ms));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], scale_log2, neg_ms));
+            lsum += p0 + p1;
+            pb[r >> 3][r & 7] = (_Float16)p0;
+            pb[2 + (r >> 3)][r & 7] = (_Float16)p1;
+        }
+        {
+            uint32_t x0 = __builtin_bit_cast(uint32_t, lsum), x1 = x0;
+            dev::permlane32_swap(x0, x1);
+            lsum = __builtin_bit_cast(float, x0) + __builtin_bit_cast(float, x1);
+        }
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+        if (__any(alpha != 1.0f)) {   // no lane's max grew: nothing to rescale
 #pragma unroll
             for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-            // O^T[d][q] += sum_key V^T[d][key] P^T[key][q]. k-slot 8*hl+i of half j maps to
-            // key 16*j + 8*(i/4) + 4*hl + i%4 — the key held in pb[j][i].
+        }
+        // O^T[d][q] += sum_key V^T[d][key] P^T[key][q]: for each 32-dim block and each
+        // 16-key group j, two transposed reads give keys 16j + 4*hl + [0,4) and +8.
 #pragma unroll
-            for (int dt = 0; dt < HD / 32; ++dt) {
-                const uint32_t d = dt * 32 + (lane & 31);
+        for (int dt = 0; dt < HD / 32; ++dt) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint32_t kl = sub * 32 + 16 * j + 4 * hl;
-                    const u32x2 lo = *reinterpret_cast<const u32x2*>(&Vt[d * VS + kl]);
-                    const u32x2 hi = *reinterpret_cast<const u32x2*>(&Vt[d * VS + kl + 8]);
-                    const u32x4 packed = {lo[0], lo[1], hi[0], hi[1]};
-                    const h8_t vf = __builtin_bit_cast(h8_t, packed);
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[j], o[dt], 0, 0, 0);
-                }
+            for (int j = 0; j < 4; ++j) {
+                const _Float16* base = &Vs[(16 * j + tr_row) * VSR + 32 * dt + tr_col];
+                const u32x2 lo = lds_read_tr16(base);
+                const u32x2 hi = lds_read_tr16(base + 8 * VSR);
+                const u32x4 packed = {lo[0], lo[1], hi[0], hi[1]};
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, packed), pb[j], o[dt], 0, 0, 0);
             }
         }
     }
@@ -422,6 +479,7 @@ hipError_t launch_attn_prefill(const __half* q, uint32_t ldq, const __half* k, c
                                uint32_t KVH, uint32_t hd, float scale, bool causal,
                                hipStream_t st) {
     if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
+    if (!(scale > 0.0f && scale < INFINITY)) return hipErrorInvalidValue;   // the kernel's max needs scale > 0
     if (!S || !H) return hipSuccess;
     dim3 grid((S + QT - 1) / QT, H);
     const float sl2 = scale * kLog2e;

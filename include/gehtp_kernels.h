@@ -60,7 +60,8 @@ int gehtp_rmsnorm2(const void* x, const void* gamma, const void* beta, void* y, 
 /* OP_SOFTMAX_F16 (oplist_exec.c:1163-1194). */
 int gehtp_softmax(const void* x, void* y, uint32_t rows, uint32_t n, void* stream);
 
-/* Fused causal GQA attention (OP_ATTN_F16): q [S,H,128], k/v [S,KVH,128] -> out [S,H,128]. */
+/* Fused causal GQA attention (OP_ATTN_F16): q [S,H,128], k/v [S,KVH,128] -> out [S,H,128].
+ * scale > 0 and finite, else GEHTP_EINVAL. */
 int gehtp_attn_prefill(const void* q, const void* k, const void* v, void* out, uint32_t S,
                        uint32_t H, uint32_t KVH, uint32_t hd, float scale, int causal, void* stream);
 /* Decode attention (OP_ATTN_DECODE_F16) over positions [0, n_kv) of a KV ring of

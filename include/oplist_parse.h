@@ -113,7 +113,8 @@ enum {
     /* OP_ATTN_F16: fused causal GQA attention over a prefill chunk.
      *   args [q_ref, k_ref, v_ref, out_t, S, H, KVH, hd, scale_f32_bits, flags]
      *   q [S, H, hd], k/v [S, KVH, hd] token-major, out [S, H, hd].
-     *   flags bit0 = causal. q head h reads kv head h / (H / KVH).
+     *   flags bit0 = causal. q head h reads kv head h / (H / KVH). scale must be
+     *   positive and finite (the chain form below takes any scale).
      *   Replaces the runlist chain MATMUL_F16(batched) -> BINARY mul -> BINARY add
      *   (mask) -> SOFTMAX -> MATMUL_F16 (reference oplist_exec.c:1081-1194,1709-1813). */
     OP_ATTN_F16 = 41,
