@@ -46,6 +46,9 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the GEMV roofline replay + a 256 MiB copy (for PMC counter runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the two prefills (weight upload, then the timed one), for kernel traces "
+                         "and counter runs of the prefill kernels")
     return ap.parse_args()
 
 
@@ -114,6 +117,10 @@ def main() -> int:
     tok = int(np.frombuffer(out, np.int32)[0])
     logits = np.frombuffer(eng.temp(tp["logits"]), np.float16)[:cfg.vocab].astype(np.float32)
     top2 = np.sort(logits)[-2:]
+    if args.prefill_only:
+        print(json.dumps({"prefill_only": True, "prompt": S, "prefill_ms": round(t_prefill * 1e3, 2),
+                          "first_token": tok}), flush=True)
+        return 0
     log(f"prefill S={S}: {t_prefill * 1e3:.1f} ms, first token {tok}, logits finite "
         f"{np.isfinite(logits).all()}, max {top2[1]:.3f}, top-1 margin {top2[1] - top2[0]:.3f}")
     if not np.isfinite(logits).all():
