@@ -17,21 +17,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float h2f(__half h) { return __half2float(h); }
 __device__ __forceinline__ __half f2h(float f) { return __float2half(f); }   // RNE
 
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
+// Wave-wide reductions over DPP (dev_reduce.h); every lane gets the result.
+__device__ __forceinline__ float wave_sum_f(float v) { return dev::wave_sum(v); }
+__device__ __forceinline__ double wave_sum_d(double v) { return dev::wave_sum(v); }
+__device__ __forceinline__ float wave_max_f(float v) { return dev::wave_max(v); }
 
 using dev::f64_to_f16_bits;
 
@@ -69,10 +58,37 @@ __global__ __launch_bounds__(256) void rmsnorm2_kernel(const __half* __restrict_
     }
     acc = wave_sum_d(acc);
     const float rms = (float)sqrt(acc / (double)rw + 1e-6);
-    for (uint32_t i = lane; i < rw; i += 64) {
-        float v = __fdiv_rn(h2f(xr[i]), rms);
-        v = __fadd_rn(__fmul_rn(v, h2f(g[i])), b ? h2f(b[i]) : 0.0f);
-        yr[i] = f2h(v);
+    const float rcp = __fdiv_rn(1.0f, rms);   // x / rms via dev::div_markstein (exact)
+    const bool vec_out = vec && ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(b) |
+                                  reinterpret_cast<uintptr_t>(yr)) & 15u) == 0;
+    if (vec_out) {
+        for (uint32_t i = lane * 8; i < rw; i += 512) {
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(xr + i);
+            const u32x4 gv = *reinterpret_cast<const u32x4*>(g + i);
+            const u32x4 bv = b ? *reinterpret_cast<const u32x4*>(b + i) : u32x4{0u, 0u, 0u, 0u};
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const uint32_t sh = 16 * hh;
+                    const float xf = dev::bits_f((uint16_t)(xv[e] >> sh));
+                    const float q = dev::div_markstein(xf, rms, rcp);
+                    v[hh] = __fadd_rn(__fmul_rn(q, dev::bits_f((uint16_t)(gv[e] >> sh))),
+                                      dev::bits_f((uint16_t)(bv[e] >> sh)));
+                }
+                o[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[0]) |
+                       ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[1]) << 16);
+            }
+            *reinterpret_cast<u32x4*>(yr + i) = o;
+        }
+    } else {
+        for (uint32_t i = lane; i < rw; i += 64) {
+            float v = dev::div_markstein(h2f(xr[i]), rms, rcp);
+            v = __fadd_rn(__fmul_rn(v, h2f(g[i])), b ? h2f(b[i]) : 0.0f);
+            yr[i] = f2h(v);
+        }
     }
 }
 
