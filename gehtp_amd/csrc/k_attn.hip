@@ -53,7 +53,7 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const _Float16* p) {
 // lane l^32. O^T = V^T P^T: the V^T operand comes from the row-major V tile through the
 // transposing LDS read, P^T straight from the score registers.
 template <bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     const __half* __restrict__ q, uint32_t ldq, const __half* __restrict__ k,
     const __half* __restrict__ v, uint32_t ldkv, __half* __restrict__ out, uint32_t ldo,
     uint32_t S, uint32_t H, uint32_t KVH, float scale_log2) {
@@ -124,18 +124,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
         f16x_t s0, s1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) { s0[r] = 0.0f; s1[r] = 0.0f; }
-        {
-            h8_t kf0[HD / 16], kf1[HD / 16];
 #pragma unroll
-            for (int kk = 0; kk < HD / 16; ++kk) {
-                kf0[kk] = *reinterpret_cast<const h8_t*>(&Ks[(lane & 31) * KS + kk * 16 + hl * 8]);
-                kf1[kk] = *reinterpret_cast<const h8_t*>(&Ks[(32 + (lane & 31)) * KS + kk * 16 + hl * 8]);
-            }
-#pragma unroll
-            for (int kk = 0; kk < HD / 16; ++kk) {
-                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf0[kk], qf[kk], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf1[kk], qf[kk], s1, 0, 0, 0);
-            }
+        for (int kk = 0; kk < HD / 16; ++kk) {
+            const h8_t kf0 = *reinterpret_cast<const h8_t*>(&Ks[(lane & 31) * KS + kk * 16 + hl * 8]);
+            const h8_t kf1 = *reinterpret_cast<const h8_t*>(&Ks[(32 + (lane & 31)) * KS + kk * 16 + hl * 8]);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf0, qf[kk], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf1, qf[kk], s1, 0, 0, 0);
         }
         // s0[r] / s1[r]: key kb (+32) + 8*(r/4) + 4*hl + r%4, query my_q. Scores stay raw
         // (the launcher guarantees scale > 0, so max commutes with the scaling); a stage
