@@ -2,9 +2,10 @@
 
     python -m gehtp_amd.build        # or gehtp_amd.build.build()
 
-Objects go to gehtp_amd/_build/, the library to gehtp_amd/libgehtp.so. Every
-source is compiled on every call (the build is a correctness check as much as a
-build); the compile units run in parallel.
+Objects go to gehtp_amd/_build/, the library to gehtp_amd/libgehtp.so, and the
+resident decode server (host code over the library's C ABI) to
+gehtp_amd/gehtp_persistent. Every source is compiled on every call (the build is a
+correctness check as much as a build); the compile units run in parallel.
 """
 from __future__ import annotations
 
@@ -19,6 +20,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "_build"
 LIB = PKG / "libgehtp.so"
+SERVER = PKG / "gehtp_persistent"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -61,6 +63,13 @@ def build(verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    tmp = SERVER.with_name(SERVER.name + ".tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", f"-I{ROOT / 'include'}",
+           str(CSRC / "persistent.cpp"), f"-L{PKG}", "-lgehtp", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"server build failed\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, SERVER)
     return LIB
 
 

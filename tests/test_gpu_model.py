@@ -83,3 +83,46 @@ def test_decode_graph_replay_matches_direct(engine):
     assert c1 - c0 >= 1 and r1 - r0 >= 6, (c1 - c0, r1 - r0)
     for step, (a, b) in enumerate(zip(direct, graphed)):
         assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"step {step}"
+
+
+def test_persistent_server_decode_matches_engine(engine, tmp_path):
+    """Decode steps served by gehtp_persistent (a separate process holding the blob,
+    its weights and the KV states) give the same logits bits as the same blob run in
+    this process, and its token is the first maximum of those logits."""
+    from gehtp_amd.persistent import SERVER, PersistentRuntime
+    if not SERVER.exists():
+        pytest.skip("server not built")
+    cfg, steps = SMALL, 5
+    w = Weights(cfg, seed=11)
+    dec, td = emit_decode(cfg, w, 64)
+    blob = tmp_path / "decode.wtop"
+    blob.write_bytes(dec)
+    (tmp_path / "decode.weights.bin").write_bytes(w.image.tobytes())
+    emb = w.embed()
+    ids = np.random.default_rng(12).integers(0, cfg.vocab, steps)
+    bodies = [np.ascontiguousarray(emb[i]).tobytes() for i in ids]
+
+    rt = PersistentRuntime(tmp_path / "persist", timeout=60.0)
+    rt.start_server(blob, out_temp=td["logits"], in_bytes=len(bodies[0]), weights_size=w.image.nbytes)
+    served = []
+    try:
+        for b in bodies:
+            tok, resp, out = rt.run(b, want_out=True)
+            served.append((tok, np.frombuffer(out, np.float16).copy()))
+            assert resp["steps"] == len(served)
+        rt.reset()                                   # fresh KV: step 0 again
+        tok0, _, out0 = rt.run(bodies[0], want_out=True)
+    finally:
+        assert rt.stop_server() == 0
+
+    engine.shutdown()
+    engine.set_ext_weights(w.image.ctypes.data)
+    engine.state_reset()
+    pd = engine.parse(dec)
+    for step, (b, (tok, logits)) in enumerate(zip(bodies, served)):
+        engine.run_io(pd, b, td["logits"])
+        mine = np.frombuffer(engine.temp(td["logits"]), np.float16)
+        assert np.array_equal(mine.view(np.uint16), logits.view(np.uint16)), f"step {step}"
+        assert tok == int(np.argmax(logits.astype(np.float32)))
+    assert tok0 == served[0][0] and np.array_equal(np.frombuffer(out0, np.uint16), served[0][1].view(np.uint16))
+    engine.shutdown()
