@@ -933,6 +933,7 @@ int op_qk_rope_kv(Ctx& cx) {
     const float theta = f32_from_bits(A(11));
     if (hd != 128) return ERR("qk_rope_kv head_dim %u unsupported (128 only)", hd);
     if (!n_tok || !H || !KVH) return ERR("qk_rope_kv empty shape");
+    if (H + KVH > 64) return ERR("qk_rope_kv supports at most 64 q + kv heads (got %u)", H + KVH);
     const __half* qkv = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
     const __half* qg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(9)));
     const __half* kg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(10)));

@@ -391,26 +391,49 @@ struct QkRopeKvArgs {
     int advance;    // single-workgroup launch: advance the counter in-kernel
 };
 
+// One workgroup per token: wave 0 computes the token's RoPE table (64 frequency pairs,
+// evaluated in double) into LDS once; each wave then loads the inputs of all its heads
+// (heads wave, wave+4, ...; loads unconditional with clamped head indices so they are
+// all in flight together) before normalizing and rotating them one by one.
+constexpr uint32_t kQkMaxHeadsPerWave = 16;   // H + KVH <= 64
+
 __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QkRopeKvArgs A) {
     constexpr uint32_t HD = 128;
     __shared__ uint32_t s_pos;
+    __shared__ float s_c[64], s_s[64];
     const uint32_t t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (tid == 0) s_pos = *A.count;
     __syncthreads();
     const uint32_t pos = s_pos + t;
+    if (wave == 0) {
+        float c, s;
+        dev::rope_cs(pos, lane, A.theta, c, s);
+        s_c[lane] = c;
+        s_s[lane] = s;
+    }
     const uint32_t slot = pos % A.nslots;
-    float c, s;
-    dev::rope_cs(pos, lane, A.theta, c, s);
     const __half* row = A.qkv + (size_t)t * A.ld;
     __half* kface = reinterpret_cast<__half*>(A.ring + (size_t)slot * A.slot_bytes);
     __half* vface = kface + A.KVH * HD;
-    for (uint32_t r = wave; r < A.H + A.KVH; r += 4) {
+    const uint32_t nh = A.H + A.KVH;
+    float x1[kQkMaxHeadsPerWave], x2[kQkMaxHeadsPerWave];
+#pragma unroll
+    for (uint32_t j = 0; j < kQkMaxHeadsPerWave; ++j) {
+        const uint32_t r = min(wave + 4 * j, nh - 1);   // k heads follow the q heads
+        x1[j] = h2f(row[(size_t)r * HD + lane]);
+        x2[j] = h2f(row[(size_t)r * HD + lane + 64]);
+    }
+    const float qg1 = h2f(A.qg[lane]), qg2 = h2f(A.qg[lane + 64]);
+    const float kg1 = h2f(A.kg[lane]), kg2 = h2f(A.kg[lane + 64]);
+    __syncthreads();
+    const float c = s_c[lane], s = s_s[lane];
+#pragma unroll
+    for (uint32_t j = 0; j < kQkMaxHeadsPerWave; ++j) {
+        const uint32_t r = wave + 4 * j;
+        if (r >= nh) break;   // wave-uniform
         const bool is_q = r < A.H;
-        const __half* src = row + (size_t)r * HD;   // k heads follow the q heads
-        const __half* gm = is_q ? A.qg : A.kg;
         float y1f, y2f;
-        dev::head_norm_rope(h2f(src[lane]), h2f(src[lane + 64]), h2f(gm[lane]), h2f(gm[lane + 64]), c, s,
-                            y1f, y2f);
+        dev::head_norm_rope(x1[j], x2[j], is_q ? qg1 : kg1, is_q ? qg2 : kg2, c, s, y1f, y2f);
         const __half y1 = f2h(y1f), y2 = f2h(y2f);
         if (is_q) {
             __half* qo = A.q_out + (size_t)t * A.H * HD + (size_t)r * HD;
@@ -427,7 +450,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QkRopeKvArgs A) {
             }
         }
     }
-    const __half* v = row + (size_t)(A.H + A.KVH) * HD;
+    const __half* v = row + (size_t)nh * HD;
     for (uint32_t i = tid; i < A.KVH * HD; i += 256) {
         vface[i] = v[i];
         if (A.v_out) A.v_out[(size_t)t * A.KVH * HD + i] = v[i];
@@ -604,6 +627,7 @@ hipError_t launch_qk_rope_kv(const __half* qkv, uint32_t n_tok, uint32_t H, uint
                              const __half* q_gamma, const __half* k_gamma, float theta, __half* q_out,
                              __half* k_out, __half* v_out, uint8_t* ring, uint32_t slot_bytes,
                              uint32_t nslots, uint32_t* count_dev, hipStream_t st) {
+    if (!H || !KVH || H + KVH > 4 * kQkMaxHeadsPerWave) return hipErrorInvalidValue;
     if (!n_tok) return hipSuccess;
     QkRopeKvArgs A{qkv, (H + 2 * KVH) * 128u, H, KVH, q_gamma, k_gamma, theta, q_out, k_out, v_out,
                    ring, slot_bytes, nslots, count_dev, n_tok == 1 ? 1 : 0};

@@ -40,7 +40,7 @@ int gehtp_w4g_gemm(const void* x, uint32_t ldx, const void* wq, const void* ws, 
 int gehtp_w4g_fused(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y,
                     uint32_t ldy, uint32_t M, uint32_t N, uint32_t K, const void* gamma,
                     const void* res, uint32_t ldr, uint32_t mode, void* stream);
-/* OP_QK_ROPE_KV_F16 on device buffers: qkv [n_tok, (H+2KVH)*128]; ring of state_bytes;
+/* OP_QK_ROPE_KV_F16 on device buffers: qkv [n_tok, (H+2KVH)*128], H + KVH <= 64; ring of state_bytes;
  * count_dev = device uint32 auto-position counter (read, then advanced by n_tok);
  * k_out / v_out may be NULL. */
 int gehtp_qk_rope_kv(const void* qkv, uint32_t n_tok, uint32_t H, uint32_t KVH,

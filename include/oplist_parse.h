@@ -150,7 +150,7 @@ enum {
     /* OP_QK_ROPE_KV_F16: per-head QK RMSNorm + RoPE + KV append for a fused QKV row.
      *   args [qkv_ref, q_out_t, k_out_t, v_out_t, state_ref, n_tok, H, KVH, hd,
      *         q_gamma_ref, k_gamma_ref, theta_f32_bits]
-     *   qkv [n_tok, (H + 2*KVH)*hd] rows [q | k | v]; hd == 128.
+     *   qkv [n_tok, (H + 2*KVH)*hd] rows [q | k | v]; hd == 128; H + KVH <= 64.
      *   q_out[t] = ROPE(RMSNORM2(q_t, q_gamma)), k_t = ROPE(RMSNORM2(k_t, k_gamma)) and
      *   v_t are appended to the ring at the state's counter (advanced by n_tok);
      *   k_out_t / v_out_t (WT_REF_NONE to skip) receive k_t / v_t token-major.
