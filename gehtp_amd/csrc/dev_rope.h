@@ -43,10 +43,20 @@ __device__ __forceinline__ float rne_f16(float f) { return (float)(_Float16)f; }
 
 // RoPE table entry of pair i of a 128-dim head at position pos:
 // c, s = f16(cos / sin(pos * theta^(-2i/128))) evaluated in double.
+__device__ __forceinline__ double rope_inv(uint32_t i, float theta) {
+    return 1.0 / pow((double)theta, (double)(2 * i) / 128.0);
+}
+// The pair as f16 bits: cos in bits 0-15, sin in bits 16-31.
+__device__ __forceinline__ uint32_t rope_cs_bits(uint32_t pos, double inv) {
+    return (uint32_t)f64_to_f16_bits(cos((double)pos * inv)) | ((uint32_t)f64_to_f16_bits(sin((double)pos * inv)) << 16);
+}
+__device__ __forceinline__ void rope_cs_inv(uint32_t pos, double inv, float& c, float& s) {
+    const uint32_t w = rope_cs_bits(pos, inv);
+    c = bits_f((uint16_t)(w & 0xFFFFu));
+    s = bits_f((uint16_t)(w >> 16));
+}
 __device__ __forceinline__ void rope_cs(uint32_t pos, uint32_t i, float theta, float& c, float& s) {
-    const double inv = 1.0 / pow((double)theta, (double)(2 * i) / 128.0);
-    c = bits_f(f64_to_f16_bits(cos((double)pos * inv)));
-    s = bits_f(f64_to_f16_bits(sin((double)pos * inv)));
+    rope_cs_inv(pos, rope_inv(i, theta), c, s);
 }
 
 // One 128-dim head held by a full wavefront, lane l owning (x[l], x[l+64]):

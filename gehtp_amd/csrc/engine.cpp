@@ -961,7 +961,7 @@ int op_qk_rope_kv(Ctx& cx) {
 }
 
 // Attention workspace shared by the decode ops (grown on demand). Zeroed when
-// allocated: the fused op's merge completion counter must start at zero.
+// allocated: the fused op's RoPE records must start empty (tag 0).
 int attn_workspace(uint32_t need, char* err, size_t errn) {
     if (need <= g.attn_work_floats) return 0;
     if (g.attn_work) dev_free(g.attn_work);

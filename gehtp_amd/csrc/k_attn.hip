@@ -228,11 +228,22 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
 // arithmetic of qk_rope_kv_kernel, so the bits match), and the workgroup whose chunk
 // holds the new position also normalizes/rotates k of head g, writes k and v into the
 // ring slot and uses them for that key. The position is the state's device counter;
-// the merge pass advances it.
+// the merge pass advances it. The RoPE cos/sin (fp64 pow, cos, sin per lane) are the
+// slow part of that prologue, so an extra workgroup of the merge pass computes them
+// for this call's position and the next one into two workspace records, each tagged
+// with (position + 1, theta): the next layer of the same step (one workspace serves
+// every layer) or the next step of the same layer (one workspace per layer) finds its
+// values there; a call that finds neither (the first after a prefill or a reset)
+// computes its own. A record is a pure function of its tag, so the bits are the same
+// either way.
 constexpr int DC = 64;          // keys per chunk
 constexpr int MAX_REP = 8;
 constexpr int PS = HD + 4;      // partial record: O[HD], m, l, 2 pad (16-byte aligned)
-constexpr uint32_t kMergeSlots = 4;   // workspace head: merge completion counter (uint32)
+// Workspace head (uint32 words): [1] n_kv of the last fused call; RoPE records j = 0, 1:
+// [4 + j] position + 1 (0 = empty), [6 + j] theta bits, [8 + 64j + i] pair i as
+// f16 cos | f16 sin << 16. Partials follow the head.
+constexpr uint32_t kWsSnap = 1, kWsRopeTag = 4, kWsRopeTheta = 6, kWsRope = 8;
+constexpr uint32_t kWsHead = kWsRope + HD;
 
 struct DecodeArgs {
     const __half* q;         // [H, HD] ready queries (plain op)
@@ -247,6 +258,7 @@ struct DecodeArgs {
     float scale_log2;
     float* part;             // partials [KVH][max_chunks][REP][PS]
     uint32_t max_chunks;
+    uint32_t* ws;            // fused: workspace head (snapshot, RoPE records)
 };
 
 template <int REP, bool FUSED>
@@ -256,12 +268,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     __shared__ __align__(16) _Float16 s_q[REP][HD];
     __shared__ __align__(16) _Float16 s_kv[2][HD];
     const uint32_t c = blockIdx.x, g = blockIdx.y;
-    const uint32_t pos = FUSED ? *A.count : 0u;   // position of the new token
-    const uint32_t n_kv = FUSED ? pos + 1 : (A.count ? *A.count : A.n_kv_host);
-    if (c * DC >= n_kv) return;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t ch = lane & 15;   // 8-dim chunk of the head
     const uint32_t ks = tid >> 4;    // key stream: keys ks, ks+16, ks+32, ks+48
+    uint32_t rtag[2] = {0u, 0u}, rtheta[2] = {0u, 0u}, rw[2] = {0u, 0u};
+    if constexpr (FUSED) {   // issued with the counter load: neither depends on it
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            rtag[j] = A.ws[kWsRopeTag + j];
+            rtheta[j] = A.ws[kWsRopeTheta + j];
+            rw[j] = A.ws[kWsRope + HD / 2 * j + lane];
+        }
+    }
+    const uint32_t pos = FUSED ? *A.count : 0u;   // position of the new token
+    const uint32_t n_kv = FUSED ? pos + 1 : (A.count ? *A.count : A.n_kv_host);
+    if (c * DC >= n_kv) return;
+    if (FUSED && c == 0 && g == 0 && tid == 0) A.ws[kWsSnap] = n_kv;
 
     // Issue every load of the chunk first: K and V rows of this thread's keys.
     u32x4 kv4[DC / 16], vv4[DC / 16];
@@ -278,7 +300,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     if constexpr (FUSED) {
         const bool owns_new = pos / DC == c;
         float cr, sr;
-        dev::rope_cs(pos, lane, A.theta, cr, sr);
+        const uint32_t tb = __float_as_uint(A.theta);
+        const bool hit0 = rtag[0] == pos + 1 && rtheta[0] == tb, hit1 = rtag[1] == pos + 1 && rtheta[1] == tb;
+        if (hit0 || hit1) {   // wave-uniform
+            const uint32_t w = hit0 ? rw[0] : rw[1];
+            cr = dev::bits_f((uint16_t)(w & 0xFFFFu));
+            sr = dev::bits_f((uint16_t)(w >> 16));
+        } else {
+            dev::rope_cs_inv(pos, dev::rope_inv(lane, A.theta), cr, sr);
+        }
         for (uint32_t r = wave; r < (uint32_t)REP; r += 4) {
             const __half* src = A.qkv + (size_t)(g * REP + r) * HD;
             float y1, y2;
@@ -361,10 +391,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
 #pragma unroll
     for (int it = 0; it < DC / 16; ++it) {
         const uint32_t kl = ks + 16 * it;
+        // V rows past n_kv (read from slots not yet written) may hold anything: zero them
+        // so that p = 0 times a non-finite value cannot reach the sums.
+        const u32x4 vw = c * DC + kl < n_kv ? vv4[it] : u32x4{0u, 0u, 0u, 0u};
         float ve[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const h2_t v2 = as_h2(vv4[it][e]);
+            const h2_t v2 = as_h2(vw[e]);
             ve[2 * e] = (float)v2[0];
             ve[2 * e + 1] = (float)v2[1];
         }
@@ -402,17 +435,30 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
 // M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c - M) / L, in one pass:
 // thread (grp, d4) merges chunks grp, grp+8, ... of dims 4*d4..4*d4+3 online (running
 // max, rescaling its sums when the max grows), then the 8 groups are merged in LDS.
-// With `advance`, n_kv = *count + 1 and the last workgroup to finish increments the
-// counter (every workgroup has read it by then) and re-arms the completion counter.
+// With `advance` (fused), n_kv is the chunk pass's snapshot (the counter + 1): query
+// head 0 stores it as the new counter value (no other workgroup of this pass reads the
+// counter), and the extra last workgroup writes the two RoPE records.
 __global__ __launch_bounds__(256) void attn_merge_kernel(
-    const float* __restrict__ part, uint32_t* __restrict__ done, uint32_t n_kv_host,
-    uint32_t* __restrict__ count, int advance, uint32_t rep, uint32_t max_chunks, __half* __restrict__ out) {
+    const float* __restrict__ part, uint32_t n_kv_host, uint32_t* __restrict__ count, int advance,
+    uint32_t rep, uint32_t max_chunks, __half* __restrict__ out, uint32_t* __restrict__ ws, float theta) {
     __shared__ __align__(16) float4 s_o[256];
     __shared__ float s_m[8], s_l[8];
-    const uint32_t n_kv = count ? *count + (advance ? 1u : 0u) : n_kv_host;
+    const uint32_t n_kv = advance ? ws[kWsSnap] : count ? *count : n_kv_host;
     const uint32_t nc = (n_kv + DC - 1) / DC;
     const uint32_t h = blockIdx.x, g = h / rep, r = h % rep;
     const uint32_t tid = threadIdx.x;
+    if (advance && h == gridDim.x - 1) {
+        // RoPE records for positions n_kv - 1 (wave 0) and n_kv (wave 1).
+        const uint32_t j = tid >> 6, i = tid & 63;
+        if (j < 2) {
+            ws[kWsRope + HD / 2 * j + i] = dev::rope_cs_bits(n_kv - 1 + j, dev::rope_inv(i, theta));
+            if (i == 0) {
+                ws[kWsRopeTag + j] = n_kv + j;
+                ws[kWsRopeTheta + j] = __float_as_uint(theta);
+            }
+        }
+        return;
+    }
     const float* base = part + ((size_t)g * max_chunks * rep + r) * PS;   // chunk c at + c*rep*PS
     const size_t cstride = (size_t)rep * PS;
 
@@ -458,12 +504,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
                    (_Float16)(L > 0.0f ? o.z / L : 0.0f), (_Float16)(L > 0.0f ? o.w / L : 0.0f)};
         *reinterpret_cast<h4_t*>(out + (size_t)h * HD + 4 * tid) = hv;
     }
-    if (advance && tid == 0) {
-        if (atomicAdd(done, 1u) == gridDim.x - 1) {
-            atomicAdd(count, 1u);
-            atomicExch(done, 0u);
-        }
-    }
+    if (advance && h == 0 && tid == 0) *count = n_kv;
 }
 
 }  // namespace
@@ -486,11 +527,11 @@ hipError_t launch_attn_prefill(const __half* q, uint32_t ldq, const __half* k, c
     return hipGetLastError();
 }
 
-// Workspace: a 16-byte head (merge completion counter, zero before first use and left
-// zero by every call) then per (kv head, chunk, query head) partial records of PS floats.
+// Workspace: the head (fused-call snapshot and RoPE records; zero before the first fused
+// call) then per (kv head, chunk, query head) partial records of PS floats.
 uint32_t attn_decode_work_floats(uint32_t max_kv, uint32_t H, uint32_t hd) {
     (void)hd;
-    return kMergeSlots + ((max_kv + DC - 1) / DC) * H * PS;
+    return kWsHead + ((max_kv + DC - 1) / DC) * H * PS;
 }
 
 namespace {
@@ -506,8 +547,8 @@ hipError_t decode_launch(const DecodeArgs& A, uint32_t rep, int advance, __half*
     case 8: hipLaunchKernelGGL((attn_decode_kernel<8, FUSED>), grid, dim3(256), 0, st, A); break;
     default: return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(A.H), dim3(256), 0, st, A.part,
-                       reinterpret_cast<uint32_t*>(work), A.n_kv_host, A.count, advance, rep, A.max_chunks, out);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(A.H + (advance ? 1 : 0)), dim3(256), 0, st, A.part, A.n_kv_host,
+                       A.count, advance, rep, A.max_chunks, out, reinterpret_cast<uint32_t*>(work), A.theta);
     return hipGetLastError();
 }
 
@@ -527,7 +568,7 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
     if (attn_decode_work_floats(max_kv, H, hd) > work_floats) return hipErrorInvalidValue;
     if (!max_chunks) return hipSuccess;
     DecodeArgs A{q, nullptr, nullptr, nullptr, 0.0f, const_cast<uint8_t*>(ring), slot_bytes, nslots, KVH, H,
-                 n_kv_host, const_cast<uint32_t*>(count_dev), scale * kLog2e, work + kMergeSlots, max_chunks};
+                 n_kv_host, const_cast<uint32_t*>(count_dev), scale * kLog2e, work + kWsHead, max_chunks, nullptr};
     return decode_launch<false>(A, rep, 0, out, work, st);
 }
 
@@ -541,7 +582,8 @@ hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, cons
     const uint32_t max_chunks = (nslots + DC - 1) / DC;
     if (attn_decode_work_floats(nslots, H, HD) > work_floats) return hipErrorInvalidValue;
     DecodeArgs A{nullptr, qkv, q_gamma, k_gamma, theta, ring, slot_bytes, nslots, KVH, H,
-                 0u, count_dev, scale * kLog2e, work + kMergeSlots, max_chunks};
+                 0u, count_dev, scale * kLog2e, work + kWsHead, max_chunks,
+                 reinterpret_cast<uint32_t*>(work)};
     return decode_launch<true>(A, rep, 1, out, work, st);
 }
 

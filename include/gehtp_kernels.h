@@ -76,7 +76,9 @@ uint32_t gehtp_attn_decode_work_floats(uint32_t n_kv, uint32_t H, uint32_t hd);
  * ((H + 2*KVH)*128 fp16); q/k RMSNorm (gammas [128]) and RoPE (theta) at position
  * *count_dev, k/v written to the ring, attention over positions 0..*count_dev, then
  * *count_dev += 1. work: 16-byte aligned, gehtp_attn_decode_work_floats(ring slots, H,
- * 128) floats, zeroed before its first use (every call leaves its head zero again). */
+ * 128) floats, zeroed before its first use; its head then carries the RoPE cos/sin of
+ * the current and next position from call to call (one work buffer may serve every
+ * layer, or one per layer). */
 int gehtp_attn_decode_qkv(const void* qkv, uint32_t H, uint32_t KVH, const void* q_gamma,
                           const void* k_gamma, float theta, float scale, void* ring,
                           uint32_t state_bytes, void* count_dev, void* out, void* work,
