@@ -6,6 +6,7 @@
 #include "kernels.h"
 #include "dev_rope.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace gehtp {
@@ -89,6 +90,67 @@ __global__ __launch_bounds__(256) void rmsnorm2_kernel(const __half* __restrict_
             v = __fadd_rn(__fmul_rn(v, h2f(g[i])), b ? h2f(b[i]) : 0.0f);
             yr[i] = f2h(v);
         }
+    }
+}
+
+// Same arithmetic with the whole row in registers: lane l owns the 16-byte chunks
+// l, l+64, ..., l+64(C-1) of x, gamma and bias, all loaded before any arithmetic
+// (chunk indices past the row are clamped to its last chunk and not used), so a row
+// costs one memory round trip instead of one per loop trip. Needs rw % 8 == 0,
+// rw <= 512*C and 16-byte aligned x, gamma, bias and y.
+template <int C, bool HAS_B>
+__global__ __launch_bounds__(256) void rmsnorm2_reg_kernel(const __half* __restrict__ x,
+                                                           const __half* __restrict__ g,
+                                                           const __half* __restrict__ b,
+                                                           __half* __restrict__ y, uint32_t rows,
+                                                           uint32_t rw) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint32_t nch = rw / 8;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(x + (size_t)row * rw);
+    const u32x4* g4 = reinterpret_cast<const u32x4*>(g);
+    const u32x4* b4 = reinterpret_cast<const u32x4*>(b);
+    u32x4 xv[C], gv[C], bv[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        const uint32_t i = min(lane + 64u * j, nch - 1);
+        xv[j] = xr[i];
+        gv[j] = g4[i];
+        bv[j] = HAS_B ? b4[i] : u32x4{0u, 0u, 0u, 0u};
+    }
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        const bool valid = lane + 64u * j < nch;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const double f = valid ? (double)dev::bits_f((uint16_t)(xv[j][e / 2] >> (16 * (e & 1)))) : 0.0;
+            acc += f * f;
+        }
+    }
+    acc = wave_sum_d(acc);
+    const float rms = (float)sqrt(acc / (double)rw + 1e-6);
+    const float rcp = __fdiv_rn(1.0f, rms);   // x / rms via dev::div_markstein (exact)
+    u32x4* yr = reinterpret_cast<u32x4*>(y + (size_t)row * rw);
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        if (lane + 64u * j >= nch) continue;
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float v[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const uint32_t sh = 16 * hh;
+                const float q = dev::div_markstein(dev::bits_f((uint16_t)(xv[j][e] >> sh)), rms, rcp);
+                v[hh] = __fadd_rn(__fmul_rn(q, dev::bits_f((uint16_t)(gv[j][e] >> sh))),
+                                  dev::bits_f((uint16_t)(bv[j][e] >> sh)));
+            }
+            o[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[0]) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[1]) << 16);
+        }
+        yr[lane + 64u * j] = o;
     }
 }
 
@@ -205,40 +267,51 @@ __global__ void unary_kernel(const __half* __restrict__ x, __half* __restrict__ 
 
 // ---------------------------------------------------------------------------
 // Argmax: first index of the strict maximum above -1e30 (oplist_exec.c:1990-2004).
-__global__ __launch_bounds__(1024) void argmax_kernel(const __half* __restrict__ x, uint32_t n,
-                                                      int32_t* __restrict__ out) {
-    __shared__ float sv[16];
-    __shared__ int32_t si[16];
+// Pass 1: each workgroup reduces its part to (value, first index) and folds it into one
+// device-wide 64-bit key with atomicMax: the high word orders the value (-0 folded to
+// +0, so equal values tie), the low word is ~index, so the larger key is the larger
+// value and, among equal values, the smaller index. Pass 2 writes the index (0 when no
+// value exceeds -1e30) and clears the key for the next call; the kernel boundary
+// between the passes makes every atomic visible. Calls on one device must not overlap.
+__device__ unsigned long long g_argmax_key;   // 0 between calls
+
+__device__ __forceinline__ unsigned long long argmax_pack(float v, int32_t i) {
+    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (uint32_t)~(uint32_t)i;
+}
+
+constexpr uint32_t kArgmaxChunks = 4;   // 16-byte chunks per thread in pass 1
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(const __half* __restrict__ x, uint32_t n,
+                                                          uint32_t n8) {
+    __shared__ float sv[4];
+    __shared__ int32_t si[4];
     float bv = -1e30f;
     int32_t bi = 0;
-    // 16-byte loads (8 values) when x is aligned, four in flight per thread; each
-    // thread scans its indices in increasing order, so "first strict max" survives.
-    const uint32_t n8 = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) ? n / 8 : 0;
-    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    uint32_t i = threadIdx.x;
-    for (; i + 3 * 1024 < n8; i += 4 * 1024) {
-        u32x4 v[4];
+    const uint32_t tid = threadIdx.x;
+    // This thread's chunks c = blockIdx.x*1024 + 256u + tid (u = 0..3), all loads first
+    // (indices past the end clamped and not used), scanned in increasing index order.
+    if (n8) {
+        const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+        const uint32_t c0 = blockIdx.x * (256 * kArgmaxChunks) + tid;
+        u32x4 v[kArgmaxChunks];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = xv[i + u * 1024];
+        for (uint32_t u = 0; u < kArgmaxChunks; ++u) v[u] = xv[min(c0 + 256 * u, n8 - 1)];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (uint32_t u = 0; u < kArgmaxChunks; ++u) {
+            if (c0 + 256 * u >= n8) break;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float f = h2f(__ushort_as_half((uint16_t)(v[u][e / 2] >> (16 * (e & 1)))));
-                if (f > bv) { bv = f; bi = (int32_t)((i + u * 1024) * 8 + e); }
+                if (f > bv) { bv = f; bi = (int32_t)((c0 + 256 * u) * 8 + e); }
             }
-    }
-    for (; i < n8; i += 1024) {
-        const u32x4 v = xv[i];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float f = h2f(__ushort_as_half((uint16_t)(v[e / 2] >> (16 * (e & 1)))));
-            if (f > bv) { bv = f; bi = (int32_t)(i * 8 + e); }
         }
     }
-    for (uint32_t j = n8 * 8 + threadIdx.x; j < n; j += 1024) {
-        const float v = h2f(x[j]);
-        if (v > bv) { bv = v; bi = (int32_t)j; }
+    // Elements past the 16-byte chunks (all of them when x is not 16-byte aligned).
+    for (uint32_t j = n8 * 8 + blockIdx.x * 256 + tid; j < n; j += gridDim.x * 256) {
+        const float f = h2f(x[j]);
+        if (f > bv) { bv = f; bi = (int32_t)j; }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -246,14 +319,20 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const __half* __restrict__
         const int32_t oi = __shfl_xor(bi, off, 64);
         if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
     }
-    const uint32_t wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
+    const uint32_t wave = tid >> 6;
+    if ((tid & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 16; ++w)
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w)
             if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
-        out[0] = bi;
+        if (bv > -1e30f) atomicMax(&g_argmax_key, argmax_pack(bv, bi));
     }
+}
+
+__global__ void argmax_final_kernel(int32_t* __restrict__ out) {
+    const unsigned long long k = g_argmax_key;
+    out[0] = k ? (int32_t)~(uint32_t)k : 0;
+    g_argmax_key = 0ull;
 }
 
 __global__ void copy_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, size_t n) {
@@ -488,9 +567,35 @@ inline uint32_t blocks_for(size_t n, uint32_t bs) { return (uint32_t)((n + bs - 
 
 }  // namespace
 
+namespace {
+template <int C>
+void rmsnorm2_reg(const __half* x, const __half* g, const __half* b, __half* y, uint32_t rows, uint32_t rw,
+                  hipStream_t st) {
+    if (b)
+        hipLaunchKernelGGL((rmsnorm2_reg_kernel<C, true>), dim3(blocks_for(rows, 4)), dim3(256), 0, st, x, g, b, y,
+                           rows, rw);
+    else
+        hipLaunchKernelGGL((rmsnorm2_reg_kernel<C, false>), dim3(blocks_for(rows, 4)), dim3(256), 0, st, x, g, b,
+                           y, rows, rw);
+}
+}  // namespace
+
 hipError_t launch_rmsnorm2(const __half* x, const __half* g, const __half* b, __half* y,
                            uint32_t rows, uint32_t rw, hipStream_t st) {
-    if (!rows) return hipSuccess;
+    if (!rows || !rw) return hipSuccess;
+    const bool al = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(g) |
+                      reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+    const uint32_t c = (rw + 511) / 512;   // 16-byte chunks per lane
+    if (al && rw % 8 == 0 && c <= 16) {
+        if (c <= 1) rmsnorm2_reg<1>(x, g, b, y, rows, rw, st);
+        else if (c <= 2) rmsnorm2_reg<2>(x, g, b, y, rows, rw, st);
+        else if (c <= 4) rmsnorm2_reg<4>(x, g, b, y, rows, rw, st);
+        else if (c <= 5) rmsnorm2_reg<5>(x, g, b, y, rows, rw, st);
+        else if (c <= 8) rmsnorm2_reg<8>(x, g, b, y, rows, rw, st);
+        else if (c <= 10) rmsnorm2_reg<10>(x, g, b, y, rows, rw, st);
+        else rmsnorm2_reg<16>(x, g, b, y, rows, rw, st);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(rmsnorm2_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, st, x, g, b, y,
                        rows, rw);
     return hipGetLastError();
@@ -525,7 +630,12 @@ hipError_t launch_unary(const __half* x, __half* y, uint32_t n, uint32_t subtype
 }
 
 hipError_t launch_argmax(const __half* x, uint32_t n, int32_t* out, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, x, n, out);
+    const uint32_t n8 = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) ? n / 8 : 0;
+    const uint32_t tail = n - 8 * n8;
+    const uint32_t blocks = std::max({1u, (n8 + 256 * kArgmaxChunks - 1) / (256 * kArgmaxChunks),
+                                      std::min(1024u, (tail + 4095) / 4096)});
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(blocks), dim3(256), 0, st, x, n, n8);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1), 0, st, out);
     return hipGetLastError();
 }
 

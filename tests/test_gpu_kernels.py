@@ -117,7 +117,8 @@ def test_w4g_gemv_equals_gemm_small_m(lib, torch_dev):
 
 
 # ---------------------------------------------------------------- rows -------
-@pytest.mark.parametrize("rows,rw", [(512, 1024), (1, 2560), (4096, 128), (3, 100)])
+@pytest.mark.parametrize("rows,rw", [(512, 1024), (1, 2560), (4096, 128), (3, 100), (5, 8192), (2, 9728),
+                                     (7, 1536), (9, 24)])
 def test_rmsnorm2(lib, oracle, torch_dev, rows, rw):
     import torch
     rng = np.random.default_rng(rows + rw)
@@ -173,6 +174,12 @@ def test_argmax_first_max(lib, oracle, torch_dev):
         assert lib.gehtp_argmax(ptr(xd) + 2 * off, n2, ptr(out), stream_ptr()) == 0
         _sync()
         assert int(out.item()) == oracle.argmax(tail[off:off + n2]) == 1002 - off
+    # several load batches per thread (20 x 1024 16-byte chunks each); ties across batches
+    big = normal_f16(rng, 400003)
+    big[[170001, 390000, 400002]] = np.float16(11.0)
+    assert lib.gehtp_argmax(ptr(to_dev(big, torch_dev)), big.size, ptr(out), stream_ptr()) == 0
+    _sync()
+    assert int(out.item()) == oracle.argmax(big) == 170001
 
 
 def test_rope_bit_exact(lib, oracle, torch_dev):
