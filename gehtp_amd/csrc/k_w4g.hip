@@ -346,135 +346,143 @@ __global__ __launch_bounds__(256) void w4g_dequant_kernel(const uint4* __restric
 }
 
 // ---------------------------------------------------------------------------
-// Prefill GEMM: C[M,N] = A[M,K] . dequant(W)^T on v_mfma_f32_32x32x16_f16.
-// Workgroup tile 128x128, K step 64 (one scale group), 4 waves in a 2x2 layout, each
-// wave 64x64 = 2x2 MFMA tiles. Software pipeline: global loads run two K steps ahead
-// in two register stages, and A plus the dequantized W tile go to a double-buffered
-// LDS stage (16-byte row pad), so a K step has one barrier: MFMAs on stage k, then
-// stage k+1 from registers into the other LDS buffer, then the barrier.
-// Loads are unconditional with clamped rows (rows past M or N are computed, never
-// stored), which keeps the compiler from waiting on each load in turn.
-constexpr int GB_M = 128, GB_N = 128, GB_K = 64, GB_LDS = GB_K + 8;
+// Prefill GEMM: C[M,N] = A[M,K] . dequant(W)^T on v_mfma_f32_32x32x16_f16, with the B
+// operand dequantized straight from global memory into registers. Lane l of a wave
+// supplies B[k][n] for n = l%32 and 8 k's; with lane half h = l/32 owning bytes
+// 16h..16h+15 of a weight row's 32-byte K step (64 k), one 16-byte load gives the 4
+// words of the step's 4 MFMAs (word q: k = 32h + 8q + 0..7, dequantized in pair order
+// (k0,k4)(k1,k5)(k2,k6)(k3,k7)). A goes through LDS with the same k assignment: each
+// 16-byte chunk of an A row is stored in that pair order, so lane (row m = l%32, half h)
+// reads the chunk at k = 32h + 8q for MFMA q. W never touches LDS.
+// Workgroup tile 128 x 128, K step 64 (one scale group), 4 waves side by side in N,
+// each 128 x 32 = 4 x 1 MFMA tiles (16 MFMAs per K step): every weight is dequantized
+// once per workgroup, and the LDS carries only A (16 KiB written, 64 KiB read per K step).
+// Three workgroups per CU (168 VGPRs); their barriers are independent, so one's LDS and
+// load phases overlap another's MFMAs. Pipeline: global loads two K steps ahead in two
+// register stages; during the MFMAs of step k, the dequantized B of step k+1 is built
+// in the other B register set and the A chunks of step k+1 are written to the other LDS
+// buffer; one barrier per K step. Loads are unconditional with clamped rows (rows past
+// M or N are computed, never stored), which keeps the compiler from waiting on each
+// load in turn.
+// The 1-D grid runs m tiles fastest: workgroup i goes to XCD i % 8, so with 16 m tiles
+// (M = 2048) every XCD keeps two bands of A in its L2 while W streams.
+constexpr int WI = 4, GB_M = 32 * WI, GB_N = 128, GB_K = 64, GB_LDS = GB_K + 8;
 
-__global__ __launch_bounds__(256) void w4g_gemm_kernel(
-    const __half* __restrict__ a, uint32_t lda, const uint4* __restrict__ wq,
+__device__ __forceinline__ u32x4 pair_order16(u32x4 v) {   // k0..k7 -> (k0,k4)(k1,k5)(k2,k6)(k3,k7)
+    return u32x4{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
+                 __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
+}
+
+__global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
+    const __half* __restrict__ a, uint32_t lda, const uint8_t* __restrict__ wq,
     const __half* __restrict__ ws, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
-    uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu) {
-    constexpr int AP = GB_K / 8;             // 16-byte A pieces per row
-    constexpr int CA = GB_M * AP / 256;      // A pieces per thread
+    uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu, uint32_t mtiles) {
+    constexpr int CA = GB_M * (GB_K / 8) / 256;   // 16-byte A chunks per thread per K step
     __shared__ __align__(16) _Float16 As[2][GB_M * GB_LDS];
-    __shared__ __align__(16) _Float16 Bs[2][GB_N * GB_LDS];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t m0 = blockIdx.y * GB_M, n0 = blockIdx.x * GB_N;
-    const uint32_t G = K / 64, nsteps = K / GB_K;
-    const uint32_t wr = tid >> 1, wh = tid & 1;          // W piece: tile row, half
-    const size_t wrow = min(n0 + wr, N - 1);
+    const uint32_t m0 = (blockIdx.x % mtiles) * GB_M, n0 = (blockIdx.x / mtiles) * GB_N;
+    const uint32_t G = K / 64, nsteps = K / GB_K, rowbytes = K / 2;
+    constexpr int WJ = 1;   // MFMA tiles per wave: WI (M) x WJ (N)
+    const uint32_t wn = wave, half = lane >> 5, l32 = lane & 31;
+    size_t wrow[WJ];
+#pragma unroll
+    for (int j = 0; j < WJ; ++j) wrow[j] = min(n0 + wn * 32 * WJ + j * 32 + l32, N - 1);
+    const uint32_t arow = tid / 8, apiece = tid % 8;   // A chunk: rows arow + 32i, piece apiece
 
-    // A register stage holds this thread's 16-byte pieces of the A tile, 32 weights
-    // (half a row of the W tile) and their scale.
-    // Stage st in registers (st is a literal at every call, so the arrays stay in VGPRs;
-    // native vectors, not HIP's uint4 struct, whose copies lower to memcpy through
-    // private memory).
-    u32x4 ra[2][CA], rw[2];
-    uint16_t rs[2];
+    u32x4 ra[2][CA], rw[2][WJ];
+    uint16_t rs[2][WJ];
     auto load = [&](int st, uint32_t kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < CA; ++i) {
-            const uint32_t c = tid + 256u * i;
-            const size_t r = min(m0 + c / AP, M - 1);
-            ra[st][i] = *reinterpret_cast<const u32x4*>(a + r * lda + kb * GB_K + (c % AP) * 8);
+            const size_t r = min(m0 + arow + 32u * i, M - 1);
+            ra[st][i] = *reinterpret_cast<const u32x4*>(a + r * lda + kb * GB_K + apiece * 8);
         }
-        rw[st] = reinterpret_cast<const u32x4*>(wq)[wrow * (K / 32) + kb * 2 + wh];
-        rs[st] = __builtin_bit_cast(uint16_t, ws[wrow * G + kb]);
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            rw[st][j] = *reinterpret_cast<const u32x4*>(wq + wrow[j] * rowbytes + kb * 32 + 16 * half);
+            rs[st][j] = __builtin_bit_cast(uint16_t, ws[wrow[j] * G + kb]);
+        }
     };
-    auto store = [&](int st, int buf) __attribute__((always_inline)) {
+    auto store_a = [&](int st, int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            const uint32_t c = tid + 256u * i;
-            *reinterpret_cast<u32x4*>(&As[buf][(c / AP) * GB_LDS + (c % AP) * 8]) = ra[st][i];
-        }
-        const _Float16 sh = __builtin_bit_cast(_Float16, rs[st]);
-        const h2_t s2 = {sh, sh};
-        const uint32_t words[4] = {rw[st][0], rw[st][1], rw[st][2], rw[st][3]};
+        for (int i = 0; i < CA; ++i)
+            *reinterpret_cast<u32x4*>(&As[buf][(arow + 32 * i) * GB_LDS + apiece * 8]) = pair_order16(ra[st][i]);
+    };
+    h8_t bop[2][WJ][4];   // [B set][n block][MFMA q]
+    auto dequant_b = [&](int st, int set) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            h2_t d[4];
-            dequant_word(words[q], s2, d);
-            uint4 o;   // pair order (k0,k4)(k1,k5)(k2,k6)(k3,k7) back to k0..k7
-            o.x = __builtin_amdgcn_perm(as_u32(d[1]), as_u32(d[0]), 0x05040100u);
-            o.y = __builtin_amdgcn_perm(as_u32(d[3]), as_u32(d[2]), 0x05040100u);
-            o.z = __builtin_amdgcn_perm(as_u32(d[1]), as_u32(d[0]), 0x07060302u);
-            o.w = __builtin_amdgcn_perm(as_u32(d[3]), as_u32(d[2]), 0x07060302u);
-            *reinterpret_cast<uint4*>(&Bs[buf][wr * GB_LDS + wh * 32 + q * 8]) = o;
+        for (int j = 0; j < WJ; ++j) {
+            const _Float16 sh = __builtin_bit_cast(_Float16, rs[st][j]);
+            const h2_t s2 = {sh, sh};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                h2_t d[4];
+                dequant_word(rw[st][j][q], s2, d);
+                bop[set][j][q] = h8_t{d[0][0], d[0][1], d[1][0], d[1][1], d[2][0], d[2][1], d[3][0], d[3][1]};
+            }
         }
     };
 
-    f16x_t acc[2][2];
+    f16x_t acc[WI][WJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const uint32_t wm = wave >> 1, wn = wave & 1;
-    auto mfma = [&](int buf) __attribute__((always_inline)) {
+    auto mfma = [&](int buf, int set) __attribute__((always_inline)) {
 #pragma unroll
-        for (int kk = 0; kk < GB_K / 16; ++kk) {
-            h8_t af[2], bf[2];
-            const uint32_t kof = kk * 16 + 8 * (lane >> 5);
+        for (int q = 0; q < 4; ++q) {
+            h8_t af[WI];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *reinterpret_cast<const h8_t*>(&As[buf][(wm * 64 + i * 32 + (lane & 31)) * GB_LDS + kof]);
+            for (int i = 0; i < WI; ++i)
+                af[i] = *reinterpret_cast<const h8_t*>(&As[buf][(i * 32 + l32) * GB_LDS + 32 * half + 8 * q]);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bf[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][(wn * 64 + j * 32 + (lane & 31)) * GB_LDS + kof]);
+            for (int i = 0; i < WI; ++i)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < WJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bop[set][j][q], acc[i][j], 0, 0, 0);
         }
     };
-    // K steps in pairs, register stage 0 / LDS buffer 0 alternating with stage 1 / buffer 1:
-    // during the MFMAs on stage k, stage k+1 waits in registers and stage k+2 is being
-    // loaded. Nothing is conditional (past the end, the last stage is loaded and stored
-    // again, unread): a load under a branch makes the compiler wait for every
-    // outstanding load before the LDS stores.
+
+    // Step k: MFMAs on LDS buffer k%2 and B set k%2; loads of step k+2 into register
+    // stage k%2 (its previous contents, step k, were consumed during step k-1); A and B
+    // of step k+1 (register stage (k+1)%2) into LDS buffer / B set (k+1)%2. Past the
+    // end the last step is loaded and stored again, unread (nothing conditional).
     const uint32_t last = nsteps - 1;
     load(0, 0);
     load(1, min(1u, last));
-    store(0, 0);
+    store_a(0, 0);
+    dequant_b(0, 0);
     __syncthreads();
     uint32_t kb = 0;
-    // sched_barrier keeps the scheduler from sinking the loads below the MFMAs and
-    // stores of the step (which would shorten the prefetch distance to one step).
     for (; kb + 1 < nsteps; kb += 2) {
         load(0, min(kb + 2, last));
         __builtin_amdgcn_sched_barrier(0);
-        mfma(0);
-        __builtin_amdgcn_sched_barrier(0);
-        store(1, 1);
+        mfma(0, 0);
+        store_a(1, 1);
+        dequant_b(1, 1);
         __syncthreads();
         load(1, min(kb + 3, last));
         __builtin_amdgcn_sched_barrier(0);
-        mfma(1);
-        __builtin_amdgcn_sched_barrier(0);
-        store(0, 0);
+        mfma(1, 1);
+        store_a(0, 0);
+        dequant_b(0, 0);
         __syncthreads();
     }
-    if (kb < nsteps) mfma(0);   // odd step count: the last stage is in buffer 0
+    if (kb < nsteps) mfma(0, 0);   // odd step count: the last step is in buffer / set 0
 
     // Accumulator layout (32x32): lane l, reg r -> col l%32, row 8*(r/4) + 4*(l/32) + r%4.
     // With SwiGLU, columns 2c / 2c+1 (gate / up of output c) sit in lanes l, l^1.
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+        for (int j = 0; j < WJ; ++j) {
+            const uint32_t col = n0 + wn * 32 * WJ + j * 32 + l32;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                 const float partner = __shfl_xor(acc[i][j][r], 1, 64);
                 if (col >= N || row >= M) continue;
                 uint16_t v;
@@ -570,8 +578,9 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
                            hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.gamma || (epi.swiglu && (N & 1))) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(w4g_gemm_kernel, dim3((N + GB_N - 1) / GB_N, (M + GB_M - 1) / GB_M), dim3(256), 0, st, a, lda,
-                       reinterpret_cast<const uint4*>(wq), ws, y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0);
+    const uint32_t mt = (M + GB_M - 1) / GB_M, nt = (N + GB_N - 1) / GB_N;
+    hipLaunchKernelGGL(w4g_gemm_kernel, dim3(mt * nt), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K, epi.res,
+                       epi.ldr, epi.swiglu ? 1 : 0, mt);
     return hipGetLastError();
 }
 

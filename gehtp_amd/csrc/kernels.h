@@ -27,8 +27,8 @@ struct W4gEpilogue {
     uint32_t ldr = 0;
     bool swiglu = false;
 };
-// y[m*ldy + n] = f16( sum_k x[m*ldx + k] * fp16(q[n,k] * s[n, k/64]) ), m < M, n < N
-// (the GEMV applies s per 32-weight slice instead of rounding each q*s to fp16).
+// y[m*ldy + n] = f16( sum_k x[m*ldx + k] * fp16(q[n,k] * s[n, k/64]) ), m < M, n < N,
+// each dequantized weight rounded to fp16 as the reference does, fp32 accumulation
 // (N = weight rows; with swiglu the output has N/2 columns).
 hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,

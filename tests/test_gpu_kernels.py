@@ -102,9 +102,9 @@ def test_w4g_gemm_ragged(lib, oracle, torch_dev, M, N, K):
 
 
 def test_w4g_gemv_equals_gemm_small_m(lib, torch_dev):
-    """The two implementations agree to two fp16 ulps (4e-3 absolute near zero): the GEMM
-    rounds each dequantized weight to fp16 (the reference's fp16(q*s)), the GEMV scales
-    per slice in fp32, and each result is rounded to fp16 once."""
+    """The two implementations agree to two fp16 ulps (4e-3 absolute near zero): both round
+    each dequantized weight to fp16 (the reference's fp16(q*s)) and accumulate in fp32,
+    in different orders, and each result is rounded to fp16 once."""
     rng = np.random.default_rng(11)
     N, K = 1536, 2560
     _, wq, ws = w4g_weights(rng, N, K)
