@@ -157,6 +157,9 @@ EXPORTS = {
     "gehtp_w4g_gemm": (_i, [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "gehtp_w4g_dequant": (_i, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "gehtp_w4g_fused": (_i, [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _u32, _vp]),
+    "gehtp_w4g_split_bytes": (C.c_size_t, [_u32, _u32, _u32]),
+    "gehtp_w4g_fused_ws": (_i, [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _u32, _vp,
+                                C.c_size_t, _vp]),
     "gehtp_qk_rope_kv": (_i, [_vp, _u32, _u32, _u32, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp, _u32, _vp, _vp]),
     "gehtp_matmul_f16": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp]),
     "gehtp_rmsnorm2": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _vp]),

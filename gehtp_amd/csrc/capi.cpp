@@ -48,15 +48,27 @@ int gehtp_w4g_matmul(const void* x, uint32_t ldx, const void* wq, const void* ws
 int gehtp_w4g_fused(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y, uint32_t ldy,
                     uint32_t M, uint32_t N, uint32_t K, const void* gamma, const void* res, uint32_t ldr,
                     uint32_t mode, void* stream) {
+    return gehtp_w4g_fused_ws(x, ldx, wq, ws, y, ldy, M, N, K, gamma, res, ldr, mode, nullptr, 0, stream);
+}
+
+size_t gehtp_w4g_split_bytes(uint32_t M, uint32_t N, uint32_t K) {
+    return (M > kW4gGemvMaxM && K && K % 64 == 0) ? w4g_gemm_split_bytes(M, N, K) : 0;
+}
+
+int gehtp_w4g_fused_ws(const void* x, uint32_t ldx, const void* wq, const void* ws, void* y, uint32_t ldy,
+                       uint32_t M, uint32_t N, uint32_t K, const void* gamma, const void* res, uint32_t ldr,
+                       uint32_t mode, void* work, size_t work_bytes, void* stream) {
     const uint32_t n_out = mode == 1 ? N / 2 : N;
     if (mode > 1 || (mode == 1 && (N & 1)) || !w4g_args_ok(x, ldx, wq, ws, y, ldy, n_out, K) ||
-        (gamma && !al16(gamma)) || (res && ldr < n_out))
+        (gamma && !al16(gamma)) || (res && ldr < n_out) || (work && !al16(work)))
         return GEHTP_EINVAL;
     W4gEpilogue epi;
     epi.gamma = H(gamma);
     epi.res = H(res);
     epi.ldr = ldr;
     epi.swiglu = mode == 1;
+    epi.split_ws = static_cast<float*>(work);
+    epi.split_ws_bytes = work ? work_bytes : 0;
     if (w4g_gemv_supported(M, K))
         return rc(launch_w4g_gemv(H(x), ldx, static_cast<const uint8_t*>(wq), H(ws), Hm(y), ldy, M, N, K,
                                   S(stream), epi));

@@ -102,6 +102,8 @@ struct Engine {
     uint32_t attn_work_floats = 0;
     uint8_t* norm_buf = nullptr;   // normalized rows for OP_W4G_FUSED_F16 on the GEMM path
     size_t norm_cap = 0;
+    uint8_t* split_buf = nullptr;  // fp32 K-split partials of the W4G GEMM
+    size_t split_cap = 0;
 
     // OP_MATMUL_W4A16 engine surfaces (the reference's HMX engine: shape, act, out,
     // weights, bias), read by OP_DMA's 0xC000 references; engine_m reports w4_m.
@@ -478,6 +480,7 @@ void kv_mark(State& s, uint32_t p) {
 }
 
 int attn_workspace(uint32_t need, char* err, size_t errn);
+int gemm_split_ws(W4gEpilogue& epi, uint32_t M, uint32_t N, uint32_t K, char* err, size_t errn);
 
 int kv_check(const State& s, uint32_t n_kv, char* err, size_t errn) {
     if (n_kv > s.valid_prefix) return ERR("kv gather miss pos %u (state bug)", s.valid_prefix);
@@ -572,10 +575,13 @@ int op_matmul_w4g(Ctx& cx) {
     if (sb && sb < (uint64_t)N * (K / 64) * 2u) return ERR("w4g scale slot %zu < N*K/64*2", sb);
     if (((uintptr_t)a | (uintptr_t)wq) % 16) return ERR("w4g operands not 16-byte aligned");
     g.stats.matmul++;
-    if (M <= kW4gGemvMaxM)
+    if (M <= kW4gGemvMaxM) {
         CHECK_LAUNCH(launch_w4g_gemv(a, K, wq, ws, y, ldy, M, N, K, g.stream));
-    else
-        CHECK_LAUNCH(launch_w4g_gemm(a, K, wq, ws, y, ldy, M, N, K, g.stream));
+    } else {
+        W4gEpilogue epi;
+        if (gemm_split_ws(epi, M, N, K, err, errn)) return -1;
+        CHECK_LAUNCH(launch_w4g_gemm(a, K, wq, ws, y, ldy, M, N, K, g.stream, epi));
+    }
     return 0;
 }
 
@@ -872,6 +878,16 @@ int scratch(uint8_t** p, size_t* cap, size_t bytes, char* err, size_t errn) {
     return 0;
 }
 
+// Attach the engine's K-split workspace to a W4G GEMM epilogue (grown on demand).
+int gemm_split_ws(W4gEpilogue& epi, uint32_t M, uint32_t N, uint32_t K, char* err, size_t errn) {
+    const size_t need = w4g_gemm_split_bytes(M, N, K);
+    if (!need) return 0;
+    if (scratch(&g.split_buf, &g.split_cap, need, err, errn)) return -1;
+    epi.split_ws = reinterpret_cast<float*>(g.split_buf);
+    epi.split_ws_bytes = g.split_cap;
+    return 0;
+}
+
 int op_w4g_fused(Ctx& cx) {
     char* err = cx.err; size_t errn = cx.errn;
     const uint32_t M = A(4), K = A(5), N = A(6), mode = A(9), flags = A(10);
@@ -923,6 +939,7 @@ int op_w4g_fused(Ctx& cx) {
         CHECK_LAUNCH(launch_rmsnorm2(a, gamma, nullptr, reinterpret_cast<__half*>(g.norm_buf), M, K, g.stream));
         src = reinterpret_cast<const __half*>(g.norm_buf);
     }
+    if (gemm_split_ws(epi, M, N, K, err, errn)) return -1;
     CHECK_LAUNCH(launch_w4g_gemm(src, K, wq, ws, y, ldy, M, N, K, g.stream, epi));
     return 0;
 }
@@ -1749,6 +1766,9 @@ void wt_exec_shutdown(void) {
     if (g.norm_buf) dev_free(g.norm_buf);
     g.norm_buf = nullptr;
     g.norm_cap = 0;
+    if (g.split_buf) dev_free(g.split_buf);
+    g.split_buf = nullptr;
+    g.split_cap = 0;
     if (g.w4_out) dev_free(g.w4_out);
     g.w4_out = nullptr;
     g.w4_out_cap = 0;

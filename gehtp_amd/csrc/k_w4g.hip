@@ -368,6 +368,24 @@ __global__ __launch_bounds__(256) void w4g_dequant_kernel(const uint4* __restric
 // (M = 2048) every XCD keeps two bands of A in its L2 while W streams.
 constexpr int WI = 4, GB_M = 32 * WI, GB_N = 128, GB_K = 64, GB_LDS = GB_K + 8;
 
+// Output of one GEMM element pair: plain (two columns, each rounded to fp16, plus the
+// residual) or SwiGLU (gate = column 2c, up = column 2c+1 -> output column c), the
+// roundings of MATMUL_W4G followed by UNARY silu, BINARY mul and ADD.
+__device__ __forceinline__ void w4g_store(__half* __restrict__ y, uint32_t ldy, const __half* __restrict__ res,
+                                          uint32_t ldr, uint32_t row, uint32_t col, float acc) {
+    uint16_t v = f2hb(acc);
+    if (res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, res[(size_t)row * ldr + col]))));
+    reinterpret_cast<uint16_t*>(y)[(size_t)row * ldy + col] = v;
+}
+__device__ __forceinline__ void w4g_store_swiglu(__half* __restrict__ y, uint32_t ldy, const __half* __restrict__ res,
+                                                 uint32_t ldr, uint32_t row, uint32_t oc, float gate, float up) {
+    const float gv = h2f(f2hb(gate)), uv = h2f(f2hb(up));
+    const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
+    uint16_t v = f2hb(__fmul_rn(act, uv));
+    if (res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, res[(size_t)row * ldr + oc]))));
+    reinterpret_cast<uint16_t*>(y)[(size_t)row * ldy + oc] = v;
+}
+
 __device__ __forceinline__ u32x4 pair_order16(u32x4 v) {   // k0..k7 -> (k0,k4)(k1,k5)(k2,k6)(k3,k7)
     return u32x4{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
                  __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
@@ -376,12 +394,18 @@ __device__ __forceinline__ u32x4 pair_order16(u32x4 v) {   // k0..k7 -> (k0,k4)(
 __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
     const __half* __restrict__ a, uint32_t lda, const uint8_t* __restrict__ wq,
     const __half* __restrict__ ws, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
-    uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu, uint32_t mtiles) {
+    uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu, uint32_t mtiles, uint32_t ntiles,
+    uint32_t split_steps, float* __restrict__ part) {
     constexpr int CA = GB_M * (GB_K / 8) / 256;   // 16-byte A chunks per thread per K step
     __shared__ __align__(16) _Float16 As[2][GB_M * GB_LDS];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t m0 = (blockIdx.x % mtiles) * GB_M, n0 = (blockIdx.x / mtiles) * GB_N;
-    const uint32_t G = K / 64, nsteps = K / GB_K, rowbytes = K / 2;
+    // Workgroup -> (m tile, n tile, K part): m fastest, K part slowest. With `part`,
+    // K part s covers K steps [s*split_steps, (s+1)*split_steps) and its fp32 sums go to
+    // part[s][M][N] for w4g_splitk_reduce_kernel; otherwise one part covers all of K.
+    const uint32_t m0 = (blockIdx.x % mtiles) * GB_M, n0 = (blockIdx.x / mtiles % ntiles) * GB_N;
+    const uint32_t split = blockIdx.x / (mtiles * ntiles);
+    const uint32_t G = K / 64, rowbytes = K / 2;
+    const uint32_t kbase = split * split_steps, nsteps = min(split_steps, K / GB_K - kbase);
     constexpr int WJ = 1;   // MFMA tiles per wave: WI (M) x WJ (N)
     const uint32_t wn = wave, half = lane >> 5, l32 = lane & 31;
     size_t wrow[WJ];
@@ -395,12 +419,12 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
 #pragma unroll
         for (int i = 0; i < CA; ++i) {
             const size_t r = min(m0 + arow + 32u * i, M - 1);
-            ra[st][i] = *reinterpret_cast<const u32x4*>(a + r * lda + kb * GB_K + apiece * 8);
+            ra[st][i] = *reinterpret_cast<const u32x4*>(a + r * lda + (kbase + kb) * GB_K + apiece * 8);
         }
 #pragma unroll
         for (int j = 0; j < WJ; ++j) {
-            rw[st][j] = *reinterpret_cast<const u32x4*>(wq + wrow[j] * rowbytes + kb * 32 + 16 * half);
-            rs[st][j] = __builtin_bit_cast(uint16_t, ws[wrow[j] * G + kb]);
+            rw[st][j] = *reinterpret_cast<const u32x4*>(wq + wrow[j] * rowbytes + (kbase + kb) * 32 + 16 * half);
+            rs[st][j] = __builtin_bit_cast(uint16_t, ws[wrow[j] * G + kbase + kb]);
         }
     };
     auto store_a = [&](int st, int buf) __attribute__((always_inline)) {
@@ -485,21 +509,37 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
                 const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                 const float partner = __shfl_xor(acc[i][j][r], 1, 64);
                 if (col >= N || row >= M) continue;
-                uint16_t v;
-                uint32_t oc = col;
-                if (swiglu) {
-                    if (lane & 1) continue;
-                    const float gv = h2f(f2hb(acc[i][j][r])), uv = h2f(f2hb(partner));
-                    const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
-                    v = f2hb(__fmul_rn(act, uv));
-                    oc = col >> 1;
-                } else {
-                    v = f2hb(acc[i][j][r]);
-                }
-                if (res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, res[(size_t)row * ldr + oc]))));
-                reinterpret_cast<uint16_t*>(y)[(size_t)row * ldy + oc] = v;
+                if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
+                else if (!swiglu) w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
+                else if (!(lane & 1)) w4g_store_swiglu(y, ldy, res, ldr, row, col >> 1, acc[i][j][r], partner);
             }
         }
+}
+
+// Split-K finish: element pair (row, 2p..2p+1) sums the fp32 parts in part order and
+// stores through the GEMM's own epilogue.
+__global__ __launch_bounds__(256) void w4g_splitk_reduce_kernel(const float* __restrict__ part, uint32_t parts,
+                                                                __half* __restrict__ y, uint32_t ldy, uint32_t M,
+                                                                uint32_t N, const __half* __restrict__ res,
+                                                                uint32_t ldr, int swiglu) {
+    const uint32_t np = (N + 1) / 2;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)M * np) return;
+    const uint32_t row = (uint32_t)(i / np), c = 2 * (uint32_t)(i % np);
+    const bool two = c + 1 < N;
+    const float* p = part + (size_t)row * N + c;
+    float s0 = p[0], s1 = two ? p[1] : 0.0f;
+    for (uint32_t k = 1; k < parts; ++k) {
+        p += (size_t)M * N;
+        s0 = __fadd_rn(s0, p[0]);
+        if (two) s1 = __fadd_rn(s1, p[1]);
+    }
+    if (swiglu) {
+        w4g_store_swiglu(y, ldy, res, ldr, row, c >> 1, s0, s1);
+    } else {
+        w4g_store(y, ldy, res, ldr, row, c, s0);
+        if (two) w4g_store(y, ldy, res, ldr, row, c + 1, s1);
+    }
 }
 
 }  // namespace
@@ -578,10 +618,34 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
                            hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.gamma || (epi.swiglu && (N & 1))) return hipErrorInvalidValue;
-    const uint32_t mt = (M + GB_M - 1) / GB_M, nt = (N + GB_N - 1) / GB_N;
+    const uint32_t mt = (M + GB_M - 1) / GB_M, nt = (N + GB_N - 1) / GB_N, steps = K / GB_K;
+    const uint32_t parts = w4g_gemm_split_parts(M, N, K);
+    const size_t need = (size_t)parts * M * N * sizeof(float);
+    if (parts > 1 && epi.split_ws && epi.split_ws_bytes >= need) {
+        const uint32_t per = (steps + parts - 1) / parts;
+        hipLaunchKernelGGL(w4g_gemm_kernel, dim3(mt * nt * parts), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K,
+                           epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, nt, per, epi.split_ws);
+        const size_t pairs = (size_t)M * ((N + 1) / 2);
+        hipLaunchKernelGGL(w4g_splitk_reduce_kernel, dim3((uint32_t)((pairs + 255) / 256)), dim3(256), 0, st,
+                           epi.split_ws, parts, y, ldy, M, N, epi.res, epi.ldr, epi.swiglu ? 1 : 0);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(w4g_gemm_kernel, dim3(mt * nt), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K, epi.res,
-                       epi.ldr, epi.swiglu ? 1 : 0, mt);
+                       epi.ldr, epi.swiglu ? 1 : 0, mt, nt, steps, static_cast<float*>(nullptr));
     return hipGetLastError();
+}
+
+// Two K parts when the tile grid alone would give fewer than two workgroups per CU
+// (three fit at once) and each part still has 16 or more K steps: the narrow-N
+// projections (N = hidden) otherwise run one latency-bound workgroup on most CUs.
+uint32_t w4g_gemm_split_parts(uint32_t M, uint32_t N, uint32_t K) {
+    const size_t tiles = (size_t)((M + GB_M - 1) / GB_M) * ((N + GB_N - 1) / GB_N);
+    return (tiles < 2 * (size_t)device_cu_count() && K / GB_K >= 32) ? 2u : 1u;
+}
+
+size_t w4g_gemm_split_bytes(uint32_t M, uint32_t N, uint32_t K) {
+    const uint32_t parts = w4g_gemm_split_parts(M, N, K);
+    return parts > 1 ? (size_t)parts * M * N * sizeof(float) : 0;
 }
 
 hipError_t launch_w4g_dequant(const uint8_t* wq, const __half* ws, __half* w, uint32_t N,

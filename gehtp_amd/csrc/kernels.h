@@ -26,6 +26,10 @@ struct W4gEpilogue {
     const __half* res = nullptr;
     uint32_t ldr = 0;
     bool swiglu = false;
+    // GEMM only: fp32 workspace for a K split (w4g_gemm_split_bytes); without one, or
+    // when too small, the GEMM runs unsplit. Calls that share it must not overlap.
+    float* split_ws = nullptr;
+    size_t split_ws_bytes = 0;
 };
 // y[m*ldy + n] = f16( sum_k x[m*ldx + k] * fp16(q[n,k] * s[n, k/64]) ), m < M, n < N,
 // each dequantized weight rounded to fp16 as the reference does, fp32 accumulation
@@ -36,6 +40,10 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
 hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
                            hipStream_t st, const W4gEpilogue& epi = W4gEpilogue());
+// K parts the GEMM uses for (M, N, K) when given a workspace, and the workspace bytes
+// (0 when it runs unsplit).
+uint32_t w4g_gemm_split_parts(uint32_t M, uint32_t N, uint32_t K);
+size_t w4g_gemm_split_bytes(uint32_t M, uint32_t N, uint32_t K);
 // w[n*K + k] = fp16(q * s) (bit-exact dequant; used by tests and the fp16 fallback).
 hipError_t launch_w4g_dequant(const uint8_t* wq, const __half* ws, __half* w,
                               uint32_t N, uint32_t K, hipStream_t st);

@@ -357,6 +357,49 @@ def test_w4g_fused_gemm_epilogues(lib, oracle, torch_dev):
     assert_close(from_dev(y), ref, what="gemm swiglu+res")
 
 
+@pytest.mark.parametrize("mode,use_res,M", [(0, False, 384), (0, True, 200), (1, False, 384), (1, True, 131)])
+def test_w4g_gemm_split_k(lib, oracle, torch_dev, mode, use_res, M):
+    """Narrow N, long K: with a workspace the GEMM splits K in two (fp32 sums of each half,
+    added in a second pass through the same epilogue). Checked against the oracle and
+    against the one-pass GEMM (only the fp32 sum order differs: almost everywhere identical).
+    K = 4160 has 65 K steps, so the two halves are unequal."""
+    import torch
+    rng = np.random.default_rng(60 + 2 * mode + use_res)
+    N, K = (2 * 640 if mode else 1280), 4160
+    n_out = N // 2 if mode else N
+    need = lib.gehtp_w4g_split_bytes(M, N, K)
+    assert need == 2 * M * N * 4
+    assert lib.gehtp_w4g_split_bytes(2, N, K) == 0            # GEMV sizes never split
+    assert lib.gehtp_w4g_split_bytes(M, 1 << 16, K) == 0       # enough tiles already
+    _, wq, ws = w4g_weights(rng, N, K)
+    # x / 4 keeps the 4160-term sums near unit size (as in the shorter-K tests), so a
+    # rounding flip of a SwiGLU gate is not multiplied by a large up value
+    x = normal_f16(rng, M, K) * np.float16(0.25)
+    res = normal_f16(rng, M, n_out)
+    xd, wqd, wsd = to_dev(x, torch_dev), to_dev(wq, torch_dev), to_dev(ws, torch_dev)
+    rd = ptr(to_dev(res, torch_dev)) if use_res else None
+    work = torch.empty(need // 4, dtype=torch.float32, device=torch_dev)
+    y1 = torch.empty((M, n_out), dtype=torch.float16, device=torch_dev)
+    y2 = torch.empty((M, n_out), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_w4g_fused_ws(ptr(xd), K, ptr(wqd), ptr(wsd), ptr(y1), n_out, M, N, K, None, rd, n_out, mode,
+                                  ptr(work), need, stream_ptr()) == 0
+    assert lib.gehtp_w4g_fused_ws(ptr(xd), K, ptr(wqd), ptr(wsd), ptr(y2), n_out, M, N, K, None, rd, n_out, mode,
+                                  None, 0, stream_ptr()) == 0
+    _sync()
+    acc = oracle.matmul_w4g(x, wq, ws, threads=8)
+    ref = oracle.binary(oracle.unary(acc[:, 0::2].copy(), 12), acc[:, 1::2].copy(), 2) if mode else acc
+    if use_res:
+        ref = oracle.binary(ref, res, 0)
+    a, b = from_dev(y1), from_dev(y2)
+    assert_close(a, ref, what=f"split-K gemm mode={mode} res={use_res}")
+    # fp32 reordering over K = 4160 terms moves a sum by ~1e-5, which flips the fp16
+    # rounding of a few outputs (and, where the residual cancels the product, shows as
+    # that product's ulp on a small result): both stay within the parity bar.
+    assert_close(b, ref, what=f"one-pass gemm mode={mode} res={use_res}")
+    assert np.abs(a.astype(np.float32) - b.astype(np.float32)).max() <= 2e-2
+    assert (a == b).mean() > 0.99
+
+
 @pytest.mark.parametrize("n_tok", [1, 37])
 def test_qk_rope_kv(lib, oracle, torch_dev, n_tok):
     """OP_QK_ROPE_KV_F16 = per-head RMSNORM2 (q_norm / k_norm), ROPE at the counter
