@@ -105,7 +105,7 @@ class Engine:
         n = self.lib.wt_exec_temp_last_bytes(tid)
         p = self.lib.wt_exec_temp(tid)
         if not p:
-            raise KeyError(f"temp {tid} not allocated")
+            raise KeyError(f"temp {tid} not allocated, or an intermediate of an attention chain that ran fused")
         return C.string_at(p, n)
 
     def temp_bytes(self, tid: int) -> int:
@@ -141,6 +141,17 @@ class Engine:
         c, r = C.c_uint32(0), C.c_uint32(0)
         self.lib.wt_exec_graph_stats(C.byref(c), C.byref(r))
         return c.value, r.value
+
+    def set_fusion(self, on: bool) -> bool:
+        """Fuse the reference attention op chain into one kernel (default on);
+        returns the previous setting."""
+        return bool(self.lib.wt_exec_set_fusion(1 if on else 0))
+
+    def fusion_stats(self) -> tuple[int, int]:
+        """(attention chains found in the blobs seen, chain executions run fused)."""
+        f, r = C.c_uint64(0), C.c_uint64(0)
+        self.lib.wt_exec_fusion_stats(C.byref(f), C.byref(r))
+        return f.value, r.value
 
 
 WT_ERR = WT_ERR

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -39,6 +40,8 @@ int device_cu_count() {
     }
     return cus;
 }
+
+extern std::atomic<uint64_t> g_parse_epoch;   // wt_parse.cpp
 
 }  // namespace gehtp
 
@@ -121,6 +124,8 @@ struct Engine {
     bool replay = false;    // host pass of a graph replay: device work is not enqueued
     bool variant = false;   // an op of this run passed host-side step state to a kernel
     int graphs = -1;        // -1: not yet read from the environment; 0 off; 1 on
+    int fusion = -1;        // attention-chain fusion: -1 not yet read from the environment
+    uint64_t chains_found = 0, fused_runs = 0;
     bool graphs_broken = false;
     uint32_t n_captures = 0, n_replays = 0;
 
@@ -139,6 +144,38 @@ struct Engine {
 
 Engine g;
 
+// ---- load-time fusion of the reference attention chain: observation hooks ----
+// The first full run of a blob runs its attention chains op by op and watches their
+// intermediate temps: a read of one after the chain (before it is written again), or a
+// read before any write in the run (a value carried over from the previous run), keeps
+// that chain unfused. ref_ptr reports reads, temp_get writes.
+struct FuseObs {
+    bool on = false;
+    std::vector<int32_t> armed;      // temp id -> chain whose finished chain wrote it
+    std::vector<int32_t> inter_of;   // temp id -> chain it is an intermediate of
+    std::vector<uint8_t> written;    // temp written during this run
+    std::vector<uint8_t>* live = nullptr;
+};
+FuseObs g_obs;
+// Temps a fused chain left unwritten (its intermediates) since their last write:
+// wt_exec_temp returns NULL for them.
+std::vector<uint8_t> g_unmat;
+uint32_t g_run_out_temp = 0xFFFFFFFFu;   // run_io's output temp (read after the run)
+
+inline void obs_read(uint32_t arg) {
+    if (!g_obs.on || (arg & 0x8000u) || (arg & 0xE000u) == WT_REF_STATE_FLAG) return;
+    const uint32_t t = arg & 0x3FFFu;
+    if (t >= kMaxTemps) return;
+    int32_t c = g_obs.armed[t];
+    if (c < 0 && !g_obs.written[t]) c = g_obs.inter_of[t];
+    if (c >= 0) (*g_obs.live)[c] = 1;
+}
+inline void obs_write(uint32_t id) {
+    if (!g_obs.on || id >= kMaxTemps) return;
+    g_obs.written[id] = 1;
+    g_obs.armed[id] = -1;
+}
+
 #define ERR(...) (std::snprintf(err, errn, __VA_ARGS__), -1)
 
 // Every device allocation and free of the engine goes through these two, so that a
@@ -154,13 +191,14 @@ void dev_free(void* p) {
 
 int ensure_ready(char* err, size_t errn) {
     if (g.ready) return 0;
+    if (const char* t = std::getenv("GEHTP_TRACE"); t && t[0] && t[0] != '0') g.trace = true;
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return ERR("no HIP device visible");
     if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess)
         return ERR("hipStreamCreate failed");
     if (dev_malloc(reinterpret_cast<void**>(&g.counters_dev), WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
         return ERR("counter alloc failed");
-    if (hipMemset(g.counters_dev, 0, WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
+    if (launch_fill_zero(g.counters_dev, WT_MAX_STATES * sizeof(uint32_t), g.stream) != hipSuccess)
         return ERR("counter clear failed");
     g.ready = true;
     return 0;
@@ -216,7 +254,10 @@ int upload(uint8_t** dev, size_t* cap, const uint8_t* host, size_t bytes, char* 
             return ERR("device alloc of %zu bytes failed", bytes);
         *cap = bytes;
     }
-    if (bytes && hipMemcpy(*dev, host, bytes, hipMemcpyHostToDevice) != hipSuccess)
+    // On the engine's stream (created non-blocking: null-stream copies and memsets are
+    // not ordered with its kernels), then drained so the host image may change after.
+    if (bytes && (hipMemcpyAsync(*dev, host, bytes, hipMemcpyHostToDevice, g.stream) != hipSuccess ||
+                  hipStreamSynchronize(g.stream) != hipSuccess))
         return ERR("weight upload failed");
     return 0;
 }
@@ -253,6 +294,7 @@ uint8_t* slot_ptr(const wt_blob* b, uint32_t s) {
 }
 
 uint8_t* ref_ptr(const wt_blob* b, uint32_t arg) {
+    obs_read(arg);
     if (arg & 0x8000u) return slot_ptr(b, arg & 0x7FFFu);
     if ((arg & 0xE000u) == WT_REF_STATE_FLAG) {
         const uint32_t s = arg & 0x1FFFu;
@@ -294,6 +336,8 @@ size_t ref_bytes(const wt_blob* b, uint32_t arg) {
 // a 128-byte aligned bump that only grows; earlier pools are kept alive.
 uint8_t* temp_get(uint32_t id, uint32_t bytes) {
     if (id >= kMaxTemps) return nullptr;
+    obs_write(id);
+    if (!g_unmat.empty()) g_unmat[id] = 0;
     if (g.vtcm_off_arr[id] != kNone) {
         const uint32_t off = g.vtcm_off_arr[id];
         if (!g.vtcm_pool || (uint64_t)off + bytes > g.vtcm_pool_size) return nullptr;
@@ -422,7 +466,9 @@ int load_states(const wt_blob* b, char* err, size_t errn) {
             g.st[i] = State{};
         }
         g.n_states = 0;
-        if (g.counters_dev && hipMemset(g.counters_dev, 0, WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
+        // Clears go on the engine's stream: a null-stream memset is not ordered with the
+        // kernels of a non-blocking stream and could land after the first KV append.
+        if (g.counters_dev && launch_fill_zero(g.counters_dev, WT_MAX_STATES * sizeof(uint32_t), g.stream) != hipSuccess)
             return ERR("counter clear failed");
         for (uint32_t i = 0; i < n; ++i) {
             uint32_t bytes;
@@ -430,7 +476,7 @@ int load_states(const wt_blob* b, char* err, size_t errn) {
             if (bytes == 0 || bytes > (1u << 30)) return ERR("state %u bytes bad %u", i, bytes);
             void* d = nullptr;
             if (dev_malloc(&d, bytes) != hipSuccess) return ERR("state %u alloc %u", i, bytes);
-            if (hipMemset(d, 0, bytes) != hipSuccess) return ERR("state %u clear", i);
+            if (launch_fill_zero(d, bytes, g.stream) != hipSuccess) return ERR("state %u clear", i);
             g.st[i] = State{};
             g.st[i].dev = static_cast<uint8_t*>(d);
             g.st[i].bytes = bytes;
@@ -673,6 +719,7 @@ int op_unary(Ctx& cx) {
 int op_silu(Ctx& cx) {
     char* err = cx.err; size_t errn = cx.errn;
     const uint32_t x_t = A(0), n = A(2);
+    obs_read(x_t);
     if (x_t >= kMaxTemps || !g.temps[x_t]) return ERR("silu src temp %u empty", x_t);
     if (g.temp_bytes[x_t] != n * 2u)
         return ERR("silu n_elem mismatch (%u vs face %u)", n, g.temp_bytes[x_t] / 2u);
@@ -986,7 +1033,8 @@ int attn_workspace(uint32_t need, char* err, size_t errn) {
     g.attn_work_floats = 0;
     if (dev_malloc(reinterpret_cast<void**>(&g.attn_work), (size_t)need * 4u) != hipSuccess)
         return ERR("attn_decode workspace alloc");
-    if (hipMemset(g.attn_work, 0, (size_t)need * 4u) != hipSuccess) return ERR("attn_decode workspace clear");
+    if (launch_fill_zero(g.attn_work, (size_t)need * 4u, g.stream) != hipSuccess)
+        return ERR("attn_decode workspace clear");
     g.attn_work_floats = need;
     return 0;
 }
@@ -1081,6 +1129,7 @@ int op_rmsnorm_crouton(Ctx& cx) {
     char* err = cx.err; size_t errn = cx.errn;
     const uint32_t x_t = A(0), w_s = A(1), y_t = A(2), n = A(3), m = *cx.engine_m;
     g.stats.rmsnorm++;
+    obs_read(x_t);
     if (x_t >= kMaxTemps || !g.temps[x_t]) return ERR("rmsnorm src temp %u empty", x_t);
     if (w_s >= cx.b->n_slots || cx.b->slots[w_s].len != n * 2u) return ERR("rms w slot len mismatch");
     if (!m || m % 32u || n % 32u) return ERR("rms shape m%u n%u", m, n);
@@ -1260,6 +1309,7 @@ uint8_t* dma_resolve(const wt_blob* b, uint32_t ref, uint32_t off, uint32_t byte
         uint8_t* p = slot_ptr(b, s);
         return p ? p + off : nullptr;
     }
+    if (!is_dst) obs_read(ref);
     if (ref & 0x4000u) {
         const uint32_t t = ref & 0x3FFFu;
         if (t >= kMaxTemps || g.vtcm_off_arr[t] == kNone || !g.vtcm_pool) return nullptr;
@@ -1530,9 +1580,200 @@ void keep_graph(const wt_blob* b, uint32_t first, uint32_t count, hipGraphExec_t
     g_graphs.push_back(std::move(r));
 }
 
+// ---- load-time fusion of the reference attention chain ----
+// The reference composes prefill attention from runlist ops (oplist_exec.c:1081-1194,
+// 1709-1813): batched MATMUL_F16 q.k^T (w stored [N,K]) -> BINARY mul by a constant
+// scale slot -> BINARY add of a causal mask slot (optional) -> SOFTMAX over rows ->
+// batched MATMUL_F16 p.v, heads in the batch dimension ([H, S, 128], K/V already
+// expanded to H heads). A chain whose shapes, scale and mask match, and whose
+// intermediates no later op reads (observed on the blob's first full run), runs as one
+// flash-attention launch on later runs; the other ops of the chain are skipped. Results
+// are within the fp16 tolerance of the chain, not its exact per-op roundings.
+struct AttnChain {
+    uint32_t head = 0, len = 0, S = 0, H = 0;
+    float scale = 0.0f;
+    bool causal = false;
+    uint32_t q = 0, k = 0, v = 0, out = 0;
+    uint32_t inter[4] = {0, 0, 0, 0};
+    uint32_t n_inter = 0;
+};
+struct FusionPlan {
+    const wt_blob* b = nullptr;
+    uint32_t n_ops = 0;
+    uint64_t parse_epoch = 0;
+    bool observed = false;
+    std::vector<AttnChain> chains;
+    std::vector<uint8_t> live;             // per chain: an intermediate is read outside it
+    std::vector<int32_t> head_of, end_of;  // op index -> chain index (-1: none)
+    uint64_t used = 0;
+};
+constexpr size_t kMaxPlans = 8;
+std::vector<FusionPlan> g_plans;
+uint64_t g_plan_tick = 0;
+const FusionPlan* g_fplan = nullptr;   // plan applied to the current run (observed, fusion on)
+FusionPlan* g_obs_plan = nullptr;      // plan being observed during the current run
+uint32_t g_skip_until = kNone;         // ops up to here belong to a chain that ran fused
+uint32_t g_run_end = 0;                // one past the current run's last op
+
+bool fusion_on() {
+    if (g.fusion < 0) {
+        const char* e = std::getenv("GEHTP_NO_FUSE");
+        g.fusion = (e && e[0] && e[0] != '0') ? 0 : 1;
+    }
+    return g.fusion == 1;
+}
+
+bool is_temp_ref(uint32_t r) {
+    return !(r & 0x8000u) && (r & 0xE000u) != WT_REF_STATE_FLAG && (r & 0x3FFFu) < kMaxTemps;
+}
+
+// Host bytes of a constant slot reference (in-blob or external weights), or null.
+const uint16_t* slot_host_f16(const wt_blob* b, uint32_t ref, uint64_t n) {
+    if (!(ref & 0x8000u)) return nullptr;
+    const uint32_t s = ref & 0x7FFFu;
+    if (s >= b->n_slots) return nullptr;
+    const wt_slot& sl = b->slots[s];
+    if ((uint64_t)sl.len < n * 2u) return nullptr;
+    const uint8_t* p = nullptr;
+    if (sl.addr == WT_SLOT_EXT_WGT) {
+        p = g.ext_host ? g.ext_host + sl.offset : nullptr;
+    } else if (sl.addr < WT_SLOT_STATE) {
+        if ((uint64_t)sl.offset + sl.len > b->weight_bytes) return nullptr;
+        p = b->weight_base + sl.offset;
+    }
+    return (p && (reinterpret_cast<uintptr_t>(p) & 1u) == 0) ? reinterpret_cast<const uint16_t*>(p) : nullptr;
+}
+
+bool match_attn_chain(const wt_blob* b, uint32_t i, AttnChain& c) {
+    if ((uint64_t)i + 4 > b->n_ops) return false;
+    const wt_op& A = b->ops[i];
+    if (A.opcode != OP_MATMUL_F16 || A.n_args < 7) return false;
+    const uint32_t S = A.args[3], fl = A.args[6], H = fl >> 16;
+    if (S == 0 || A.args[4] != 128 || A.args[5] != S || (fl & 0xFFFFu) != 6u || H == 0) return false;
+    const uint64_t n = (uint64_t)H * S * S;
+    if (n > 0xFFFFFFFFull || !is_temp_ref(A.args[2])) return false;
+    c = AttnChain{};
+    c.head = i; c.S = S; c.H = H;
+    c.q = A.args[0]; c.k = A.args[1];
+    c.inter[c.n_inter++] = A.args[2];
+    // BINARY mul by a slot holding one positive finite value n times
+    uint32_t j = i + 1;
+    const wt_op& B = b->ops[j];
+    if (B.opcode != OP_BINARY_F16 || B.n_args < 5 || B.args[4] != 2u || B.args[0] != A.args[2] ||
+        B.args[3] != n || !is_temp_ref(B.args[2]))
+        return false;
+    const uint16_t* sc = slot_host_f16(b, B.args[1], n);
+    if (!sc) return false;
+    for (uint64_t e = 1; e < n; ++e)
+        if (sc[e] != sc[0]) return false;
+    c.scale = (float)__builtin_bit_cast(_Float16, sc[0]);
+    if (!(c.scale > 0.0f && c.scale < INFINITY)) return false;
+    uint32_t prev = B.args[2];
+    c.inter[c.n_inter++] = prev;
+    ++j;
+    // optional BINARY add of a mask slot: causal (0 where key <= query, -inf above), or all 0
+    const wt_op& C = b->ops[j];
+    if (C.opcode == OP_BINARY_F16 && C.n_args >= 5 && C.args[4] == 0u && C.args[0] == prev && C.args[3] == n &&
+        is_temp_ref(C.args[2])) {
+        const uint16_t* mk = slot_host_f16(b, C.args[1], n);
+        if (!mk) return false;
+        bool causal = true, zeros = true;
+        for (uint64_t e = 0; e < n && (causal || zeros); ++e) {
+            const uint32_t row = (uint32_t)((e / S) % S), col = (uint32_t)(e % S);
+            const bool zero = (mk[e] & 0x7FFFu) == 0;
+            zeros = zeros && zero;
+            causal = causal && (col <= row ? zero : mk[e] == 0xFC00u);
+        }
+        if (!causal && !zeros) return false;
+        c.causal = causal && S > 1;
+        prev = C.args[2];
+        c.inter[c.n_inter++] = prev;
+        ++j;
+    }
+    if ((uint64_t)j + 2 > b->n_ops) return false;
+    const wt_op& D = b->ops[j];
+    if (D.opcode != OP_SOFTMAX_F16 || D.n_args < 4 || D.args[0] != prev || D.args[2] != H * S || D.args[3] != S ||
+        !is_temp_ref(D.args[1]))
+        return false;
+    c.inter[c.n_inter++] = D.args[1];
+    const wt_op& E = b->ops[j + 1];
+    if (E.opcode != OP_MATMUL_F16 || E.n_args < 7 || E.args[0] != D.args[1] || E.args[3] != S || E.args[4] != S ||
+        E.args[5] != 128 || E.args[6] != ((H << 16) | 4u) || !is_temp_ref(E.args[2]))
+        return false;
+    c.v = E.args[1];
+    c.out = E.args[2];
+    c.len = j + 2 - i;
+    for (uint32_t t = 0; t < c.n_inter; ++t)   // inputs must come from outside the chain
+        if (c.inter[t] == c.q || c.inter[t] == c.k || c.inter[t] == c.v) return false;
+    return true;
+}
+
+// The plan of a blob (created, with its chains detected, on first sight of the blob as
+// parsed; a new plan drops the captured graphs, which may hold the blob's old form).
+FusionPlan* fusion_plan(const wt_blob* b) {
+    const uint64_t ep = g_parse_epoch.load(std::memory_order_relaxed);
+    for (FusionPlan& p : g_plans)
+        if (p.b == b && p.n_ops == b->n_ops && p.parse_epoch == ep) {
+            p.used = ++g_plan_tick;
+            return &p;
+        }
+    for (auto it = g_plans.begin(); it != g_plans.end();)   // stale plans of this blob
+        it = it->b == b ? g_plans.erase(it) : it + 1;
+    if (g_plans.size() >= kMaxPlans)
+        g_plans.erase(std::min_element(g_plans.begin(), g_plans.end(),
+                                       [](const FusionPlan& x, const FusionPlan& y) { return x.used < y.used; }));
+    drop_graphs();
+    FusionPlan p;
+    p.b = b; p.n_ops = b->n_ops; p.parse_epoch = ep; p.used = ++g_plan_tick;
+    p.head_of.assign(b->n_ops, -1);
+    p.end_of.assign(b->n_ops, -1);
+    for (uint32_t i = 0; i < b->n_ops; ++i) {
+        AttnChain c;
+        if (!match_attn_chain(b, i, c)) continue;
+        p.head_of[i] = (int32_t)p.chains.size();
+        p.end_of[i + c.len - 1] = (int32_t)p.chains.size();
+        p.chains.push_back(c);
+        i += c.len - 1;
+    }
+    p.live.assign(p.chains.size(), 0);
+    g.chains_found += p.chains.size();
+    g_plans.push_back(std::move(p));
+    return &g_plans.back();
+}
+
+int run_fused_attn(const wt_blob* b, const AttnChain& c, char* err, size_t errn) {
+    const uint32_t S = c.S, H = c.H;
+    const uint64_t bytes = (uint64_t)S * H * 128u * 2u;
+    const __half* q = reinterpret_cast<const __half*>(ref_ptr(b, c.q));
+    const __half* k = reinterpret_cast<const __half*>(ref_ptr(b, c.k));
+    const __half* v = reinterpret_cast<const __half*>(ref_ptr(b, c.v));
+    __half* o = reinterpret_cast<__half*>(temp_get(c.out, (uint32_t)bytes));
+    if (!q || !k || !v || !o) return ERR("fused attention ref fail");
+    const size_t qb = ref_bytes(b, c.q), kb = ref_bytes(b, c.k), vb = ref_bytes(b, c.v);
+    if ((qb && qb < bytes) || (kb && kb < bytes) || (vb && vb < bytes)) return ERR("fused attention operand too small");
+    CHECK_LAUNCH(launch_attn_prefill_hs(q, 128, S * 128, k, v, 128, S * 128, o, 128, S * 128, S, H, H, 128, c.scale,
+                                        c.causal, g.stream));
+    return 0;
+}
+
 // One op through its handler; returns the handler's status.
 int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* err, size_t errn) {
     const wt_op* op = &b->ops[i];
+    if (g_fplan) {
+        if (g_skip_until != kNone && i <= g_skip_until) return 0;   // part of a chain that ran fused
+        const int32_t ci = g_fplan->head_of[i];
+        if (ci >= 0 && !g_fplan->live[ci] && i + g_fplan->chains[ci].len <= g_run_end) {
+            const AttnChain& c = g_fplan->chains[ci];
+            const int rc = run_fused_attn(b, c, err, errn);
+            if (g_unmat.empty()) g_unmat.assign(kMaxTemps, 0);
+            for (uint32_t t = 0; t < c.n_inter; ++t)
+                if ((c.inter[t] & 0x3FFFu) != (c.out & 0x3FFFu)) g_unmat[c.inter[t] & 0x3FFFu] = 1;
+            g_skip_until = i + c.len - 1;
+            g.fused_runs++;
+            g.stats.ops++;
+            return rc;
+        }
+    }
     Ctx cx{b, op, engine_m, err, errn};
     const int rc = op->opcode < 64 ? kTable.fn[op->opcode](cx) : op_unsupported(cx);
     if (g.trace)
@@ -1540,6 +1781,16 @@ int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* 
                      op->args[0], op->args[1], op->args[2], op->args[3], rc, g.pool_used,
                      g.replay ? " (graph)" : "");
     g.stats.ops++;
+    if (g_obs.on && rc == 0) {
+        const int32_t ce = g_obs_plan->end_of[i];
+        if (ce >= 0) {   // the chain has run: watch its intermediates (not its output)
+            const AttnChain& c = g_obs_plan->chains[ce];
+            for (uint32_t t = 0; t < c.n_inter; ++t) {
+                const uint32_t id = c.inter[t] & 0x3FFFu;
+                if (id != (c.out & 0x3FFFu)) g_obs.armed[id] = ce;
+            }
+        }
+    }
     return rc;
 }
 
@@ -1596,7 +1847,35 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
     }
     const bool sync_each = std::getenv("GEHTP_SYNC_EACH_OP") != nullptr;
     const char* hk = hook_spec();
-    const bool can_graph = count && !timed && !sync_each && !(hk && hk[0]) && graphs_on();
+    const bool hooked = hk && hk[0];
+    // Attention-chain fusion: a blob's first full run is observed (ops run one by one);
+    // later runs launch the chains that qualified as single fused kernels. Per-op tensor
+    // hooks see every op's output, so they run without fusion.
+    g_fplan = nullptr;
+    g_obs_plan = nullptr;
+    g_skip_until = kNone;
+    g_run_end = first + count;
+    bool observing = false;
+    if (fusion_on() && !hooked) {
+        FusionPlan* fp = fusion_plan(b);
+        if (fp->observed) {
+            g_fplan = fp;
+        } else if (!fp->chains.empty() && first == 0 && count == b->n_ops) {
+            observing = true;
+            g_obs_plan = fp;
+            std::fill(fp->live.begin(), fp->live.end(), 0);
+            g_obs.armed.assign(kMaxTemps, -1);
+            g_obs.inter_of.assign(kMaxTemps, -1);
+            g_obs.written.assign(kMaxTemps, 0);
+            for (size_t c = 0; c < fp->chains.size(); ++c)
+                for (uint32_t t = 0; t < fp->chains[c].n_inter; ++t)
+                    g_obs.inter_of[fp->chains[c].inter[t] & 0x3FFFu] = (int32_t)c;
+            g_obs.live = &fp->live;
+            g_obs.on = true;
+        }
+    }
+    // The observed run neither replays nor qualifies a graph: the next run differs from it.
+    const bool can_graph = count && !timed && !sync_each && !hooked && graphs_on() && !observing;
     static HostIn hin;   // one engine per process; runs are not reentrant
     if (can_graph) {
         host_in(hin);
@@ -1627,6 +1906,13 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
         }
         if (rc == 0) hook_dump(ii);
         if (rc) fail = (int)i + 1;
+    }
+    if (observing) {
+        if (g_run_out_temp != kNone) obs_read(g_run_out_temp);   // copied to the host next
+        g_obs.on = false;
+        g_obs.live = nullptr;
+        if (!fail) g_obs_plan->observed = true;
+        g_obs_plan = nullptr;
     }
     if (capture) {
         // The captured work of this run (all of it, or the ops before a failing one)
@@ -1717,7 +2003,9 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
             g.in_active = true;
         }
     }
+    g_run_out_temp = out_ptr ? out_temp : kNone;
     int rc = wt_exec_run(b, engine_m, op_us, err, errn);
+    g_run_out_temp = kNone;
     if (rc == 0 && out_ptr && out_temp < kMaxTemps && g.temps[out_temp]) {
         if (hipMemcpy(out_ptr, g.temps[out_temp], g.last_bytes[out_temp], hipMemcpyDeviceToHost) != hipSuccess)
             rc = ERR("output copy failed");
@@ -1728,6 +2016,7 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
 
 uint8_t* wt_exec_temp(uint32_t id) {
     if (id >= kMaxTemps || !g.temps[id]) return nullptr;
+    if (!g_unmat.empty() && g_unmat[id]) return nullptr;   // intermediate of a fused chain
     std::vector<uint8_t>& m = g.mirror[id];
     m.resize(std::max<uint32_t>(g.temp_bytes[id], 1));
     if (g.stream) hipStreamSynchronize(g.stream);
@@ -1742,6 +2031,8 @@ void wt_exec_shutdown(void) {
     if (g.stream) hipStreamSynchronize(g.stream);
     g.stats = wt_exec_stats{};
     drop_graphs();
+    g_plans.clear();
+    g_fplan = nullptr;
     if (g.pool && g.pool_owned) dev_free(g.pool);
     for (void* p : g.retired_pools) dev_free(p);
     g.retired_pools.clear();
@@ -1782,12 +2073,12 @@ void wt_exec_shutdown(void) {
 void wt_exec_state_reset(void) {
     for (uint32_t i = 0; i < g.n_states; ++i) {
         State& s = g.st[i];
-        if (s.dev) hipMemset(s.dev, 0, s.bytes);
+        if (s.dev) launch_fill_zero(s.dev, s.bytes, g.stream);   // ordered before the next run's kernels
         s.count = 0;
         if (s.kv_ready) std::fill(s.posmap.begin(), s.posmap.end(), kNone);
         s.valid_prefix = 0;
     }
-    if (g.counters_dev) hipMemset(g.counters_dev, 0, WT_MAX_STATES * sizeof(uint32_t));
+    if (g.counters_dev) launch_fill_zero(g.counters_dev, WT_MAX_STATES * sizeof(uint32_t), g.stream);
 }
 
 void wt_exec_pool_init(uint8_t* base, uint32_t total_cap, uint32_t static_cap, const uint32_t* offsets) {
@@ -1829,6 +2120,21 @@ int wt_exec_set_graphs(int on) {
 void wt_exec_graph_stats(uint32_t* captures, uint32_t* replays) {
     if (captures) *captures = g.n_captures;
     if (replays) *replays = g.n_replays;
+}
+
+int wt_exec_set_fusion(int on) {
+    const int prev = fusion_on() ? 1 : 0;
+    if ((on ? 1 : 0) != prev) {
+        drop_graphs();   // graphs hold whichever form the runs that made them used
+        g_plans.clear();
+    }
+    g.fusion = on ? 1 : 0;
+    return prev;
+}
+
+void wt_exec_fusion_stats(uint64_t* chains_found, uint64_t* fused_runs) {
+    if (chains_found) *chains_found = g.chains_found;
+    if (fused_runs) *fused_runs = g.fused_runs;
 }
 
 void wt_exec_set_hook(const char* spec) { g.hook = spec; }

@@ -54,9 +54,9 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const _Float16* p) {
 // transposing LDS read, P^T straight from the score registers.
 template <bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
-    const __half* __restrict__ q, uint32_t ldq, const __half* __restrict__ k,
-    const __half* __restrict__ v, uint32_t ldkv, __half* __restrict__ out, uint32_t ldo,
-    uint32_t S, uint32_t H, uint32_t KVH, float scale_log2) {
+    const __half* __restrict__ q, uint32_t ldq, uint32_t qhs, const __half* __restrict__ k,
+    const __half* __restrict__ v, uint32_t ldkv, uint32_t kvhs, __half* __restrict__ out, uint32_t ldo,
+    uint32_t ohs, uint32_t S, uint32_t H, uint32_t KVH, float scale_log2) {
     __shared__ __align__(16) _Float16 Ks[KT * KS];
     __shared__ __align__(16) _Float16 Vs[KT * VSR];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
         const size_t qrow = min(my_q, S - 1);
 #pragma unroll
         for (int kk = 0; kk < HD / 16; ++kk)
-            qf[kk] = *reinterpret_cast<const h8_t*>(q + qrow * ldq + h * HD + kk * 16 + hl * 8);
+            qf[kk] = *reinterpret_cast<const h8_t*>(q + qrow * ldq + (size_t)h * qhs + kk * 16 + hl * 8);
     }
 
     f16x_t o[HD / 32];
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t key = min(kb + (tid >> 4) + 16 * i, S - 1);
-            const size_t off = (size_t)key * ldkv + kvh * HD + ch * 8;
+            const size_t off = (size_t)key * ldkv + (size_t)kvh * kvhs + ch * 8;
             kv4[i] = *reinterpret_cast<const u32x4*>(k + off);
             vv4[i] = *reinterpret_cast<const u32x4*>(v + off);
         }
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
 
     if (my_q < S) {
         const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-        __half* orow = out + (size_t)my_q * ldo + h * HD;
+        __half* orow = out + (size_t)my_q * ldo + (size_t)h * ohs;
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
@@ -513,17 +513,23 @@ hipError_t launch_attn_prefill(const __half* q, uint32_t ldq, const __half* k, c
                                uint32_t ldkv, __half* out, uint32_t ldo, uint32_t S, uint32_t H,
                                uint32_t KVH, uint32_t hd, float scale, bool causal,
                                hipStream_t st) {
+    return launch_attn_prefill_hs(q, ldq, HD, k, v, ldkv, HD, out, ldo, HD, S, H, KVH, hd, scale, causal, st);
+}
+
+hipError_t launch_attn_prefill_hs(const __half* q, uint32_t ldq, uint32_t qhs, const __half* k, const __half* v,
+                                  uint32_t ldkv, uint32_t kvhs, __half* out, uint32_t ldo, uint32_t ohs, uint32_t S,
+                                  uint32_t H, uint32_t KVH, uint32_t hd, float scale, bool causal, hipStream_t st) {
     if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
     if (!(scale > 0.0f && scale < INFINITY)) return hipErrorInvalidValue;   // the kernel's max needs scale > 0
     if (!S || !H) return hipSuccess;
     dim3 grid((S + QT - 1) / QT, H);
     const float sl2 = scale * kLog2e;
     if (causal)
-        hipLaunchKernelGGL(attn_prefill_kernel<true>, grid, dim3(256), 0, st, q, ldq, k, v, ldkv,
-                           out, ldo, S, H, KVH, sl2);
+        hipLaunchKernelGGL(attn_prefill_kernel<true>, grid, dim3(256), 0, st, q, ldq, qhs, k, v, ldkv, kvhs,
+                           out, ldo, ohs, S, H, KVH, sl2);
     else
-        hipLaunchKernelGGL(attn_prefill_kernel<false>, grid, dim3(256), 0, st, q, ldq, k, v, ldkv,
-                           out, ldo, S, H, KVH, sl2);
+        hipLaunchKernelGGL(attn_prefill_kernel<false>, grid, dim3(256), 0, st, q, ldq, qhs, k, v, ldkv, kvhs,
+                           out, ldo, ohs, S, H, KVH, sl2);
     return hipGetLastError();
 }
 

@@ -119,6 +119,12 @@ hipError_t launch_attn_prefill(const __half* q, uint32_t ldq, const __half* k, c
                                uint32_t ldkv, __half* out, uint32_t ldo, uint32_t S, uint32_t H,
                                uint32_t KVH, uint32_t hd, float scale, bool causal,
                                hipStream_t st);
+// The same with head strides (elements between heads h and h+1 of q, k/v and out; the
+// plain form uses 128, token-major [S, H, 128]); head-major [H, S, 128] operands pass
+// ld = 128 and head stride S*128.
+hipError_t launch_attn_prefill_hs(const __half* q, uint32_t ldq, uint32_t qhs, const __half* k, const __half* v,
+                                  uint32_t ldkv, uint32_t kvhs, __half* out, uint32_t ldo, uint32_t ohs, uint32_t S,
+                                  uint32_t H, uint32_t KVH, uint32_t hd, float scale, bool causal, hipStream_t st);
 // Split-KV decode: q [H][hd]; K/V read from the ring for positions [0, n_kv) where
 // n_kv = n_kv_host, or *count_dev when count_dev is non-null.
 hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slot_bytes,

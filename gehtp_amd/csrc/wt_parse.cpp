@@ -4,6 +4,7 @@
 // the same checks in the same order, so every malformed blob yields the same
 // WT_ERR_* code. The op metadata (arity, which argument positions are slot
 // references) lives in one table instead of two switch statements.
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 
@@ -83,6 +84,12 @@ inline const OpInfo* op_info(uint16_t opcode) {
 
 }  // namespace
 
+namespace gehtp {
+// Bumped by every successful wt_parse: the engine's per-blob caches (fused op chains)
+// are keyed by it, so a re-parsed blob, even at the same address, is analysed afresh.
+std::atomic<uint64_t> g_parse_epoch{0};
+}  // namespace gehtp
+
 extern "C" int wt_parse(const uint8_t* buf, size_t size, struct wt_blob* out) {
     if (!buf || !out || size < 16u) return WT_ERR_SHORT;
     if (std::memcmp(buf, "WTOP", 4) != 0) return WT_ERR_MAGIC;
@@ -159,6 +166,7 @@ extern "C" int wt_parse(const uint8_t* buf, size_t size, struct wt_blob* out) {
             if ((v & 0x8000u) && (v & 0x7FFFu) >= out->n_slots) return WT_ERR_BAD_REF;
         }
     }
+    gehtp::g_parse_epoch.fetch_add(1, std::memory_order_relaxed);
     return WT_OK;
 }
 

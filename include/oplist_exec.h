@@ -97,6 +97,19 @@ void wt_exec_set_hook(const char* spec);
 int  wt_exec_set_graphs(int on);
 void wt_exec_graph_stats(uint32_t* captures, uint32_t* replays);
 
+/* Extension: load-time fusion of the reference attention op chain. A batched
+ * MATMUL_F16 q.k^T (w stored [N,K], head dim 128) -> BINARY mul by a constant scale slot
+ * -> optional BINARY add of a causal (0 / -inf) or all-zero mask slot -> SOFTMAX ->
+ * batched MATMUL_F16 p.v, heads in the batch dimension, runs as one flash-attention
+ * kernel once the blob's first full run has shown that no other op reads the chain's
+ * intermediate temps. Results are within the fp16 tolerance of the op-by-op chain.
+ * Default on unless the environment sets GEHTP_NO_FUSE=1; wt_exec_set_fusion returns
+ * the previous setting; wt_exec_fusion_stats reports chains found in the blobs seen
+ * and chain executions run fused. After a fused run, wt_exec_temp returns NULL for the
+ * chain's intermediate temps (they were not computed). */
+int  wt_exec_set_fusion(int on);
+void wt_exec_fusion_stats(uint64_t* chains_found, uint64_t* fused_runs);
+
 /* W3 inspect report: one JSON line per call of emit (reference wt_w3.c). */
 void wt_w3_report(const char* blob_name, const uint8_t* buf, size_t size,
                   const struct wt_blob* w,

@@ -118,6 +118,106 @@ def test_attention_chain_vs_fused_vs_oracle(engine, oracle):
     assert_close(fused, ref, what="fused vs oracle")
 
 
+def test_attention_chain_fusion(engine, oracle):
+    """Load-time fusion: the blob's first full run executes the reference chain op by op
+    and finds its intermediates unread elsewhere; later runs execute it as one flash
+    attention kernel (the third as a graph capture, the fourth as a replay). Every run
+    stays within the parity tolerance of the oracle and of the op-by-op chain, and the
+    chain's intermediates are no longer readable once it ran fused."""
+    rng = np.random.default_rng(14)
+    S, H, KVH, hd = 192, 4, 2, 128
+    q, k, v = normal_f16(rng, S, H, hd), normal_f16(rng, S, KVH, hd), normal_f16(rng, S, KVH, hd)
+    bb, t_chain, _ = _attention_chain_blob(S, H, KVH, hd, q, k, v)
+    ref = oracle.attn_prefill(q, k, v, SCALE, True)
+    prev = engine.set_fusion(True)
+    try:
+        pb = engine.parse(bb.build())
+        found0, fused0 = engine.fusion_stats()
+        outs = []
+        for _ in range(4):
+            engine.run(pb)
+            outs.append(_h(engine.temp(t_chain), (H, S, hd)).transpose(1, 0, 2).copy())
+        found1, fused1 = engine.fusion_stats()
+        with pytest.raises(KeyError):
+            engine.temp(3)   # the softmax output (temps 0..4 are the chain's), not computed
+    finally:
+        engine.set_fusion(prev)
+    assert found1 - found0 == 1
+    assert fused1 - fused0 == 3
+    for i, o in enumerate(outs):
+        assert_close(o, ref, what=f"run {i}")
+    assert_close(outs[1], outs[0], what="fused vs op-by-op chain")
+    assert np.array_equal(outs[3].view(np.uint16), outs[2].view(np.uint16))   # replay == capture
+    assert np.array_equal(outs[2].view(np.uint16), outs[1].view(np.uint16))   # capture == direct
+
+
+def test_attention_chain_unfused_when_intermediate_read(engine):
+    """A later op reading the softmax output keeps the chain op by op: every run gives
+    bit-identical results and the probabilities stay readable."""
+    rng = np.random.default_rng(15)
+    S, H, KVH, hd = 96, 2, 1, 128
+    q, k, v = normal_f16(rng, S, H, hd), normal_f16(rng, S, KVH, hd), normal_f16(rng, S, KVH, hd)
+    bb, t_chain, _ = _attention_chain_blob(S, H, KVH, hd, q, k, v)
+    t_x = bb.temp()
+    bb.op(OP.BINARY_F16, 3, 3, t_x, H * S * S, 0)   # p + p, after the chain
+    pb = engine.parse(bb.build())
+    found0, fused0 = engine.fusion_stats()
+    outs = []
+    for _ in range(3):
+        engine.run(pb)
+        outs.append(engine.temp(t_chain))
+    p = _h(engine.temp(3), (H, S, S)).astype(np.float32)
+    found1, fused1 = engine.fusion_stats()
+    assert found1 - found0 == 1 and fused1 == fused0
+    assert outs[0] == outs[1] == outs[2]
+    assert np.allclose(p.sum(-1), 1.0, atol=2e-2)
+    x = _h(engine.temp(t_x), (H, S, S)).astype(np.float32)
+    assert np.array_equal(x, 2 * p)
+
+
+@pytest.mark.parametrize("zero_mask", [True, False])
+def test_attention_chain_fusion_noncausal(engine, oracle, zero_mask):
+    """Chains with an all-zero mask op, or without a mask op, fuse as non-causal
+    attention; with fusion switched off the same blob runs op by op."""
+    rng = np.random.default_rng(16 + zero_mask)
+    S, H, hd = 130, 2, 128
+    q, k, v = normal_f16(rng, S, H, hd), normal_f16(rng, S, H, hd), normal_f16(rng, S, H, hd)
+    bb = BlobBuilder()
+    sq = bb.add_slot(np.ascontiguousarray(q.transpose(1, 0, 2)))
+    sk = bb.add_slot(np.ascontiguousarray(k.transpose(1, 0, 2)))
+    sv = bb.add_slot(np.ascontiguousarray(v.transpose(1, 0, 2)))
+    scale = bb.add_slot(np.full(H * S * S, np.float16(SCALE), np.float16))
+    t_s, t_sc, t_m, t_p, t_o = (bb.temp() for _ in range(5))
+    bb.op(OP.MATMUL_F16, bb.slot_ref(sq), bb.slot_ref(sk), t_s, S, hd, S, (H << 16) | 4 | 2)
+    bb.op(OP.BINARY_F16, t_s, bb.slot_ref(scale), t_sc, H * S * S, 2)
+    src = t_sc
+    if zero_mask:
+        smask = bb.add_slot(np.zeros(H * S * S, np.float16))
+        bb.op(OP.BINARY_F16, t_sc, bb.slot_ref(smask), t_m, H * S * S, 0)
+        src = t_m
+    bb.op(OP.SOFTMAX_F16, src, t_p, H * S, S)
+    bb.op(OP.MATMUL_F16, t_p, bb.slot_ref(sv), t_o, S, S, hd, (H << 16) | 4)
+    ref = oracle.attn_prefill(q, k, v, SCALE, False)
+    found0, fused0 = engine.fusion_stats()
+    prev = engine.set_fusion(False)
+    try:
+        pb = engine.parse(bb.build())
+        for _ in range(2):
+            engine.run(pb)
+        chain = _h(engine.temp(t_o), (H, S, hd)).transpose(1, 0, 2).copy()
+        assert engine.fusion_stats()[1] == fused0
+    finally:
+        engine.set_fusion(prev)
+    pb = engine.parse(bb.build())
+    for _ in range(2):
+        engine.run(pb)
+    fused = _h(engine.temp(t_o), (H, S, hd)).transpose(1, 0, 2)
+    found1, fused1 = engine.fusion_stats()
+    assert found1 - found0 == 1 and fused1 - fused0 == 1
+    assert_close(chain, ref, what="op-by-op non-causal chain")
+    assert_close(fused, ref, what="fused non-causal chain")
+
+
 def _decode_blob(H, KVH, hd, max_pos):
     bb = BlobBuilder()
     kv_elems = KVH * hd
