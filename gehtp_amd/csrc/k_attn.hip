@@ -52,17 +52,27 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const _Float16* p) {
 // and its 32 scores of a stage; the online-softmax statistics need one exchange with
 // lane l^32. O^T = V^T P^T: the V^T operand comes from the row-major V tile through the
 // transposing LDS read, P^T straight from the score registers.
+//
+// Two halves of 4 waves split a tile's key stages: half p runs stages
+// [p*ns0, min(ns, (p+1)*ns0)) (ns0 = ceil(ns/2)) on its own LDS tiles, both halves in
+// lockstep (the shorter one idles through its last step), and half 1 hands its partial
+// (O, max, sum) to half 0 through LDS at the end. A causal tile then costs half its
+// stages: the heaviest tiles no longer set the kernel's time (the grid runs the heavy
+// tiles of every head first, one 8-wave workgroup per CU, the light ones behind them).
+constexpr uint32_t KV_HALF = KT * KS + KT * VSR;   // halves of one LDS K + V stage
+
 template <bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
+__global__ __launch_bounds__(512) void attn_prefill_kernel(
     const __half* __restrict__ q, uint32_t ldq, uint32_t qhs, const __half* __restrict__ k,
     const __half* __restrict__ v, uint32_t ldkv, uint32_t kvhs, __half* __restrict__ out, uint32_t ldo,
     uint32_t ohs, uint32_t S, uint32_t H, uint32_t KVH, float scale_log2) {
-    __shared__ __align__(16) _Float16 Ks[KT * KS];
-    __shared__ __align__(16) _Float16 Vs[KT * VSR];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __align__(16) _Float16 kvbuf[2 * KV_HALF];
+    const uint32_t part = threadIdx.x >> 8, tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
+    _Float16* const Ks = kvbuf + part * KV_HALF;
+    _Float16* const Vs = Ks + KT * KS;
     const uint32_t n_qt = (S + QT - 1) / QT;
-    const uint32_t qtile = n_qt - 1 - blockIdx.x;      // heaviest causal tiles first
-    const uint32_t h = blockIdx.y;
+    const uint32_t qtile = n_qt - 1 - blockIdx.y;      // heaviest causal tiles first
+    const uint32_t h = blockIdx.x;
     const uint32_t kvh = h / (H / KVH);
     const uint32_t q0 = qtile * QT;
     const uint32_t qw = q0 + wave * 32;                 // this wave's first query
@@ -106,8 +116,12 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     const uint32_t tr_row = 4 * hl + ((lane & 15) >> 2);
     const uint32_t tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-    load_kv(0);
-    for (uint32_t kb = 0; kb < kend; kb += KT) {
+    const uint32_t ns = (kend + KT - 1) / KT, ns0 = (ns + 1) / 2;
+    const uint32_t st0 = part * ns0, st1 = min(ns, st0 + ns0);   // this half's stages
+    const uint32_t klast = st1 > st0 ? min(st1 * KT, kend) - 1 : kend - 1;
+    load_kv(min(st0 * KT, kend - 1));
+    for (uint32_t it = 0; it < ns0; ++it) {
+        const uint32_t kb = (st0 + it) * KT;
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -116,7 +130,8 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
             *reinterpret_cast<u32x4*>(&Vs[key * VSR + ch * 8]) = vv4[i];
         }
         __syncthreads();
-        load_kv(min(kb + KT, kend - 1));
+        load_kv(min(kb + KT, klast));
+        if (st0 + it >= st1) continue;          // the shorter half's idle step
         if (CAUSAL && kb > qw + 31) continue;   // the whole stage is masked for this wave
 
         // Scores of the stage's two 32-key halves: two independent MFMA chains, all K
@@ -199,6 +214,32 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
         }
     }
 
+    // Half 1 hands (O, max, sum) to half 0 through the K/V tiles (lane-major floats: 66
+    // per lane, 64 lanes x 4 waves); half 0 rescales both to the common max.
+    __syncthreads();
+    float* xch = reinterpret_cast<float*>(kvbuf);
+    const uint32_t xl = wave * 64 + lane;
+    if (part == 1) {
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xch[(dt * 16 + r) * 256 + xl] = o[dt][r];
+        xch[64 * 256 + xl] = m_run;
+        xch[65 * 256 + xl] = l_run;
+    }
+    __syncthreads();
+    if (part == 1) return;
+    {
+        const float m1 = xch[64 * 256 + xl], l1 = xch[65 * 256 + xl];
+        const float m = fmaxf(m_run, m1);
+        const float a0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m) * scale_log2);
+        const float a1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m1 - m) * scale_log2);
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a0 + xch[(dt * 16 + r) * 256 + xl] * a1;
+        l_run = l_run * a0 + l1 * a1;
+    }
     if (my_q < S) {
         const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
         __half* orow = out + (size_t)my_q * ldo + (size_t)h * ohs;
@@ -522,13 +563,13 @@ hipError_t launch_attn_prefill_hs(const __half* q, uint32_t ldq, uint32_t qhs, c
     if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
     if (!(scale > 0.0f && scale < INFINITY)) return hipErrorInvalidValue;   // the kernel's max needs scale > 0
     if (!S || !H) return hipSuccess;
-    dim3 grid((S + QT - 1) / QT, H);
+    dim3 grid(H, (S + QT - 1) / QT);   // heads fastest: the heavy tiles of every head go first
     const float sl2 = scale * kLog2e;
     if (causal)
-        hipLaunchKernelGGL(attn_prefill_kernel<true>, grid, dim3(256), 0, st, q, ldq, qhs, k, v, ldkv, kvhs,
+        hipLaunchKernelGGL(attn_prefill_kernel<true>, grid, dim3(512), 0, st, q, ldq, qhs, k, v, ldkv, kvhs,
                            out, ldo, ohs, S, H, KVH, sl2);
     else
-        hipLaunchKernelGGL(attn_prefill_kernel<false>, grid, dim3(256), 0, st, q, ldq, qhs, k, v, ldkv, kvhs,
+        hipLaunchKernelGGL(attn_prefill_kernel<false>, grid, dim3(512), 0, st, q, ldq, qhs, k, v, ldkv, kvhs,
                            out, ldo, ohs, S, H, KVH, sl2);
     return hipGetLastError();
 }
