@@ -103,17 +103,22 @@ def main() -> int:
     prompt = rng.integers(0, cfg.vocab, S)
     x_prompt = np.ascontiguousarray(emb[prompt]).tobytes()
 
-    # Prefill: the first run also uploads the weight image; time the second.
+    # Prefill: the first run also uploads the weight image.
     eng.state_reset()
     t0 = time.perf_counter()
     eng.run_io(pp, x_prompt, tp["tok"])
     log(f"prefill #1 (incl. weight upload) {time.perf_counter() - t0:.2f}s")
-    eng.state_reset()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    out, _ = eng.run_io(pp, x_prompt, tp["tok"])
-    torch.cuda.synchronize()
-    t_prefill = time.perf_counter() - t0
+    # Then the median of three timed prefills, each from reset states (single runs vary
+    # by a few percent).
+    times = []
+    for _ in range(3):
+        eng.state_reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out, _ = eng.run_io(pp, x_prompt, tp["tok"])
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    t_prefill = sorted(times)[1]
     tok = int(np.frombuffer(out, np.int32)[0])
     logits = np.frombuffer(eng.temp(tp["logits"]), np.float16)[:cfg.vocab].astype(np.float32)
     top2 = np.sort(logits)[-2:]
