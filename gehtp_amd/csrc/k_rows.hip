@@ -540,6 +540,122 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QkRopeKvArgs A) {
     }
 }
 
+// Prefill form of qk_rope_kv_kernel: TOK tokens per workgroup, one 128-dim head row per
+// 8-lane group, lane g owning elements [8g, 8g+8) and [64+8g, 64+8g+8) — both halves of
+// its RoPE pairs, so the rotation needs no lane exchange. The per-head work (sum of
+// squares reduced over 8 lanes instead of 64, the rms and its reciprocal) is shared by
+// 8 heads per instruction. The token's RoPE table (64 cos / sin pairs, evaluated in
+// double) is built in LDS by one thread per entry while the head rows are in flight.
+// RoPE runs on packed f16 operations: each product and sum of two f16 values rounded
+// once to f16 equals the f32 operation rounded to f16 (24 >= 2*11 + 1 bits, so the
+// double rounding is innocuous), the arithmetic of rope_kernel. Pointers, row stride and
+// ring slot size must be 16-byte aligned; the counter is not advanced here.
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2v u2h2(uint32_t w) { return __builtin_bit_cast(h2v, w); }
+__device__ __forceinline__ uint32_t h22u(h2v v) { return __builtin_bit_cast(uint32_t, v); }
+
+template <uint32_t TOK>
+__global__ __launch_bounds__(256) void qk_rope_kv_rows_kernel(QkRopeKvArgs A, uint32_t n_tok) {
+    constexpr uint32_t HD = 128, IT = TOK * 64 / 32;   // head rows per lane group, at most
+    __shared__ uint32_t s_pos;
+    __shared__ __align__(16) _Float16 s_cos[TOK][64], s_sin[TOK][64];
+    const uint32_t tid = threadIdx.x, t0 = blockIdx.x * TOK;
+    const uint32_t nt = min(TOK, n_tok - t0), nh = A.H + A.KVH, nrows = nt * nh;
+    const uint32_t grp = tid >> 3, g = tid & 7;
+    if (tid == 0) s_pos = *A.count;
+    // Head rows grp, grp + 32, ...; loads of rows past the workgroup's are skipped by a
+    // workgroup-uniform test, the last group of a partial pass loads a clamped row.
+    u32x4 xl[IT], xh[IT];
+#pragma unroll
+    for (uint32_t it = 0; it < IT; ++it) {
+        if (32 * it >= nrows) break;
+        const uint32_t hr = min(grp + 32 * it, nrows - 1), tk = hr / nh, r = hr - tk * nh;
+        const __half* row = A.qkv + (size_t)(t0 + tk) * A.ld + (size_t)r * HD;
+        xl[it] = *reinterpret_cast<const u32x4*>(row + 8 * g);
+        xh[it] = *reinterpret_cast<const u32x4*>(row + 64 + 8 * g);
+    }
+    const u32x4 qgl = *reinterpret_cast<const u32x4*>(A.qg + 8 * g), qgh = *reinterpret_cast<const u32x4*>(A.qg + 64 + 8 * g);
+    const u32x4 kgl = *reinterpret_cast<const u32x4*>(A.kg + 8 * g), kgh = *reinterpret_cast<const u32x4*>(A.kg + 64 + 8 * g);
+    __syncthreads();
+    const uint32_t pos0 = s_pos + t0;
+    for (uint32_t e = tid; e < TOK * 64; e += 256) {
+        const uint32_t tk = e >> 6, i = e & 63;
+        const uint32_t w = dev::rope_cs_bits(pos0 + tk, dev::rope_inv(i, A.theta));
+        s_cos[tk][i] = __builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+        s_sin[tk][i] = __builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (uint32_t it = 0; it < IT; ++it) {
+        if (32 * it >= nrows) break;
+        const uint32_t hr = grp + 32 * it, hc = min(hr, nrows - 1), tk = hc / nh, r = hc - tk * nh;
+        const bool is_q = r < A.H;
+        const u32x4 gl = is_q ? qgl : kgl, gh = is_q ? qgh : kgh;
+        float x[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x[2 * k] = dev::bits_f((uint16_t)(xl[it][k] & 0xFFFFu));
+            x[2 * k + 1] = dev::bits_f((uint16_t)(xl[it][k] >> 16));
+            x[8 + 2 * k] = dev::bits_f((uint16_t)(xh[it][k] & 0xFFFFu));
+            x[8 + 2 * k + 1] = dev::bits_f((uint16_t)(xh[it][k] >> 16));
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) ss += (double)x[k] * (double)x[k];
+        ss += dev::dpp<dev::kDppQuadSwap1>(ss);
+        ss += dev::dpp<dev::kDppQuadSwap2>(ss);
+        ss += dev::dpp<dev::kDppRowHalfMirror>(ss);
+        const float rms = (float)sqrt(ss / 128.0 + 1e-6);
+        const float y = __fdiv_rn(1.0f, rms);
+        uint32_t hw[8];   // normalized halves as f16 pairs: [0,4) low half, [4,8) high half
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t gw = k < 4 ? gl[k] : gh[k - 4];
+            const float h0 = __fadd_rn(__fmul_rn(dev::div_markstein(x[2 * k], rms, y), dev::bits_f((uint16_t)(gw & 0xFFFFu))), 0.0f);
+            const float h1 = __fadd_rn(__fmul_rn(dev::div_markstein(x[2 * k + 1], rms, y), dev::bits_f((uint16_t)(gw >> 16))), 0.0f);
+            hw[k] = h22u(h2v{(_Float16)h0, (_Float16)h1});
+        }
+        const u32x4 cw = *reinterpret_cast<const u32x4*>(&s_cos[tk][8 * g]);
+        const u32x4 sw = *reinterpret_cast<const u32x4*>(&s_sin[tk][8 * g]);
+        u32x4 yl, yh;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const h2v a = u2h2(hw[k]), b = u2h2(hw[4 + k]), c = u2h2(cw[k]), sn = u2h2(sw[k]);
+            const h2v ac = a * c, bs = b * sn, bc = b * c, as = a * sn;
+            yl[k] = h22u(ac - bs);
+            yh[k] = h22u(bc + as);
+        }
+        if (hr >= nrows) continue;
+        const uint32_t tok = t0 + tk;
+        if (is_q) {
+            __half* qo = A.q_out + (size_t)tok * A.H * HD + (size_t)r * HD;
+            *reinterpret_cast<u32x4*>(qo + 8 * g) = yl;
+            *reinterpret_cast<u32x4*>(qo + 64 + 8 * g) = yh;
+        } else {
+            const uint32_t kh = r - A.H;
+            __half* kf = reinterpret_cast<__half*>(A.ring + (size_t)((pos0 + tk) % A.nslots) * A.slot_bytes) + kh * HD;
+            *reinterpret_cast<u32x4*>(kf + 8 * g) = yl;
+            *reinterpret_cast<u32x4*>(kf + 64 + 8 * g) = yh;
+            if (A.k_out) {
+                __half* ko = A.k_out + (size_t)tok * A.KVH * HD + (size_t)kh * HD;
+                *reinterpret_cast<u32x4*>(ko + 8 * g) = yl;
+                *reinterpret_cast<u32x4*>(ko + 64 + 8 * g) = yh;
+            }
+        }
+    }
+    // V rows: 16-byte chunks copied to the ring (and v_out).
+    const uint32_t vc = A.KVH * HD / 8;
+    for (uint32_t i = tid; i < nt * vc; i += 256) {
+        const uint32_t tk = i / vc, c = i - tk * vc;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(A.qkv + (size_t)(t0 + tk) * A.ld + (size_t)nh * HD + 8 * c);
+        __half* vf = reinterpret_cast<__half*>(A.ring + (size_t)((pos0 + tk) % A.nslots) * A.slot_bytes) + A.KVH * HD;
+        *reinterpret_cast<u32x4*>(vf + 8 * c) = v;
+        if (A.v_out) *reinterpret_cast<u32x4*>(A.v_out + (size_t)(t0 + tk) * A.KVH * HD + 8 * c) = v;
+    }
+}
+constexpr uint32_t kQkRowsTok = 4;
+
 // KV gather with GQA expansion (oplist_exec.c:2183-2231): kT[h][d][p], v[h][p][d].
 __global__ void kv_gather_kernel(const uint8_t* __restrict__ ring, uint32_t slot_bytes,
                                  uint32_t nslots, __half* __restrict__ kT, __half* __restrict__ vo,
@@ -741,7 +857,14 @@ hipError_t launch_qk_rope_kv(const __half* qkv, uint32_t n_tok, uint32_t H, uint
     if (!n_tok) return hipSuccess;
     QkRopeKvArgs A{qkv, (H + 2 * KVH) * 128u, H, KVH, q_gamma, k_gamma, theta, q_out, k_out, v_out,
                    ring, slot_bytes, nslots, count_dev, n_tok == 1 ? 1 : 0};
-    hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(n_tok), dim3(256), 0, st, A);
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    const bool rows = n_tok > 1 && al16(qkv) && al16(q_gamma) && al16(k_gamma) && al16(q_out) && al16(k_out) &&
+                      al16(v_out) && al16(ring) && slot_bytes % 16 == 0;
+    if (rows)
+        hipLaunchKernelGGL(qk_rope_kv_rows_kernel<kQkRowsTok>, dim3((n_tok + kQkRowsTok - 1) / kQkRowsTok), dim3(256),
+                           0, st, A, n_tok);
+    else
+        hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(n_tok), dim3(256), 0, st, A);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || n_tok == 1) return e;
     hipLaunchKernelGGL(counter_add_kernel, dim3(1), dim3(1), 0, st, count_dev, n_tok);

@@ -400,13 +400,16 @@ def test_w4g_gemm_split_k(lib, oracle, torch_dev, mode, use_res, M):
     assert (a == b).mean() > 0.99
 
 
-@pytest.mark.parametrize("n_tok", [1, 37])
-def test_qk_rope_kv(lib, oracle, torch_dev, n_tok):
+@pytest.mark.parametrize("n_tok,H,KVH", [(1, 8, 2), (37, 8, 2), (130, 32, 8), (6, 16, 8), (3, 40, 24)])
+def test_qk_rope_kv(lib, oracle, torch_dev, n_tok, H, KVH):
     """OP_QK_ROPE_KV_F16 = per-head RMSNORM2 (q_norm / k_norm), ROPE at the counter
-    position, KV append into the reference ring layout; counter advances by n_tok."""
+    position, KV append into the reference ring layout; counter advances by n_tok.
+    One token runs the one-workgroup kernel, more tokens the multi-token row kernel
+    (partial last workgroup, 64 heads per token at most)."""
     import torch
     rng = np.random.default_rng(50 + n_tok)
-    H, KVH, hd, nslots, pos0 = 8, 2, 128, 64, 5
+    hd, pos0 = 128, 5
+    nslots = 64 if pos0 + n_tok <= 64 else 256
     qkv = normal_f16(rng, n_tok, (H + 2 * KVH) * hd) * np.float16(3)
     qg = rng.uniform(0.8, 1.2, hd).astype(np.float16)
     kg = rng.uniform(0.8, 1.2, hd).astype(np.float16)
@@ -415,11 +418,13 @@ def test_qk_rope_kv(lib, oracle, torch_dev, n_tok):
     count = torch.tensor([pos0], dtype=torch.int32, device=torch_dev)
     q_out = torch.empty((n_tok, H * hd), dtype=torch.float16, device=torch_dev)
     k_out = torch.empty((n_tok, KVH * hd), dtype=torch.float16, device=torch_dev)
+    v_out = torch.empty((n_tok, KVH * hd), dtype=torch.float16, device=torch_dev)
     assert lib.gehtp_qk_rope_kv(ptr(to_dev(qkv, torch_dev)), n_tok, H, KVH, ptr(to_dev(qg, torch_dev)),
-                                ptr(to_dev(kg, torch_dev)), 1e6, ptr(q_out), ptr(k_out), None, ptr(ring),
+                                ptr(to_dev(kg, torch_dev)), 1e6, ptr(q_out), ptr(k_out), ptr(v_out), ptr(ring),
                                 state_bytes, ptr(count), stream_ptr()) == 0
     _sync()
     assert int(count.item()) == pos0 + n_tok
+    assert np.array_equal(from_dev(v_out), qkv[:, (H + KVH) * hd:])
     q = qkv[:, :H * hd]
     k = qkv[:, H * hd:(H + KVH) * hd]
     v = qkv[:, (H + KVH) * hd:]
