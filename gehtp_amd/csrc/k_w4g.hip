@@ -516,6 +516,62 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
         }
 }
 
+// Split-K finish, vector form (N, ldy, ldr multiples of 8, 16-byte aligned rows): a
+// thread sums 8 consecutive fp32 columns over the parts in part order (two 16-byte loads
+// per part) and stores 8 (plain) or 4 (SwiGLU) outputs at once, with the arithmetic of
+// w4g_store / w4g_store_swiglu.
+__global__ __launch_bounds__(256) void w4g_splitk_reduce8_kernel(const float* __restrict__ part, uint32_t parts,
+                                                                 __half* __restrict__ y, uint32_t ldy, uint32_t M,
+                                                                 uint32_t N, const __half* __restrict__ res,
+                                                                 uint32_t ldr, int swiglu) {
+    const uint32_t n8 = N / 8;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)M * n8) return;
+    const uint32_t row = (uint32_t)(i / n8), c = 8 * (uint32_t)(i % n8);
+    const float* p = part + (size_t)row * N + c;
+    float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    for (uint32_t k = 1; k < parts; ++k) {
+        p += (size_t)M * N;
+        const float4 u = *reinterpret_cast<const float4*>(p), v = *reinterpret_cast<const float4*>(p + 4);
+        a.x = __fadd_rn(a.x, u.x); a.y = __fadd_rn(a.y, u.y); a.z = __fadd_rn(a.z, u.z); a.w = __fadd_rn(a.w, u.w);
+        b.x = __fadd_rn(b.x, v.x); b.y = __fadd_rn(b.y, v.y); b.z = __fadd_rn(b.z, v.z); b.w = __fadd_rn(b.w, v.w);
+    }
+    const float sum[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    if (!swiglu) {
+        u32x4 rv = {0u, 0u, 0u, 0u};
+        if (res) rv = *reinterpret_cast<const u32x4*>(res + (size_t)row * ldr + c);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint16_t lo = f2hb(sum[2 * e]), hi = f2hb(sum[2 * e + 1]);
+            if (res) {
+                lo = f2hb(__fadd_rn(h2f(lo), h2f((uint16_t)(rv[e] & 0xFFFFu))));
+                hi = f2hb(__fadd_rn(h2f(hi), h2f((uint16_t)(rv[e] >> 16))));
+            }
+            o[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        *reinterpret_cast<u32x4*>(y + (size_t)row * ldy + c) = o;
+    } else {
+        const uint32_t oc = c / 2;
+        uint32_t rv[2] = {0u, 0u};
+        if (res) {
+            const uint2 r2 = *reinterpret_cast<const uint2*>(res + (size_t)row * ldr + oc);
+            rv[0] = r2.x; rv[1] = r2.y;
+        }
+        uint16_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float gv = h2f(f2hb(sum[2 * j])), uv = h2f(f2hb(sum[2 * j + 1]));
+            const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
+            uint16_t v = f2hb(__fmul_rn(act, uv));
+            if (res) v = f2hb(__fadd_rn(h2f(v), h2f((uint16_t)(rv[j >> 1] >> (16 * (j & 1))))));
+            o[j] = v;
+        }
+        *reinterpret_cast<uint2*>(y + (size_t)row * ldy + oc) =
+            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+    }
+}
+
 // Split-K finish: element pair (row, 2p..2p+1) sums the fp32 parts in part order and
 // stores through the GEMM's own epilogue.
 __global__ __launch_bounds__(256) void w4g_splitk_reduce_kernel(const float* __restrict__ part, uint32_t parts,
@@ -625,9 +681,19 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
         const uint32_t per = (steps + parts - 1) / parts;
         hipLaunchKernelGGL(w4g_gemm_kernel, dim3(mt * nt * parts), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K,
                            epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, nt, per, epi.split_ws);
-        const size_t pairs = (size_t)M * ((N + 1) / 2);
-        hipLaunchKernelGGL(w4g_splitk_reduce_kernel, dim3((uint32_t)((pairs + 255) / 256)), dim3(256), 0, st,
-                           epi.split_ws, parts, y, ldy, M, N, epi.res, epi.ldr, epi.swiglu ? 1 : 0);
+        const uint32_t oal = epi.swiglu ? 4u : 8u;   // output elements per vector store
+        const bool vec = N % 8 == 0 && ldy % oal == 0 && (uintptr_t)y % (2 * oal) == 0 &&
+                         (!epi.res || (epi.ldr % oal == 0 && (uintptr_t)epi.res % (2 * oal) == 0)) &&
+                         (uintptr_t)epi.split_ws % 16 == 0;
+        if (vec) {
+            const size_t n8 = (size_t)M * (N / 8);
+            hipLaunchKernelGGL(w4g_splitk_reduce8_kernel, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, st,
+                               epi.split_ws, parts, y, ldy, M, N, epi.res, epi.ldr, epi.swiglu ? 1 : 0);
+        } else {
+            const size_t pairs = (size_t)M * ((N + 1) / 2);
+            hipLaunchKernelGGL(w4g_splitk_reduce_kernel, dim3((uint32_t)((pairs + 255) / 256)), dim3(256), 0, st,
+                               epi.split_ws, parts, y, ldy, M, N, epi.res, epi.ldr, epi.swiglu ? 1 : 0);
+        }
         return hipGetLastError();
     }
     hipLaunchKernelGGL(w4g_gemm_kernel, dim3(mt * nt), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K, epi.res,

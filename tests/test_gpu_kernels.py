@@ -357,15 +357,17 @@ def test_w4g_fused_gemm_epilogues(lib, oracle, torch_dev):
     assert_close(from_dev(y), ref, what="gemm swiglu+res")
 
 
-@pytest.mark.parametrize("mode,use_res,M", [(0, False, 384), (0, True, 200), (1, False, 384), (1, True, 131)])
-def test_w4g_gemm_split_k(lib, oracle, torch_dev, mode, use_res, M):
+@pytest.mark.parametrize("mode,use_res,M,N", [(0, False, 384, 1280), (0, True, 200, 1280), (1, False, 384, 1280),
+                                              (1, True, 131, 1280), (0, True, 77, 1276), (1, True, 45, 1284)])
+def test_w4g_gemm_split_k(lib, oracle, torch_dev, mode, use_res, M, N):
     """Narrow N, long K: with a workspace the GEMM splits K in two (fp32 sums of each half,
-    added in a second pass through the same epilogue). Checked against the oracle and
+    added in a second pass through the same epilogue: 8 columns per thread when N and the
+    output rows allow 16-byte access, else column pairs). Checked against the oracle and
     against the one-pass GEMM (only the fp32 sum order differs: almost everywhere identical).
     K = 4160 has 65 K steps, so the two halves are unequal."""
     import torch
-    rng = np.random.default_rng(60 + 2 * mode + use_res)
-    N, K = (2 * 640 if mode else 1280), 4160
+    rng = np.random.default_rng(60 + 2 * mode + use_res + N)
+    K = 4160
     n_out = N // 2 if mode else N
     need = lib.gehtp_w4g_split_bytes(M, N, K)
     assert need == 2 * M * N * 4
