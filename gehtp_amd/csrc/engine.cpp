@@ -939,6 +939,16 @@ int gemm_split_ws(W4gEpilogue& epi, uint32_t M, uint32_t N, uint32_t K, char* er
     return 0;
 }
 
+// Normalized rows that a K-split GEMM's finishing pass already wrote into norm_buf for
+// the next op (an OP_W4G_FUSED_F16 whose RMSNorm input is that GEMM's output).
+struct PreNorm {
+    const wt_op* op = nullptr;   // the op they are for
+    const void* src = nullptr;
+    const void* gamma = nullptr;
+    uint32_t M = 0, K = 0;
+};
+PreNorm g_prenorm;
+
 int op_w4g_fused(Ctx& cx) {
     char* err = cx.err; size_t errn = cx.errn;
     const uint32_t M = A(4), K = A(5), N = A(6), mode = A(9), flags = A(10);
@@ -985,13 +995,37 @@ int op_w4g_fused(Ctx& cx) {
         return 0;
     }
     const __half* src = a;
-    if (gamma) {   // normalize the rows into scratch, then the GEMM
-        if (scratch(&g.norm_buf, &g.norm_cap, (size_t)M * K * 2, err, errn)) return -1;
-        CHECK_LAUNCH(launch_rmsnorm2(a, gamma, nullptr, reinterpret_cast<__half*>(g.norm_buf), M, K, g.stream));
+    const PreNorm pre = g_prenorm;
+    g_prenorm = PreNorm{};
+    if (gamma) {   // normalize the rows into scratch (unless the previous op did), then the GEMM
+        const bool done = pre.op == cx.op && pre.src == a && pre.gamma == gamma && pre.M == M && pre.K == K &&
+                          g.norm_buf && g.norm_cap >= (size_t)M * K * 2;
+        if (!done) {
+            if (scratch(&g.norm_buf, &g.norm_cap, (size_t)M * K * 2, err, errn)) return -1;
+            CHECK_LAUNCH(launch_rmsnorm2(a, gamma, nullptr, reinterpret_cast<__half*>(g.norm_buf), M, K, g.stream));
+        }
         src = reinterpret_cast<const __half*>(g.norm_buf);
     }
     if (gemm_split_ws(epi, M, N, K, err, errn)) return -1;
+    // The next op normalizing this output for its own GEMM: the split's finishing pass
+    // writes those rows too (one pass over the output instead of two).
+    bool norm_done = false;
+    const wt_op* nx = cx.op + 1;
+    const __half* ngamma = nullptr;
+    if (!gamma && !swiglu && ldy == n_out && epi.split_ws && nx < cx.b->ops + cx.b->n_ops &&
+        nx->opcode == OP_W4G_FUSED_F16 && nx->n_args >= 11 && nx->args[0] == A(3) && nx->args[4] == M &&
+        nx->args[5] == n_out && !w4g_gemv_supported(M, n_out) && (nx->args[7] & 0x8000u) &&
+        (nx->args[7] & 0x7FFFu) < cx.b->n_slots && cx.b->slots[nx->args[7] & 0x7FFFu].len >= (uint64_t)n_out * 2u) {
+        ngamma = reinterpret_cast<const __half*>(slot_ptr(cx.b, nx->args[7] & 0x7FFFu));
+        if (ngamma) {
+            if (scratch(&g.norm_buf, &g.norm_cap, (size_t)M * n_out * 2, err, errn)) return -1;
+            epi.norm_gamma = ngamma;
+            epi.norm_out = reinterpret_cast<__half*>(g.norm_buf);
+            epi.norm_done = &norm_done;
+        }
+    }
     CHECK_LAUNCH(launch_w4g_gemm(src, K, wq, ws, y, ldy, M, N, K, g.stream, epi));
+    if (norm_done) g_prenorm = PreNorm{nx, y, ngamma, M, n_out};
     return 0;
 }
 
@@ -1765,6 +1799,7 @@ int run_fused_attn(const wt_blob* b, const AttnChain& c, char* err, size_t errn)
 // One op through its handler; returns the handler's status.
 int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* err, size_t errn) {
     const wt_op* op = &b->ops[i];
+    if (g_prenorm.op != op) g_prenorm = PreNorm{};   // only ever for the very next op
     if (g_fplan) {
         if (g_skip_until != kNone && i <= g_skip_until) return 0;   // part of a chain that ran fused
         const int32_t ci = g_fplan->head_of[i];
@@ -1832,6 +1867,7 @@ extern "C" {
 
 int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, uint32_t* engine_m,
                       int64_t* op_us, char* err, size_t errn) {
+    g_prenorm = PreNorm{};
     char dummy_err[8];
     if (!err || !errn) { err = dummy_err; errn = sizeof dummy_err; }
     uint32_t dummy_m = 0;

@@ -572,6 +572,75 @@ __global__ __launch_bounds__(256) void w4g_splitk_reduce8_kernel(const float* __
     }
 }
 
+// Split-K finish fused with the RMSNorm of the finished rows (the next op's input): one
+// workgroup per row, each thread finishing 8-column groups as w4g_splitk_reduce8_kernel
+// does (plain epilogue) and keeping them in registers; then RMSNORM2_F16 without bias
+// over the row as the decode GEMV's prologue computes it (squares of the fp16 row in
+// double, rms = sqrt(sum / N + 1e-6) rounded to float, x / rms as Markstein's corrected
+// quotient, times gamma, + 0, rounded to fp16) into xn [M, N].
+constexpr uint32_t kRedNormG = 2;   // 8-column groups per thread: N <= 4096
+__global__ __launch_bounds__(256) void w4g_splitk_reduce_norm_kernel(
+    const float* __restrict__ part, uint32_t parts, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
+    const __half* __restrict__ res, uint32_t ldr, const __half* __restrict__ gamma, __half* __restrict__ xn) {
+    __shared__ double s_ss[4];
+    const uint32_t row = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6, n8 = N / 8;
+    u32x4 xv[kRedNormG];
+    double ss = 0.0;
+#pragma unroll
+    for (uint32_t j = 0; j < kRedNormG; ++j) {
+        const uint32_t q = t + 256 * j;
+        xv[j] = u32x4{0u, 0u, 0u, 0u};
+        if (q >= n8) continue;
+        const float* p = part + (size_t)row * N + 8 * q;
+        float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+        for (uint32_t k = 1; k < parts; ++k) {
+            p += (size_t)M * N;
+            const float4 u = *reinterpret_cast<const float4*>(p), v = *reinterpret_cast<const float4*>(p + 4);
+            a.x = __fadd_rn(a.x, u.x); a.y = __fadd_rn(a.y, u.y); a.z = __fadd_rn(a.z, u.z); a.w = __fadd_rn(a.w, u.w);
+            b.x = __fadd_rn(b.x, v.x); b.y = __fadd_rn(b.y, v.y); b.z = __fadd_rn(b.z, v.z); b.w = __fadd_rn(b.w, v.w);
+        }
+        const float sum[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        u32x4 rv = {0u, 0u, 0u, 0u};
+        if (res) rv = *reinterpret_cast<const u32x4*>(res + (size_t)row * ldr + 8 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint16_t lo = f2hb(sum[2 * e]), hi = f2hb(sum[2 * e + 1]);
+            if (res) {
+                lo = f2hb(__fadd_rn(h2f(lo), h2f((uint16_t)(rv[e] & 0xFFFFu))));
+                hi = f2hb(__fadd_rn(h2f(hi), h2f((uint16_t)(rv[e] >> 16))));
+            }
+            xv[j][e] = (uint32_t)lo | ((uint32_t)hi << 16);
+            const double dl = (double)h2f(lo), dh = (double)h2f(hi);
+            ss += dl * dl;
+            ss += dh * dh;
+        }
+        *reinterpret_cast<u32x4*>(y + (size_t)row * ldy + 8 * q) = xv[j];
+    }
+    ss = dev::wave_sum(ss);
+    if (lane == 0) s_ss[wave] = ss;
+    __syncthreads();
+    const double tot = ((s_ss[0] + s_ss[1]) + s_ss[2]) + s_ss[3];
+    const float rms = (float)sqrt(tot / (double)N + 1e-6);
+    const float rcp = __fdiv_rn(1.0f, rms);
+    auto norm = [&](uint16_t xb, uint16_t gb) {
+        const float x = h2f(xb), qt = x * rcp;
+        const float d = __builtin_fmaf(__builtin_fmaf(-qt, rms, x), rcp, qt);
+        return f2hb(__fadd_rn(__fmul_rn(d, h2f(gb)), 0.0f));
+    };
+#pragma unroll
+    for (uint32_t j = 0; j < kRedNormG; ++j) {
+        const uint32_t q = t + 256 * j;
+        if (q >= n8) continue;
+        const u32x4 g4 = *reinterpret_cast<const u32x4*>(gamma + 8 * q);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = (uint32_t)norm((uint16_t)(xv[j][e] & 0xFFFFu), (uint16_t)(g4[e] & 0xFFFFu)) |
+                   ((uint32_t)norm((uint16_t)(xv[j][e] >> 16), (uint16_t)(g4[e] >> 16)) << 16);
+        *reinterpret_cast<u32x4*>(xn + (size_t)row * N + 8 * q) = o;
+    }
+}
+
 // Split-K finish: element pair (row, 2p..2p+1) sums the fp32 parts in part order and
 // stores through the GEMM's own epilogue.
 __global__ __launch_bounds__(256) void w4g_splitk_reduce_kernel(const float* __restrict__ part, uint32_t parts,
@@ -685,7 +754,13 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
         const bool vec = N % 8 == 0 && ldy % oal == 0 && (uintptr_t)y % (2 * oal) == 0 &&
                          (!epi.res || (epi.ldr % oal == 0 && (uintptr_t)epi.res % (2 * oal) == 0)) &&
                          (uintptr_t)epi.split_ws % 16 == 0;
-        if (vec) {
+        const bool fuse_norm = vec && !epi.swiglu && epi.norm_gamma && epi.norm_out && N <= 256 * 8 * kRedNormG &&
+                               (uintptr_t)epi.norm_gamma % 16 == 0 && (uintptr_t)epi.norm_out % 16 == 0;
+        if (fuse_norm) {
+            hipLaunchKernelGGL(w4g_splitk_reduce_norm_kernel, dim3(M), dim3(256), 0, st, epi.split_ws, parts, y, ldy,
+                               M, N, epi.res, epi.ldr, epi.norm_gamma, epi.norm_out);
+            if (epi.norm_done) *epi.norm_done = true;
+        } else if (vec) {
             const size_t n8 = (size_t)M * (N / 8);
             hipLaunchKernelGGL(w4g_splitk_reduce8_kernel, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, st,
                                epi.split_ws, parts, y, ldy, M, N, epi.res, epi.ldr, epi.swiglu ? 1 : 0);

@@ -30,6 +30,12 @@ struct W4gEpilogue {
     // when too small, the GEMM runs unsplit. Calls that share it must not overlap.
     float* split_ws = nullptr;
     size_t split_ws_bytes = 0;
+    // GEMM with a K split, plain epilogue: when set, the split's finishing pass also
+    // writes RMSNORM2_F16(y rows, norm_gamma, no bias) to norm_out (M x N, dense) and
+    // sets *norm_done; shapes it cannot take leave *norm_done false.
+    const __half* norm_gamma = nullptr;
+    __half* norm_out = nullptr;
+    bool* norm_done = nullptr;
 };
 // y[m*ldy + n] = f16( sum_k x[m*ldx + k] * fp16(q[n,k] * s[n, k/64]) ), m < M, n < N,
 // each dequantized weight rounded to fp16 as the reference does, fp32 accumulation

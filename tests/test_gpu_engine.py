@@ -11,7 +11,7 @@ import pytest
 from helpers import assert_close, normal_f16, w4g_weights
 
 from gehtp_amd import WtExecError
-from gehtp_amd.abi import WT_KV_POS_AUTO, opcodes as OP
+from gehtp_amd.abi import WT_KV_POS_AUTO, WT_REF_NONE, opcodes as OP
 from gehtp_amd.runlist import BlobBuilder, f32_bits
 
 pytestmark = pytest.mark.gpu
@@ -89,6 +89,46 @@ def test_run_io_device_bound_input(engine, oracle, torch_dev):
             engine.run_io(pb, None, t)
     finally:
         engine.set_input_device(None)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_split_k_finish_normalizes_next_op(engine, oracle, mode):
+    """OP_W4G_FUSED_F16 with a K split and a residual (o-proj-like), then OP_W4G_FUSED_F16
+    normalizing that output (RMSNORM2 -> linear, SwiGLU for mode 1): the split's
+    finishing pass also writes the normalized rows the second op's GEMM reads. Both
+    outputs match the oracle's op chain, and the second op run alone (normalizing by
+    itself) gives the same output."""
+    rng = np.random.default_rng(70 + mode)
+    M, K1, N1, N2 = 256, 4096, 1024, 1024 if mode else 512
+    _, wq1, ws1 = w4g_weights(rng, N1, K1)
+    _, wq2, ws2 = w4g_weights(rng, N2, N1)
+    a = normal_f16(rng, M, K1) * np.float16(0.25)
+    r = normal_f16(rng, M, N1)
+    gam = rng.uniform(0.8, 1.2, N1).astype(np.float16)
+    bb = BlobBuilder()
+    xs = bb.add_input_slot(M * K1 * 2)
+    q1, s1 = bb.add_slot(wq1, count=N1 * K1), bb.add_slot(ws1)
+    q2, s2 = bb.add_slot(wq2, count=N2 * N1), bb.add_slot(ws2)
+    rs, gs = bb.add_slot(r), bb.add_slot(gam)
+    t1, t2 = bb.temp(), bb.temp()
+    n_out = N2 // 2 if mode else N2
+    bb.op(OP.W4G_FUSED_F16, bb.slot_ref(xs), bb.slot_ref(q1), bb.slot_ref(s1), t1, M, K1, N1, WT_REF_NONE,
+          bb.slot_ref(rs), 0, 2)
+    bb.op(OP.W4G_FUSED_F16, t1, bb.slot_ref(q2), bb.slot_ref(s2), t2, M, N1, N2, bb.slot_ref(gs), WT_REF_NONE,
+          mode, 2)
+    pb = engine.parse(bb.build())
+    out, _ = engine.run_io(pb, a.tobytes(), t2, out_bytes=M * n_out * 2)
+    y1 = _h(engine.temp(t1), (M, N1))
+    y1_ref = oracle.binary(oracle.matmul_w4g(a, wq1, ws1, threads=8), r, 0)
+    assert_close(y1, y1_ref, what="split-K output")
+    acc = oracle.matmul_w4g(oracle.rmsnorm2(y1, gam, np.zeros(N1, np.float16)), wq2, ws2, threads=8)
+    ref = oracle.binary(oracle.unary(acc[:, 0::2].copy(), 12), acc[:, 1::2].copy(), 2) if mode else acc
+    fused = _h(out, (M, n_out))
+    assert_close(fused, ref, what="next op on the pre-normalized rows")
+    engine.run(pb, first=1, count=1)   # the second op alone normalizes its input itself
+    alone = _h(engine.temp(t2), (M, n_out))
+    assert np.abs(fused.astype(np.float32) - alone.astype(np.float32)).max() <= 2e-2
+    assert (fused == alone).mean() > 0.999
 
 
 def test_rmsnorm_then_w4g_gemm_runlist(engine, oracle):
