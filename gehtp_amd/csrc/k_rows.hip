@@ -200,7 +200,15 @@ __global__ __launch_bounds__(256) void softmax_kernel(const __half* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// Element-wise binary ops, subtypes 0..5 (oplist_exec.c:1143-1158).
+// f16 store of the element-wise ops: RNE, with a NaN stored as the Inf of its sign, as
+// the reference's converters do (oplist_exec.c:401, hvx_binary.c hb_f32_to_f16).
+__device__ __forceinline__ __half f2h_ew(float f) {
+    return f != f ? __ushort_as_half((uint16_t)((__float_as_uint(f) >> 16 & 0x8000u) | 0x7C00u)) : f2h(f);
+}
+
+// Element-wise binary ops, subtypes 0..5 (oplist_exec.c:1143-1158). exec_binary's
+// dispatch: for n >= 32 the division runs hvhx_v2_div_f32, which has no zero test
+// (hvx_binary.c:66-86, oplist_exec.c:1126-1145); below 32 elements x / 0 gives 0.
 __global__ void binary_kernel(const __half* __restrict__ a, const __half* __restrict__ b,
                               __half* __restrict__ y, uint32_t n, uint32_t subtype) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -211,12 +219,12 @@ __global__ void binary_kernel(const __half* __restrict__ a, const __half* __rest
     case 0: r = __fadd_rn(x0, x1); break;
     case 1: r = __fsub_rn(x0, x1); break;
     case 2: r = __fmul_rn(x0, x1); break;
-    case 3: r = (x1 != 0.0f) ? __fdiv_rn(x0, x1) : 0.0f; break;
+    case 3: r = (n >= 32u || x1 != 0.0f) ? __fdiv_rn(x0, x1) : 0.0f; break;
     case 4: r = (x0 == x1) ? 1.0f : 0.0f; break;
     case 5: r = ((uint32_t)x0 & (uint32_t)x1) ? 1.0f : 0.0f; break;
     default: break;
     }
-    y[i] = f2h(r);
+    y[i] = f2h_ew(r);
 }
 
 __global__ void select_kernel(const __half* __restrict__ c, uint32_t cn, const __half* __restrict__ t,
@@ -227,14 +235,19 @@ __global__ void select_kernel(const __half* __restrict__ c, uint32_t cn, const _
     const float cv = h2f(c[cn <= 1 ? 0 : (cn < n ? i % cn : i)]);
     const float r = cv != 0.0f ? h2f(t[tn <= 1 ? 0 : (tn < n ? i % tn : i)])
                                : h2f(f[fn <= 1 ? 0 : (fn < n ? i % fn : i)]);
-    y[i] = f2h(r);
+    y[i] = f2h_ew(r);
 }
 
-// Element-wise unary ops, subtypes 0..16 (oplist_exec.c:1047-1078).
+// Element-wise unary ops, subtypes 0..16 (oplist_exec.c:1047-1078); COPY (14) over 32
+// or more elements is a bit copy, as exec_unary's memcpy (oplist_exec.c:1042-1044).
 __global__ void unary_kernel(const __half* __restrict__ x, __half* __restrict__ y, uint32_t n,
                              uint32_t subtype) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
+    if (subtype == 14u && n >= 32u) {
+        y[i] = x[i];
+        return;
+    }
     const float v = h2f(x[i]);
     float r = v;
     switch (subtype) {
@@ -262,7 +275,7 @@ __global__ void unary_kernel(const __half* __restrict__ x, __half* __restrict__ 
     case 16: r = (v == v && (v > 3.4e38f || v < -3.4e38f)) ? 1.0f : 0.0f; break;
     default: break;
     }
-    y[i] = f2h(r);
+    y[i] = f2h_ew(r);
 }
 
 // ---------------------------------------------------------------------------

@@ -245,8 +245,10 @@ static int matmul_nk_mt(const uint16_t* a, const uint16_t* w_nk, uint16_t* y,
     return rc;
 }
 
-int go_matmul_w4g(const uint16_t* a, const uint8_t* wq, const uint16_t* ws, uint16_t* y,
-                  uint32_t M, uint32_t K, uint32_t N, uint32_t group, int n_threads) {
+/* Scalar forms of the two linears (the vector forms in gehtp_oracle_fast.c fall back
+ * to these on CPUs without AVX2/F16C; tests compare both with go_matmul_f16). */
+int go_matmul_w4g_ref(const uint16_t* a, const uint8_t* wq, const uint16_t* ws, uint16_t* y,
+                      uint32_t M, uint32_t K, uint32_t N, uint32_t group, int n_threads) {
     uint16_t* w = (uint16_t*)malloc((size_t)N * K * 2);
     if (!w) return -1;
     if (go_w4g_dequant(wq, ws, N, K, group, w)) { free(w); return -1; }
@@ -255,8 +257,8 @@ int go_matmul_w4g(const uint16_t* a, const uint8_t* wq, const uint16_t* ws, uint
     return rc;
 }
 
-int go_matmul_f16_nk_mt(const uint16_t* a, const uint16_t* w, uint16_t* y,
-                        uint32_t M, uint32_t K, uint32_t N, int n_threads) {
+int go_matmul_f16_nk_ref(const uint16_t* a, const uint16_t* w, uint16_t* y,
+                         uint32_t M, uint32_t K, uint32_t N, int n_threads) {
     return matmul_nk_mt(a, w, y, M, K, N, n_threads);
 }
 
@@ -267,6 +269,7 @@ int go_rmsnorm2(const uint16_t* x, const uint16_t* gamma, const uint16_t* beta,
                 uint16_t* y, uint32_t n, uint32_t rw) {
     if (rw == 0 || n % rw) return -1;
     uint32_t m = n / rw;
+#pragma omp parallel for schedule(static) if (n >= (1u << 16))
     for (uint32_t r = 0; r < m; r++) {
         const uint16_t* xr = x + (size_t)r * rw;
         double acc = 0.0;
@@ -328,16 +331,21 @@ void go_softmax(const uint16_t* x, uint16_t* y, uint32_t rows, uint32_t n) {
     else go_softmax_scalar(x, y, rows, n);
 }
 
-/* OP_BINARY_F16 element-wise subtypes 0..5: oplist_exec.c:1143-1158. */
+/* OP_BINARY_F16 element-wise subtypes 0..5: oplist_exec.c:1143-1158, with exec_binary's
+ * dispatch (:1126-1145): for n >= 32, subtypes 0..3 run hvhx_v2_{add,sub,mul,div}_f32
+ * between the f16 conversions of hvx_binary.c; on a host build those are the plain f32
+ * ops (hvx_binary.c:38-86), so division is NOT guarded against a zero divisor there. */
 int go_binary(const uint16_t* a, const uint16_t* b, uint16_t* y, uint32_t n, uint32_t subtype) {
     if (subtype > 5) return -1;
+    const int vec = n >= 32u;
+#pragma omp parallel for schedule(static) if (n >= (1u << 16))
     for (uint32_t i = 0; i < n; i++) {
         float x0 = F(a[i]), x1 = F(b[i]), r = x0;
         switch (subtype) {
         case 0: r = x0 + x1; break;
         case 1: r = x0 - x1; break;
         case 2: r = x0 * x1; break;
-        case 3: r = (x1 != 0) ? x0 / x1 : 0.0f; break;
+        case 3: r = vec ? x0 / x1 : ((x1 != 0) ? x0 / x1 : 0.0f); break;
         case 4: r = (x0 == x1) ? 1.0f : 0.0f; break;
         case 5: r = ((uint32_t)x0 & (uint32_t)x1) ? 1.0f : 0.0f; break;
         }
@@ -346,9 +354,17 @@ int go_binary(const uint16_t* a, const uint16_t* b, uint16_t* y, uint32_t n, uin
     return 0;
 }
 
-/* OP_UNARY_F16 scalar subtypes: oplist_exec.c:1047-1078. */
+/* OP_UNARY_F16 scalar subtypes: oplist_exec.c:1047-1078, with exec_unary's dispatch
+ * (:1021-1045): for n >= 32, subtypes 1/8/9/12 run hvhx_v2_{exp,sigmoid,tanh,silu}_f32,
+ * whose host bodies are the same f32 formulas (hvx_unary.c:44-156), and COPY (14) is a
+ * bit copy (NaN payloads kept) instead of the f16 -> f32 -> f16 round trip. */
 int go_unary(const uint16_t* x, uint16_t* y, uint32_t n, uint32_t subtype) {
     if (subtype > 16) return -1;
+    if (subtype == 14 && n >= 32u) {
+        memcpy(y, x, (size_t)n * 2u);
+        return 0;
+    }
+#pragma omp parallel for schedule(static) if (n >= (1u << 16))
     for (uint32_t i = 0; i < n; i++) {
         float v = F(x[i]), r = v;
         switch (subtype) {
@@ -460,8 +476,8 @@ int go_kv_gather(struct go_kv* c, uint16_t* kT, uint16_t* vo, uint32_t n_kv,
  *   s = BINARY add (s, mask)  mask 0 / -inf f16 out
  *   p = SOFTMAX(s) over S keys              exec_softmax dispatch
  *   o = MATMUL_F16(p, V_kv)                 f16 out, j ascending */
-int go_attn_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
-                    uint32_t S, uint32_t H, uint32_t KVH, uint32_t hd, float scale, int causal) {
+int go_attn_prefill_ref(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                        uint32_t S, uint32_t H, uint32_t KVH, uint32_t hd, float scale, int causal) {
     if (!S || !H || !KVH || H % KVH) return -1;
     const uint32_t rep = H / KVH;
     const float sc = F(H(scale));
@@ -544,6 +560,7 @@ int go_rope(const uint16_t* x, uint16_t* y, uint32_t n_tok, uint32_t n_heads, ui
             uint32_t pos0, float theta, uint32_t row_stride) {
     if (hd % 2 || row_stride < n_heads * hd) return -1;
     const uint32_t half = hd / 2;
+#pragma omp parallel for schedule(static) if (n_tok >= 64)
     for (uint32_t t = 0; t < n_tok; t++) {
         const double pos = (double)(pos0 + t);
         for (uint32_t i = 0; i < half; i++) {

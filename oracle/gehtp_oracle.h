@@ -41,6 +41,16 @@ int go_matmul_w4g(const uint16_t* a, const uint8_t* wq, const uint16_t* ws, uint
 /* Same for fp16 weights stored [N,K] (the lm_head). */
 int go_matmul_f16_nk_mt(const uint16_t* a, const uint16_t* w, uint16_t* y,
                         uint32_t M, uint32_t K, uint32_t N, int n_threads);
+/* Scalar forms of the two above (go_matmul_w4g / go_matmul_f16_nk_mt are the
+ * vectorised forms in gehtp_oracle_fast.c, bit-identical for NaN-free results). */
+int go_matmul_w4g_ref(const uint16_t* a, const uint8_t* wq, const uint16_t* ws, uint16_t* y,
+                      uint32_t M, uint32_t K, uint32_t N, uint32_t group, int n_threads);
+int go_matmul_f16_nk_ref(const uint16_t* a, const uint16_t* w, uint16_t* y,
+                         uint32_t M, uint32_t K, uint32_t N, int n_threads);
+/* 1 when the vector forms run (AVX2 + F16C present); go_fast_disable(1) forces the
+ * scalar forms, go_fast_disable(0) re-enables detection. */
+int go_fast_available(void);
+void go_fast_disable(int off);
 
 /* ---- row ops ---- */
 int  go_rmsnorm2(const uint16_t* x, const uint16_t* gamma, const uint16_t* beta,
@@ -71,9 +81,22 @@ int go_kv_gather(struct go_kv* c, uint16_t* kT, uint16_t* vo, uint32_t n_kv,
  * value f16(scale) (it arrives as an f16 constant slot in reference blobs). */
 int go_attn_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
                     uint32_t S, uint32_t H, uint32_t KVH, uint32_t hd, float scale, int causal);
+/* The same over n_threads OpenMP threads (heads in parallel; each head's arithmetic
+ * unchanged), and its scalar form (go_attn_prefill is the vectorised one). */
+int go_attn_prefill_mt(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                       uint32_t S, uint32_t H, uint32_t KVH, uint32_t hd, float scale, int causal,
+                       int n_threads);
+int go_attn_prefill_ref(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                        uint32_t S, uint32_t H, uint32_t KVH, uint32_t hd, float scale, int causal);
 /* One query token against the ring: q [H,hd] -> out [H,hd]. */
 int go_attn_decode(struct go_kv* c, const uint16_t* q, uint16_t* out, uint32_t n_kv,
                    uint32_t H, uint32_t KVH, uint32_t hd, float scale);
+/* go_attn_decode over a ring given as raw bytes + posmap (oracle.KVRing's state):
+ * positions [0, n_kv) must be present (else -2). Vectorised; the arithmetic of
+ * go_attn_decode. */
+int go_attn_decode_ring(const uint8_t* buf, const uint32_t* posmap, uint32_t nslots, uint32_t slot_bytes,
+                        const uint16_t* q, uint16_t* out, uint32_t n_kv, uint32_t H, uint32_t KVH,
+                        uint32_t hd, float scale);
 /* Rotary embedding as the runlist's mul/slice/neg/concat/add chain computes it. */
 int go_rope(const uint16_t* x, uint16_t* y, uint32_t n_tok, uint32_t n_heads, uint32_t hd,
             uint32_t pos0, float theta, uint32_t row_stride);

@@ -42,6 +42,13 @@ def lib():
             "go_matmul_f16": (C.c_int, [_p, _p, _p, u, u, u, u, u, u]),
             "go_matmul_w4g": (C.c_int, [_p, _p, _p, _p, u, u, u, u, C.c_int]),
             "go_matmul_f16_nk_mt": (C.c_int, [_p, _p, _p, u, u, u, C.c_int]),
+            "go_matmul_w4g_ref": (C.c_int, [_p, _p, _p, _p, u, u, u, u, C.c_int]),
+            "go_matmul_f16_nk_ref": (C.c_int, [_p, _p, _p, u, u, u, C.c_int]),
+            "go_fast_available": (C.c_int, []),
+            "go_fast_disable": (None, [C.c_int]),
+            "go_attn_prefill_mt": (C.c_int, [_p, _p, _p, _p, u, u, u, u, C.c_float, C.c_int, C.c_int]),
+            "go_attn_prefill_ref": (C.c_int, [_p, _p, _p, _p, u, u, u, u, C.c_float, C.c_int]),
+            "go_attn_decode_ring": (C.c_int, [_p, _p, u, u, _p, _p, u, u, u, u, C.c_float]),
             "go_rmsnorm2": (C.c_int, [_p, _p, _p, _p, u, u]),
             "go_softmax_scalar": (None, [_p, _p, u, u]),
             "go_softmax_host": (None, [_p, _p, u, u]),
@@ -130,26 +137,35 @@ def matmul_f16(a, w, M, K, N_full, n0=0, N=None, flags=0, out=None) -> np.ndarra
     return y
 
 
-def matmul_w4g(a, wq, ws, threads: int = 1) -> np.ndarray:
+def matmul_w4g(a, wq, ws, threads: int = 1, form: str = "fast") -> np.ndarray:
+    """y = a . dequant(W)^T (OP_MATMUL_F16 scalar arithmetic on fp16(q*s)); form "ref"
+    runs the scalar restatement, "fast" its vectorised, bit-identical form."""
     a = _h(a)
     wq = np.ascontiguousarray(wq, dtype=np.uint8)
     ws = _h(ws)
     M, K = a.shape
     N = wq.shape[0]
     y = np.empty((M, N), np.float16)
-    if lib().go_matmul_w4g(_p(a), _p(wq), _p(ws), _p(y), M, K, N, 64, threads):
+    fn = lib().go_matmul_w4g if form == "fast" else lib().go_matmul_w4g_ref
+    if fn(_p(a), _p(wq), _p(ws), _p(y), M, K, N, 64, threads):
         raise ValueError("bad w4g shape")
     return y
 
 
-def matmul_f16_nk(a, w, threads: int = 1) -> np.ndarray:
+def matmul_f16_nk(a, w, threads: int = 1, form: str = "fast") -> np.ndarray:
     """y = a . w^T with w [N, K] fp16 (the lm_head form), sequential-k arithmetic."""
     a, w = _h(a), _h(w)
     M, K = a.shape
     N = w.shape[0]
     y = np.empty((M, N), np.float16)
-    lib().go_matmul_f16_nk_mt(_p(a), _p(w), _p(y), M, K, N, threads)
+    fn = lib().go_matmul_f16_nk_mt if form == "fast" else lib().go_matmul_f16_nk_ref
+    if fn(_p(a), _p(w), _p(y), M, K, N, threads):
+        raise MemoryError("matmul_f16_nk")
     return y
+
+
+def fast_available() -> bool:
+    return bool(lib().go_fast_available())
 
 
 # ---- rows ----
@@ -191,13 +207,19 @@ def argmax(x) -> int:
     return int(lib().go_argmax(_p(x), x.size))
 
 
-def attn_prefill(q, k, v, scale: float, causal: bool = True) -> np.ndarray:
-    """q [S,H,hd], k/v [S,KVH,hd] -> [S,H,hd], reference runlist composition."""
+def attn_prefill(q, k, v, scale: float, causal: bool = True, threads: int = 1,
+                 form: str = "fast") -> np.ndarray:
+    """q [S,H,hd], k/v [S,KVH,hd] -> [S,H,hd], reference runlist composition
+    (form "ref": the scalar restatement; "fast": vectorised, heads over threads)."""
     q, k, v = _h(q), _h(k), _h(v)
     S, H, hd = q.shape
     KVH = k.shape[1]
     out = np.empty_like(q)
-    if lib().go_attn_prefill(_p(q), _p(k), _p(v), _p(out), S, H, KVH, hd, scale, int(causal)):
+    if form == "fast":
+        rc = lib().go_attn_prefill_mt(_p(q), _p(k), _p(v), _p(out), S, H, KVH, hd, scale, int(causal), threads)
+    else:
+        rc = lib().go_attn_prefill_ref(_p(q), _p(k), _p(v), _p(out), S, H, KVH, hd, scale, int(causal))
+    if rc:
         raise ValueError("bad attention shape")
     return out
 
@@ -257,7 +279,21 @@ class KVRing:
         return kT, vo
 
     def attn_decode(self, q, n_kv: int, H: int, KVH: int, hd: int, scale: float) -> np.ndarray:
-        """One-token attention as the reference decode chain computes it (f16 at each op)."""
+        """One-token attention over positions [0, n_kv) as the reference decode chain
+        computes it (go_attn_decode's arithmetic, vectorised in C)."""
+        q = _h(q).reshape(H, hd)
+        out = np.empty((H, hd), np.float16)
+        rc = lib().go_attn_decode_ring(_p(self.buf), _p(self.posmap), self.nslots, self.slot_bytes, _p(q),
+                                       _p(out), n_kv, H, KVH, hd, scale)
+        if rc == -2:
+            raise KeyError("kv gather miss")
+        if rc:
+            raise ValueError("bad decode attention shape")
+        return out
+
+    def attn_decode_chain(self, q, n_kv: int, H: int, KVH: int, hd: int, scale: float) -> np.ndarray:
+        """The same, op by op: KV_GATHER, MATMUL_F16, BINARY mul, SOFTMAX, MATMUL_F16
+        (scripts/surgery_decode_graph.py:143-168), each an oracle op with f16 output."""
         kT, vo = self.gather(n_kv, H, KVH, hd)
         q = _h(q).reshape(H, hd)
         out = np.empty((H, hd), np.float16)
