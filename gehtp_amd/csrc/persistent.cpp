@@ -237,8 +237,13 @@ bool handle(Server& sv, const std::vector<uint8_t>& req) {
     } else {
         const uint32_t nb = wt_exec_temp_last_bytes(sv.out_temp);
         const uint8_t* host = wt_exec_temp(sv.out_temp);
+        if (!host || nb < 2) {
+            // never written by this blob, or an intermediate a fused chain skipped
+            write_resp(sv.resp_p, "{\"rc\":-1,\"err\":\"out_temp unavailable\"}");
+            return false;
+        }
         const int32_t tok = argmax_f16(host, nb);
-        if (want_out && host) {
+        if (want_out) {
             const std::string tmp = sv.out_p + ".tmp";
             if (FILE* f = std::fopen(tmp.c_str(), "wb")) {
                 std::fwrite(host, 1, nb, f);
@@ -276,6 +281,10 @@ int main(int argc, char** argv) {
         return 1;
     }
     sv.out_temp = (uint32_t)std::strtoul(out_s.c_str(), nullptr, 10);
+    if (sv.out_temp >= WT_EXEC_MAX_TEMPS) {
+        std::fprintf(stderr, "[FAIL] out_temp %u out of range (temps are 0..%u)\n", sv.out_temp, WT_EXEC_MAX_TEMPS - 1u);
+        return 2;
+    }
     sv.in_bytes = (uint32_t)std::strtoul(in_s.c_str(), nullptr, 10);
     const long idle_exit_s = job_get(job, "idle_exit_s", idle_s) ? std::strtol(idle_s.c_str(), nullptr, 10) : 600;
     const bool trace = job_get(job, "trace", trace_s) && std::strtol(trace_s.c_str(), nullptr, 10) != 0;

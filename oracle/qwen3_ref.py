@@ -54,7 +54,8 @@ class RefModel:
             for t in range(S):
                 self.rings[l].append(kr[t], v[t])
             a = o.attn_prefill(qr.reshape(S, c.heads, c.head_dim), kr.reshape(S, c.kv_heads, c.head_dim),
-                               v.reshape(S, c.kv_heads, c.head_dim), c.scale, True).reshape(S, c.q_dim)
+                               v.reshape(S, c.kv_heads, c.head_dim), c.scale, True,
+                               threads=self.threads).reshape(S, c.q_dim)
             x1 = o.binary(x, self._lin(a, l, "wo"), 0)
             x = self._ffn(x1, l)
         self.pos += S

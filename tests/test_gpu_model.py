@@ -59,10 +59,10 @@ def test_small_model_prefill_and_decode(engine):
 
 
 def test_config4_layer_prefill_then_decode(engine):
-    """BASELINE config 4 geometry (one 0.8B-class layer: hidden 1024, 16Q/8KV hd128, FFN 3072,
-    vocab 151936), prefill then greedy-position decode steps, teacher forced. The prefill is
-    shortened to 128 tokens and 4 decode steps to keep the CPU oracle within seconds."""
-    got, refl = _run(engine, CONFIG_08B_LAYER, S=128, n_dec=4, seed=5)
+    """BASELINE config 4 at its stated size: one 0.8B-class layer (hidden 1024, 16Q/8KV hd128,
+    FFN 3072, vocab 151936), a 512-token prefill then 128 decode steps, teacher forced
+    (engine and oracle consume the same ids), every step's logits against the oracle."""
+    got, refl = _run(engine, CONFIG_08B_LAYER, S=512, n_dec=128, seed=5, max_pos=1024)
     _check(got, refl, 0.9999)
 
 

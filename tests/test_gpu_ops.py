@@ -171,6 +171,38 @@ def test_engine_w4a16_errors(engine, oracle):
         engine.run(engine.parse(bb2.build()))
 
 
+@pytest.mark.parametrize("nz_byte", [0, 1, 2 * 512 - 1])
+def test_engine_w4a16_nonzero_folded_bias_fails(engine, oracle, nz_byte):
+    """The folded bias term of opcode 1 (+ bias_fold[n], kernels/docs/api_v22_w4a16.md:11)
+    lives in the HMX engine's own (N/32) x 512-byte packing, which no readable source
+    defines: a non-zero bias slot fails the op (first op, error names the slot), and the
+    same blob with the bias zeroed runs and matches the oracle."""
+    from gehtp_amd import WtExecError
+    M, K, N = 32, 64, 64
+    rng = np.random.default_rng(nz_byte)
+    A = rng.integers(0, 65536, size=(M, K), dtype=np.uint16)
+    W = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    act, wslot = oracle.crouton_encode(A), oracle.w4a16_pack(W)
+    for nonzero in (True, False):
+        bias = np.zeros((N // 32) * 512, np.uint8)
+        if nonzero:
+            bias[nz_byte] = 1
+        bb = BlobBuilder()
+        s_act = bb.add_slot(act.view(np.uint8))
+        s_w = bb.add_slot(wslot)
+        s_b = bb.add_slot(bias)
+        bb.add_slot(np.zeros(8 * (K // 32) * 4, np.uint8))
+        bb.add_slot(np.zeros(8 * (K // 32) * 4, np.uint8))
+        bb.op(OP.MATMUL_W4A16, s_act, s_w, 0, M, K, N)
+        pb = engine.parse(bb.build())
+        if nonzero:
+            with pytest.raises(WtExecError, match=f"folded bias slot {s_b} is non-zero"):
+                engine.run(pb)
+        else:
+            engine.run(pb)
+            assert np.array_equal(np.frombuffer(engine.temp(0), np.uint16), oracle.matmul_w4a16(act, wslot, M, K, N))
+
+
 def test_engine_data_ops(engine, oracle):
     """FILL, TRANSPOSE, CONCAT, SPLIT, REDUCE, CUMSUM, GATHER, PAD and DMA in one runlist,
     each output temp bit-exact against the oracle."""
