@@ -170,6 +170,7 @@ EXPORTS = {
     "gehtp_attn_prefill": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, C.c_float, _i, _vp]),
     "gehtp_attn_decode": (_i, [_vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32, C.c_float, _vp, _u32, _vp]),
     "gehtp_attn_decode_work_floats": (_u32, [_u32, _u32, _u32]),
+    "gehtp_attn_decode_noalloc": (_i, [_vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32, C.c_float, _vp]),
     "gehtp_attn_decode_qkv": (_i, [_vp, _u32, _u32, _vp, _vp, C.c_float, C.c_float, _vp, _u32, _vp, _vp, _vp,
                                    _u32, _vp]),
     "gehtp_kv_append": (_i, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _vp]),

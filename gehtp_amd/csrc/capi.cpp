@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 #include "gehtp_kernels.h"
 #include "kernels.h"
@@ -21,6 +22,37 @@ bool w4g_args_ok(const void* x, uint32_t ldx, const void* wq, const void* ws, co
                  uint32_t ldy, uint32_t N, uint32_t K) {
     return x && wq && ws && y && K && K % 64 == 0 && ldx >= K && ldx % 8 == 0 && ldy >= N &&
            al16(x) && al16(wq) && ((reinterpret_cast<uintptr_t>(ws) & 1u) == 0);
+}
+
+// Scratch of gehtp_attn_decode_noalloc: the decode attention's per-chunk partial records
+// in a file-scope device array instead of a caller's or an allocated workspace. Every GPU
+// the library runs on holds its own copy from code-object load until the process ends,
+// and every call on that GPU shares it (calls that overlap on one GPU race). In host code
+// `scratch` is only a stand-in for the symbol, not a device address: the address is
+// looked up once per device with hipGetSymbolAddress and only that pointer is handed to
+// kernels. Nothing in it needs to start at zero: each chunk workgroup writes its whole
+// record before the merge pass reads it, and the merge reads only the chunks of n_kv.
+__device__ __align__(256) float scratch[GEHTP_ATTN_DECODE_NOALLOC_MAX_FLOATS];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call per device,
+// with that device current). 0 on success, else a hipError_t / GEHTP_EINVAL.
+int noalloc_scratch(float** out) {
+    int dev = -1;
+    if (const hipError_t e = hipGetDevice(&dev)) return (int)e;
+    if (dev < 0 || dev >= kMaxScratchDevices) return GEHTP_EINVAL;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) return (int)e;
+        if (!p) return (int)hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
 }
 
 }  // namespace
@@ -148,6 +180,21 @@ int gehtp_attn_decode_qkv(const void* qkv, uint32_t Hh, uint32_t KVH, const void
     return rc(launch_attn_decode_qkv(H(qkv), H(q_gamma), H(k_gamma), theta, static_cast<uint8_t*>(ring), slot_bytes,
                                      state_bytes / slot_bytes, static_cast<uint32_t*>(count_dev), Hm(out), Hh, KVH,
                                      scale, static_cast<float*>(work), work_floats, S(stream)));
+}
+
+int gehtp_attn_decode_noalloc(const void* q, const void* ring, uint32_t state_bytes, void* out, uint32_t n_kv,
+                              uint32_t Hh, uint32_t KVH, uint32_t hd, float scale, void* stream) {
+    const uint32_t slot_bytes = KVH * hd * 4u;
+    if (!q || !ring || !out || hd != 128 || !KVH || Hh % KVH || !slot_bytes || state_bytes % slot_bytes ||
+        !al16(q) || !al16(ring))
+        return GEHTP_EINVAL;
+    const uint32_t nslots = state_bytes / slot_bytes;
+    if (!n_kv || n_kv > nslots) return GEHTP_EINVAL;
+    if (attn_decode_work_floats(n_kv, Hh, hd) > GEHTP_ATTN_DECODE_NOALLOC_MAX_FLOATS) return GEHTP_E2BIG;
+    float* work = nullptr;
+    if (const int e = noalloc_scratch(&work)) return e;
+    return rc(launch_attn_decode(H(q), static_cast<const uint8_t*>(ring), slot_bytes, nslots, Hm(out), n_kv, nullptr,
+                                 Hh, KVH, hd, scale, work, GEHTP_ATTN_DECODE_NOALLOC_MAX_FLOATS, S(stream)));
 }
 
 int gehtp_kv_append(void* ring, uint32_t state_bytes, const void* k, const void* v, uint32_t kv_elems,

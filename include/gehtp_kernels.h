@@ -8,7 +8,8 @@
  *
  * Conventions: every pointer is a DEVICE pointer; `stream` is a hipStream_t
  * (NULL = the legacy default stream); the call only enqueues work. Return 0 on
- * success, GEHTP_EINVAL for a rejected shape/alignment, or a positive hipError_t.
+ * success, GEHTP_EINVAL for a rejected shape/alignment, GEHTP_E2BIG for a request beyond
+ * a fixed scratch, or a positive hipError_t.
  */
 #ifndef GEHTP_KERNELS_H
 #define GEHTP_KERNELS_H
@@ -21,6 +22,7 @@ extern "C" {
 #endif
 
 #define GEHTP_EINVAL (-22)
+#define GEHTP_E2BIG (-7)   /* request larger than a fixed-size scratch */
 
 /* y[M, ldy] = x[M, ldx] . dequant(W)^T, W4G int4 group-64 (OP_MATMUL_W4G_F16):
  * M <= 4 runs the GEMV, larger M the MFMA GEMM. Mirrors exec_matmul_f16's scalar
@@ -83,6 +85,20 @@ int gehtp_attn_decode(const void* q, const void* ring, uint32_t state_bytes, voi
                       uint32_t n_kv, uint32_t H, uint32_t KVH, uint32_t hd, float scale,
                       void* work, uint32_t work_floats, void* stream);
 uint32_t gehtp_attn_decode_work_floats(uint32_t n_kv, uint32_t H, uint32_t hd);
+/* gehtp_attn_decode without a workspace argument, allocating nothing. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The per-chunk
+ * partials live in a fixed scratch array of GEHTP_ATTN_DECODE_NOALLOC_MAX_FLOATS floats
+ * (4 MiB) that each GPU holds until the process ends: a call needing more than that
+ * (gehtp_attn_decode_work_floats(n_kv, H, hd) > the maximum, e.g. n_kv > 15872 at H = 32)
+ * returns GEHTP_E2BIG and launches nothing. Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (other streams, other threads) race. Same
+ * arguments, checks and results as gehtp_attn_decode; call it with the stream's device
+ * current. */
+#define GEHTP_ATTN_DECODE_NOALLOC_MAX_FLOATS (1u << 20)
+int gehtp_attn_decode_noalloc(const void* q, const void* ring, uint32_t state_bytes, void* out,
+                              uint32_t n_kv, uint32_t H, uint32_t KVH, uint32_t hd, float scale,
+                              void* stream);
 /* OP_ATTN_DECODE_QKV_F16 on device buffers: qkv = raw [q | k | v] row of the new token
  * ((H + 2*KVH)*128 fp16); q/k RMSNorm (gammas [128]) and RoPE (theta) at position
  * *count_dev, k/v written to the ring, attention over positions 0..*count_dev, then
