@@ -1651,13 +1651,25 @@ void keep_graph(const wt_blob* b, uint32_t first, uint32_t count, hipGraphExec_t
 // intermediates no later op reads (observed on the blob's first full run), runs as one
 // flash-attention launch on later runs; the other ops of the chain are skipped. Results
 // are within the fp16 tolerance of the chain, not its exact per-op roundings.
+//
+// The decode form (scripts/surgery_decode_graph.py:143-168, oplist_exec.c:2183-2231):
+// KV_GATHER of a state (kT [H, hd, P], v [H, P, hd]; P = the ring's slots with the
+// automatic count, whose tail it zero-fills) -> batched MATMUL_F16 q.kT -> [BINARY mul
+// by a constant scale] -> [BINARY add of a mask operand [H, P], e.g. the step input's
+// -inf tail] -> SOFTMAX -> batched MATMUL_F16 p.v runs as the split-KV decode kernel
+// reading the ring in place, with the mask applied as the chain adds it (positions past
+// the count score the mask value alone). The gather's count travels as the state's
+// device counter, so the fused step stays graph-capturable.
 struct AttnChain {
     uint32_t head = 0, len = 0, S = 0, H = 0;
     float scale = 0.0f;
     bool causal = false;
     uint32_t q = 0, k = 0, v = 0, out = 0;
-    uint32_t inter[4] = {0, 0, 0, 0};
+    uint32_t inter[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint32_t n_inter = 0;
+    bool decode = false;
+    uint32_t state = 0, KVH = 0, P = 0, n_kv = 0;   // decode: gather's state, kv heads, layout, n_kv arg
+    uint32_t mask = kNone;                           // decode: mask operand, or kNone
 };
 struct FusionPlan {
     const wt_blob* b = nullptr;
@@ -1770,6 +1782,99 @@ bool match_attn_chain(const wt_blob* b, uint32_t i, AttnChain& c) {
     return true;
 }
 
+// Bytes of state idx in the blob's STATE table (0 if absent).
+uint32_t blob_state_bytes(const wt_blob* b, uint32_t idx) {
+    for (uint32_t s = 0; s < b->n_slots; ++s) {
+        const wt_slot& sl = b->slots[s];
+        if (sl.addr != WT_SLOT_STATE || (uint64_t)sl.offset + sl.len > b->weight_bytes || sl.len < 4u) continue;
+        const uint8_t* p = b->weight_base + sl.offset;
+        uint32_t n;
+        std::memcpy(&n, p, 4);
+        if (idx >= n || sl.len < 4u + 4u * (idx + 1u)) return 0;
+        uint32_t bytes;
+        std::memcpy(&bytes, p + 4 + 4 * idx, 4);
+        return bytes;
+    }
+    return 0;
+}
+
+bool match_decode_chain(const wt_blob* b, uint32_t i, AttnChain& c) {
+    if ((uint64_t)i + 4 > b->n_ops) return false;
+    const wt_op& G = b->ops[i];
+    if (G.opcode != OP_KV_GATHER_F16 || G.n_args < 7) return false;
+    const uint32_t st = G.args[0], kT = G.args[1], vv = G.args[2], n_kv = G.args[3];
+    const uint32_t H = G.args[4], KVH = G.args[5], hd = G.args[6];
+    if ((st & 0xE000u) != WT_REF_STATE_FLAG || hd != 128 || !KVH || !H || H % KVH || H > 0xFFFFu) return false;
+    const uint32_t rep = H / KVH;
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return false;
+    if (!kT || !vv || !is_temp_ref(kT) || !is_temp_ref(vv) || (kT & 0x3FFFu) == (vv & 0x3FFFu)) return false;
+    uint32_t P = n_kv;
+    if (n_kv == WT_KV_POS_AUTO) {
+        const uint32_t bytes = blob_state_bytes(b, st & 0x1FFFu), slot = KVH * hd * 4u;
+        if (!bytes || bytes % slot) return false;
+        P = bytes / slot;
+    }
+    if (!P) return false;
+    const uint64_t n = (uint64_t)H * P;
+    c = AttnChain{};
+    c.decode = true;
+    c.head = i; c.H = H; c.KVH = KVH; c.P = P; c.n_kv = n_kv; c.state = st; c.S = 1;
+    c.inter[c.n_inter++] = kT;
+    c.inter[c.n_inter++] = vv;
+    uint32_t j = i + 1;
+    const wt_op& A = b->ops[j];
+    if (A.opcode != OP_MATMUL_F16 || A.n_args < 7 || A.args[1] != kT || A.args[3] != 1u || A.args[4] != hd ||
+        A.args[5] != P || A.args[6] != ((H << 16) | 4u) || !is_temp_ref(A.args[2]))
+        return false;
+    c.q = A.args[0];
+    uint32_t prev = A.args[2];
+    c.inter[c.n_inter++] = prev;
+    ++j;
+    c.scale = 1.0f;
+    if ((uint64_t)j + 3 > b->n_ops) return false;
+    const wt_op& B = b->ops[j];   // optional: BINARY mul by a constant slot
+    if (B.opcode == OP_BINARY_F16 && B.n_args >= 5 && B.args[4] == 2u && B.args[0] == prev && B.args[3] == n &&
+        is_temp_ref(B.args[2])) {
+        const uint16_t* sc = slot_host_f16(b, B.args[1], n);
+        if (!sc) return false;
+        for (uint64_t e = 1; e < n; ++e)
+            if (sc[e] != sc[0]) return false;
+        c.scale = (float)__builtin_bit_cast(_Float16, sc[0]);
+        if (!(c.scale > 0.0f && c.scale < INFINITY)) return false;
+        prev = B.args[2];
+        c.inter[c.n_inter++] = prev;
+        ++j;
+    }
+    const wt_op& C = b->ops[j];   // optional: BINARY add of a mask operand [H, P]
+    if (C.opcode == OP_BINARY_F16 && C.n_args >= 5 && C.args[4] == 0u && C.args[0] == prev && C.args[3] == n &&
+        is_temp_ref(C.args[2])) {
+        c.mask = C.args[1];
+        prev = C.args[2];
+        c.inter[c.n_inter++] = prev;
+        ++j;
+    } else if (n_kv == WT_KV_POS_AUTO && P > 1) {
+        return false;   // without a mask the zero-filled tail takes part in the softmax
+    }
+    if ((uint64_t)j + 2 > b->n_ops) return false;
+    const wt_op& D = b->ops[j];
+    if (D.opcode != OP_SOFTMAX_F16 || D.n_args < 4 || D.args[0] != prev || D.args[2] != H || D.args[3] != P ||
+        !is_temp_ref(D.args[1]))
+        return false;
+    c.inter[c.n_inter++] = D.args[1];
+    const wt_op& E = b->ops[j + 1];
+    if (E.opcode != OP_MATMUL_F16 || E.n_args < 7 || E.args[0] != D.args[1] || E.args[1] != vv || E.args[3] != 1u ||
+        E.args[4] != P || E.args[5] != hd || E.args[6] != ((H << 16) | 4u) || !is_temp_ref(E.args[2]))
+        return false;
+    c.out = E.args[2];
+    c.len = j + 2 - i;
+    for (uint32_t t = 0; t < c.n_inter; ++t)   // inputs must come from outside the chain
+        if ((c.q & 0x3FFFu) == (c.inter[t] & 0x3FFFu) && is_temp_ref(c.q)) return false;
+    if (c.mask != kNone && is_temp_ref(c.mask))
+        for (uint32_t t = 0; t < c.n_inter; ++t)
+            if ((c.mask & 0x3FFFu) == (c.inter[t] & 0x3FFFu)) return false;
+    return true;
+}
+
 // The plan of a blob (created, with its chains detected, on first sight of the blob as
 // parsed; a new plan drops the captured graphs, which may hold the blob's old form).
 FusionPlan* fusion_plan(const wt_blob* b) {
@@ -1791,7 +1896,7 @@ FusionPlan* fusion_plan(const wt_blob* b) {
     p.end_of.assign(b->n_ops, -1);
     for (uint32_t i = 0; i < b->n_ops; ++i) {
         AttnChain c;
-        if (!match_attn_chain(b, i, c)) continue;
+        if (!match_attn_chain(b, i, c) && !match_decode_chain(b, i, c)) continue;
         p.head_of[i] = (int32_t)p.chains.size();
         p.end_of[i + c.len - 1] = (int32_t)p.chains.size();
         p.chains.push_back(c);
@@ -1803,7 +1908,38 @@ FusionPlan* fusion_plan(const wt_blob* b) {
     return &g_plans.back();
 }
 
+int run_fused_decode(const wt_blob* b, const AttnChain& c, char* err, size_t errn) {
+    const uint32_t H = c.H, KVH = c.KVH, hd = 128, P = c.P;
+    State* s = state_kv(c.state, KVH * hd, err, errn);
+    if (!s) return -1;
+    const uint32_t si = c.state & 0x1FFFu;
+    const bool autopos = c.n_kv == WT_KV_POS_AUTO;
+    uint32_t n_kv = c.n_kv;
+    if (autopos) {   // the gather's checks (oplist_exec.c:2199-2205)
+        if (s->count == 0 || s->count > s->nslots)
+            return ERR("kv gather state %u count=%u bad (append first?)", si, s->count);
+        if (s->nslots != P) return ERR("fused decode attention: state %u has %u slots, chain %u", si, s->nslots, P);
+        n_kv = s->count;
+    } else if (n_kv > s->nslots) {
+        return ERR("kv gather n_kv %u > nslots %u", n_kv, s->nslots);
+    }
+    if (kv_check(*s, n_kv, err, errn)) return -1;
+    const __half* q = reinterpret_cast<const __half*>(ref_ptr(b, c.q));
+    const __half* mask = c.mask != kNone ? reinterpret_cast<const __half*>(ref_ptr(b, c.mask)) : nullptr;
+    __half* o = reinterpret_cast<__half*>(temp_get(c.out, H * hd * 2u));
+    if (!q || !o || (c.mask != kNone && !mask)) return ERR("fused decode attention ref fail");
+    const size_t qb = ref_bytes(b, c.q), mb = c.mask != kNone ? ref_bytes(b, c.mask) : 0;
+    if ((qb && qb < (uint64_t)H * hd * 2u) || (mb && mb < (uint64_t)H * P * 2u))
+        return ERR("fused decode attention operand too small");
+    if (attn_workspace(attn_decode_work_floats(autopos ? s->nslots : n_kv, H, hd), err, errn)) return -1;
+    CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o, autopos ? 0u : n_kv,
+                                    autopos ? g.counters_dev + si : nullptr, H, KVH, hd, c.scale, g.attn_work,
+                                    g.attn_work_floats, g.stream, mask, mask ? P : 0u));
+    return 0;
+}
+
 int run_fused_attn(const wt_blob* b, const AttnChain& c, char* err, size_t errn) {
+    if (c.decode) return run_fused_decode(b, c, err, errn);
     const uint32_t S = c.S, H = c.H;
     const uint64_t bytes = (uint64_t)S * H * 128u * 2u;
     const __half* q = reinterpret_cast<const __half*>(ref_ptr(b, c.q));

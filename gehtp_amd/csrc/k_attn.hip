@@ -300,6 +300,11 @@ struct DecodeArgs {
     float* part;             // partials [KVH][max_chunks][REP][PS]
     uint32_t max_chunks;
     uint32_t* ws;            // fused: workspace head (snapshot, RoPE records)
+    // Additive mask (plain op only, may be null): row h (query head) at mask + h * P,
+    // one value per position of a gathered layout of P positions; positions [n_kv, P)
+    // hold zero K/V there, so they score the mask value alone (added by the merge pass).
+    const __half* mask;
+    uint32_t P;
 };
 
 template <int REP, bool FUSED>
@@ -394,6 +399,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
             qv[r] = *reinterpret_cast<const u32x4*>(A.q + (size_t)(g * REP + r) * HD + ch * 8);
     }
 
+    // Mask values of this thread's keys (lanes ch == 0 store the scores).
+    float mk[DC / 16][REP];
+#pragma unroll
+    for (int it = 0; it < DC / 16; ++it)
+#pragma unroll
+        for (int r = 0; r < REP; ++r) mk[it][r] = 0.0f;
+    if (!FUSED && A.mask) {
+#pragma unroll
+        for (int it = 0; it < DC / 16; ++it) {
+            const uint32_t key = min(c * DC + ks + 16 * it, n_kv - 1u);
+#pragma unroll
+            for (int r = 0; r < REP; ++r) mk[it][r] = __half2float(A.mask[(size_t)(g * REP + r) * A.P + key]) * kLog2e;
+        }
+    }
+
     // Scores: 16 lanes per key, 4 keys per wave per step.
 #pragma unroll
     for (int it = 0; it < DC / 16; ++it) {
@@ -406,7 +426,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
             for (int e = 0; e < 4; ++e)
                 a = __builtin_amdgcn_fdot2(as_h2(kv4[it][e]), as_h2(qv[r][e]), a, false);
             a = dev::row_sum16(a);   // the 16 lanes of a key form one DPP row
-            if (ch == 0) sc[r][kl] = valid ? a * A.scale_log2 : -INFINITY;
+            if (ch == 0) sc[r][kl] = valid ? a * A.scale_log2 + mk[it][r] : -INFINITY;
         }
     }
     __syncthreads();
@@ -416,7 +436,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     for (uint32_t r = wave; r < REP; r += 4) {
         const float x = sc[r][lane];
         const float m = dev::wave_max(x);
-        const float p = exp2f(x - m);
+        const float p = m == -INFINITY ? 0.0f : exp2f(x - m);   // a chunk whose keys are all masked
         const float l = dev::wave_sum(p);
         sc[r][lane] = p;
         if (lane == 0) { wchunk[r * PS + HD] = m; wchunk[r * PS + HD + 1] = l; }
@@ -479,11 +499,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
 // With `advance` (fused), n_kv is the chunk pass's snapshot (the counter + 1): query
 // head 0 stores it as the new counter value (no other workgroup of this pass reads the
 // counter), and the extra last workgroup writes the two RoPE records.
+// With a mask over a gathered layout of P > n_kv positions, positions [n_kv, P) (zero K
+// and V) add their mask values to the softmax denominator: one more partial (m, l) with
+// O = 0, reduced over the workgroup.
 __global__ __launch_bounds__(256) void attn_merge_kernel(
     const float* __restrict__ part, uint32_t n_kv_host, uint32_t* __restrict__ count, int advance,
-    uint32_t rep, uint32_t max_chunks, __half* __restrict__ out, uint32_t* __restrict__ ws, float theta) {
+    uint32_t rep, uint32_t max_chunks, __half* __restrict__ out, uint32_t* __restrict__ ws, float theta,
+    const __half* __restrict__ mask, uint32_t P) {
     __shared__ __align__(16) float4 s_o[256];
-    __shared__ float s_m[8], s_l[8];
+    __shared__ float s_m[8], s_l[8], s_t[4];
     const uint32_t n_kv = advance ? ws[kWsSnap] : count ? *count : n_kv_host;
     const uint32_t nc = (n_kv + DC - 1) / DC;
     const uint32_t h = blockIdx.x, g = h / rep, r = h % rep;
@@ -517,7 +541,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
             lg *= sc;
             mg = mc;
         }
-        const float wt = exp2f(mc - mg);
+        const float wt = mc == -INFINITY ? 0.0f : exp2f(mc - mg);   // a chunk whose keys are all masked
         o.x = fmaf(wt, v.x, o.x);
         o.y = fmaf(wt, v.y, o.y);
         o.z = fmaf(wt, v.z, o.z);
@@ -526,14 +550,33 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
     }
     s_o[tid] = o;
     if (d4 == 0) { s_m[grp] = mg; s_l[grp] = lg; }
+    // Tail of a masked gathered layout: max, then sum of 2^(mask - max), over the workgroup.
+    float tm = -INFINITY, tl = 0.0f;
+    const bool tail = mask && P > n_kv;
+    if (tail) {
+        const __half* mrow = mask + (size_t)h * P;
+        for (uint32_t j = n_kv + tid; j < P; j += 256) tm = fmaxf(tm, __half2float(mrow[j]) * kLog2e);
+        tm = dev::wave_max(tm);
+        if ((tid & 63) == 0) s_t[tid >> 6] = tm;
+        __syncthreads();
+        tm = fmaxf(fmaxf(s_t[0], s_t[1]), fmaxf(s_t[2], s_t[3]));
+        if (tm != -INFINITY)
+            for (uint32_t j = n_kv + tid; j < P; j += 256) tl += exp2f(__half2float(mrow[j]) * kLog2e - tm);
+        tl = dev::wave_sum(tl);
+        __syncthreads();
+        if ((tid & 63) == 0) s_t[tid >> 6] = tl;
+        __syncthreads();
+        tl = s_t[0] + s_t[1] + s_t[2] + s_t[3];
+    }
     __syncthreads();
     if (tid < 32) {
         float M = s_m[0];
         for (uint32_t k = 1; k < 8; ++k) M = fmaxf(M, s_m[k]);
-        float L = 0.0f;
+        M = fmaxf(M, tm);
+        float L = tm == -INFINITY ? 0.0f : exp2f(tm - M) * tl;
         o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (uint32_t k = 0; k < 8; ++k) {
-            const float wk = exp2f(s_m[k] - M);   // 0 for a group without chunks
+            const float wk = s_m[k] == -INFINITY ? 0.0f : exp2f(s_m[k] - M);   // 0 for a group without chunks
             const float4 p = s_o[tid + 32 * k];
             o.x = fmaf(wk, p.x, o.x);
             o.y = fmaf(wk, p.y, o.y);
@@ -595,7 +638,8 @@ hipError_t decode_launch(const DecodeArgs& A, uint32_t rep, int advance, __half*
     default: return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(attn_merge_kernel, dim3(A.H + (advance ? 1 : 0)), dim3(256), 0, st, A.part, A.n_kv_host,
-                       A.count, advance, rep, A.max_chunks, out, reinterpret_cast<uint32_t*>(work), A.theta);
+                       A.count, advance, rep, A.max_chunks, out, reinterpret_cast<uint32_t*>(work), A.theta,
+                       A.mask, A.P);
     return hipGetLastError();
 }
 
@@ -604,8 +648,10 @@ hipError_t decode_launch(const DecodeArgs& A, uint32_t rep, int advance, __half*
 hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slot_bytes,
                               uint32_t nslots, __half* out, uint32_t n_kv_host,
                               const uint32_t* count_dev, uint32_t H, uint32_t KVH, uint32_t hd,
-                              float scale, float* work, uint32_t work_floats, hipStream_t st) {
+                              float scale, float* work, uint32_t work_floats, hipStream_t st,
+                              const __half* mask, uint32_t P) {
     if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
+    if (mask && (P == 0 || P > nslots || (!count_dev && n_kv_host > P))) return hipErrorInvalidValue;
     const uint32_t rep = H / KVH;
     if (rep > MAX_REP || slot_bytes != KVH * HD * 4) return hipErrorInvalidValue;
     // Chunks cover every position the ring can hold, so a device-side count never
@@ -615,7 +661,8 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
     if (attn_decode_work_floats(max_kv, H, hd) > work_floats) return hipErrorInvalidValue;
     if (!max_chunks) return hipSuccess;
     DecodeArgs A{q, nullptr, nullptr, nullptr, 0.0f, const_cast<uint8_t*>(ring), slot_bytes, nslots, KVH, H,
-                 n_kv_host, const_cast<uint32_t*>(count_dev), scale * kLog2e, work + kWsHead, max_chunks, nullptr};
+                 n_kv_host, const_cast<uint32_t*>(count_dev), scale * kLog2e, work + kWsHead, max_chunks, nullptr,
+                 mask, mask ? P : 0u};
     return decode_launch<false>(A, rep, 0, out, work, st);
 }
 
@@ -630,7 +677,7 @@ hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, cons
     if (attn_decode_work_floats(nslots, H, HD) > work_floats) return hipErrorInvalidValue;
     DecodeArgs A{nullptr, qkv, q_gamma, k_gamma, theta, ring, slot_bytes, nslots, KVH, H,
                  0u, count_dev, scale * kLog2e, work + kWsHead, max_chunks,
-                 reinterpret_cast<uint32_t*>(work)};
+                 reinterpret_cast<uint32_t*>(work), nullptr, 0u};
     return decode_launch<true>(A, rep, 1, out, work, st);
 }
 
