@@ -120,6 +120,10 @@ int go_cumsum(const uint16_t* x, uint16_t* y, uint32_t rows, uint32_t n, uint32_
 int go_gather(const uint16_t* tbl, const int32_t* idx, uint16_t* y, uint32_t n, uint32_t packed,
               const uint32_t* td, const uint32_t* xd);
 int go_transpose4(const uint16_t* x, uint16_t* y, uint32_t Hh, uint32_t W, uint32_t Cc, uint32_t perm);
+int go_broadcast(const uint16_t* x, uint16_t* y, uint32_t n, const uint32_t* in_d, const uint32_t* out_d);
+int go_transpose_gen(const uint16_t* x, uint16_t* y, uint32_t rk, const uint32_t* dims, uint32_t perm);
+int go_slice(const uint16_t* x, uint16_t* y, uint32_t n_out, uint32_t rk, const uint32_t* b, const uint32_t* e,
+             const uint32_t* s, const uint32_t* d);
 
 #ifdef __cplusplus
 }

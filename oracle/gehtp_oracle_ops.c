@@ -275,3 +275,84 @@ int go_transpose4(const uint16_t* x, uint16_t* y, uint32_t Hh, uint32_t W, uint3
                 }
     return 0;
 }
+
+/* ---- OP_BROADCAST_F16 (oplist_exec.c:1876-1907): right-aligned broadcast of b [in_d]
+ * to [out_d] (4 dims each, trailing 1s of out_d trimmed, in_d taken to the same rank);
+ * an input dim of 1 repeats, any other dim d indexes (coordinate mod d). */
+int go_broadcast(const uint16_t* x, uint16_t* y, uint32_t n, const uint32_t* in_d, const uint32_t* out_d) {
+    uint32_t r = 4;
+    while (r > 0 && out_d[r - 1] == 1) r--;
+    uint32_t ir = 4;
+    if (r == 0) r = 1;
+    if (ir > r) ir = r;
+    uint32_t istr[4] = {1, 1, 1, 1}, ostr[4] = {1, 1, 1, 1};
+    for (int i = (int)ir - 2; i >= 0; i--) istr[i] = istr[i + 1] * in_d[i + 1];
+    for (int i = (int)r - 2; i >= 0; i--) ostr[i] = ostr[i + 1] * out_d[i + 1];
+    const uint32_t lead = r - ir;
+    for (uint32_t i = 0; i < n; i++) {
+        uint32_t rem = i, in_lin = 0;
+        for (uint32_t d = 0; d < r; d++) {
+            const uint32_t c = rem / ostr[d];
+            rem %= ostr[d];
+            if (d < lead) continue;
+            const uint32_t idim = in_d[d - lead];
+            if (idim > 1) in_lin += (c % idim) * istr[d - lead];
+        }
+        y[i] = x[in_lin];
+    }
+    return 0;
+}
+
+/* ---- OP_TRANSPOSE_GEN_F16 (oplist_exec.c:1910-1948): C-order rank-2..4 transpose of
+ * x [dims], output axis i = input axis perm byte i. */
+int go_transpose_gen(const uint16_t* x, uint16_t* y, uint32_t rk, const uint32_t* dims, uint32_t perm) {
+    if (rk < 2 || rk > 4) return -1;
+    const uint32_t p[4] = {perm & 0xFF, (perm >> 8) & 0xFF, (perm >> 16) & 0xFF, (perm >> 24) & 0xFF};
+    size_t n = 1;
+    for (uint32_t i = 0; i < rk; i++) n *= dims[i];
+    uint32_t si[4], so[4];
+    si[rk - 1] = 1;
+    so[rk - 1] = 1;
+    for (int i = (int)rk - 2; i >= 0; i--) {
+        si[i] = si[i + 1] * dims[i + 1];
+        so[i] = so[i + 1] * (p[i + 1] >= rk ? 1u : dims[p[i + 1]]);
+    }
+    for (size_t t = 0; t < n; t++) {
+        uint32_t rem = (uint32_t)t, ic[4] = {0, 0, 0, 0};
+        for (uint32_t i = 0; i < rk; i++) { ic[i] = rem / si[i]; rem %= si[i]; }
+        uint32_t ot = 0;
+        for (uint32_t ax = 0; ax < rk; ax++) ot += ic[p[ax]] * so[ax];
+        y[ot] = x[t];
+    }
+    return 0;
+}
+
+/* ---- OP_STRIDED_SLICE_F16 (oplist_exec.c:1950-1988): rank 1..3, output element i at
+ * input coordinates b[ax] + c[ax] * s[ax] (c = C-order coordinates of i over the slice
+ * extents ceil((e - b) / s)); stride 0 reads as 1. */
+int go_slice(const uint16_t* x, uint16_t* y, uint32_t n_out, uint32_t rk, const uint32_t* b, const uint32_t* e,
+             const uint32_t* s, const uint32_t* d) {
+    if (rk < 1 || rk > 3) return -1;
+    uint32_t ss[3], od[3] = {1, 1, 1}, istr[3], ostr[3];
+    for (uint32_t ax = 0; ax < rk; ax++) {
+        ss[ax] = s[ax] ? s[ax] : 1u;
+        const uint32_t span = e[ax] > b[ax] ? e[ax] - b[ax] : 0;
+        od[ax] = (span + ss[ax] - 1) / ss[ax];
+    }
+    istr[rk - 1] = 1;
+    ostr[rk - 1] = 1;
+    for (int i = (int)rk - 2; i >= 0; i--) {
+        istr[i] = istr[i + 1] * d[i + 1];
+        ostr[i] = ostr[i + 1] * od[i + 1];
+    }
+    for (uint32_t i = 0; i < n_out; i++) {
+        uint32_t rem = i, in_lin = 0;
+        for (uint32_t ax = 0; ax < rk; ax++) {
+            const uint32_t c = rem / ostr[ax];
+            rem %= ostr[ax];
+            in_lin += (b[ax] + c * ss[ax]) * istr[ax];
+        }
+        y[i] = x[in_lin];
+    }
+    return 0;
+}

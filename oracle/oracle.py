@@ -69,6 +69,9 @@ def lib():
             "go_cumsum": (C.c_int, [_p, _p, u, u, u, u]),
             "go_gather": (C.c_int, [_p, _p, _p, u, u, _p, _p]),
             "go_transpose4": (C.c_int, [_p, _p, u, u, u, u]),
+            "go_broadcast": (C.c_int, [_p, _p, u, _p, _p]),
+            "go_transpose_gen": (C.c_int, [_p, _p, u, _p, u]),
+            "go_slice": (C.c_int, [_p, _p, u, u, _p, _p, _p, _p]),
         }
         for name, (res, args) in sig.items():
             f = getattr(_lib, name)
@@ -426,4 +429,40 @@ def transpose4(x, Hh: int, W: int, Cc: int, perm) -> np.ndarray:
     pv = perm[0] | (perm[1] << 8) | (perm[2] << 16) | (perm[3] << 24)
     if lib().go_transpose4(_p(x), _p(y), Hh, W, Cc, pv):
         raise ValueError("transpose perm")
+    return y
+
+
+def _u32v(vals, n):
+    v = list(vals) + [1] * (n - len(vals))
+    return (C.c_uint32 * n)(*v)
+
+
+def broadcast(x, in_d, out_d) -> np.ndarray:
+    """OP_BROADCAST_F16: x (in_d elements) -> out_d (up to 4 dims each)."""
+    x = _h(x)
+    n = int(np.prod(out_d))
+    y = np.empty(n, np.float16)
+    lib().go_broadcast(_p(x), _p(y), n, C.cast(_u32v(in_d, 4), C.c_void_p), C.cast(_u32v(out_d, 4), C.c_void_p))
+    return y
+
+
+def transpose_gen(x, dims, perm) -> np.ndarray:
+    """OP_TRANSPOSE_GEN_F16: x [dims] (rank 2..4), output axis i = input axis perm[i]."""
+    x = _h(x)
+    rk = len(dims)
+    pv = sum(int(p) << (8 * i) for i, p in enumerate(perm))
+    y = np.empty(int(np.prod(dims)), np.float16)
+    if lib().go_transpose_gen(_p(x), _p(y), rk, C.cast(_u32v(dims, 4), C.c_void_p), pv):
+        raise ValueError("transpose_gen rank")
+    return y
+
+
+def strided_slice(x, n_out, b, e, s, d) -> np.ndarray:
+    """OP_STRIDED_SLICE_F16 (rank len(d) <= 3)."""
+    x = _h(x)
+    rk = len(d)
+    y = np.empty(n_out, np.float16)
+    args = [C.cast(_u32v(v, 3), C.c_void_p) for v in (b, e, s, d)]
+    if lib().go_slice(_p(x), _p(y), n_out, rk, *args):
+        raise ValueError("slice rank")
     return y
