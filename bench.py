@@ -51,6 +51,12 @@ def parse_args():
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the two prefills (weight upload, then the timed one), for kernel traces "
                          "and counter runs of the prefill kernels")
+    ap.add_argument("--kernel-configs", action="store_true",
+                    help="BASELINE configs 1-3 kernel by kernel (GEMV, RMSNorm + GEMM, prefill and decode "
+                         "attention), operands rotated over copies totalling > 256 MB and, beside it, "
+                         "one copy repeated (cache-resident); prints one JSON line")
+    ap.add_argument("--only", default=None,
+                    help="with --kernel-configs: comma-separated subset of c1,c2,c3p,c3d")
     return ap.parse_args()
 
 
@@ -79,6 +85,8 @@ def main() -> int:
         return 2
     if args.roofline_only:
         return roofline_only(args)
+    if args.kernel_configs:
+        return kernel_configs(args)
     import numpy as np
     import torch
 
@@ -297,6 +305,163 @@ def roofline_only(args) -> int:
     print(json.dumps({"roofline_only": True, "avg_launch_us": avg_s * 1e6, "bytes_per_launch": bpl,
                       "achieved_gbs": gbs, "copy_bytes": 256 << 20}), flush=True)
     return 0
+
+
+def kernel_configs(args) -> int:
+    """BASELINE configs 1-3 as single kernels on device buffers (C entry points of
+    include/gehtp_kernels.h), each timed with HIP events on the launch stream over
+    back-to-back launches. "rotated": every launch reads its own copy of the weights /
+    KV cache / attention inputs, the copies totalling more than 256 MB (the 256 MB
+    Infinity Cache cannot hold them), so operands stream from HBM; "resident": one copy
+    launched repeatedly (operands served from the caches). Algorithmic work per launch:
+      c1  GEMV x[1,1024] . W[3072,1024] int4 g64: bytes W 1,572,864 + scales 98,304 +
+          x 2,048 + y 6,144 = 1,679,360
+      c2  RMSNorm x[512,1024] (bytes 2 * 512*1024*2 + gamma 2,048) then the GEMM
+          512 x 3072 x 1024 (flops 2*M*N*K = 3.22 G)
+      c3p causal GQA prefill S=1024, 16 Q / 8 KV heads, hd 128: flops 4*H*hd*S(S+1)/2
+          = 4.30 G
+      c3d decode over 4096 keys of the ring, 16 Q / 8 KV heads: bytes K + V =
+          4096*8*128*2*2 = 16,777,216 (the 4 KB query and output aside)"""
+    import numpy as np
+    import torch
+
+    from gehtp_amd import load_library, lib_path
+    lib = load_library(lib_path)
+    assert torch.cuda.is_available(), "needs a GPU"
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3p", "c3d"}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    results = {}
+
+    def timed(launch, n_copies, reps):
+        """Mean seconds per launch over reps rounds of n_copies launches (copy i each)."""
+        for i in range(n_copies):
+            launch(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            for i in range(n_copies):
+                launch(i)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / (reps * n_copies)
+
+    def w4g_copies(n, k, copies):
+        q = torch.randint(0, 256, (copies, n, k // 2), dtype=torch.uint8, device=dev, generator=gen)
+        sc = (torch.rand((copies, n, k // 64), device=dev, generator=gen) * 0.015 + 0.005).half()
+        return q, sc
+
+    if "c1" in only:
+        N, K, copies = 3072, 1024, 192      # 192 x 1.68 MB = 322 MB
+        q, sc = w4g_copies(N, K, copies)
+        x = torch.randn(K, device=dev, generator=gen).half()
+        y = torch.empty((copies, N), dtype=torch.float16, device=dev)
+        nbytes = N * K // 2 + N * (K // 64) * 2 + K * 2 + N * 2
+
+        def c1(i):
+            assert lib.gehtp_w4g_gemv(x.data_ptr(), K, q[i].data_ptr(), sc[i].data_ptr(), y[i].data_ptr(), N, 1, N,
+                                      K, sp) == 0
+        t_rot = timed(c1, copies, 10)
+        t_res = timed(lambda i: c1(0), 64, 10)
+        results["c1_gemv"] = {"kernel": "w4g_gemv_kernel<1>", "bytes": nbytes, "copies": copies,
+                              "rotated_us": round(t_rot * 1e6, 3), "rotated_gbs": round(nbytes / t_rot / 1e9, 1),
+                              "resident_us": round(t_res * 1e6, 3), "resident_gbs": round(nbytes / t_res / 1e9, 1)}
+        log(f"c1 gemv: rotated {t_rot * 1e6:.2f} us ({nbytes / t_rot / 1e9:.0f} GB/s), "
+            f"resident {t_res * 1e6:.2f} us")
+        del q, sc, y
+
+    if "c2" in only:
+        M, N, K, copies = 512, 3072, 1024, 192
+        q, sc = w4g_copies(N, K, copies)
+        x = torch.randn((M, K), device=dev, generator=gen).half()
+        gamma = (torch.rand(K, device=dev, generator=gen) * 0.4 + 0.8).half()
+        h = torch.empty((M, K), dtype=torch.float16, device=dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        flops = 2.0 * M * N * K
+        nb_norm = 2 * M * K * 2 + K * 2
+
+        def norm(i):
+            assert lib.gehtp_rmsnorm2(x.data_ptr(), gamma.data_ptr(), None, h.data_ptr(), M, K, sp) == 0
+
+        def gemm(i):
+            assert lib.gehtp_w4g_gemm(h.data_ptr(), K, q[i].data_ptr(), sc[i].data_ptr(), y.data_ptr(), N, M, N, K,
+                                      sp) == 0
+
+        def both(i):
+            norm(i)
+            gemm(i)
+        t_norm = timed(norm, 64, 10)
+        t_rot = timed(gemm, copies, 5)
+        t_res = timed(lambda i: gemm(0), 64, 5)
+        t_both = timed(both, copies, 5)
+        results["c2_rmsnorm_gemm"] = {
+            "kernels": "rmsnorm2_reg_kernel + w4g_gemm_kernel", "gemm_flops": flops, "copies": copies,
+            "rmsnorm_us": round(t_norm * 1e6, 3), "rmsnorm_gbs": round(nb_norm / t_norm / 1e9, 1),
+            "gemm_rotated_us": round(t_rot * 1e6, 3), "gemm_rotated_tflops": round(flops / t_rot / 1e12, 1),
+            "gemm_resident_us": round(t_res * 1e6, 3), "gemm_resident_tflops": round(flops / t_res / 1e12, 1),
+            "norm_plus_gemm_rotated_us": round(t_both * 1e6, 3)}
+        log(f"c2: rmsnorm {t_norm * 1e6:.2f} us, gemm rotated {t_rot * 1e6:.2f} us "
+            f"({flops / t_rot / 1e12:.0f} TFLOPS), resident {t_res * 1e6:.2f} us")
+        del q, sc
+
+    if "c3p" in only:
+        S, H, KVH, copies = 1024, 16, 8, 24    # 24 x (4 + 2 + 2 + 4) MB = 288 MB
+        qq = torch.randn((copies, S, H, HD_ATTN), device=dev, generator=gen).half()
+        kk = torch.randn((copies, S, KVH, HD_ATTN), device=dev, generator=gen).half()
+        vv = torch.randn((copies, S, KVH, HD_ATTN), device=dev, generator=gen).half()
+        oo = torch.empty((copies, S, H, HD_ATTN), dtype=torch.float16, device=dev)
+        scale = float(np.float16(1.0 / np.sqrt(HD_ATTN)))
+        flops = 4.0 * H * HD_ATTN * S * (S + 1) / 2
+
+        def c3p(i):
+            assert lib.gehtp_attn_prefill(qq[i].data_ptr(), kk[i].data_ptr(), vv[i].data_ptr(), oo[i].data_ptr(), S,
+                                          H, KVH, HD_ATTN, scale, 1, sp) == 0
+        t_rot = timed(c3p, copies, 5)
+        t_res = timed(lambda i: c3p(0), 32, 5)
+        results["c3_attn_prefill"] = {"kernel": "attn_prefill_kernel<true>", "flops": flops, "copies": copies,
+                                      "rotated_us": round(t_rot * 1e6, 3),
+                                      "rotated_tflops": round(flops / t_rot / 1e12, 1),
+                                      "resident_us": round(t_res * 1e6, 3),
+                                      "resident_tflops": round(flops / t_res / 1e12, 1)}
+        log(f"c3 prefill: rotated {t_rot * 1e6:.2f} us ({flops / t_rot / 1e12:.0f} TFLOPS), "
+            f"resident {t_res * 1e6:.2f} us")
+        del qq, kk, vv, oo
+
+    if "c3d" in only:
+        n_kv, H, KVH, copies = 4096, 16, 8, 20   # 20 x 16.8 MB = 336 MB
+        kv_elems = KVH * HD_ATTN
+        state_bytes = n_kv * kv_elems * 4
+        rings = torch.empty((copies, state_bytes), dtype=torch.uint8, device=dev)
+        rings.view(torch.float16).copy_(torch.randn(rings.numel() // 2, device=dev, generator=gen).half()
+                                        .view(copies, -1))
+        qd = torch.randn((H, HD_ATTN), device=dev, generator=gen).half()
+        od = torch.empty((H, HD_ATTN), dtype=torch.float16, device=dev)
+        wf = lib.gehtp_attn_decode_work_floats(n_kv, H, HD_ATTN)
+        work = torch.empty(wf, dtype=torch.float32, device=dev)
+        scale = float(np.float16(1.0 / np.sqrt(HD_ATTN)))
+        nbytes = n_kv * kv_elems * 2 * 2
+
+        def c3d(i):
+            assert lib.gehtp_attn_decode(qd.data_ptr(), rings[i].data_ptr(), state_bytes, od.data_ptr(), n_kv, H, KVH,
+                                         HD_ATTN, scale, work.data_ptr(), wf, sp) == 0
+        t_rot = timed(c3d, copies, 10)
+        t_res = timed(lambda i: c3d(0), 32, 10)
+        results["c3_attn_decode"] = {"kernels": "attn_decode_kernel<2,false> + attn_merge_kernel", "bytes": nbytes,
+                                     "copies": copies, "rotated_us": round(t_rot * 1e6, 3),
+                                     "rotated_gbs": round(nbytes / t_rot / 1e9, 1),
+                                     "resident_us": round(t_res * 1e6, 3),
+                                     "resident_gbs": round(nbytes / t_res / 1e9, 1)}
+        log(f"c3 decode: rotated {t_rot * 1e6:.2f} us ({nbytes / t_rot / 1e9:.0f} GB/s), "
+            f"resident {t_res * 1e6:.2f} us")
+    print(json.dumps({"kernel_configs": True, **results}), flush=True)
+    return 0
+
+
+HD_ATTN = 128
 
 
 def cpu_baseline(cfg, w):

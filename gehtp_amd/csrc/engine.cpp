@@ -914,7 +914,7 @@ int op_attn_decode(Ctx& cx) {
     if (attn_workspace(attn_decode_work_floats(autopos ? s->nslots : n_kv, H, hd), err, errn)) return -1;
     CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o, autopos ? 0u : n_kv,
                                     autopos ? g.counters_dev + (A(1) & 0x1FFFu) : nullptr, H, KVH, hd,
-                                    scale, g.attn_work, g.attn_work_floats, g.stream));
+                                    scale, g.attn_work, g.attn_work_floats, g.stream, nullptr, 0u, n_kv));
     return 0;
 }
 
@@ -1105,7 +1105,7 @@ int op_attn_decode_qkv(Ctx& cx) {
     kv_mark(*s, s->count);
     s->count += 1;
     CHECK_LAUNCH(launch_attn_decode_qkv(qkv, qg, kg, theta, s->dev, s->slot_bytes, s->nslots, g.counters_dev + si,
-                                        o, H, KVH, scale, g.attn_work, g.attn_work_floats, g.stream));
+                                        o, H, KVH, scale, g.attn_work, g.attn_work_floats, g.stream, s->count));
     return 0;
 }
 
@@ -1934,7 +1934,7 @@ int run_fused_decode(const wt_blob* b, const AttnChain& c, char* err, size_t err
     if (attn_workspace(attn_decode_work_floats(autopos ? s->nslots : n_kv, H, hd), err, errn)) return -1;
     CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o, autopos ? 0u : n_kv,
                                     autopos ? g.counters_dev + si : nullptr, H, KVH, hd, c.scale, g.attn_work,
-                                    g.attn_work_floats, g.stream, mask, mask ? P : 0u));
+                                    g.attn_work_floats, g.stream, mask, mask ? P : 0u, n_kv));
     return 0;
 }
 

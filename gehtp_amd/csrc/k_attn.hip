@@ -10,6 +10,7 @@
 #include "dev_reduce.h"
 #include "dev_rope.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace gehtp {
@@ -305,6 +306,7 @@ struct DecodeArgs {
     // hold zero K/V there, so they score the mask value alone (added by the merge pass).
     const __half* mask;
     uint32_t P;
+    uint32_t spec_chunks;    // chunks whose keys are known to lie below the count
 };
 
 template <int REP, bool FUSED>
@@ -326,21 +328,29 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
             rw[j] = A.ws[kWsRope + HD / 2 * j + lane];
         }
     }
+    // K and V rows of this thread's keys. Chunks below spec_chunks (a count the launcher
+    // knows is reached, e.g. the host's mirror when the step was captured) issue them
+    // before the count arrives; the others after it, for keys inside the count only.
+    // Rows of slots past the count are stale and masked below.
+    u32x4 kv4[DC / 16], vv4[DC / 16];
+    auto load_kv = [&](uint32_t lim) {
+#pragma unroll
+        for (int it = 0; it < DC / 16; ++it) {
+            const uint32_t key = c * DC + ks + 16 * it;
+            const uint32_t slot = (key < lim ? key : c * DC) % A.nslots;
+            const uint8_t* base = A.ring + (size_t)slot * A.slot_bytes + ((size_t)g * HD + ch * 8) * 2;
+            kv4[it] = *reinterpret_cast<const u32x4*>(base);
+            vv4[it] = *reinterpret_cast<const u32x4*>(base + A.slot_bytes / 2);
+        }
+    };
+    const bool early = c < A.spec_chunks;
+    if (early) load_kv(0xFFFFFFFFu);
+    asm volatile("" ::: "memory");
     const uint32_t pos = FUSED ? *A.count : 0u;   // position of the new token
     const uint32_t n_kv = FUSED ? pos + 1 : (A.count ? *A.count : A.n_kv_host);
     if (c * DC >= n_kv) return;
     if (FUSED && c == 0 && g == 0 && tid == 0) A.ws[kWsSnap] = n_kv;
-
-    // Issue every load of the chunk first: K and V rows of this thread's keys.
-    u32x4 kv4[DC / 16], vv4[DC / 16];
-#pragma unroll
-    for (int it = 0; it < DC / 16; ++it) {
-        const uint32_t key = c * DC + ks + 16 * it;
-        const uint32_t slot = (key < n_kv ? key : c * DC) % A.nslots;
-        const uint8_t* base = A.ring + (size_t)slot * A.slot_bytes + ((size_t)g * HD + ch * 8) * 2;
-        kv4[it] = *reinterpret_cast<const u32x4*>(base);
-        vv4[it] = *reinterpret_cast<const u32x4*>(base + A.slot_bytes / 2);
-    }
+    if (!early) load_kv(n_kv);
 
     u32x4 qv[REP];
     if constexpr (FUSED) {
@@ -508,11 +518,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
     const __half* __restrict__ mask, uint32_t P) {
     __shared__ __align__(16) float4 s_o[256];
     __shared__ float s_m[8], s_l[8], s_t[4];
-    const uint32_t n_kv = advance ? ws[kWsSnap] : count ? *count : n_kv_host;
-    const uint32_t nc = (n_kv + DC - 1) / DC;
     const uint32_t h = blockIdx.x, g = h / rep, r = h % rep;
     const uint32_t tid = threadIdx.x;
     if (advance && h == gridDim.x - 1) {
+        const uint32_t n_kv = ws[kWsSnap];
         // RoPE records for positions n_kv - 1 (wave 0) and n_kv (wave 1).
         const uint32_t j = tid >> 6, i = tid & 63;
         if (j < 2) {
@@ -530,11 +539,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
     const uint32_t d4 = tid & 31, grp = tid >> 5;
     float mg = -INFINITY, lg = 0.0f;
     float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 4
-    for (uint32_t c = grp; c < nc; c += 8) {
-        const float* w = base + c * cstride;
-        const float mc = w[HD], lc = w[HD + 1];
-        const float4 v = *reinterpret_cast<const float4*>(w + 4 * d4);
+    auto merge_one = [&](float mc, float lc, const float4& v) {
         if (mc > mg) {   // 2^-inf = 0 on the first chunk
             const float sc = exp2f(mg - mc);
             o.x *= sc; o.y *= sc; o.z *= sc; o.w *= sc;
@@ -547,6 +552,29 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
         o.z = fmaf(wt, v.z, o.z);
         o.w = fmaf(wt, v.w, o.w);
         lg = fmaf(wt, lc, lg);
+    };
+    // The first kSpec records of each thread group are loaded whatever n_kv turns out to
+    // be (records of chunks past it hold stale values and are never merged), so their
+    // loads overlap the counter's instead of waiting for it; chunks beyond, if any, follow.
+    constexpr uint32_t kSpec = 8;
+    float sm[kSpec], sl[kSpec];
+    float4 sv[kSpec];
+#pragma unroll
+    for (uint32_t k = 0; k < kSpec; ++k) {
+        const float* w = base + (size_t)min(grp + 8 * k, max_chunks - 1) * cstride;
+        sm[k] = w[HD];
+        sl[k] = w[HD + 1];
+        sv[k] = *reinterpret_cast<const float4*>(w + 4 * d4);
+    }
+    asm volatile("" ::: "memory");   // the count is read after the records are requested
+    const uint32_t n_kv = advance ? ws[kWsSnap] : count ? *count : n_kv_host;
+    const uint32_t nc = (n_kv + DC - 1) / DC;
+#pragma unroll
+    for (uint32_t k = 0; k < kSpec; ++k)
+        if (grp + 8 * k < nc) merge_one(sm[k], sl[k], sv[k]);
+    for (uint32_t c = grp + 8 * kSpec; c < nc; c += 8) {
+        const float* w = base + c * cstride;
+        merge_one(w[HD], w[HD + 1], *reinterpret_cast<const float4*>(w + 4 * d4));
     }
     s_o[tid] = o;
     if (d4 == 0) { s_m[grp] = mg; s_l[grp] = lg; }
@@ -649,7 +677,7 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
                               uint32_t nslots, __half* out, uint32_t n_kv_host,
                               const uint32_t* count_dev, uint32_t H, uint32_t KVH, uint32_t hd,
                               float scale, float* work, uint32_t work_floats, hipStream_t st,
-                              const __half* mask, uint32_t P) {
+                              const __half* mask, uint32_t P, uint32_t n_kv_known) {
     if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
     if (mask && (P == 0 || P > nslots || (!count_dev && n_kv_host > P))) return hipErrorInvalidValue;
     const uint32_t rep = H / KVH;
@@ -662,14 +690,15 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
     if (!max_chunks) return hipSuccess;
     DecodeArgs A{q, nullptr, nullptr, nullptr, 0.0f, const_cast<uint8_t*>(ring), slot_bytes, nslots, KVH, H,
                  n_kv_host, const_cast<uint32_t*>(count_dev), scale * kLog2e, work + kWsHead, max_chunks, nullptr,
-                 mask, mask ? P : 0u};
+                 mask, mask ? P : 0u, (count_dev ? std::min(n_kv_known, nslots) : n_kv_host) / DC};
     return decode_launch<false>(A, rep, 0, out, work, st);
 }
 
 hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, const __half* k_gamma,
                                   float theta, uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
                                   uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH,
-                                  float scale, float* work, uint32_t work_floats, hipStream_t st) {
+                                  float scale, float* work, uint32_t work_floats, hipStream_t st,
+                                  uint32_t n_kv_known) {
     if (!KVH || H % KVH || !count_dev) return hipErrorInvalidValue;
     const uint32_t rep = H / KVH;
     if (rep > MAX_REP || slot_bytes != KVH * HD * 4 || !nslots) return hipErrorInvalidValue;
@@ -677,7 +706,7 @@ hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, cons
     if (attn_decode_work_floats(nslots, H, HD) > work_floats) return hipErrorInvalidValue;
     DecodeArgs A{nullptr, qkv, q_gamma, k_gamma, theta, ring, slot_bytes, nslots, KVH, H,
                  0u, count_dev, scale * kLog2e, work + kWsHead, max_chunks,
-                 reinterpret_cast<uint32_t*>(work), nullptr, 0u};
+                 reinterpret_cast<uint32_t*>(work), nullptr, 0u, std::min(n_kv_known, nslots) / DC};
     return decode_launch<true>(A, rep, 1, out, work, st);
 }
 
