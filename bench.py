@@ -510,11 +510,88 @@ def cpu_baseline(cfg, w):
     t_token = t_layers * cfg.layers + t_head
     log(f"cpu baseline: {t_layers * 1e3:.0f} ms/layer, lm_head {t_head * 1e3:.0f} ms, "
         f"{t_token:.2f} s/token on {threads} threads")
+    one = cpu_one_core(cfg, w)
+    pre = cpu_prefill(cfg, w, threads)
     return {"value": round(1.0 / t_token, 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"1 decode token: {sample_layers} of {cfg.layers} layers (W4A16 linears dequantized "
                       f"per call, attention over 2048 positions) + 16384 of {cfg.vocab} lm_head rows, "
-                      f"extrapolated linearly to the full model",
-            "cpu": _cpu_model()}
+                      f"extrapolated linearly to the full model; the vectorised oracle (bit-identical to its "
+                      f"scalar form) on all host threads",
+            "one_core": one, "prefill": pre, "cpu": _cpu_model()}
+
+
+def cpu_one_core(cfg, w):
+    """The reference-faithful scalar restatement (sequential-k fp32 sums, fp16(q*s) per
+    weight, the runlist's f16 rounding points) on one core: one decode layer's linears
+    and its attention over 2048 positions, plus 4096 lm_head rows, extrapolated."""
+    import numpy as np
+
+    from oracle import oracle as o
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((1, cfg.hidden)).astype(np.float16)
+    t0 = time.perf_counter()
+    h = o.rmsnorm2(x, w.f16("0.g_attn"))
+    outs = {nm: o.matmul_w4g(h, *w.linear(0, nm), 1, form="ref") for nm in ("wq", "wk", "wv")}
+    ctx = 2048
+    kT = rng.standard_normal((cfg.head_dim, ctx)).astype(np.float16)
+    vv = rng.standard_normal((ctx, cfg.head_dim)).astype(np.float16)
+    for hh in range(cfg.heads):
+        sc = o.matmul_f16(outs["wq"][0, hh * 128:(hh + 1) * 128], kT, 1, 128, ctx)
+        o.matmul_f16(o.softmax(sc, 1, ctx), vv, 1, ctx, 128)
+    x1 = o.binary(x, o.matmul_w4g(outs["wq"], *w.linear(0, "wo"), 1, form="ref"), 0)
+    h2 = o.rmsnorm2(x1, w.f16("0.g_ffn"))
+    g = o.matmul_w4g(h2, *w.linear(0, "wg"), 1, form="ref")
+    u = o.matmul_w4g(h2, *w.linear(0, "wu"), 1, form="ref")
+    m = o.binary(o.unary(g, 12), u, 2)
+    o.binary(x1, o.matmul_w4g(m, *w.linear(0, "wd"), 1, form="ref"), 0)
+    t_layer = time.perf_counter() - t0
+    rows = 4096
+    t1 = time.perf_counter()
+    o.matmul_f16_nk(x, w.embed()[:rows], 1, form="ref")
+    t_head = (time.perf_counter() - t1) * cfg.vocab / rows
+    t_token = t_layer * cfg.layers + t_head
+    log(f"cpu baseline, 1 core scalar: {t_layer * 1e3:.0f} ms/layer, lm_head {t_head * 1e3:.0f} ms, "
+        f"{t_token:.2f} s/token")
+    return {"value": round(1.0 / t_token, 5), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"1 decode token with the scalar restatement (sequential k, as oplist_exec.c's "
+                      f"host path): layer 0 of {cfg.layers} (attention over 2048 positions) + 4096 of "
+                      f"{cfg.vocab} lm_head rows, extrapolated linearly"}
+
+
+def cpu_prefill(cfg, w, threads):
+    """Prefill on the host: one layer over 256 prompt tokens (linears, RMSNorms, SwiGLU) with
+    the vectorised oracle on all threads, and the causal attention chain of one layer at
+    S = 256; linear parts extrapolated x8 tokens, attention x(2048/256)^2, both x layers."""
+    import numpy as np
+
+    from oracle import oracle as o
+    rng = np.random.default_rng(9)
+    S = 256
+    x = rng.standard_normal((S, cfg.hidden)).astype(np.float16)
+    t0 = time.perf_counter()
+    h = o.rmsnorm2(x, w.f16("0.g_attn"))
+    for nm in ("wq", "wk", "wv"):
+        o.matmul_w4g(h, *w.linear(0, nm), threads)
+    a = rng.standard_normal((S, cfg.q_dim)).astype(np.float16)
+    x1 = o.binary(x, o.matmul_w4g(a, *w.linear(0, "wo"), threads), 0)
+    h2 = o.rmsnorm2(x1, w.f16("0.g_ffn"))
+    g = o.matmul_w4g(h2, *w.linear(0, "wg"), threads)
+    u = o.matmul_w4g(h2, *w.linear(0, "wu"), threads)
+    o.binary(x1, o.matmul_w4g(o.binary(o.unary(g, 12), u, 2), *w.linear(0, "wd"), threads), 0)
+    t_lin = time.perf_counter() - t0
+    Sa = 256
+    q = rng.standard_normal((Sa, cfg.heads, cfg.head_dim)).astype(np.float16)
+    k = rng.standard_normal((Sa, cfg.kv_heads, cfg.head_dim)).astype(np.float16)
+    v = rng.standard_normal((Sa, cfg.kv_heads, cfg.head_dim)).astype(np.float16)
+    t1 = time.perf_counter()
+    o.attn_prefill(q, k, v, cfg.scale, True, threads=threads)
+    t_attn = time.perf_counter() - t1
+    t_total = (t_lin * (2048 / S) + t_attn * (2048 / Sa) ** 2) * cfg.layers
+    log(f"cpu prefill sample: linears {t_lin * 1e3:.0f} ms / {S} tokens / layer, attention "
+        f"{t_attn * 1e3:.0f} ms at S=256 -> {t_total:.1f} s for 2048 tokens")
+    return {"value": round(2048 / t_total, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "prefill of 2048 tokens estimated from layer 0: linears over 256 tokens (x8) and the "
+                      "causal attention chain at S=256 (x64), both x36 layers; vectorised oracle on all threads"}
 
 
 def _cpu_model() -> str:

@@ -84,7 +84,8 @@ struct Engine {
     uint32_t n_states = 0;
     State st[WT_MAX_STATES];
     bool states_loaded = false;
-    uint32_t* counters_dev = nullptr;   // one auto-position counter per state
+    uint32_t* counters_dev = nullptr;   // per state: auto-position counter, then [WT_MAX_STATES + i] a
+                                        // workgroups-finished counter of the prefill QK/RoPE kernel
 
     // Device copy of the blob's weight region and its identity.
     uint8_t* w_dev = nullptr;
@@ -200,9 +201,9 @@ int ensure_ready(char* err, size_t errn) {
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return ERR("no HIP device visible");
     if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess)
         return ERR("hipStreamCreate failed");
-    if (dev_malloc(reinterpret_cast<void**>(&g.counters_dev), WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
+    if (dev_malloc(reinterpret_cast<void**>(&g.counters_dev), 2 * WT_MAX_STATES * sizeof(uint32_t)) != hipSuccess)
         return ERR("counter alloc failed");
-    if (launch_fill_zero(g.counters_dev, WT_MAX_STATES * sizeof(uint32_t), g.stream) != hipSuccess)
+    if (launch_fill_zero(g.counters_dev, 2 * WT_MAX_STATES * sizeof(uint32_t), g.stream) != hipSuccess)
         return ERR("counter clear failed");
     g.ready = true;
     return 0;
@@ -472,7 +473,7 @@ int load_states(const wt_blob* b, char* err, size_t errn) {
         g.n_states = 0;
         // Clears go on the engine's stream: a null-stream memset is not ordered with the
         // kernels of a non-blocking stream and could land after the first KV append.
-        if (g.counters_dev && launch_fill_zero(g.counters_dev, WT_MAX_STATES * sizeof(uint32_t), g.stream) != hipSuccess)
+        if (g.counters_dev && launch_fill_zero(g.counters_dev, 2 * WT_MAX_STATES * sizeof(uint32_t), g.stream) != hipSuccess)
             return ERR("counter clear failed");
         for (uint32_t i = 0; i < n; ++i) {
             uint32_t bytes;
@@ -1058,7 +1059,7 @@ int op_qk_rope_kv(Ctx& cx) {
     s->count += n_tok;
     for (uint32_t t = 0; t < n_tok; ++t) kv_mark(*s, pos + t);
     CHECK_LAUNCH(launch_qk_rope_kv(qkv, n_tok, H, KVH, qg, kg, theta, q_out, k_out, v_out, s->dev, s->slot_bytes,
-                                   s->nslots, g.counters_dev + si, g.stream));
+                                   s->nslots, g.counters_dev + si, g.stream, g.counters_dev + WT_MAX_STATES + si));
     return 0;
 }
 
@@ -2297,7 +2298,7 @@ void wt_exec_state_reset(void) {
         if (s.kv_ready) std::fill(s.posmap.begin(), s.posmap.end(), kNone);
         s.valid_prefix = 0;
     }
-    if (g.counters_dev) launch_fill_zero(g.counters_dev, WT_MAX_STATES * sizeof(uint32_t), g.stream);
+    if (g.counters_dev) launch_fill_zero(g.counters_dev, 2 * WT_MAX_STATES * sizeof(uint32_t), g.stream);
 }
 
 void wt_exec_pool_init(uint8_t* base, uint32_t total_cap, uint32_t static_cap, const uint32_t* offsets) {

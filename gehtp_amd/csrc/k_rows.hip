@@ -481,6 +481,8 @@ struct QkRopeKvArgs {
     uint32_t slot_bytes, nslots;
     uint32_t* count;
     int advance;    // single-workgroup launch: advance the counter in-kernel
+    uint32_t* done;      // rows kernel: workgroups-finished counter (zero between launches);
+                         // the last workgroup to finish advances *count (all have read it)
 };
 
 // One workgroup per token: wave 0 computes the token's RoPE table (64 frequency pairs,
@@ -665,6 +667,16 @@ __global__ __launch_bounds__(256) void qk_rope_kv_rows_kernel(QkRopeKvArgs A, ui
         __half* vf = reinterpret_cast<__half*>(A.ring + (size_t)((pos0 + tk) % A.nslots) * A.slot_bytes) + A.KVH * HD;
         *reinterpret_cast<u32x4*>(vf + 8 * c) = v;
         if (A.v_out) *reinterpret_cast<u32x4*>(A.v_out + (size_t)(t0 + tk) * A.KVH * HD + 8 * c) = v;
+    }
+    // Counter advance by the last workgroup to finish: every workgroup read *count at its
+    // start (thread 0, waited for before the first barrier), so once all have counted
+    // themselves done nobody reads it again in this launch.
+    if (A.done && tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(A.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == gridDim.x - 1) {
+            *A.done = 0u;
+            *A.count = s_pos + n_tok;
+        }
     }
 }
 constexpr uint32_t kQkRowsTok = 4;
@@ -865,21 +877,23 @@ hipError_t launch_kv_append(uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
 hipError_t launch_qk_rope_kv(const __half* qkv, uint32_t n_tok, uint32_t H, uint32_t KVH,
                              const __half* q_gamma, const __half* k_gamma, float theta, __half* q_out,
                              __half* k_out, __half* v_out, uint8_t* ring, uint32_t slot_bytes,
-                             uint32_t nslots, uint32_t* count_dev, hipStream_t st) {
+                             uint32_t nslots, uint32_t* count_dev, hipStream_t st, uint32_t* done_dev) {
     if (!H || !KVH || H + KVH > 4 * kQkMaxHeadsPerWave) return hipErrorInvalidValue;
     if (!n_tok) return hipSuccess;
     QkRopeKvArgs A{qkv, (H + 2 * KVH) * 128u, H, KVH, q_gamma, k_gamma, theta, q_out, k_out, v_out,
-                   ring, slot_bytes, nslots, count_dev, n_tok == 1 ? 1 : 0};
+                   ring, slot_bytes, nslots, count_dev, n_tok == 1 ? 1 : 0, nullptr};
     auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
     const bool rows = n_tok > 1 && al16(qkv) && al16(q_gamma) && al16(k_gamma) && al16(q_out) && al16(k_out) &&
                       al16(v_out) && al16(ring) && slot_bytes % 16 == 0;
-    if (rows)
+    if (rows) {
+        A.done = done_dev;
         hipLaunchKernelGGL(qk_rope_kv_rows_kernel<kQkRowsTok>, dim3((n_tok + kQkRowsTok - 1) / kQkRowsTok), dim3(256),
                            0, st, A, n_tok);
-    else
+    } else {
         hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(n_tok), dim3(256), 0, st, A);
+    }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || n_tok == 1) return e;
+    if (e != hipSuccess || n_tok == 1 || (rows && done_dev)) return e;
     hipLaunchKernelGGL(counter_add_kernel, dim3(1), dim3(1), 0, st, count_dev, n_tok);
     return hipGetLastError();
 }

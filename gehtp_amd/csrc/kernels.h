@@ -109,10 +109,13 @@ hipError_t launch_kv_append_n(uint8_t* ring, uint32_t slot_bytes, uint32_t nslot
 // q_out[t] = rope(rmsnorm_128(q, q_gamma)), k = rope(rmsnorm_128(k, k_gamma)) and v go to
 // ring slot (*count_dev + t) % nslots (and to k_out / v_out when non-null); then
 // *count_dev += n_tok. Positions for RoPE are *count_dev + t. head_dim is 128.
+// done_dev (optional): a device counter, zero between launches, with which the
+// multi-token kernel advances *count_dev itself (no separate add launch).
 hipError_t launch_qk_rope_kv(const __half* qkv, uint32_t n_tok, uint32_t H, uint32_t KVH,
                              const __half* q_gamma, const __half* k_gamma, float theta, __half* q_out,
                              __half* k_out, __half* v_out, uint8_t* ring, uint32_t slot_bytes,
-                             uint32_t nslots, uint32_t* count_dev, hipStream_t st);
+                             uint32_t nslots, uint32_t* count_dev, hipStream_t st,
+                             uint32_t* done_dev = nullptr);
 // kT [H][hd][pstride], v [H][pstride][hd]; positions >= n_kv of the pstride are zero.
 hipError_t launch_kv_gather(const uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
                             __half* kT, __half* vo, uint32_t n_kv, uint32_t pstride, uint32_t H,
