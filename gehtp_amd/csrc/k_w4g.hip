@@ -582,10 +582,10 @@ constexpr uint32_t kRedNormG = 2;   // 8-column groups per thread: N <= 4096
 __global__ __launch_bounds__(256) void w4g_splitk_reduce_norm_kernel(
     const float* __restrict__ part, uint32_t parts, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
     const __half* __restrict__ res, uint32_t ldr, const __half* __restrict__ gamma, __half* __restrict__ xn) {
-    __shared__ double s_ss[4];
+    __shared__ double s_ss;
+    __shared__ __align__(16) u32x4 s_row[256 * kRedNormG];
     const uint32_t row = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6, n8 = N / 8;
     u32x4 xv[kRedNormG];
-    double ss = 0.0;
 #pragma unroll
     for (uint32_t j = 0; j < kRedNormG; ++j) {
         const uint32_t q = t + 256 * j;
@@ -610,16 +610,30 @@ __global__ __launch_bounds__(256) void w4g_splitk_reduce_norm_kernel(
                 hi = f2hb(__fadd_rn(h2f(hi), h2f((uint16_t)(rv[e] >> 16))));
             }
             xv[j][e] = (uint32_t)lo | ((uint32_t)hi << 16);
-            const double dl = (double)h2f(lo), dh = (double)h2f(hi);
-            ss += dl * dl;
-            ss += dh * dh;
         }
         *reinterpret_cast<u32x4*>(y + (size_t)row * ldy + 8 * q) = xv[j];
+        s_row[q] = xv[j];
     }
-    ss = dev::wave_sum(ss);
-    if (lane == 0) s_ss[wave] = ss;
     __syncthreads();
-    const double tot = ((s_ss[0] + s_ss[1]) + s_ss[2]) + s_ss[3];
+    // The sum of squares in exactly the order of the standalone RMSNORM2 kernel
+    // (rmsnorm2_reg_kernel: lane l takes 8-value chunks l, l + 64, ... in turn, each value
+    // squared and added in double, then the same wave reduction), so a row normalized here
+    // and the same row normalized by that kernel are bit-identical.
+    if (wave == 0) {
+        double ss = 0.0;
+        for (uint32_t q = lane; q < n8; q += 64) {
+            const u32x4 v = s_row[q];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const double f = (double)h2f((uint16_t)(v[e / 2] >> (16 * (e & 1))));
+                ss += f * f;
+            }
+        }
+        ss = dev::wave_sum(ss);
+        if (lane == 0) s_ss = ss;
+    }
+    __syncthreads();
+    const double tot = s_ss;
     const float rms = (float)sqrt(tot / (double)N + 1e-6);
     const float rcp = __fdiv_rn(1.0f, rms);
     auto norm = [&](uint16_t xb, uint16_t gb) {

@@ -127,8 +127,8 @@ def test_split_k_finish_normalizes_next_op(engine, oracle, mode):
     assert_close(fused, ref, what="next op on the pre-normalized rows")
     engine.run(pb, first=1, count=1)   # the second op alone normalizes its input itself
     alone = _h(engine.temp(t2), (M, n_out))
-    assert np.abs(fused.astype(np.float32) - alone.astype(np.float32)).max() <= 2e-2
-    assert (fused == alone).mean() > 0.999
+    # the fused finish sums the squares in the standalone RMSNORM2 kernel's order
+    assert np.array_equal(fused.view(np.uint16), alone.view(np.uint16))
 
 
 def test_rmsnorm_then_w4g_gemm_runlist(engine, oracle):
