@@ -19,14 +19,9 @@ namespace {
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f16x_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-// Reinterpret a 32-bit word as two halves. Takes the word BY VALUE: a bit cast applied
-// directly to an ext_vector element (v[e]) miscompiles to always reading element 0.
-__device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 
 constexpr int HD = 128;          // head dim this kernel is built for
 constexpr int QT = 128;          // queries per workgroup (4 waves x 32)
@@ -309,16 +304,43 @@ struct DecodeArgs {
     uint32_t spec_chunks;    // chunks whose keys are known to lie below the count
 };
 
+// MFMA operand layouts of v_mfma_f32_16x16x32_f16 (lane l, column lc = l % 16, row group
+// lr = l / 16): A (16 x 32) row lc, k = 8lr .. 8lr+7; B (32 x 16) column lc, the same k;
+// D (16 x 16, four floats) rows 4lr .. 4lr+3, column lc.
+//
+// The four waves stage the chunk's K and V rows (16 keys each) in LDS and apply the
+// query heads' norm + RoPE; then one wave does the arithmetic and the others leave.
+// Scores S^T = K . Q^T: the 64 keys as four 16-row A tiles, the REP query heads as B
+// columns (zero past REP), four dims steps of 32. Each lane then holds the 16 scores
+// (keys 16t + 4lr + i) of head lc, so the chunk's max and sum take two cross-row steps.
+// P . V runs transposed, O^T = V^T . P^T: step j's B operand is the probabilities of
+// tiles 2j and 2j+1 as the registers hold them, rounded to fp16 (k index 8lr + i <->
+// key 32j + 4lr + i, 8lr + 4 + i <-> key 32j + 16 + 4lr + i); the A operand (dim 16u +
+// lc, the same keys) comes from the row-major V tile through the transposing LDS read,
+// each lane pointing at the 8-byte piece (key 32j + 4lr + lc/4, dims 16u + 4(lc%4) ..)
+// so that lane lc receives element lc%4 of the pieces of lanes lc/4 + 4i.
+constexpr int VSD = HD + 16;   // V tile row stride (halves): a 16-lane transposed read hits 32 banks
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float cross_row_max(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    dev::permlane32_swap(a, b);
+    v = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    a = __builtin_bit_cast(uint32_t, v);
+    b = a;
+    dev::permlane16_swap(a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
 template <int REP, bool FUSED>
 __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
-    __shared__ float sc[REP][DC];
-    __shared__ __align__(16) float red[4][REP][HD];
+    __shared__ __align__(16) _Float16 s_v[DC * VSD];
+    __shared__ __align__(16) _Float16 s_kt[DC * VSD];
     __shared__ __align__(16) _Float16 s_q[REP][HD];
-    __shared__ __align__(16) _Float16 s_kv[2][HD];
+    __shared__ __align__(16) _Float16 s_k[HD];
     const uint32_t c = blockIdx.x, g = blockIdx.y;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t ch = lane & 15;   // 8-dim chunk of the head
-    const uint32_t ks = tid >> 4;    // key stream: keys ks, ks+16, ks+32, ks+48
+    const uint32_t lc = lane & 15, lr = lane >> 4;
     uint32_t rtag[2] = {0u, 0u}, rtheta[2] = {0u, 0u}, rw[2] = {0u, 0u};
     if constexpr (FUSED) {   // issued with the counter load: neither depends on it
 #pragma unroll
@@ -328,19 +350,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
             rw[j] = A.ws[kWsRope + HD / 2 * j + lane];
         }
     }
-    // K and V rows of this thread's keys. Chunks below spec_chunks (a count the launcher
-    // knows is reached, e.g. the host's mirror when the step was captured) issue them
-    // before the count arrives; the others after it, for keys inside the count only.
-    // Rows of slots past the count are stale and masked below.
-    u32x4 kv4[DC / 16], vv4[DC / 16];
+    // Wave w's 16 K and V rows (key 16w + lc, dims 32s + 8lr .. +8) for the LDS tiles.
+    // Chunks below spec_chunks (see spec_chunks on the host) request them before the
+    // count arrives; the others after it, for keys inside the count only. Rows of slots
+    // past the count are stale and masked below.
+    u32x4 kr[4], vr[4];
+    auto row = [&](uint32_t key, uint32_t lim) -> const uint8_t* {
+        const uint32_t slot = (key < lim ? key : c * DC) % A.nslots;
+        return A.ring + (size_t)slot * A.slot_bytes + ((size_t)g * HD + 8 * lr) * 2;
+    };
     auto load_kv = [&](uint32_t lim) {
+        const uint8_t* kb = row(c * DC + 16 * wave + lc, lim);
 #pragma unroll
-        for (int it = 0; it < DC / 16; ++it) {
-            const uint32_t key = c * DC + ks + 16 * it;
-            const uint32_t slot = (key < lim ? key : c * DC) % A.nslots;
-            const uint8_t* base = A.ring + (size_t)slot * A.slot_bytes + ((size_t)g * HD + ch * 8) * 2;
-            kv4[it] = *reinterpret_cast<const u32x4*>(base);
-            vv4[it] = *reinterpret_cast<const u32x4*>(base + A.slot_bytes / 2);
+        for (int s = 0; s < 4; ++s) {
+            kr[s] = *reinterpret_cast<const u32x4*>(kb + 64 * s);
+            vr[s] = *reinterpret_cast<const u32x4*>(kb + A.slot_bytes / 2 + 64 * s);
         }
     };
     const bool early = c < A.spec_chunks;
@@ -351,10 +375,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     if (c * DC >= n_kv) return;
     if (FUSED && c == 0 && g == 0 && tid == 0) A.ws[kWsSnap] = n_kv;
     if (!early) load_kv(n_kv);
+    const bool owns_new = FUSED && pos / DC == c;
 
-    u32x4 qv[REP];
     if constexpr (FUSED) {
-        const bool owns_new = pos / DC == c;
         float cr, sr;
         const uint32_t tb = __float_as_uint(A.theta);
         const bool hit0 = rtag[0] == pos + 1 && rtheta[0] == tb, hit1 = rtag[1] == pos + 1 && rtheta[1] == tb;
@@ -374,131 +397,127 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
             s_q[r][lane + 64] = (_Float16)y2;
         }
         if (owns_new && wave == (REP < 4 ? (uint32_t)REP : 0u) % 4) {
-            // k of head g: norm + RoPE; v raw. Written to the ring and kept for this chunk.
+            // k of head g: norm + RoPE; v raw. Written to the ring; k kept for this chunk.
             const __half* ksrc = A.qkv + (size_t)(A.H + g) * HD;
             const __half* vsrc = A.qkv + (size_t)(A.H + A.KVH + g) * HD;
             float y1, y2;
             dev::head_norm_rope(__half2float(ksrc[lane]), __half2float(ksrc[lane + 64]), __half2float(A.kg[lane]),
                                 __half2float(A.kg[lane + 64]), cr, sr, y1, y2);
-            s_kv[0][lane] = (_Float16)y1;
-            s_kv[0][lane + 64] = (_Float16)y2;
-            s_kv[1][lane] = __builtin_bit_cast(_Float16, __half_as_ushort(vsrc[lane]));
-            s_kv[1][lane + 64] = __builtin_bit_cast(_Float16, __half_as_ushort(vsrc[lane + 64]));
+            s_k[lane] = (_Float16)y1;
+            s_k[lane + 64] = (_Float16)y2;
             _Float16* kface = reinterpret_cast<_Float16*>(A.ring + (size_t)(pos % A.nslots) * A.slot_bytes);
             _Float16* vface = kface + A.KVH * HD;
             kface[g * HD + lane] = (_Float16)y1;
             kface[g * HD + lane + 64] = (_Float16)y2;
-            vface[g * HD + lane] = s_kv[1][lane];
-            vface[g * HD + lane + 64] = s_kv[1][lane + 64];
+            vface[g * HD + lane] = __builtin_bit_cast(_Float16, __half_as_ushort(vsrc[lane]));
+            vface[g * HD + lane + 64] = __builtin_bit_cast(_Float16, __half_as_ushort(vsrc[lane + 64]));
         }
-        __syncthreads();
+    }
+    // K and V tiles. The new token's V row comes from the QKV row (its ring slot was read
+    // before this launch wrote it; its K row is replaced below). V rows past n_kv are
+    // zero, since slots not yet written may hold anything and p = 0 times a non-finite
+    // value would reach the sums; their scores are -inf whatever K holds.
+    {
+        const uint32_t kl = 16 * wave + lc, key = c * DC + kl;
+        const __half* vnew = FUSED ? A.qkv + (size_t)(A.H + A.KVH + g) * HD + 8 * lr : nullptr;
 #pragma unroll
-        for (int r = 0; r < REP; ++r) qv[r] = *reinterpret_cast<const u32x4*>(&s_q[r][ch * 8]);
-        if (owns_new) {
+        for (int s = 0; s < 4; ++s) {
+            u32x4 v = vr[s];
+            if (FUSED && key == pos) v = *reinterpret_cast<const u32x4*>(vnew + 32 * s);
+            if (key >= n_kv) v = u32x4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(&s_v[kl * VSD + 32 * s + 8 * lr]) = v;
+            *reinterpret_cast<u32x4*>(&s_kt[kl * VSD + 32 * s + 8 * lr]) = kr[s];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+
+    // Queries as B columns; K rows as A tiles (key 16t + lc), the new token's k in place
+    // of its stale ring row.
+    h8_t qb[4];
+    const uint32_t qh = min(lc, (uint32_t)REP - 1u);
 #pragma unroll
-            for (int it = 0; it < DC / 16; ++it) {
-                if (c * DC + ks + 16 * it == pos) {
-                    kv4[it] = *reinterpret_cast<const u32x4*>(&s_kv[0][ch * 8]);
-                    vv4[it] = *reinterpret_cast<const u32x4*>(&s_kv[1][ch * 8]);
-                }
+    for (int s = 0; s < 4; ++s) {
+        const h8_t v = FUSED ? *reinterpret_cast<const h8_t*>(&s_q[qh][32 * s + 8 * lr])
+                             : *reinterpret_cast<const h8_t*>(A.q + (size_t)(g * REP + qh) * HD + 32 * s + 8 * lr);
+        qb[s] = lc < (uint32_t)REP ? v : h8_t{};
+    }
+    u32x4 kf[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) kf[t][s] = *reinterpret_cast<const u32x4*>(&s_kt[(16 * t + lc) * VSD + 32 * s + 8 * lr]);
+    if (owns_new) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            if (c * DC + 16 * t + lc == pos) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) kf[t][s] = *reinterpret_cast<const u32x4*>(&s_k[32 * s + 8 * lr]);
             }
-        }
-    } else {
+    }
+    f4_t sa[4];
 #pragma unroll
-        for (int r = 0; r < REP; ++r)
-            qv[r] = *reinterpret_cast<const u32x4*>(A.q + (size_t)(g * REP + r) * HD + ch * 8);
+    for (int t = 0; t < 4; ++t) {
+        sa[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            sa[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, kf[t][s]), qb[s], sa[t], 0, 0, 0);
     }
 
-    // Mask values of this thread's keys (lanes ch == 0 store the scores).
-    float mk[DC / 16][REP];
+    // Scores in log2 units plus the mask; this lane: head lc, keys 16t + 4lr + i.
+    float x[4][4];
 #pragma unroll
-    for (int it = 0; it < DC / 16; ++it)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int r = 0; r < REP; ++r) mk[it][r] = 0.0f;
-    if (!FUSED && A.mask) {
-#pragma unroll
-        for (int it = 0; it < DC / 16; ++it) {
-            const uint32_t key = min(c * DC + ks + 16 * it, n_kv - 1u);
-#pragma unroll
-            for (int r = 0; r < REP; ++r) mk[it][r] = __half2float(A.mask[(size_t)(g * REP + r) * A.P + key]) * kLog2e;
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t key = c * DC + 16 * t + 4 * lr + i;
+            float mk = 0.0f;
+            if (!FUSED && A.mask) mk = __half2float(A.mask[(size_t)(g * REP + qh) * A.P + min(key, n_kv - 1u)]) * kLog2e;
+            x[t][i] = key < n_kv ? sa[t][i] * A.scale_log2 + mk : -INFINITY;
         }
-    }
-
-    // Scores: 16 lanes per key, 4 keys per wave per step.
+    float mx = -INFINITY;
 #pragma unroll
-    for (int it = 0; it < DC / 16; ++it) {
-        const uint32_t kl = ks + 16 * it;
-        const bool valid = c * DC + kl < n_kv;
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int r = 0; r < REP; ++r) {
-            float a = 0.0f;
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, x[t][i]);
+    const float m = cross_row_max(mx);
+    float p[4][4], ls = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                a = __builtin_amdgcn_fdot2(as_h2(kv4[it][e]), as_h2(qv[r][e]), a, false);
-            a = dev::row_sum16(a);   // the 16 lanes of a key form one DPP row
-            if (ch == 0) sc[r][kl] = valid ? a * A.scale_log2 + mk[it][r] : -INFINITY;
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[t][i] = m == -INFINITY ? 0.0f : exp2f(x[t][i] - m);   // a chunk whose keys are all masked
+            ls += p[t][i];
         }
-    }
-    __syncthreads();
-
-    // Per-head max and exponentials over the chunk (one wave per head).
+    const float l = dev::cross_row_sum(ls);
     float* wchunk = A.part + ((size_t)g * A.max_chunks + c) * REP * PS;
-    for (uint32_t r = wave; r < REP; r += 4) {
-        const float x = sc[r][lane];
-        const float m = dev::wave_max(x);
-        const float p = m == -INFINITY ? 0.0f : exp2f(x - m);   // a chunk whose keys are all masked
-        const float l = dev::wave_sum(p);
-        sc[r][lane] = p;
-        if (lane == 0) { wchunk[r * PS + HD] = m; wchunk[r * PS + HD + 1] = l; }
+    if (lr == 0 && lc < (uint32_t)REP) {
+        wchunk[lc * PS + HD] = m;
+        wchunk[lc * PS + HD + 1] = l;
     }
-    __syncthreads();
 
-    // O[r][d] = sum_key p[r][key] V[key][d] over this thread's 4 keys and 8 dims.
-    float acc[REP][8];
+    f4_t oa[HD / 16];
 #pragma unroll
-    for (int r = 0; r < REP; ++r)
+    for (int u = 0; u < HD / 16; ++u) oa[u] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
+    for (int j = 0; j < 2; ++j) {
+        const h8_t pb = {(_Float16)p[2 * j][0], (_Float16)p[2 * j][1], (_Float16)p[2 * j][2], (_Float16)p[2 * j][3],
+                         (_Float16)p[2 * j + 1][0], (_Float16)p[2 * j + 1][1], (_Float16)p[2 * j + 1][2],
+                         (_Float16)p[2 * j + 1][3]};
+        const _Float16* r0 = &s_v[(32 * j + 4 * lr + lc / 4) * VSD + 4 * (lc % 4)];
 #pragma unroll
-    for (int it = 0; it < DC / 16; ++it) {
-        const uint32_t kl = ks + 16 * it;
-        // V rows past n_kv (read from slots not yet written) may hold anything: zero them
-        // so that p = 0 times a non-finite value cannot reach the sums.
-        const u32x4 vw = c * DC + kl < n_kv ? vv4[it] : u32x4{0u, 0u, 0u, 0u};
-        float ve[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const h2_t v2 = as_h2(vw[e]);
-            ve[2 * e] = (float)v2[0];
-            ve[2 * e + 1] = (float)v2[1];
-        }
-#pragma unroll
-        for (int r = 0; r < REP; ++r) {
-            const float p = sc[r][kl];   // 0 for keys past n_kv
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(p, ve[e], acc[r][e]);
+        for (int u = 0; u < HD / 16; ++u) {
+            const u32x2 lo = lds_read_tr16(r0 + 16 * u);
+            const u32x2 hi = lds_read_tr16(r0 + 16 * VSD + 16 * u);
+            const h8_t af = __builtin_bit_cast(h8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+            oa[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, pb, oa[u], 0, 0, 0);
         }
     }
-    // Reduce the 4 key streams of a wave (lanes l, l^16, l^32, l^48), then across waves.
+    if (lc < (uint32_t)REP) {
 #pragma unroll
-    for (int r = 0; r < REP; ++r)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r][e] = dev::cross_row_sum(acc[r][e]);
-    if (lane < 16) {
-#pragma unroll
-        for (int r = 0; r < REP; ++r)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) red[wave][r][ch * 8 + e] = acc[r][e];
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < REP * HD / 4; i += 256) {
-        const uint32_t r = i / (HD / 4), d = (i % (HD / 4)) * 4;
-        float4 o;
-        o.x = red[0][r][d] + red[1][r][d] + red[2][r][d] + red[3][r][d];
-        o.y = red[0][r][d + 1] + red[1][r][d + 1] + red[2][r][d + 1] + red[3][r][d + 1];
-        o.z = red[0][r][d + 2] + red[1][r][d + 2] + red[2][r][d + 2] + red[3][r][d + 2];
-        o.w = red[0][r][d + 3] + red[1][r][d + 3] + red[2][r][d + 3] + red[3][r][d + 3];
-        *reinterpret_cast<float4*>(wchunk + r * PS + d) = o;
+        for (int u = 0; u < HD / 16; ++u)
+            *reinterpret_cast<float4*>(wchunk + lc * PS + 16 * u + 4 * lr) =
+                make_float4(oa[u][0], oa[u][1], oa[u][2], oa[u][3]);
     }
 }
 
