@@ -96,6 +96,12 @@ __device__ __forceinline__ float cross_row_sum(float v) {
     permlane16_swap(a, b);
     return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
+// v[l] + v[l^16] in every lane: the two 16-lane rows of each half-wave.
+__device__ __forceinline__ float pair_row_sum(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    permlane16_swap(a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
 
 }  // namespace dev
 }  // namespace gehtp

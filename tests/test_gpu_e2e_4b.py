@@ -13,7 +13,10 @@ same top-1):
     0.9999 allows); top-1 identical at every step whose golden margin exceeds twice that
     step's largest top-64 logit error, and at the remaining near-tie steps (random-init
     logits put a few leaders within 2-3 ulps of each other) the engine's top-1 must be
-    one of the golden's leaders within that band; margins and ties are reported;
+    one of the golden's leaders within that band; a top-1 that differs from the golden's
+    is allowed only where the golden margin is at most 4 fp16 ulps of its leading logit
+    (the logits' own rounding step), and at no more than 3 of the sampled steps;
+    margins and ties are reported;
   - the decode steps are teacher forced: the engine consumes the fixture's ids, which are
     the oracle's own greedy choices, so with top-1 identical it runs the same greedy path;
   - every one of the 256 steps: finite logits, and the token the blob's ARGMAX op returns
@@ -126,9 +129,14 @@ def test_config5_e2e_vs_cpu_golden(engine, model4b):
             assert got in cand, f"step {t}: near-tie (margin {margin:.4g} <= {noise:.4g}), top-1 {got} not in {cand}"
             ties.append((t, margin, got == want))
     print(f"config 5: {exact} of {len(margins)} golden rows top-1 identical with a margin above twice the logit "
-          f"error; near ties {ties}; margins min {min(margins):.4g} median {float(np.median(margins)):.4g}; "
-          f"top-64 worst relative error {worst_rel:.3g}; {STEPS} greedy steps")
-    assert exact >= len(margins) - 5, "more near-ties than the fixture's margins allow"
+          f"error; near ties (step, margin, same top-1) {ties}; margins min {min(margins):.4g} median "
+          f"{float(np.median(margins)):.4g}; top-64 worst relative error {worst_rel:.3g}; {STEPS} greedy steps")
+    flips = [(t, m) for t, m, same in ties if not same]
+    for t, m in flips:
+        lead = float(np.abs(fx["top2"][t][0]))
+        ulp = 2.0 ** (np.floor(np.log2(max(lead, 2.0 ** -14))) - 10)
+        assert m <= 4 * ulp, f"step {t}: top-1 differs at a golden margin of {m:.4g} (> 4 fp16 ulps = {4 * ulp:.4g})"
+    assert len(flips) <= 3, f"top-1 differs from the golden at {len(flips)} of {len(margins)} sampled steps: {flips}"
 
     direct, dtoks = _generate(engine, model4b, graphs=False)
     assert dtoks == toks
