@@ -70,6 +70,42 @@ def test_w4g_gemv_shapes(lib, oracle, torch_dev, N, K):
     assert_close(got, ref, what=f"gemv {N}x{K}")
 
 
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("N", [2000, 4000, 6144, 8000, 9728])
+def test_w4g_gemv_pass_forms(lib, oracle, torch_dev, M, N):
+    """K = 2560 (80 threads per row, 4 rows per pass, ~512 workgroups): N = 2000 / 4000 /
+    6144 / 8000 run 1 / 2 / 3 / 4 passes per thread in the straight-line form, N = 9728
+    runs 5 passes in the batched loop; each for M = 1, 2, 4 against the oracle."""
+    rng = np.random.default_rng(N + M)
+    K = 2560
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, M, K)
+    got = _w4g(lib, torch_dev, x, wq, ws, M, N, K, "gemv")
+    ref = oracle.matmul_w4g(x, wq, ws, threads=8)
+    assert_close(got, ref, what=f"gemv M={M} {N}x{K}")
+
+
+@pytest.mark.parametrize("N,K", [(7, 192), (9, 64), (301, 576)])
+def test_w4g_gemv_scales_off_word(lib, oracle, torch_dev, N, K):
+    """Scales read as the aligned 32-bit word holding each one: a scale array starting 2
+    bytes past a 4-byte boundary with an odd number of scales (its last word reaches 2
+    bytes past the array, never past the page) gives the oracle's result."""
+    import torch
+    rng = np.random.default_rng(N * K)
+    _, wq, ws = w4g_weights(rng, N, K)
+    assert (N * (K // 64)) % 2 == 1
+    x = normal_f16(rng, 1, K)
+    buf = torch.zeros(ws.size + 2, dtype=torch.float16, device=torch_dev)
+    buf[1:1 + ws.size] = torch.from_numpy(ws.reshape(-1)).to(torch_dev)
+    sd = buf[1:]
+    assert sd.data_ptr() % 4 == 2
+    xd, qd = to_dev(x, torch_dev), to_dev(wq, torch_dev)
+    yd = torch.empty((1, N), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_w4g_gemv(ptr(xd), K, ptr(qd), sd.data_ptr(), ptr(yd), N, 1, N, K, stream_ptr()) == 0
+    _sync()
+    assert_close(from_dev(yd), oracle.matmul_w4g(x, wq, ws, threads=8), what=f"gemv {N}x{K} scales at +2 bytes")
+
+
 def test_w4g_gemm_config2(lib, oracle, torch_dev):
     """Config 2: RMSNorm(eps 1e-6, gamma U(0.8,1.2)) then W4A16 GEMM [512,1024] x [3072,1024]^T."""
     import torch
