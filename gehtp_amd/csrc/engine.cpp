@@ -105,6 +105,11 @@ struct Engine {
     uint8_t* in_bound = nullptr;
     size_t in_bound_bytes = 0;
     uint8_t* in_src = nullptr;
+    // Pinned buffer for wt_exec_run_io's output: the copy is queued behind the run so one
+    // wait covers both (out_pending = bytes queued by the current run, 0 if none).
+    uint8_t* out_host = nullptr;
+    size_t out_cap = 0;
+    size_t out_pending = 0;
 
     float* attn_work = nullptr;
     uint32_t attn_work_floats = 0;
@@ -1994,6 +1999,17 @@ int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* 
     return rc;
 }
 
+// Waits for a run's work. When wt_exec_run_io asked for an output that fits the pinned
+// output buffer, its device-to-host copy is queued first, so the one wait covers both.
+hipError_t end_run_sync() {
+    g.out_pending = 0;
+    const uint32_t t = g_run_out_temp;
+    if (t < kMaxTemps && g.temps[t] && g.last_bytes[t] && g.last_bytes[t] <= g.out_cap &&
+        hipMemcpyAsync(g.out_host, g.temps[t], g.last_bytes[t], hipMemcpyDeviceToHost, g.stream) == hipSuccess)
+        g.out_pending = g.last_bytes[t];
+    return hipStreamSynchronize(g.stream);
+}
+
 int replay_graph(RunGraph& r, const wt_blob* b, uint32_t first, uint32_t count, uint32_t* engine_m, char* err,
                  size_t errn) {
     const hipError_t le = hipGraphLaunch(r.exec, g.stream);
@@ -2006,7 +2022,7 @@ int replay_graph(RunGraph& r, const wt_blob* b, uint32_t first, uint32_t count, 
     for (uint32_t ii = 0; ii < count && !fail; ++ii)
         if (run_op(b, first + ii, ii, engine_m, err, errn)) fail = (int)(first + ii) + 1;
     g.replay = false;
-    const hipError_t e = hipStreamSynchronize(g.stream);
+    const hipError_t e = end_run_sync();
     if (e != hipSuccess) return ERR("device error: %s", hipGetErrorString(e));
     if (fail || g.epoch != ep0 || g.variant) {
         // The preflight makes this unreachable for the ops this engine implements; if
@@ -2149,7 +2165,7 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
         hipStreamSynchronize(g.stream);
         return fail;
     }
-    const hipError_t e = hipStreamSynchronize(g.stream);
+    const hipError_t e = end_run_sync();
     if (e != hipSuccess) return ERR("device error: %s", hipGetErrorString(e));
     if (timed) {
         for (uint32_t ii = 0; ii < count; ++ii) {
@@ -2214,12 +2230,28 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
         }
     }
     g_run_out_temp = out_ptr ? out_temp : kNone;
+    g.out_pending = 0;
     int rc = wt_exec_run(b, engine_m, op_us, err, errn);
     g_run_out_temp = kNone;
     if (rc == 0 && out_ptr && out_temp < kMaxTemps && g.temps[out_temp]) {
-        if (hipMemcpy(out_ptr, g.temps[out_temp], g.last_bytes[out_temp], hipMemcpyDeviceToHost) != hipSuccess)
-            rc = ERR("output copy failed");
+        const size_t n = g.last_bytes[out_temp];
+        if (n && g.out_pending == n) {
+            std::memcpy(out_ptr, g.out_host, n);   // copied during the run's final wait
+        } else {
+            if (hipMemcpy(out_ptr, g.temps[out_temp], n, hipMemcpyDeviceToHost) != hipSuccess)
+                rc = ERR("output copy failed");
+            // Size the pinned output buffer for the next run (outputs up to 4 MiB).
+            constexpr size_t kOutPinnedMax = 4u << 20;
+            if (rc == 0 && n > g.out_cap && n <= kOutPinnedMax) {
+                if (g.out_host) hipHostFree(g.out_host);
+                g.out_host = nullptr;
+                g.out_cap = 0;
+                if (hipHostMalloc(reinterpret_cast<void**>(&g.out_host), n, hipHostMallocDefault) == hipSuccess)
+                    g.out_cap = n;
+            }
+        }
     }
+    g.out_pending = 0;
     g.in_active = false;
     g.in_src = nullptr;
     return rc;
