@@ -536,20 +536,35 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
     if (kb < nsteps) mfma(0, 0);   // odd step count: the last step is in buffer / set 0
 
     // Accumulator layout (32x32): lane l, reg r -> col l%32, row 8*(r/4) + 4*(l/32) + r%4.
-    // With SwiGLU, columns 2c / 2c+1 (gate / up of output c) sit in lanes l, l^1.
+    // With SwiGLU, columns 2c / 2c+1 (gate / up of output c) sit in lanes l, l^1; registers
+    // r, r+1 (r even) hold rows q, q+1. One exchange per register pair (the even lane hands
+    // over its row-(q+1) gate, the odd lane its row-q up) lets the even lane finish row q
+    // and the odd lane row q+1, so every lane computes an activation.
+    const bool odd = lane & 1;
 #pragma unroll
     for (int i = 0; i < WI; ++i)
 #pragma unroll
         for (int j = 0; j < WJ; ++j) {
             const uint32_t col = n0 + wn * 32 * WJ + j * 32 + l32;
+            if (part || !swiglu) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                const float partner = __shfl_xor(acc[i][j][r], 1, 64);
-                if (col >= N || row >= M) continue;
-                if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
-                else if (!swiglu) w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
-                else if (!(lane & 1)) w4g_store_swiglu(y, ldy, res, ldr, row, col >> 1, acc[i][j][r], partner);
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    if (col >= N || row >= M) continue;
+                    if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
+                    else w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    const float got = __shfl_xor(odd ? acc[i][j][r] : acc[i][j][r + 1], 1, 64);
+                    const float gate = odd ? got : acc[i][j][r];
+                    const float up = odd ? acc[i][j][r + 1] : got;
+                    const uint32_t rr = r + (odd ? 1 : 0);
+                    const uint32_t row = m0 + i * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
+                    if (col >= N || row >= M) continue;   // N is even: both lanes of a pair agree
+                    w4g_store_swiglu(y, ldy, res, ldr, row, col >> 1, gate, up);
+                }
             }
         }
 }
