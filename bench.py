@@ -164,9 +164,12 @@ def main() -> int:
 
     # Decode: W warmup steps, then K timed steps (each = one run_io of the decode blob).
     assert S + args.warmup + args.steps <= args.max_pos
+    first_tok = tok
+    warm_toks = []
     for _ in range(args.warmup):
         out, _ = eng.run_io(pd, emb[tok].tobytes(), td["tok"])
         tok = int(np.frombuffer(out, np.int32)[0])
+        warm_toks.append(tok)
     toks = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -184,6 +187,36 @@ def main() -> int:
     # Per-op device time of one decode step (engine's HIP events).
     _, op_us = eng.run_io(pd, emb[tok].tobytes(), td["tok"], timing=True)
     gpu_us_step = float(sum(op_us))
+
+    # Chained decode: the same greedy decode from the same prefill, on the token-id blob
+    # (embedding row gathered on the device) through wt_exec_run_steps, which feeds each
+    # step's token to the next on the device and waits once per call; W warmup steps in
+    # one call, then K timed steps in one call. Its tokens must equal the host loop's.
+    chained = None
+    if args.warmup > 0:
+        dect_blob, tdt = emit_decode(cfg, w, args.max_pos, token_input=True)
+        pt = eng.parse(dect_blob)
+        eng.set_input_device(x_dev.data_ptr(), x_dev.numel())
+        try:
+            eng.state_reset()
+            out_c, _ = eng.run_io(pp, None, tp["tok"])
+        finally:
+            eng.set_input_device(None)
+        if int(np.frombuffer(out_c, np.int32)[0]) != first_tok:
+            raise RuntimeError("chained-decode prefill gives another first token")
+        warm_c = np.frombuffer(eng.run_steps(pt, args.warmup, np.int32(first_tok).tobytes(), tdt["tok"]), np.int32)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out_c = eng.run_steps(pt, args.steps, np.int32(warm_c[-1]).tobytes(), tdt["tok"])
+        torch.cuda.synchronize()
+        t_ch = time.perf_counter() - t0
+        toks_c = np.frombuffer(out_c, np.int32)
+        if warm_c.tolist() != warm_toks or toks_c.tolist() != toks:
+            raise RuntimeError("chained decode and the host loop give different tokens")
+        chained = {"tok_s": round(args.steps / t_ch, 2), "ms_per_step": round(t_ch / args.steps * 1e3, 3),
+                   "entry": "wt_exec_run_steps (token fed back on the device, one wait per call)",
+                   "tokens_equal_host_loop": True}
+        log(f"chained decode: {args.steps} steps in {t_ch * 1e3:.1f} ms -> {args.steps / t_ch:.1f} tok/s")
 
     avg_s, bytes_per_launch, gemv_gbs = gemv_roofline(cfg, w, lib, args.roofline_reps)
 
@@ -216,6 +249,7 @@ def main() -> int:
         "prefill_tok_s": round(S / t_prefill, 1),
         "prefill_tflops": round(prefill_flops / t_prefill / 1e12, 2),
         "decode_gpu_us_per_step": round(gpu_us_step, 1),
+        "decode_chained": chained,
         "decode_weight_bytes_per_token": cfg.decode_weight_bytes(),
         "decode_ideal_tok_s_at_hbm_peak": round(HBM_PEAK_GBS * 1e9 / cfg.decode_weight_bytes(), 1),
         "roofline": {"bound": "hbm", "kernel": "w4g_gemv_kernel<1, NP> (decode W4A16 GEMV; NP = passes per thread, 3/4 straight-line, 0 batched)",

@@ -100,6 +100,18 @@ class Engine:
         n = self.lib.wt_exec_temp_last_bytes(out_temp)
         return C.string_at(self._obuf, n), (list(us) if timing else None)
 
+    def run_steps(self, pb: ParsedBlob, steps: int, inp: bytes, out_temp: int) -> bytes:
+        """wt_exec_run_steps: `steps` runs chained on the device (each run's out_temp bytes
+        become the next run's input); returns the steps' outputs concatenated."""
+        err = C.create_string_buffer(512)
+        m = C.c_uint32(0)
+        n = len(inp)
+        obuf = C.create_string_buffer(max(steps * n, 1))
+        rc = self.lib.wt_exec_run_steps(C.byref(pb.blob), steps, C.c_char_p(bytes(inp)), obuf, out_temp, C.byref(m),
+                                        err, 512)
+        self._check(rc, err)
+        return obuf.raw[:steps * n]
+
     def temp(self, tid: int) -> bytes:
         """Bytes last written to temp tid (host copy)."""
         n = self.lib.wt_exec_temp_last_bytes(tid)

@@ -136,6 +136,7 @@ EXPORTS = {
                                C.c_char_p, C.c_size_t]),
     "wt_exec_run_io": (_i, [C.POINTER(WtBlob), _vp, _vp, _u32, C.POINTER(_u32), C.POINTER(C.c_int64),
                             C.c_char_p, C.c_size_t]),
+    "wt_exec_run_steps": (_i, [C.POINTER(WtBlob), _u32, _vp, _vp, _u32, C.POINTER(_u32), C.c_char_p, C.c_size_t]),
     "wt_exec_temp": (_u8p, [_u32]),
     "wt_exec_temp_bytes": (_u32, [_u32]),
     "wt_exec_temp_last_bytes": (_u32, [_u32]),

@@ -171,6 +171,7 @@ FuseObs g_obs;
 // wt_exec_temp returns NULL for them.
 std::vector<uint8_t> g_unmat;
 uint32_t g_run_out_temp = 0xFFFFFFFFu;   // run_io's output temp (read after the run)
+bool g_defer_wait = false;               // wt_exec_run_steps: a replayed run returns unwaited
 
 inline void obs_read(uint32_t arg) {
     if (!g_obs.on || (arg & 0x8000u) || (arg & 0xE000u) == WT_REF_STATE_FLAG) return;
@@ -2000,11 +2001,12 @@ int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* 
 }
 
 // Waits for a run's work. When wt_exec_run_io asked for an output that fits the pinned
-// output buffer, its device-to-host copy is queued first, so the one wait covers both.
+// output buffer, its device-to-host copy is queued first, so the one wait covers both
+// (wt_exec_run_steps queues its own copies).
 hipError_t end_run_sync() {
     g.out_pending = 0;
     const uint32_t t = g_run_out_temp;
-    if (t < kMaxTemps && g.temps[t] && g.last_bytes[t] && g.last_bytes[t] <= g.out_cap &&
+    if (!g_defer_wait && t < kMaxTemps && g.temps[t] && g.last_bytes[t] && g.last_bytes[t] <= g.out_cap &&
         hipMemcpyAsync(g.out_host, g.temps[t], g.last_bytes[t], hipMemcpyDeviceToHost, g.stream) == hipSuccess)
         g.out_pending = g.last_bytes[t];
     return hipStreamSynchronize(g.stream);
@@ -2022,9 +2024,10 @@ int replay_graph(RunGraph& r, const wt_blob* b, uint32_t first, uint32_t count, 
     for (uint32_t ii = 0; ii < count && !fail; ++ii)
         if (run_op(b, first + ii, ii, engine_m, err, errn)) fail = (int)(first + ii) + 1;
     g.replay = false;
-    const hipError_t e = end_run_sync();
+    const hipError_t e = g_defer_wait && !fail ? hipSuccess : end_run_sync();
     if (e != hipSuccess) return ERR("device error: %s", hipGetErrorString(e));
     if (fail || g.epoch != ep0 || g.variant) {
+        if (g_defer_wait) hipStreamSynchronize(g.stream);
         // The preflight makes this unreachable for the ops this engine implements; if
         // the host pass ever disagrees with the capture, stop using graphs.
         g.graphs_broken = true;
@@ -2191,6 +2194,45 @@ int wt_exec_run(const struct wt_blob* b, uint32_t* engine_m, int64_t* op_us, cha
     return wt_exec_run_range(b, 0, b ? b->n_ops : 0, engine_m, op_us, err, errn);
 }
 
+}  // extern "C"
+
+namespace {
+
+// Bytes of the blob's EXT_IN input slot (0 if it has none).
+size_t input_bytes(const wt_blob* b) {
+    size_t need = 0;
+    for (uint32_t i = 0; i < b->n_slots; ++i)
+        if (b->slots[i].addr == WT_SLOT_EXT_IN) need = std::max<size_t>(need, b->slots[i].len);
+    return need;
+}
+
+// Host input of `need` bytes staged through pinned memory into in_dev (the previous run
+// drained the stream, so the staging buffer is free); the runs that follow read in_dev.
+int stage_input(const void* in_ptr, size_t need, char* err, size_t errn) {
+    if (ensure_ready(err, errn)) return -1;
+    if (!need) return 0;
+    if (need > g.in_cap) {
+        if (g.in_dev) dev_free(g.in_dev);
+        if (g.in_host) hipHostFree(g.in_host);
+        g.in_dev = g.in_host = nullptr;
+        g.in_cap = 0;
+        if (dev_malloc(reinterpret_cast<void**>(&g.in_dev), need) != hipSuccess ||
+            hipHostMalloc(reinterpret_cast<void**>(&g.in_host), need, hipHostMallocDefault) != hipSuccess)
+            return ERR("input buffer alloc");
+        g.in_cap = need;
+    }
+    std::memcpy(g.in_host, in_ptr, need);
+    if (hipMemcpyAsync(g.in_dev, g.in_host, need, hipMemcpyHostToDevice, g.stream) != hipSuccess)
+        return ERR("input upload failed");
+    g.in_active = true;
+    g.in_src = g.in_dev;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
 int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, uint32_t out_temp,
                    uint32_t* engine_m, int64_t* op_us, char* err, size_t errn) {
     char dummy_err[8];
@@ -2198,9 +2240,7 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
     if (!b) return ERR("null blob");
     g.in_active = false;
     g.in_src = nullptr;
-    size_t need = 0;
-    for (uint32_t i = 0; i < b->n_slots; ++i)
-        if (b->slots[i].addr == WT_SLOT_EXT_IN) need = std::max<size_t>(need, b->slots[i].len);
+    const size_t need = input_bytes(b);
     if (!in_ptr && g.in_bound && need) {
         // Device-resident input bound by wt_exec_set_input_device: no host staging.
         if (need > g.in_bound_bytes)
@@ -2208,27 +2248,7 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
         g.in_active = true;
         g.in_src = g.in_bound;
     }
-    if (in_ptr) {
-        if (ensure_ready(err, errn)) return -1;
-        if (need) {
-            if (need > g.in_cap) {
-                if (g.in_dev) dev_free(g.in_dev);
-                if (g.in_host) hipHostFree(g.in_host);
-                g.in_dev = g.in_host = nullptr;
-                g.in_cap = 0;
-                if (dev_malloc(reinterpret_cast<void**>(&g.in_dev), need) != hipSuccess ||
-                    hipHostMalloc(reinterpret_cast<void**>(&g.in_host), need, hipHostMallocDefault) != hipSuccess)
-                    return ERR("input buffer alloc");
-                g.in_cap = need;
-            }
-            // The previous run drained the stream, so the staging buffer is free.
-            std::memcpy(g.in_host, in_ptr, need);
-            if (hipMemcpyAsync(g.in_dev, g.in_host, need, hipMemcpyHostToDevice, g.stream) != hipSuccess)
-                return ERR("input upload failed");
-            g.in_active = true;
-            g.in_src = g.in_dev;
-        }
-    }
+    if (in_ptr && stage_input(in_ptr, need, err, errn)) return -1;
     g_run_out_temp = out_ptr ? out_temp : kNone;
     g.out_pending = 0;
     int rc = wt_exec_run(b, engine_m, op_us, err, errn);
@@ -2252,6 +2272,60 @@ int wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr, u
         }
     }
     g.out_pending = 0;
+    g.in_active = false;
+    g.in_src = nullptr;
+    return rc;
+}
+
+int wt_exec_run_steps(const struct wt_blob* b, uint32_t steps, const void* in_ptr, void* out_ptr, uint32_t out_temp,
+                      uint32_t* engine_m, char* err, size_t errn) {
+    char dummy_err[8];
+    if (!err || !errn) { err = dummy_err; errn = sizeof dummy_err; }
+    if (!b || !in_ptr || !out_ptr) return ERR("run_steps: null blob, input or output");
+    if (!steps) return 0;
+    if (out_temp >= kMaxTemps) return ERR("run_steps: out_temp %u out of range", out_temp);
+    const size_t need = input_bytes(b);
+    if (!need || need > 4096) return ERR("run_steps: the blob's input slot holds %zu bytes (1..4096)", need);
+    g.in_active = false;
+    g.in_src = nullptr;
+    if (stage_input(in_ptr, need, err, errn)) return -1;
+    // One pinned row per step for the outputs, read back after the final wait.
+    if ((size_t)steps * need > g.out_cap) {
+        if (g.out_host) hipHostFree(g.out_host);
+        g.out_host = nullptr;
+        g.out_cap = 0;
+        if (hipHostMalloc(reinterpret_cast<void**>(&g.out_host), (size_t)steps * need, hipHostMallocDefault) !=
+            hipSuccess)
+            return ERR("run_steps: output buffer alloc");
+        g.out_cap = (size_t)steps * need;
+    }
+    int rc = 0;
+    for (uint32_t s = 0; s < steps && rc == 0; ++s) {
+        g.in_active = true;
+        g.in_src = g.in_dev;
+        g_run_out_temp = out_temp;
+        g_defer_wait = true;
+        rc = wt_exec_run(b, engine_m, nullptr, err, errn);
+        g_defer_wait = false;
+        g_run_out_temp = kNone;
+        if (rc) break;
+        if (!g.temps[out_temp] || g.last_bytes[out_temp] != need) {
+            hipStreamSynchronize(g.stream);
+            rc = ERR("run_steps: output temp %u holds %u bytes, the input slot %zu", out_temp,
+                     g.last_bytes[out_temp], need);
+            break;
+        }
+        // This step's output is the next step's input, and one row of the result.
+        if (hipMemcpyAsync(g.in_dev, g.temps[out_temp], need, hipMemcpyDeviceToDevice, g.stream) != hipSuccess ||
+            hipMemcpyAsync(g.out_host + (size_t)s * need, g.temps[out_temp], need, hipMemcpyDeviceToHost,
+                           g.stream) != hipSuccess) {
+            hipStreamSynchronize(g.stream);
+            rc = ERR("run_steps: output copy failed");
+        }
+    }
+    const hipError_t e = hipStreamSynchronize(g.stream);
+    if (rc == 0 && e != hipSuccess) rc = ERR("device error: %s", hipGetErrorString(e));
+    if (rc == 0) std::memcpy(out_ptr, g.out_host, (size_t)steps * need);
     g.in_active = false;
     g.in_src = nullptr;
     return rc;

@@ -237,13 +237,21 @@ class _Emitter:
         bb.op(OP.MATMUL_F16, src, self.ref("embed"), t["logits"], 1, c.hidden, c.vocab, 2)
         bb.op(OP.ARGMAX_F16, t["logits"], t["tok"], c.vocab)
 
-    def emit(self, S: int, decode: bool) -> bytes:
-        c = self.cfg
-        xin = self.bb.add_input_slot(S * c.hidden * 2)
+    def emit(self, S: int, decode: bool, token_input: bool = False) -> bytes:
+        c, bb = self.cfg, self.bb
+        if token_input:   # int32 token ids in; the embedding rows gathered in-graph
+            ids = bb.add_input_slot(S * 4)
+            x0 = bb.temp()
+            self.t["x0"] = x0
+            bb.op(OP.GATHER_F16, self.ref("embed"), bb.slot_ref(ids), x0, S * c.hidden, 0 | (1 << 8) | (2 << 16),
+                  c.vocab, c.hidden, 1, 1, 1, S, 1, 1, 1, 1)
+            x_in = x0
+        else:
+            x_in = bb.slot_ref(bb.add_input_slot(S * c.hidden * 2))
         for l in range(c.layers):
-            self.layer(l, S, self.bb.slot_ref(xin) if l == 0 else self.t["x"], decode)
+            self.layer(l, S, x_in if l == 0 else self.t["x"], decode)
         self.head(S)
-        return self.bb.build()
+        return bb.build()
 
 
 def emit_prefill(cfg: Qwen3Config, w: Weights, S: int, max_pos: int):
@@ -252,9 +260,11 @@ def emit_prefill(cfg: Qwen3Config, w: Weights, S: int, max_pos: int):
     return e.emit(S, decode=False), dict(e.t)
 
 
-def emit_decode(cfg: Qwen3Config, w: Weights, max_pos: int, fused: bool = True):
-    """(blob bytes, temp ids): one decode step; input = the token's embedding [hidden].
+def emit_decode(cfg: Qwen3Config, w: Weights, max_pos: int, fused: bool = True, token_input: bool = False):
+    """(blob bytes, temp ids): one decode step; input = the token's embedding [hidden],
+    or with token_input its int32 id (the row gathered in-graph from the lm_head / embedding
+    table, so the step's ARGMAX output can feed the next step: wt_exec_run_steps).
     fused: attention as one OP_ATTN_DECODE_QKV_F16 per layer instead of
     OP_QK_ROPE_KV_F16 + OP_ATTN_DECODE_F16."""
     e = _Emitter(cfg, w, max_pos, fused_decode=fused)
-    return e.emit(1, decode=True), dict(e.t)
+    return e.emit(1, decode=True, token_input=token_input), dict(e.t)

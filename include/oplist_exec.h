@@ -62,6 +62,18 @@ int  wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr,
                     uint32_t out_temp,
                     uint32_t* engine_m, int64_t* op_us, char* err, size_t errn);
 
+/* Extension: `steps` runs of a blob whose output feeds its own input, chained on the
+ * device: in_ptr (HOST, the blob's EXT_IN slot bytes) is the first step's input; after
+ * each step, out_temp's bytes (they must be as many as the input slot's) become the next
+ * step's input and row s of out_ptr (HOST, steps * input bytes). Steps replayed from the
+ * blob's captured HIP graph are queued without waiting for the one before, and one wait
+ * at the end covers them all; an error stops at the failing step. For greedy decoding
+ * with a token-id input (the blob gathers the embedding row itself): the reference has
+ * no counterpart (its host loop feeds one step at a time, oplist_exec.c:2587-2602,
+ * scripts/persistent_runtime.py:43-62). */
+int  wt_exec_run_steps(const struct wt_blob* b, uint32_t steps, const void* in_ptr, void* out_ptr,
+                       uint32_t out_temp, uint32_t* engine_m, char* err, size_t errn);
+
 /* Extension: bind a caller-owned DEVICE buffer of `bytes` bytes as the EXT_IN input of
  * the following wt_exec_run_io calls made with in_ptr NULL (a non-NULL in_ptr still
  * stages that host input). No host copy is made: the caller keeps the buffer alive and

@@ -126,3 +126,48 @@ def test_persistent_server_decode_matches_engine(engine, tmp_path):
         assert tok == int(np.argmax(logits.astype(np.float32)))
     assert tok0 == served[0][0] and np.array_equal(np.frombuffer(out0, np.uint16), served[0][1].view(np.uint16))
     engine.shutdown()
+
+
+@pytest.mark.parametrize("graphs", [True, False], ids=["graphs", "direct"])
+def test_run_steps_matches_host_loop(engine, graphs):
+    """wt_exec_run_steps with the token-id decode blob (embedding row gathered in-graph,
+    each step's ARGMAX output fed back on the device) gives the tokens of the host loop
+    that feeds wt_exec_run_io the embedding row of the previous token, step for step, and
+    the same last-step logits bit for bit; the ring positions advance the same way."""
+    cfg, S, n, max_pos = SMALL, 24, 40, 96
+    w = Weights(cfg, seed=71)
+    emb = w.embed()
+    prev = engine.set_graphs(graphs)
+    try:
+        engine.shutdown()
+        engine.set_ext_weights(w.image.ctypes.data)
+        pre, tp = emit_prefill(cfg, w, S, max_pos)
+        dec, td = emit_decode(cfg, w, max_pos)
+        dect, tdt = emit_decode(cfg, w, max_pos, token_input=True)
+        pp, pd, pt = engine.parse(pre), engine.parse(dec), engine.parse(dect)
+        x_prompt = np.ascontiguousarray(emb[np.random.default_rng(72).integers(0, cfg.vocab, S)]).tobytes()
+
+        engine.state_reset()
+        out, _ = engine.run_io(pp, x_prompt, tp["tok"])
+        tok = int(np.frombuffer(out, np.int32)[0])
+        first = tok
+        loop = []
+        for _ in range(n):
+            out, _ = engine.run_io(pd, emb[tok].tobytes(), td["tok"])
+            tok = int(np.frombuffer(out, np.int32)[0])
+            loop.append(tok)
+        last_loop = np.frombuffer(engine.temp(td["logits"]), np.float16)[:cfg.vocab].copy()
+
+        engine.state_reset()
+        engine.run_io(pp, x_prompt, tp["tok"])
+        c0, r0 = engine.graph_stats()
+        chained = np.frombuffer(engine.run_steps(pt, n, np.int32(first).tobytes(), tdt["tok"]), np.int32)
+        c1, r1 = engine.graph_stats()
+        last_chained = np.frombuffer(engine.temp(tdt["logits"]), np.float16)[:cfg.vocab].copy()
+        engine.shutdown()
+    finally:
+        engine.set_graphs(prev)
+    assert chained.tolist() == loop
+    assert np.array_equal(last_chained.view(np.uint16), last_loop.view(np.uint16))
+    if graphs:
+        assert r1 - r0 >= n - 4, (c1 - c0, r1 - r0)
