@@ -569,6 +569,148 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
         }
 }
 
+// Wide variant for the wide-N shapes: a 128 x 256 workgroup tile, each wave 128 x 64
+// (4 x 2 MFMA tiles), so every A fragment read from LDS feeds two MFMAs (half the LDS
+// read traffic per MFMA of the 128 x 128 tile, whose A reads keep LDS as busy as the
+// MFMAs keep the matrix pipes) while each weight is still dequantized once per 128
+// rows. To fit two workgroups per CU (256 registers per lane, 128 of them
+// accumulators), B is dequantized just before the MFMAs of each 16-deep sub-step
+// instead of a whole K step ahead, raw W is held in three register stages (loaded two
+// steps ahead) and A one step (loaded at the start of a step, stored to LDS after its
+// MFMAs). The K order, operand layouts and MFMA sequence per output are those of
+// w4g_gemm_kernel, so both kernels give the same bits.
+constexpr int GW_WJ = 2;
+constexpr uint32_t GW_N = 4 * 32 * GW_WJ;   // workgroup tile width
+
+__global__ __launch_bounds__(256, 2) void w4g_gemm_wide_kernel(
+    const __half* __restrict__ a, uint32_t lda, const uint8_t* __restrict__ wq,
+    const __half* __restrict__ ws, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
+    uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu, uint32_t mtiles, uint32_t ntiles,
+    uint32_t split_steps, float* __restrict__ part) {
+    constexpr int CA = GB_M * (GB_K / 8) / 256;
+    constexpr int WJ = GW_WJ;
+    __shared__ __align__(16) _Float16 As[2][GB_M * GB_LDS];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t m0 = (blockIdx.x % mtiles) * GB_M, n0 = (blockIdx.x / mtiles % ntiles) * GW_N;
+    const uint32_t split = blockIdx.x / (mtiles * ntiles);
+    const uint32_t G = K / 64, rowbytes = K / 2;
+    const uint32_t kbase = split * split_steps, nsteps = min(split_steps, K / GB_K - kbase);
+    const uint32_t half = lane >> 5, l32 = lane & 31;
+    size_t wrow[WJ];
+#pragma unroll
+    for (int j = 0; j < WJ; ++j) wrow[j] = min(n0 + wave * 32 * WJ + j * 32 + l32, N - 1);
+    const uint32_t arow = tid / 8, apiece = tid % 8;
+    const uint32_t last = nsteps - 1;
+
+    u32x4 ra[CA], rw[3][WJ];
+    uint16_t rs[3][WJ];
+    auto load_a = [&](uint32_t kb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < CA; ++i) {
+            const size_t r = min(m0 + arow + 32u * i, M - 1);
+            ra[i] = *reinterpret_cast<const u32x4*>(a + r * lda + (kbase + kb) * GB_K + apiece * 8);
+        }
+    };
+    auto load_w = [&](int st, uint32_t kb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            rw[st][j] = *reinterpret_cast<const u32x4*>(wq + wrow[j] * rowbytes + (kbase + kb) * 32 + 16 * half);
+            rs[st][j] = __builtin_bit_cast(uint16_t, ws[wrow[j] * G + kbase + kb]);
+        }
+    };
+    auto store_a = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < CA; ++i)
+            *reinterpret_cast<u32x4*>(&As[buf][(arow + 32 * i) * GB_LDS + apiece * 8]) = pair_order16(ra[i]);
+    };
+
+    f16x_t acc[WI][WJ];
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Step kb: MFMAs on LDS buffer kb % 2 with the raw W of stage kb % 3; A of step kb + 1
+    // and W of step kb + 2 (into stage (kb + 2) % 3, free since step kb - 1) are requested
+    // first. Past the end the last step is loaded again, unread.
+    auto step = [&](int buf, int st, int st2, uint32_t kb) __attribute__((always_inline)) {
+        load_a(min(kb + 1, last));
+        load_w(st2, min(kb + 2, last));
+        __builtin_amdgcn_sched_barrier(0);
+        h2_t s2[WJ];
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            const _Float16 sh = __builtin_bit_cast(_Float16, rs[st][j]);
+            s2[j] = h2_t{sh, sh};
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            h8_t af[WI], bf[WJ];
+#pragma unroll
+            for (int i = 0; i < WI; ++i)
+                af[i] = *reinterpret_cast<const h8_t*>(&As[buf][(i * 32 + l32) * GB_LDS + 32 * half + 8 * q]);
+#pragma unroll
+            for (int j = 0; j < WJ; ++j) {
+                h2_t d[4];
+                dequant_word(rw[st][j][q], s2[j], d);
+                bf[j] = h8_t{d[0][0], d[0][1], d[1][0], d[1][1], d[2][0], d[2][1], d[3][0], d[3][1]};
+            }
+#pragma unroll
+            for (int i = 0; i < WI; ++i)
+#pragma unroll
+                for (int j = 0; j < WJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        store_a(buf ^ 1);
+        __syncthreads();
+    };
+
+    load_w(0, 0);
+    load_w(1, min(1u, last));
+    load_a(0);
+    store_a(0);
+    __syncthreads();
+    // Whole rounds of six steps (buffer and stage indices static, no exit inside a round,
+    // so no load is moved past a branch), then up to five more.
+    uint32_t kb = 0;
+    for (; kb + 6 <= nsteps; kb += 6) {
+#pragma unroll
+        for (int u = 0; u < 6; ++u) step(u % 2, u % 3, (u + 2) % 3, kb + u);
+    }
+#pragma unroll
+    for (int u = 0; u < 5; ++u)
+        if (kb + u < nsteps) step(u % 2, u % 3, (u + 2) % 3, kb + u);
+    const bool odd = lane & 1;
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            const uint32_t col = n0 + wave * 32 * WJ + j * 32 + l32;
+            if (part || !swiglu) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    if (col >= N || row >= M) continue;
+                    if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
+                    else w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    const float got = __shfl_xor(odd ? acc[i][j][r] : acc[i][j][r + 1], 1, 64);
+                    const float gate = odd ? got : acc[i][j][r];
+                    const float up = odd ? acc[i][j][r + 1] : got;
+                    const uint32_t rr = r + (odd ? 1 : 0);
+                    const uint32_t row = m0 + i * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
+                    if (col >= N || row >= M) continue;
+                    w4g_store_swiglu(y, ldy, res, ldr, row, col >> 1, gate, up);
+                }
+            }
+        }
+}
+
 // Split-K finish, vector form (N, ldy, ldr multiples of 8, 16-byte aligned rows): a
 // thread sums 8 consecutive fp32 columns over the parts in part order (two 16-byte loads
 // per part) and stores 8 (plain) or 4 (SwiGLU) outputs at once, with the arithmetic of
@@ -825,12 +967,26 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.gamma || (epi.swiglu && (N & 1))) return hipErrorInvalidValue;
     const uint32_t mt = (M + GB_M - 1) / GB_M, nt = (N + GB_N - 1) / GB_N, steps = K / GB_K;
+    const uint32_t ntw = (N + GW_N - 1) / GW_N;
     const uint32_t parts = w4g_gemm_split_parts(M, N, K);
     const size_t need = (size_t)parts * M * N * sizeof(float);
-    if (parts > 1 && epi.split_ws && epi.split_ws_bytes >= need) {
-        const uint32_t per = (steps + parts - 1) / parts;
-        hipLaunchKernelGGL(w4g_gemm_kernel, dim3(mt * nt * parts), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K,
-                           epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, nt, per, epi.split_ws);
+    const bool split = parts > 1 && epi.split_ws && epi.split_ws_bytes >= need;
+    const uint32_t per = split ? (steps + parts - 1) / parts : steps;
+    // Both tile shapes give the same bits. The wide one when its grid fills two rounds of
+    // two workgroups per CU (measured at M = 2048: gate/up N = 19456 256 vs 263 us; with
+    // fewer tiles, qkv N = 6144 and the split N = 2560 shapes, the 128 x 128 tile at
+    // three per CU is 5-9 % faster).
+    const bool wide = (size_t)mt * ntw * (split ? parts : 1u) >= 4 * (size_t)device_cu_count();
+    auto gemm = [&](float* pw) {
+        if (wide)
+            hipLaunchKernelGGL(w4g_gemm_wide_kernel, dim3(mt * ntw * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq,
+                               ws, y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, ntw, per, pw);
+        else
+            hipLaunchKernelGGL(w4g_gemm_kernel, dim3(mt * nt * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq, ws,
+                               y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, nt, per, pw);
+    };
+    if (split) {
+        gemm(epi.split_ws);
         const uint32_t oal = epi.swiglu ? 4u : 8u;   // output elements per vector store
         const bool vec = N % 8 == 0 && ldy % oal == 0 && (uintptr_t)y % (2 * oal) == 0 &&
                          (!epi.res || (epi.ldr % oal == 0 && (uintptr_t)epi.res % (2 * oal) == 0)) &&
@@ -852,8 +1008,7 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
         }
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(w4g_gemm_kernel, dim3(mt * nt), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K, epi.res,
-                       epi.ldr, epi.swiglu ? 1 : 0, mt, nt, steps, static_cast<float*>(nullptr));
+    gemm(nullptr);
     return hipGetLastError();
 }
 
