@@ -2286,6 +2286,9 @@ int wt_exec_run_steps(const struct wt_blob* b, uint32_t steps, const void* in_pt
     if (out_temp >= kMaxTemps) return ERR("run_steps: out_temp %u out of range", out_temp);
     const size_t need = input_bytes(b);
     if (!need || need > 4096) return ERR("run_steps: the blob's input slot holds %zu bytes (1..4096)", need);
+    constexpr size_t kStepsOutMax = 64u << 20;   // pinned bytes for the steps' outputs
+    if ((size_t)steps * need > kStepsOutMax)
+        return ERR("run_steps: %u steps x %zu bytes exceed the %zu-byte output limit", steps, need, kStepsOutMax);
     g.in_active = false;
     g.in_src = nullptr;
     if (stage_input(in_ptr, need, err, errn)) return -1;

@@ -67,7 +67,8 @@ int  wt_exec_run_io(const struct wt_blob* b, const void* in_ptr, void* out_ptr,
  * each step, out_temp's bytes (they must be as many as the input slot's) become the next
  * step's input and row s of out_ptr (HOST, steps * input bytes). Steps replayed from the
  * blob's captured HIP graph are queued without waiting for the one before, and one wait
- * at the end covers them all; an error stops at the failing step. For greedy decoding
+ * at the end covers them all; an error stops at the failing step; steps * input bytes
+ * is at most 64 MiB (input slot 1..4096 bytes). For greedy decoding
  * with a token-id input (the blob gathers the embedding row itself): the reference has
  * no counterpart (its host loop feeds one step at a time, oplist_exec.c:2587-2602,
  * scripts/persistent_runtime.py:43-62). */

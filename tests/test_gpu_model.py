@@ -171,3 +171,24 @@ def test_run_steps_matches_host_loop(engine, graphs):
     assert np.array_equal(last_chained.view(np.uint16), last_loop.view(np.uint16))
     if graphs:
         assert r1 - r0 >= n - 4, (c1 - c0, r1 - r0)
+
+
+def test_run_steps_errors(engine):
+    """wt_exec_run_steps refuses an output larger than its 64 MiB limit before running
+    anything, and stops with an error when out_temp does not hold as many bytes as the
+    input slot (here the logits temp of the token-id decode blob)."""
+    cfg, max_pos = SMALL, 64
+    w = Weights(cfg, seed=73)
+    engine.shutdown()
+    engine.set_ext_weights(w.image.ctypes.data)
+    dect, tdt = emit_decode(cfg, w, max_pos, token_input=True)
+    pt = engine.parse(dect)
+    engine.state_reset()
+    first = np.int32(5).tobytes()
+    with pytest.raises(RuntimeError, match="output limit"):
+        engine.run_steps(pt, 20_000_000, first, tdt["tok"])
+    with pytest.raises(RuntimeError, match="output temp"):
+        engine.run_steps(pt, 2, first, tdt["logits"])
+    ids = np.frombuffer(engine.run_steps(pt, 3, first, tdt["tok"]), np.int32)
+    assert ids.shape == (3,) and (ids >= 0).all() and (ids < cfg.vocab).all()
+    engine.shutdown()
