@@ -15,6 +15,7 @@
 #include "kernels.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 
 namespace gehtp {
@@ -78,6 +79,23 @@ struct GemvArgs {
 
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t f2hb(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// SwiGLU's silu: UNARY silu on an fp16 input, f16(h / (1 + exp(-h))) with each fp32 op
+// correctly rounded. Its input is always an fp16 value, so the whole function is a table
+// of 65536 fp16 results, filled once per device by silu_table_kernel with this same
+// expression: a lookup gives the expression's bits for a fraction of its VALU work (the
+// correctly rounded exp and division were ~5 % of the gate/up GEMM).
+__device__ __forceinline__ uint16_t silu_f16_expr(uint16_t hb) {
+    const float h = h2f(hb);
+    return f2hb(__fdiv_rn(h, __fadd_rn(1.0f, expf(-h))));
+}
+__device__ uint16_t g_silu_tab[65536];
+__device__ __forceinline__ float silu_of(float gate_f16) { return h2f(g_silu_tab[f2hb(gate_f16)]); }
+
+__global__ __launch_bounds__(256) void silu_table_kernel() {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    g_silu_tab[i] = silu_f16_expr((uint16_t)i);
+}
 
 constexpr int kGemvU = 4;   // passes per load batch
 
@@ -345,7 +363,9 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                 su = dev::row_sum16(su);
                 if (gl == 0) {
                     const float gv = h2f(f2hb(sg)), uv = h2f(f2hb(su));
-                    const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
+                    // the expression rather than the table: a table read right after
+                    // the kernel boundary would sit on this epilogue's short tail
+                    const float act = h2f(silu_f16_expr(f2hb(gv)));
                     uint16_t v = f2hb(__fmul_rn(act, uv));
                     const uint32_t col = (r0 >> 1) + k2;
                     if (A.res) v = f2hb(__fadd_rn(h2f(v), res_at(m, k2)));
@@ -418,10 +438,55 @@ __device__ __forceinline__ void w4g_store(__half* __restrict__ y, uint32_t ldy, 
 __device__ __forceinline__ void w4g_store_swiglu(__half* __restrict__ y, uint32_t ldy, const __half* __restrict__ res,
                                                  uint32_t ldr, uint32_t row, uint32_t oc, float gate, float up) {
     const float gv = h2f(f2hb(gate)), uv = h2f(f2hb(up));
-    const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
+    const float act = silu_of(gv);
     uint16_t v = f2hb(__fmul_rn(act, uv));
     if (res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, res[(size_t)row * ldr + oc]))));
     reinterpret_cast<uint16_t*>(y)[(size_t)row * ldy + oc] = v;
+}
+
+// SwiGLU epilogue of a wave's WI x WJ accumulator tiles. Accumulator layout (32x32):
+// lane l, reg r -> col l%32, row 8*(r/4) + 4*(l/32) + r%4. Columns 2c / 2c+1 (gate / up
+// of output c) sit in lanes l, l^1; registers r, r+1 (r even) hold rows q, q+1. One
+// exchange per register pair (the even lane hands over its row-(q+1) gate, the odd lane
+// its row-q up) lets the even lane finish row q and the odd lane row q+1. All silu
+// lookups are issued before any store (a store through y could alias the table for the
+// compiler, which would otherwise wait for each store before the next lookup).
+template <int WJ>
+__device__ __forceinline__ void w4g_swiglu_tiles(f16x_t (&acc)[WI][WJ], uint32_t lane, uint32_t m0, uint32_t col0,
+                                                 uint32_t M, uint32_t N, __half* __restrict__ y, uint32_t ldy,
+                                                 const __half* __restrict__ res, uint32_t ldr) {
+    const bool odd = lane & 1;
+    const uint32_t half = lane >> 5, l32 = lane & 31;
+    uint16_t tb[WI][WJ][8];
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const float got = __shfl_xor(odd ? acc[i][j][r] : acc[i][j][r + 1], 1, 64);
+                const float gate = odd ? got : acc[i][j][r];
+                const float up = odd ? acc[i][j][r + 1] : got;
+                acc[i][j][r] = gate;
+                acc[i][j][r + 1] = up;
+                tb[i][j][r / 2] = g_silu_tab[f2hb(gate)];
+            }
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            const uint32_t col = col0 + j * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const uint32_t rr = r + (odd ? 1 : 0);
+                const uint32_t row = m0 + i * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
+                if (col >= N || row >= M) continue;   // N is even: both lanes of a pair agree
+                const uint32_t oc = col >> 1;
+                uint16_t v = f2hb(__fmul_rn(h2f(tb[i][j][r / 2]), h2f(f2hb(acc[i][j][r + 1]))));
+                if (res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, res[(size_t)row * ldr + oc]))));
+                reinterpret_cast<uint16_t*>(y)[(size_t)row * ldy + oc] = v;
+            }
+        }
 }
 
 __device__ __forceinline__ u32x4 pair_order16(u32x4 v) {   // k0..k7 -> (k0,k4)(k1,k5)(k2,k6)(k3,k7)
@@ -536,35 +601,21 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
     if (kb < nsteps) mfma(0, 0);   // odd step count: the last step is in buffer / set 0
 
     // Accumulator layout (32x32): lane l, reg r -> col l%32, row 8*(r/4) + 4*(l/32) + r%4.
-    // With SwiGLU, columns 2c / 2c+1 (gate / up of output c) sit in lanes l, l^1; registers
-    // r, r+1 (r even) hold rows q, q+1. One exchange per register pair (the even lane hands
-    // over its row-(q+1) gate, the odd lane its row-q up) lets the even lane finish row q
-    // and the odd lane row q+1, so every lane computes an activation.
-    const bool odd = lane & 1;
+    if (!part && swiglu) {
+        w4g_swiglu_tiles<WJ>(acc, lane, m0, n0 + wn * 32 * WJ, M, N, y, ldy, res, ldr);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < WI; ++i)
 #pragma unroll
         for (int j = 0; j < WJ; ++j) {
             const uint32_t col = n0 + wn * 32 * WJ + j * 32 + l32;
-            if (part || !swiglu) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    if (col >= N || row >= M) continue;
-                    if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
-                    else w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
-                }
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) {
-                    const float got = __shfl_xor(odd ? acc[i][j][r] : acc[i][j][r + 1], 1, 64);
-                    const float gate = odd ? got : acc[i][j][r];
-                    const float up = odd ? acc[i][j][r + 1] : got;
-                    const uint32_t rr = r + (odd ? 1 : 0);
-                    const uint32_t row = m0 + i * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
-                    if (col >= N || row >= M) continue;   // N is even: both lanes of a pair agree
-                    w4g_store_swiglu(y, ldy, res, ldr, row, col >> 1, gate, up);
-                }
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (col >= N || row >= M) continue;
+                if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
+                else w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
             }
         }
 }
@@ -682,31 +733,21 @@ __global__ __launch_bounds__(256, 2) void w4g_gemm_wide_kernel(
 #pragma unroll
     for (int u = 0; u < 5; ++u)
         if (kb + u < nsteps) step(u % 2, u % 3, (u + 2) % 3, kb + u);
-    const bool odd = lane & 1;
+    if (!part && swiglu) {
+        w4g_swiglu_tiles<WJ>(acc, lane, m0, n0 + wave * 32 * WJ, M, N, y, ldy, res, ldr);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < WI; ++i)
 #pragma unroll
         for (int j = 0; j < WJ; ++j) {
             const uint32_t col = n0 + wave * 32 * WJ + j * 32 + l32;
-            if (part || !swiglu) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    if (col >= N || row >= M) continue;
-                    if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
-                    else w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
-                }
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) {
-                    const float got = __shfl_xor(odd ? acc[i][j][r] : acc[i][j][r + 1], 1, 64);
-                    const float gate = odd ? got : acc[i][j][r];
-                    const float up = odd ? acc[i][j][r + 1] : got;
-                    const uint32_t rr = r + (odd ? 1 : 0);
-                    const uint32_t row = m0 + i * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
-                    if (col >= N || row >= M) continue;
-                    w4g_store_swiglu(y, ldy, res, ldr, row, col >> 1, gate, up);
-                }
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (col >= N || row >= M) continue;
+                if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
+                else w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
             }
         }
 }
@@ -757,7 +798,7 @@ __global__ __launch_bounds__(256) void w4g_splitk_reduce8_kernel(const float* __
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float gv = h2f(f2hb(sum[2 * j])), uv = h2f(f2hb(sum[2 * j + 1]));
-            const float act = h2f(f2hb(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv)))));
+            const float act = silu_of(gv);
             uint16_t v = f2hb(__fmul_rn(act, uv));
             if (res) v = f2hb(__fadd_rn(h2f(v), h2f((uint16_t)(rv[j >> 1] >> (16 * (j & 1))))));
             o[j] = v;
@@ -880,6 +921,26 @@ __global__ __launch_bounds__(256) void w4g_splitk_reduce_kernel(const float* __r
 
 namespace {
 
+// Fills this device's silu table before its first SwiGLU epilogue: the filling kernel
+// goes on the caller's stream ahead of the GEMM / GEMV; outside stream capture the call
+// then waits for it once, so launches on any stream find the table filled afterwards.
+// Under capture the fill stays in the captured work (ordered before the epilogue there)
+// and a later call fills it again. Concurrent first calls both write the same values.
+hipError_t silu_table_ready(hipStream_t st) {
+    static std::atomic<uint64_t> ready{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if ((ready.load(std::memory_order_acquire) >> dev) & 1u) return hipSuccess;
+    hipLaunchKernelGGL(silu_table_kernel, dim3(65536 / 256), dim3(256), 0, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return hipSuccess;
+    e = hipStreamSynchronize(st);
+    if (e == hipSuccess) ready.fetch_or(1ull << dev, std::memory_order_release);
+    return e;
+}
+
 // Launch shape of the GEMV for (M, K); see w4g_gemv_kernel.
 struct GemvPlan {
     uint32_t nt = 0, P = 0, R = 0;
@@ -929,6 +990,10 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
                            hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.swiglu && (N & 1)) return hipErrorInvalidValue;
+    if (epi.swiglu) {
+        const hipError_t te = silu_table_ready(st);
+        if (te != hipSuccess) return te;
+    }
     const GemvPlan pl = gemv_plan(M, K);
     if (!pl.ok) {
         if (epi.gamma) return hipErrorInvalidValue;   // the engine normalizes before a GEMM
@@ -966,6 +1031,10 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
                            hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.gamma || (epi.swiglu && (N & 1))) return hipErrorInvalidValue;
+    if (epi.swiglu) {
+        const hipError_t te = silu_table_ready(st);
+        if (te != hipSuccess) return te;
+    }
     const uint32_t mt = (M + GB_M - 1) / GB_M, nt = (N + GB_N - 1) / GB_N, steps = K / GB_K;
     const uint32_t ntw = (N + GW_N - 1) / GW_N;
     const uint32_t parts = w4g_gemm_split_parts(M, N, K);

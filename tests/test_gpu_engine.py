@@ -420,3 +420,34 @@ def test_tempoff_static_plan_matches_bump(engine, oracle):
         out, _ = engine.run_io(pb, x.tobytes(), 1)
         outs.append(out)
     assert outs[0] == outs[1]
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 16384, 512), (256, 1024, 512), (3, 2048, 512), (1, 2048, 512)],
+                         ids=["gemm-wide", "gemm", "gemv-m3", "gemv-m1"])
+def test_swiglu_epilogue_matches_op_chain(engine, M, N, K):
+    """OP_W4G_FUSED_F16 with SwiGLU (its silu read from the per-device table) gives the bits
+    of the same linear without SwiGLU followed by the reference's own ops: STRIDED_SLICE of
+    the gate and up columns, UNARY silu, BINARY mul. Covers the 128x256 and 128x128 GEMM
+    tiles and the GEMV."""
+    rng = np.random.default_rng(M + N)
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, M, K) * np.float16(2.0)
+    bb = BlobBuilder()
+    xs = bb.add_input_slot(M * K * 2)
+    sq, ss = bb.add_slot(wq, count=N * K), bb.add_slot(ws)
+    t_f, t_p, t_g, t_u, t_a, t_y = (bb.temp() for _ in range(6))
+    n = M * (N // 2)
+    bb.op(OP.W4G_FUSED_F16, bb.slot_ref(xs), bb.slot_ref(sq), bb.slot_ref(ss), t_f, M, K, N, WT_REF_NONE,
+          WT_REF_NONE, 1, 2)
+    bb.op(OP.W4G_FUSED_F16, bb.slot_ref(xs), bb.slot_ref(sq), bb.slot_ref(ss), t_p, M, K, N, WT_REF_NONE,
+          WT_REF_NONE, 0, 2)
+    for t, c0 in ((t_g, 0), (t_u, 1)):
+        bb.op(OP.STRIDED_SLICE_F16, t_p, t, n, 2, 0, c0, 0, M, N, 0, 1, 2, 0, M, N, 1)
+    bb.op(OP.UNARY_F16, t_g, t_a, n, 12)
+    bb.op(OP.BINARY_F16, t_a, t_u, t_y, n, 2)
+    pb = engine.parse(bb.build())
+    engine.run_io(pb, x.tobytes(), t_f)
+    fused = _h(engine.temp(t_f))[:n]
+    chain = _h(engine.temp(t_y))[:n]
+    assert np.isfinite(fused.astype(np.float32)).all()
+    assert np.array_equal(fused.view(np.uint16), chain.view(np.uint16))
