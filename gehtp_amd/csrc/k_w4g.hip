@@ -448,7 +448,8 @@ __device__ __forceinline__ void w4g_store_swiglu(__half* __restrict__ y, uint32_
 // lane l, reg r -> col l%32, row 8*(r/4) + 4*(l/32) + r%4. Columns 2c / 2c+1 (gate / up
 // of output c) sit in lanes l, l^1; registers r, r+1 (r even) hold rows q, q+1. One
 // exchange per register pair (the even lane hands over its row-(q+1) gate, the odd lane
-// its row-q up) lets the even lane finish row q and the odd lane row q+1. All silu
+// its row-q up, a DPP quad swap) lets the even lane finish row q and the odd lane row
+// q+1. All silu
 // lookups are issued before any store (a store through y could alias the table for the
 // compiler, which would otherwise wait for each store before the next lookup).
 template <int WJ>
@@ -464,7 +465,7 @@ __device__ __forceinline__ void w4g_swiglu_tiles(f16x_t (&acc)[WI][WJ], uint32_t
         for (int j = 0; j < WJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; r += 2) {
-                const float got = __shfl_xor(odd ? acc[i][j][r] : acc[i][j][r + 1], 1, 64);
+                const float got = dev::dpp<dev::kDppQuadSwap1>(odd ? acc[i][j][r] : acc[i][j][r + 1]);
                 const float gate = odd ? got : acc[i][j][r];
                 const float up = odd ? acc[i][j][r + 1] : got;
                 acc[i][j][r] = gate;
@@ -485,6 +486,30 @@ __device__ __forceinline__ void w4g_swiglu_tiles(f16x_t (&acc)[WI][WJ], uint32_t
                 uint16_t v = f2hb(__fmul_rn(h2f(tb[i][j][r / 2]), h2f(f2hb(acc[i][j][r + 1]))));
                 if (res) v = f2hb(__fadd_rn(h2f(v), h2f(__builtin_bit_cast(uint16_t, res[(size_t)row * ldr + oc]))));
                 reinterpret_cast<uint16_t*>(y)[(size_t)row * ldy + oc] = v;
+            }
+        }
+}
+
+// Plain epilogue of a wave's WI x WJ accumulator tiles: fp16 outputs (plus the residual)
+// or, with `part`, fp32 split-K partials, one value per store (a lane-pair exchange that
+// stores two adjacent columns at once measured 3-5 % slower on the 4B shapes).
+template <int WJ>
+__device__ __forceinline__ void w4g_plain_tiles(const f16x_t (&acc)[WI][WJ], uint32_t lane, uint32_t m0,
+                                                uint32_t col0, uint32_t M, uint32_t N, __half* __restrict__ y,
+                                                uint32_t ldy, const __half* __restrict__ res, uint32_t ldr,
+                                                float* __restrict__ part, uint32_t split) {
+    const uint32_t half = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            const uint32_t col = col0 + j * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (col >= N || row >= M) continue;
+                if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
+                else w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
             }
         }
 }
@@ -605,19 +630,7 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
         w4g_swiglu_tiles<WJ>(acc, lane, m0, n0 + wn * 32 * WJ, M, N, y, ldy, res, ldr);
         return;
     }
-#pragma unroll
-    for (int i = 0; i < WI; ++i)
-#pragma unroll
-        for (int j = 0; j < WJ; ++j) {
-            const uint32_t col = n0 + wn * 32 * WJ + j * 32 + l32;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (col >= N || row >= M) continue;
-                if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
-                else w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
-            }
-        }
+    w4g_plain_tiles<WJ>(acc, lane, m0, n0 + wn * 32 * WJ, M, N, y, ldy, res, ldr, part, split);
 }
 
 // Wide variant for the wide-N shapes: a 128 x 256 workgroup tile, each wave 128 x 64
@@ -737,19 +750,7 @@ __global__ __launch_bounds__(256, 2) void w4g_gemm_wide_kernel(
         w4g_swiglu_tiles<WJ>(acc, lane, m0, n0 + wave * 32 * WJ, M, N, y, ldy, res, ldr);
         return;
     }
-#pragma unroll
-    for (int i = 0; i < WI; ++i)
-#pragma unroll
-        for (int j = 0; j < WJ; ++j) {
-            const uint32_t col = n0 + wave * 32 * WJ + j * 32 + l32;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (col >= N || row >= M) continue;
-                if (part) part[((size_t)split * M + row) * N + col] = acc[i][j][r];
-                else w4g_store(y, ldy, res, ldr, row, col, acc[i][j][r]);
-            }
-        }
+    w4g_plain_tiles<WJ>(acc, lane, m0, n0 + wave * 32 * WJ, M, N, y, ldy, res, ldr, part, split);
 }
 
 // Split-K finish, vector form (N, ldy, ldr multiples of 8, 16-byte aligned rows): a
