@@ -73,6 +73,15 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(read_lane(v, 0), read_lane(v, 16)), fmaxf(read_lane(v, 32), read_lane(v, 48)));
 }
 
+// max(a, b, c) as one v_max3_f32. fmaxf on values the compiler cannot prove canonical
+// (MFMA results, for one) gets a NaN-quieting v_max_f32 x, x, x per operand first; for
+// inputs that are never NaN this gives the same value in one instruction.
+__device__ __forceinline__ float max3_nonan(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // v[l] + v[l^16] + v[l^32] + v[l^48] in every lane: the same position in the four
 // 16-lane rows, summed with gfx950's row swaps (v_permlane32_swap: lanes 32-63 of the
 // first operand trade with lanes 0-31 of the second; v_permlane16_swap: odd rows of the

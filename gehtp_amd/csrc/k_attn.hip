@@ -146,19 +146,18 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
         // (the launcher guarantees scale > 0, so max commutes with the scaling); a stage
         // wholly below the diagonal and inside S skips the mask (a wave-uniform test).
         const bool full = kb + KT <= S && (!CAUSAL || kb + KT - 1 <= qw);
+        // (scores are finite or -inf: the max is three-input v_max3 without NaN quieting)
         float mloc = -INFINITY;
-        if (full) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
-        } else {
+        if (!full) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t key = kb + 8 * (r >> 2) + 4 * hl + (r & 3);
                 if (key >= S || (CAUSAL && key > my_q)) s0[r] = -INFINITY;
                 if (key + 32 >= S || (CAUSAL && key + 32 > my_q)) s1[r] = -INFINITY;
-                mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
             }
         }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mloc = dev::max3_nonan(mloc, s0[r], s1[r]);
         {   // the other half of this query's keys sits in lane l ^ 32
             uint32_t x0 = __builtin_bit_cast(uint32_t, mloc), x1 = x0;
             dev::permlane32_swap(x0, x1);
@@ -475,11 +474,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
             if (!FUSED && A.mask) mk = __half2float(A.mask[(size_t)(g * REP + qh) * A.P + min(key, n_kv - 1u)]) * kLog2e;
             x[t][i] = key < n_kv ? sa[t][i] * A.scale_log2 + mk : -INFINITY;
         }
-    float mx = -INFINITY;
+    float mx = -INFINITY;   // scores are finite or -inf: v_max3 without NaN quieting
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, x[t][i]);
+    for (int t = 0; t < 4; ++t) {
+        mx = dev::max3_nonan(mx, x[t][0], x[t][1]);
+        mx = dev::max3_nonan(mx, x[t][2], x[t][3]);
+    }
     const float m = cross_row_max(mx);
     float p[4][4], ls = 0.0f;
 #pragma unroll
