@@ -137,6 +137,34 @@ def test_w4g_gemm_ragged(lib, oracle, torch_dev, M, N, K):
     assert_close(got, ref, what=f"gemm {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("mode", [0, 1], ids=["plain", "swiglu"])
+def test_w4g_gemm_wide_tile_ragged(lib, oracle, torch_dev, mode):
+    """A grid large enough for the 128x256 tile, with a partial last row tile (M = 2000)
+    and a last column tile partly past N (N = 16382): every row band equals, bit for bit,
+    the same rows computed by a small call (which takes the 128x128 tile; both kernels
+    share the K order and MFMA sequence), and a sample of rows matches the oracle."""
+    import torch
+    rng = np.random.default_rng(91 + mode)
+    M, N, K = 2000, 16382, 256
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, M, K)
+    n_out = N // 2 if mode else N
+    xd, qd, sd = to_dev(x, torch_dev), to_dev(wq, torch_dev), to_dev(ws, torch_dev)
+    y = torch.empty((M, n_out), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_w4g_fused(ptr(xd), K, ptr(qd), ptr(sd), ptr(y), n_out, M, N, K, None, None, n_out, mode,
+                               stream_ptr()) == 0
+    for r0, r1 in ((0, 128), (896, 1024), (1920, 2000)):
+        ys = torch.empty((r1 - r0, n_out), dtype=torch.float16, device=torch_dev)
+        assert lib.gehtp_w4g_fused(ptr(xd) + r0 * K * 2, K, ptr(qd), ptr(sd), ptr(ys), n_out, r1 - r0, N, K, None,
+                                   None, n_out, mode, stream_ptr()) == 0
+        _sync()
+        assert np.array_equal(from_dev(y)[r0:r1].view(np.uint16), from_dev(ys).view(np.uint16)), (r0, r1)
+    rows = np.r_[0:8, 1990:2000]
+    acc = oracle.matmul_w4g(np.ascontiguousarray(x[rows]), wq, ws, threads=8)
+    ref = oracle.binary(oracle.unary(acc[:, 0::2].copy(), 12), acc[:, 1::2].copy(), 2) if mode else acc
+    assert_close(from_dev(y)[rows], ref, what=f"wide tile mode={mode}")
+
+
 def test_w4g_gemv_equals_gemm_small_m(lib, torch_dev):
     """The two implementations agree to two fp16 ulps (4e-3 absolute near zero): both round
     each dequantized weight to fp16 (the reference's fp16(q*s)) and accumulate in fp32,
