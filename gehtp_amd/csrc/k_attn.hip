@@ -27,8 +27,8 @@ constexpr int HD = 128;          // head dim this kernel is built for
 constexpr int QT = 128;          // queries per workgroup (4 waves x 32)
 constexpr int KT = 64;           // keys per LDS stage
 constexpr int KS = HD + 8;       // K tile row stride (halves)
-constexpr int VSR = HD + 16;     // V tile row stride (halves): 72 dwords, so the transposed
-                                 // 8-byte reads of one 16-lane group hit 32 distinct banks
+constexpr int VSR = HD + 32;     // V tile row stride (halves): 80 dwords, so the 4 rows x 64 bytes
+                                 // that 32 lanes of a transposed read take hit 64 distinct banks
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef short s4_t __attribute__((ext_vector_type(4)));
@@ -318,7 +318,8 @@ struct DecodeArgs {
 // lc, the same keys) comes from the row-major V tile through the transposing LDS read,
 // each lane pointing at the 8-byte piece (key 32j + 4lr + lc/4, dims 16u + 4(lc%4) ..)
 // so that lane lc receives element lc%4 of the pieces of lanes lc/4 + 4i.
-constexpr int VSD = HD + 16;   // V tile row stride (halves): a 16-lane transposed read hits 32 banks
+constexpr int VSD = HD + 16;   // V tile row stride (halves): a 32-lane transposed read hits 64 banks
+constexpr int KSD = HD + 8;    // K tile row stride (halves): 16 rows of a 16-byte access hit 64 banks
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float cross_row_max(float v) {
@@ -334,7 +335,7 @@ __device__ __forceinline__ float cross_row_max(float v) {
 template <int REP, bool FUSED>
 __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     __shared__ __align__(16) _Float16 s_v[DC * VSD];
-    __shared__ __align__(16) _Float16 s_kt[DC * VSD];
+    __shared__ __align__(16) _Float16 s_kt[DC * KSD];
     __shared__ __align__(16) _Float16 s_q[REP][HD];
     __shared__ __align__(16) _Float16 s_k[HD];
     const uint32_t c = blockIdx.x, g = blockIdx.y;
@@ -425,7 +426,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
             if (FUSED && key == pos) v = *reinterpret_cast<const u32x4*>(vnew + 32 * s);
             if (key >= n_kv) v = u32x4{0u, 0u, 0u, 0u};
             *reinterpret_cast<u32x4*>(&s_v[kl * VSD + 32 * s + 8 * lr]) = v;
-            *reinterpret_cast<u32x4*>(&s_kt[kl * VSD + 32 * s + 8 * lr]) = kr[s];
+            *reinterpret_cast<u32x4*>(&s_kt[kl * KSD + 32 * s + 8 * lr]) = kr[s];
         }
     }
     __syncthreads();
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) kf[t][s] = *reinterpret_cast<const u32x4*>(&s_kt[(16 * t + lc) * VSD + 32 * s + 8 * lr]);
+        for (int s = 0; s < 4; ++s) kf[t][s] = *reinterpret_cast<const u32x4*>(&s_kt[(16 * t + lc) * KSD + 32 * s + 8 * lr]);
     if (owns_new) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
