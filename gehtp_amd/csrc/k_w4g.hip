@@ -246,6 +246,11 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
             return __builtin_fmaf(__builtin_fmaf(-q, rms[m], a), rcp[m], q);
         };
         u32x4* xn = reinterpret_cast<u32x4*>(red + A.red_floats);
+        // 16-byte chunk i of a row sits at slot i ^ ((i >> 4) & 3): the reads below (lane p
+        // takes chunks 4p .. 4p+3, one per instruction) then hit 64 distinct banks per 16
+        // lanes instead of 4-way conflicting, and the writes (consecutive chunks) stay
+        // conflict-free; K8 is a multiple of 8, so a row's slots stay in the row.
+        auto xslot = [](uint32_t i) -> uint32_t { return i ^ ((i >> 4) & 3u); };
         for (uint32_t k = 0, i = t; i < K8; ++k, i += nt) {
             const u32x4 g4 = k < PRE ? gv[k] : reinterpret_cast<const u32x4*>(A.gamma)[i];
 #pragma unroll
@@ -260,14 +265,14 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                     hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(g4[e] >> 16))), 0.0f);
                     o[e] = (uint32_t)f2hb(lo) | ((uint32_t)f2hb(hi) << 16);
                 }
-                xn[m * K8 + i] = o;
+                xn[m * K8 + xslot(i)] = o;
             }
         }
         __syncthreads();
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) xr[m][c] = xn[m * K8 + p * 4 + c];
+            for (int c = 0; c < 4; ++c) xr[m][c] = xn[m * K8 + xslot(p * 4 + c)];
         if (A.red_floats == 0) __syncthreads();   // xn shares LDS with red
     }
 
