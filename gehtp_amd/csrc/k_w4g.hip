@@ -996,10 +996,6 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
                            hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.swiglu && (N & 1)) return hipErrorInvalidValue;
-    if (epi.swiglu) {
-        const hipError_t te = silu_table_ready(st);
-        if (te != hipSuccess) return te;
-    }
     const GemvPlan pl = gemv_plan(M, K);
     if (!pl.ok) {
         if (epi.gamma) return hipErrorInvalidValue;   // the engine normalizes before a GEMM
