@@ -97,11 +97,14 @@ __global__ __launch_bounds__(256) void silu_table_kernel() {
     g_silu_tab[i] = silu_f16_expr((uint16_t)i);
 }
 
-constexpr int kGemvU = 4;   // passes per load batch
+constexpr int kGemvU = 4;   // passes per load batch (5 for the 10-pass form)
+// Pass counts with a fully unrolled batch schedule; other counts above kGemvU run the
+// batch loop and must be multiples of kGemvU.
+__host__ __device__ constexpr bool gemv_static_np(uint32_t np) { return np == 8 || np == 10 || np == 12; }
 
 template <int MR, int NP>
 __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
-    constexpr int U = kGemvU;
+    constexpr int U = NP == 10 ? 5 : kGemvU;
     // Dynamic LDS: red = [np][MR][nt] pass partials, then (with gamma) the normalized
     // rows [MR][K] halves at a 16-byte aligned offset.
     extern __shared__ __align__(16) float red[];
@@ -111,38 +114,34 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
     const uint32_t p = t % P, rr = t / P;
     const bool active = rr < R;
     const uint32_t rows_wg = R * A.np;
-    const uint32_t r0 = blockIdx.x * rows_wg;
-    const uint32_t RB = min(rows_wg, A.N - r0);
+    // The host guarantees N >= rows_wg. The last workgroup is moved back to end at row N:
+    // it overlaps its predecessor by `skip` rows, which it computes again (same bits) and
+    // does not store. Every workgroup thus covers rows_wg rows and no load needs a
+    // clamped index.
+    const uint32_t r0n = blockIdx.x * rows_wg;
+    const uint32_t r0 = min(r0n, A.N - rows_wg);
+    const uint32_t skip = r0n - r0;
+    const uint32_t RB = rows_wg;
     const uint32_t rowbytes = A.K / 2, G = A.K / 64, K8 = A.K / 8;
     const uint32_t nb = (A.np + U - 1) / U;
 
-    // Every global load below is unconditional, with out-of-range indices clamped to
-    // valid ones: a load under a divergent branch with a zeroing else-path makes the
-    // compiler wait for each load before issuing the next. Lanes whose row lies past
-    // the workgroup's rows load the workgroup's first row; the reduction never reads
-    // their partial sums.
-    // A scale is fetched as the 4-byte-aligned word holding it (such a word never crosses
-    // a page, so it is mapped wherever the scale is) and its half is picked when it is
-    // used: any operation on the loaded value (packing two halves into one register,
-    // clearing the upper half) would make the thread wait for that load while it is
-    // still issuing the others.
-    auto row_of = [&](uint32_t i) -> size_t {   // weight row of pass i (clamped)
-        const uint32_t lr = i * R + rr;
-        return r0 + ((active && lr < RB) ? lr : 0u);
-    };
-    // Word index from ws - a2, a2 = 1 when ws sits 2 bytes past a 4-byte boundary (pointer
-    // arithmetic on the argument keeps the loads global rather than flat).
-    const uint32_t a2 = (uint32_t)(reinterpret_cast<uintptr_t>(A.ws) >> 1) & 1u;
-    const uint32_t* ws32 = reinterpret_cast<const uint32_t*>(A.ws - a2);
-    auto scale_el = [&](uint32_t i) -> size_t { return row_of(i) * G + (p >> 1) + a2; };
+    // Every global load below is unconditional: a load under a divergent branch with a
+    // zeroing else-path makes the compiler wait for each load before issuing the next.
+    // Lanes past the workgroup's R rows per pass load row rr = 0; the reduction never
+    // reads their partial sums. Each load is a workgroup-uniform base (advanced by a
+    // uniform step per pass, scalar arithmetic) plus this thread's fixed 32-bit offset
+    // (the host checks that one weight matrix spans less than 4 GiB). A scale is loaded
+    // as its own 16-bit value and only widened to a pair where it is used.
+    const uint32_t rrc = active ? rr : 0u;
+    const uint8_t* wq0 = A.wq + (size_t)r0 * rowbytes;
+    const uint16_t* ws0 = reinterpret_cast<const uint16_t*>(A.ws) + (size_t)r0 * G;
+    const uint32_t w_off = rrc * rowbytes + p * 16, s_off = rrc * G + (p >> 1);
     auto load_pass = [&](uint32_t i, u32x4& w, uint32_t& s) {
-        const size_t row = row_of(i);
-        w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(A.wq + row * rowbytes) + p);
-        s = ws32[scale_el(i) >> 1];
+        w = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(wq0 + (size_t)(i * R) * rowbytes + w_off));
+        s = ws0[(size_t)(i * R) * G + s_off];
     };
-    auto scale_of = [&](uint32_t i, uint32_t word) -> _Float16 {
-        return __builtin_bit_cast(_Float16, (uint16_t)(word >> (16 * (scale_el(i) & 1))));
-    };
+    auto scale_of = [&](uint32_t word) -> _Float16 { return __builtin_bit_cast(_Float16, (uint16_t)word); };
     auto load_batch = [&](uint32_t b, u32x4 (&w)[U], uint32_t (&s)[U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) load_pass(b * U + u, w[u], s[u]);
@@ -187,12 +186,15 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
         for (int m = 0; m < MR; ++m) res0[m] = 0;
     }
 
-    // NP > 0 (= np): all passes' loads issued here, before the prologue; NP = 0: batches
-    // of U passes, two in flight.
-    constexpr int NPA = NP > 0 ? NP : 1;
+    // NP in 1..4: straight-line, every load issued here. NP = k*U (k > 1): k batches in a
+    // fully unrolled ping-pong, so every wait counts exactly the loads it needs; NP = 0:
+    // the same ping-pong as a loop over np / U batches.
+    constexpr bool STRAIGHT = NP > 0 && NP <= U;
+    constexpr int NB = NP > U ? NP / U : 0;
+    constexpr int NPA = STRAIGHT ? NP : 1;
     u32x4 wa[U], wb[U], wall[NPA];
     uint32_t sa[U], sb[U], sall[NPA];
-    if constexpr (NP > 0) {
+    if constexpr (STRAIGHT) {
 #pragma unroll
         for (int i = 0; i < NP; ++i) load_pass(i, wall[i], sall[i]);
     } else {
@@ -216,8 +218,8 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                 for (int e = 0; e < 4; ++e) {
                     const double lo = (double)h2f((uint16_t)(v[e] & 0xFFFFu));
                     const double hi = (double)h2f((uint16_t)(v[e] >> 16));
-                    ss[m] += lo * lo;
-                    ss[m] += hi * hi;
+                    ss[m] = __builtin_fma(lo, lo, ss[m]);   // lo*lo is exact: same bits as * then +
+                    ss[m] = __builtin_fma(hi, hi, ss[m]);
                 }
             }
         }
@@ -290,7 +292,7 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
         }
 
     auto compute_pass = [&](uint32_t i, const u32x4& wc, uint32_t sc) {
-        const _Float16 sh = scale_of(i, sc);
+        const _Float16 sh = scale_of(sc);
         const h2_t s2 = {sh, sh};
         float acc[MR];
 #pragma unroll
@@ -307,19 +309,28 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                 acc[m] = __builtin_amdgcn_fdot2(d[3], as_h2(xs[m][4 * c + 3]), acc[m], false);
             }
         }
-        if (i < A.np) {
 #pragma unroll
-            for (int m = 0; m < MR; ++m) red[(i * MR + m) * nt + t] = acc[m];
-        }
+        for (int m = 0; m < MR; ++m) red[(i * MR + m) * nt + t] = acc[m];
     };
-    if constexpr (NP > 0) {
+    auto compute_batch = [&](uint32_t b, const u32x4 (&wc)[U], const uint32_t (&sc)[U]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) compute_pass(b * U + u, wc[u], sc[u]);
+    };
+    if constexpr (STRAIGHT) {
 #pragma unroll
         for (int i = 0; i < NP; ++i) compute_pass(i, wall[i], sall[i]);
-    } else {
-        auto compute_batch = [&](uint32_t b, const u32x4 (&wc)[U], const uint32_t (&sc)[U]) {
+    } else if constexpr (NB > 0) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) compute_pass(b * U + u, wc[u], sc[u]);
-        };
+        for (int b = 0; b < NB; ++b) {
+            if (b & 1) {
+                if (b + 1 < NB) load_batch(b + 1, wa, sa);
+                compute_batch(b, wb, sb);
+            } else {
+                if (b + 1 < NB) load_batch(b + 1, wb, sb);
+                compute_batch(b, wa, sa);
+            }
+        }
+    } else {
         // Ping-pong over two register buffers: the next batch is in flight while one computes.
         for (uint32_t b = 0; b < nb; b += 2) {
             if (b + 1 < nb) load_batch(b + 1, wb, sb);
@@ -345,7 +356,7 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                 s = dev::row_sum16(s);
                 if (TG == 2) s = dev::pair_row_sum(s);
                 if (TG == 4) s = dev::cross_row_sum(s);
-                if (tl == 0) {
+                if (tl == 0 && lr >= skip) {
                     uint16_t v = f2hb(s);
                     if (A.res) v = f2hb(__fadd_rn(h2f(v), res_at(m, lr)));
                     reinterpret_cast<uint16_t*>(A.y)[(size_t)m * A.ldy + r0 + lr] = v;
@@ -366,7 +377,7 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                 }
                 sg = dev::row_sum16(sg);
                 su = dev::row_sum16(su);
-                if (gl == 0) {
+                if (gl == 0 && 2 * k2 >= skip) {
                     const float gv = h2f(f2hb(sg)), uv = h2f(f2hb(su));
                     // the expression rather than the table: a table read right after
                     // the kernel boundary would sit on this epilogue's short tail
@@ -973,15 +984,20 @@ GemvPlan gemv_plan(uint32_t M, uint32_t K) {
 }
 
 // Up to 4 passes per thread run the straight-line form (all weight loads issued before
-// the RMSNorm prologue, each pass computed as soon as its own load has landed); more run
-// the batched loop (measured 12.0 against 10.6 us at the gate/up shape's 5-10 passes).
+// the RMSNorm prologue, each pass computed as soon as its own load has landed; measured
+// 12.0 against 10.6 us for batches at the gate/up shape's 5-10 passes); 8, 10 and 12
+// passes run unrolled two-buffer batch schedules, other counts the same as a loop.
 template <int MR>
 hipError_t gemv_dispatch(dim3 g3, dim3 b3, size_t lds, hipStream_t st, const GemvArgs& A) {
-    switch (A.np <= 4 ? A.np : 0u) {
+    if (A.np > (uint32_t)kGemvU && !gemv_static_np(A.np) && A.np % kGemvU) return hipErrorInvalidValue;
+    switch (A.np <= 4 || gemv_static_np(A.np) ? A.np : 0u) {
     case 1: hipLaunchKernelGGL((w4g_gemv_kernel<MR, 1>), g3, b3, lds, st, A); break;
     case 2: hipLaunchKernelGGL((w4g_gemv_kernel<MR, 2>), g3, b3, lds, st, A); break;
     case 3: hipLaunchKernelGGL((w4g_gemv_kernel<MR, 3>), g3, b3, lds, st, A); break;
     case 4: hipLaunchKernelGGL((w4g_gemv_kernel<MR, 4>), g3, b3, lds, st, A); break;
+    case 8: hipLaunchKernelGGL((w4g_gemv_kernel<MR, 8>), g3, b3, lds, st, A); break;
+    case 10: hipLaunchKernelGGL((w4g_gemv_kernel<MR, 10>), g3, b3, lds, st, A); break;
+    case 12: hipLaunchKernelGGL((w4g_gemv_kernel<MR, 12>), g3, b3, lds, st, A); break;
     default: hipLaunchKernelGGL((w4g_gemv_kernel<MR, 0>), g3, b3, lds, st, A); break;
     }
     return hipGetLastError();
@@ -1001,22 +1017,37 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
         if (epi.gamma) return hipErrorInvalidValue;   // the engine normalizes before a GEMM
         return launch_w4g_gemm(x, ldx, wq, ws, y, ldy, M, N, K, st, epi);
     }
+    // The kernel addresses weights by 32-bit offsets from a workgroup's first row.
+    if ((uint64_t)N * (K / 2) >= (1ull << 32)) return hipErrorInvalidValue;
     // Rows per workgroup: about two workgroups per CU (three when one workgroup holds a
     // single row per pass, as for K = 9728: measured 11 % faster there, slower for the
     // multi-row shapes), partial sums within 32 KiB.
     const uint32_t target = (pl.R == 1 ? 3u : 2u) * (uint32_t)device_cu_count();
-    uint32_t np = (N + pl.R * target - 1) / (pl.R * target);
+    uint32_t R = std::min(pl.R, N);   // rows per pass; a workgroup never spans more than N rows
+    uint32_t np = (N + R * target - 1) / (R * target);
     const uint32_t np_max = std::max(1u, 8192u / (M * pl.nt));
-    np = std::max(1u, std::min(np, np_max));
-    if (epi.swiglu && ((pl.R * np) & 1)) ++np;   // gate/up pairs never straddle workgroups
+    const uint32_t np_fit = std::min(np_max, N / R);
+    np = std::max(1u, std::min(np, np_fit));
+    // Other counts above kGemvU run the batch loop in whole batches of kGemvU. (The row
+    // split matters more than wasted work: the busiest CUs set the time, so the gate/up
+    // shape keeps 10 passes, 80 rows on a CU holding two workgroups, not 8 or 12 with 96.)
+    if (np > (uint32_t)kGemvU && !gemv_static_np(np)) {
+        const uint32_t up = (np + kGemvU - 1) / kGemvU * kGemvU;
+        np = up <= np_fit ? up : np / kGemvU * kGemvU;
+    }
+    if (epi.swiglu && ((R * np) & 1)) {   // gate/up pairs never straddle workgroups (N is even)
+        if (np > 1) --np;
+        else if (2 * R <= N && 2 <= np_max) np = 2;
+        else --R;                         // R odd >= 3 here
+    }
     // Normalized rows after the partials when both fit in 64 KiB; otherwise they share
     // the start of LDS (red_floats = 0) and the kernel adds a barrier between them.
     const size_t red_b = ((size_t)np * M * pl.nt * 4 + 15) & ~(size_t)15;
     const size_t xn_b = epi.gamma ? (size_t)M * K * 2 : 0;
     const bool split = red_b + xn_b <= 65536;
     const size_t lds = split ? red_b + xn_b : std::max(red_b, xn_b);
-    const uint32_t grid = (N + pl.R * np - 1) / (pl.R * np);
-    GemvArgs A{x, ldx, wq, ws, y, ldy, N, K, pl.P, pl.R, np, split ? (uint32_t)(red_b / 4) : 0u,
+    const uint32_t grid = (N + R * np - 1) / (R * np);
+    GemvArgs A{x, ldx, wq, ws, y, ldy, N, K, pl.P, R, np, split ? (uint32_t)(red_b / 4) : 0u,
                epi.gamma, epi.res, epi.ldr, epi.swiglu ? 1 : 0};
     const dim3 g3(grid), b3(pl.nt);
     switch (M) {

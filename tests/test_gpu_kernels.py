@@ -71,11 +71,14 @@ def test_w4g_gemv_shapes(lib, oracle, torch_dev, N, K):
 
 
 @pytest.mark.parametrize("M", [1, 2, 4])
-@pytest.mark.parametrize("N", [2000, 4000, 6144, 8000, 9728])
+@pytest.mark.parametrize("N", [2000, 4000, 6144, 8000, 9728, 19456, 24000, 30000])
 def test_w4g_gemv_pass_forms(lib, oracle, torch_dev, M, N):
-    """K = 2560 (80 threads per row, 4 rows per pass, ~512 workgroups): N = 2000 / 4000 /
-    6144 / 8000 run 1 / 2 / 3 / 4 passes per thread in the straight-line form, N = 9728
-    runs 5 passes in the batched loop; each for M = 1, 2, 4 against the oracle."""
+    """K = 2560 (80 threads per row, 4 rows per pass, ~512 workgroups on 256 CUs): at M = 1
+    N = 2000 / 4000 / 6144 / 8000 run 1 / 2 / 3 / 4 passes per thread in the straight-line
+    form, N = 9728 / 19456 / 24000 the unrolled 8 / 10 / 12-pass batch schedules, N = 30000
+    (15 passes, rounded to 16) the batch loop; M = 2 and 4 cap the passes by the partial-sum
+    space (12 and 6, the latter run as 4). Each against the oracle, every shape with a last
+    workgroup moved back to end at row N where N is not a multiple of its rows."""
     rng = np.random.default_rng(N + M)
     K = 2560
     _, wq, ws = w4g_weights(rng, N, K)
@@ -87,9 +90,8 @@ def test_w4g_gemv_pass_forms(lib, oracle, torch_dev, M, N):
 
 @pytest.mark.parametrize("N,K", [(7, 192), (9, 64), (301, 576)])
 def test_w4g_gemv_scales_off_word(lib, oracle, torch_dev, N, K):
-    """Scales read as the aligned 32-bit word holding each one: a scale array starting 2
-    bytes past a 4-byte boundary with an odd number of scales (its last word reaches 2
-    bytes past the array, never past the page) gives the oracle's result."""
+    """A scale array starting 2 bytes past a 4-byte boundary with an odd number of scales
+    (each scale is loaded as its own 16-bit value) gives the oracle's result."""
     import torch
     rng = np.random.default_rng(N * K)
     _, wq, ws = w4g_weights(rng, N, K)
