@@ -1076,9 +1076,9 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
     const uint32_t per = split ? (steps + parts - 1) / parts : steps;
     // Both tile shapes give the same bits. The wide one when its grid fills two rounds of
     // two workgroups per CU (measured at M = 2048: gate/up N = 19456 256 vs 263 us; with
-    // fewer tiles, qkv N = 6144 and the split N = 2560 shapes, the 128 x 128 tile at
-    // three per CU is 5-9 % faster).
-    const bool wide = (size_t)mt * ntw * (split ? parts : 1u) >= 4 * (size_t)device_cu_count();
+    // fewer tiles, qkv N = 6144 and a two-part split of N = 2560, the 128 x 128 tile at
+    // three per CU is 5-9 % faster) and for a three-part split, sized for it.
+    const bool wide = (size_t)mt * ntw * (split ? parts : 1u) >= 4 * (size_t)device_cu_count() || (split && parts == 3);
     auto gemm = [&](float* pw) {
         if (wide)
             hipLaunchKernelGGL(w4g_gemm_wide_kernel, dim3(mt * ntw * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq,
@@ -1114,12 +1114,18 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
     return hipGetLastError();
 }
 
-// Two K parts when the tile grid alone would give fewer than two workgroups per CU
-// (three fit at once) and each part still has 16 or more K steps: the narrow-N
-// projections (N = hidden) otherwise run one latency-bound workgroup on most CUs.
+// K is split when the 128 x 128 tile grid alone would give fewer than two workgroups
+// per CU (three fit at once): the narrow-N projections (N = hidden) otherwise run one
+// latency-bound workgroup on most CUs. Three parts of 16+ K steps on the 128 x 256 tile
+// when that grid fits one round at two workgroups per CU (M = 2048, N = 2560: 160 tiles,
+// 480 workgroups; the o- and down-projections measured 2.4 % faster per prefill than
+// two parts on the 128 x 128 tile, whose A reads from LDS take as long as its MFMAs);
+// otherwise two parts of 16+ steps on the 128 x 128 tile.
 uint32_t w4g_gemm_split_parts(uint32_t M, uint32_t N, uint32_t K) {
-    const size_t tiles = (size_t)((M + GB_M - 1) / GB_M) * ((N + GB_N - 1) / GB_N);
-    return (tiles < 2 * (size_t)device_cu_count() && K / GB_K >= 32) ? 2u : 1u;
+    const size_t mt = (M + GB_M - 1) / GB_M, cus = (size_t)device_cu_count();
+    if (mt * ((N + GB_N - 1) / GB_N) >= 2 * cus) return 1u;
+    if (K / GB_K >= 48 && 3 * mt * ((N + GW_N - 1) / GW_N) <= 2 * cus) return 3u;
+    return K / GB_K >= 32 ? 2u : 1u;
 }
 
 size_t w4g_gemm_split_bytes(uint32_t M, uint32_t N, uint32_t K) {

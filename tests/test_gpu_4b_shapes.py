@@ -1,7 +1,7 @@
 """Prefill W4A16 GEMMs at the 4B-class model's own shapes (M = 2048
 prompt tokens), unit-scale inputs, against the oracle: the fused q|k|v GEMM, gate/up with
 the SwiGLU epilogue (N = 2 x 9728 interleaved rows), and the o- / down-projections with
-the residual epilogue, which split K in two through an fp32 workspace (K = 4096, 9728),
+the residual epilogue, which split K in three through an fp32 workspace (K = 4096, 9728),
 also followed by the split's finishing pass that writes the next GEMM's RMSNorm rows.
 
 Tolerance (written here because these outputs are not unit-sized): the BASELINE bar is

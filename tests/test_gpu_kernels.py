@@ -423,20 +423,21 @@ def test_w4g_fused_gemm_epilogues(lib, oracle, torch_dev):
     assert_close(from_dev(y), ref, what="gemm swiglu+res")
 
 
+@pytest.mark.parametrize("K", [4160, 2624])
 @pytest.mark.parametrize("mode,use_res,M,N", [(0, False, 384, 1280), (0, True, 200, 1280), (1, False, 384, 1280),
                                               (1, True, 131, 1280), (0, True, 77, 1276), (1, True, 45, 1284)])
-def test_w4g_gemm_split_k(lib, oracle, torch_dev, mode, use_res, M, N):
-    """Narrow N, long K: with a workspace the GEMM splits K in two (fp32 sums of each half,
-    added in a second pass through the same epilogue: 8 columns per thread when N and the
-    output rows allow 16-byte access, else column pairs). Checked against the oracle and
-    against the one-pass GEMM (only the fp32 sum order differs: almost everywhere identical).
-    K = 4160 has 65 K steps, so the two halves are unequal."""
+def test_w4g_gemm_split_k(lib, oracle, torch_dev, mode, use_res, M, N, K):
+    """Narrow N, long K: with a workspace the GEMM splits K (fp32 sums of each part, added
+    in part order in a second pass through the same epilogue: 8 columns per thread when N
+    and the output rows allow 16-byte access, else column pairs). K = 4160 (65 K steps)
+    splits in three unequal parts on the 128 x 256 tile, K = 2624 (41 steps) in two on the
+    128 x 128 tile. Checked against the oracle and against the one-pass GEMM (only the
+    fp32 sum order differs: almost everywhere identical)."""
     import torch
-    rng = np.random.default_rng(60 + 2 * mode + use_res + N)
-    K = 4160
+    rng = np.random.default_rng(60 + 2 * mode + use_res + N + K)
     n_out = N // 2 if mode else N
     need = lib.gehtp_w4g_split_bytes(M, N, K)
-    assert need == 2 * M * N * 4
+    assert need == (3 if K // 64 >= 48 else 2) * M * N * 4
     assert lib.gehtp_w4g_split_bytes(2, N, K) == 0            # GEMV sizes never split
     assert lib.gehtp_w4g_split_bytes(M, 1 << 16, K) == 0       # enough tiles already
     _, wq, ws = w4g_weights(rng, N, K)
