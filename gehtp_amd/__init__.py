@@ -170,5 +170,9 @@ class Engine:
         self.lib.wt_exec_fusion_stats(C.byref(f), C.byref(r))
         return f.value, r.value
 
+    def qkv_rope_fused(self) -> int:
+        """QK-norm/RoPE/KV-append ops performed by their q|k|v GEMM's epilogue so far."""
+        return int(self.lib.wt_exec_qkv_rope_fused())
+
 
 WT_ERR = WT_ERR

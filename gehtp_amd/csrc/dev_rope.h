@@ -85,5 +85,56 @@ __device__ __forceinline__ void head_norm_rope(float x1, float x2, float g1, flo
     y2 = rne_f16(__fadd_rn(a2, b2));
 }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h2_pk __attribute__((ext_vector_type(2)));
+// A word as two f16 lanes. Words are passed by value: __builtin_bit_cast applied directly
+// to an element of an ext_vector reads element 0 whatever the index.
+__device__ __forceinline__ h2_pk h2_of(uint32_t w) { return __builtin_bit_cast(h2_pk, w); }
+
+// One 128-dim q or k head row held by an aligned group of 8 lanes: lane g owns halves
+// [8g, 8g+8) (xl) and [64+8g, 64+8g+8) (xh) — both halves of its RoPE pairs — with the
+// gamma halves at the same places (gl, gh) and the token's RoPE table entries 8g..8g+7
+// as f16 cos (cw) and sin (sw). RMSNORM2_F16 without bias: squares in double, summed in
+// the lane's element order, then over the group as ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7));
+// x / rms as Markstein's corrected quotient, times gamma, + 0, rounded to f16. RoPE on
+// packed f16: each product and sum of two f16 values rounded once to f16 equals the f32
+// operation rounded to f16 (24 >= 2*11 + 1 bits, so the double rounding is innocuous),
+// the arithmetic of the reference's rope op. All 8 lanes of the group must call it.
+__device__ __forceinline__ void qk_row8_norm_rope(const u32x4_t& xl, const u32x4_t& xh, const u32x4_t& gl,
+                                                  const u32x4_t& gh, const u32x4_t& cw, const u32x4_t& sw,
+                                                  u32x4_t& yl, u32x4_t& yh) {
+    float x[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        x[2 * k] = bits_f((uint16_t)(xl[k] & 0xFFFFu));
+        x[2 * k + 1] = bits_f((uint16_t)(xl[k] >> 16));
+        x[8 + 2 * k] = bits_f((uint16_t)(xh[k] & 0xFFFFu));
+        x[8 + 2 * k + 1] = bits_f((uint16_t)(xh[k] >> 16));
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ss += (double)x[k] * (double)x[k];
+    ss += dpp<kDppQuadSwap1>(ss);
+    ss += dpp<kDppQuadSwap2>(ss);
+    ss += dpp<kDppRowHalfMirror>(ss);
+    const float rms = (float)sqrt(ss / 128.0 + 1e-6);
+    const float y = __fdiv_rn(1.0f, rms);
+    uint32_t hw[8];   // normalized halves as f16 pairs: [0,4) low half, [4,8) high half
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t gw = k < 4 ? gl[k] : gh[k - 4];
+        const float h0 = __fadd_rn(__fmul_rn(div_markstein(x[2 * k], rms, y), bits_f((uint16_t)(gw & 0xFFFFu))), 0.0f);
+        const float h1 = __fadd_rn(__fmul_rn(div_markstein(x[2 * k + 1], rms, y), bits_f((uint16_t)(gw >> 16))), 0.0f);
+        hw[k] = __builtin_bit_cast(uint32_t, h2_pk{(_Float16)h0, (_Float16)h1});
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const h2_pk a = h2_of(hw[k]), b = h2_of(hw[4 + k]), c = h2_of(cw[k]), sn = h2_of(sw[k]);
+        const h2_pk ac = a * c, bs = b * sn, bc = b * c, as = a * sn;
+        yl[k] = __builtin_bit_cast(uint32_t, ac - bs);
+        yh[k] = __builtin_bit_cast(uint32_t, bc + as);
+    }
+}
+
 }  // namespace dev
 }  // namespace gehtp

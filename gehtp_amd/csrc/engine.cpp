@@ -117,6 +117,8 @@ struct Engine {
     size_t norm_cap = 0;
     uint8_t* split_buf = nullptr;  // fp32 K-split partials of the W4G GEMM
     size_t split_cap = 0;
+    uint8_t* rope_buf = nullptr;   // RoPE table of a q|k|v GEMM performing OP_QK_ROPE_KV_F16
+    size_t rope_cap = 0;
 
     // OP_MATMUL_W4A16 engine surfaces (the reference's HMX engine: shape, act, out,
     // weights, bias), read by OP_DMA's 0xC000 references; engine_m reports w4_m.
@@ -136,6 +138,7 @@ struct Engine {
     int graphs = -1;        // -1: not yet read from the environment; 0 off; 1 on
     int fusion = -1;        // attention-chain fusion: -1 not yet read from the environment
     uint64_t chains_found = 0, fused_runs = 0;
+    uint64_t qkv_rope_fused = 0;   // OP_QK_ROPE_KV_F16 ops performed by their GEMM's epilogue
     bool graphs_broken = false;
     uint32_t n_captures = 0, n_replays = 0;
 
@@ -955,6 +958,24 @@ struct PreNorm {
     uint32_t M = 0, K = 0;
 };
 PreNorm g_prenorm;
+// An OP_QK_ROPE_KV_F16 that the q|k|v GEMM before it performed in its epilogue.
+const wt_op* g_rope_pre = nullptr;
+// OP_QK_ROPE_KV_F16's operands, checked, with its outputs allocated.
+struct QkRope {
+    const __half* qkv = nullptr;
+    const __half* qg = nullptr;
+    const __half* kg = nullptr;
+    float theta = 0.0f;
+    uint32_t n_tok = 0, H = 0, KVH = 0, si = 0;
+    State* s = nullptr;
+    __half* q_out = nullptr;
+    __half* k_out = nullptr;
+    __half* v_out = nullptr;
+};
+int qk_rope_prep(const wt_blob* b, const wt_op* op, QkRope& r, char* err, size_t errn);
+void qk_rope_commit(const QkRope& r);
+bool fusion_on();
+extern uint32_t g_run_end;
 
 int op_w4g_fused(Ctx& cx) {
     char* err = cx.err; size_t errn = cx.errn;
@@ -1013,6 +1034,43 @@ int op_w4g_fused(Ctx& cx) {
         }
         src = reinterpret_cast<const __half*>(g.norm_buf);
     }
+    // The OP_QK_ROPE_KV_F16 that reads this q|k|v output next, in the same run: the
+    // GEMM's epilogue performs it (after a table kernel that fixes the positions and
+    // advances the counter), writing y as well, and that op then finds its work done.
+    // Shapes or operands the epilogue cannot take leave the op to run (or fail) alone.
+    const wt_op* rx = cx.op + 1;
+    if (fusion_on() && !swiglu && !res && ldy == N && (uint32_t)(rx - cx.b->ops) < g_run_end &&
+        rx->opcode == OP_QK_ROPE_KV_F16 && rx->n_args >= 12 && rx->args[0] == A(3) && rx->args[5] == M &&
+        rx->args[8] == 128 && (uint64_t)(rx->args[6] + 2ull * rx->args[7]) * 128u == N) {
+        QkRope r;
+        char rerr[8];
+        auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+        if (qk_rope_prep(cx.b, rx, r, rerr, sizeof rerr) == 0 && al16(y) && ldy % 8 == 0 && al16(r.qg) &&
+            al16(r.kg) && al16(r.q_out) && al16(r.k_out) && al16(r.v_out) && al16(r.s->dev) &&
+            r.s->slot_bytes % 16 == 0) {
+            if (scratch(&g.rope_buf, &g.rope_cap, w4g_rope_table_bytes(M), err, errn)) return -1;
+            W4gRope R;
+            R.H = r.H;
+            R.KVH = r.KVH;
+            R.q_gamma = r.qg;
+            R.k_gamma = r.kg;
+            R.table = g.rope_buf;
+            R.q_out = r.q_out;
+            R.k_out = r.k_out;
+            R.v_out = r.v_out;
+            R.ring = r.s->dev;
+            R.slot_bytes = r.s->slot_bytes;
+            R.nslots = r.s->nslots;
+            epi.rope = &R;
+            CHECK_LAUNCH(launch_rope_table(g.counters_dev + r.si, g.counters_dev + WT_MAX_STATES + r.si, r.theta, M,
+                                           g.rope_buf, g.stream));
+            CHECK_LAUNCH(launch_w4g_gemm(src, K, wq, ws, y, ldy, M, N, K, g.stream, epi));
+            qk_rope_commit(r);
+            g_rope_pre = rx;
+            g.qkv_rope_fused++;
+            return 0;
+        }
+    }
     if (gemm_split_ws(epi, M, N, K, err, errn)) return -1;
     // The next op normalizing this output for its own GEMM: the split's finishing pass
     // writes those rows too (one pass over the output instead of two).
@@ -1036,36 +1094,56 @@ int op_w4g_fused(Ctx& cx) {
     return 0;
 }
 
-int op_qk_rope_kv(Ctx& cx) {
-    char* err = cx.err; size_t errn = cx.errn;
-    const uint32_t n_tok = A(5), H = A(6), KVH = A(7), hd = A(8);
-    const float theta = f32_from_bits(A(11));
+int qk_rope_prep(const wt_blob* b, const wt_op* op, QkRope& r, char* err, size_t errn) {
+    const uint32_t* a = op->args;
+    const uint32_t n_tok = a[5], H = a[6], KVH = a[7], hd = a[8];
     if (hd != 128) return ERR("qk_rope_kv head_dim %u unsupported (128 only)", hd);
     if (!n_tok || !H || !KVH) return ERR("qk_rope_kv empty shape");
     if (H + KVH > 64) return ERR("qk_rope_kv supports at most 64 q + kv heads (got %u)", H + KVH);
-    const __half* qkv = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
-    const __half* qg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(9)));
-    const __half* kg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(10)));
-    if (!qkv || !qg || !kg) return ERR("qk_rope_kv ref fail");
+    r.qkv = reinterpret_cast<const __half*>(ref_ptr(b, a[0]));
+    r.qg = reinterpret_cast<const __half*>(ref_ptr(b, a[9]));
+    r.kg = reinterpret_cast<const __half*>(ref_ptr(b, a[10]));
+    if (!r.qkv || !r.qg || !r.kg) return ERR("qk_rope_kv ref fail");
     const uint64_t row = (uint64_t)(H + 2 * KVH) * hd;
-    const size_t xb = ref_bytes(cx.b, A(0));
+    const size_t xb = ref_bytes(b, a[0]);
     if (xb && xb < n_tok * row * 2u) return ERR("qk_rope_kv input smaller than n_tok rows");
-    const size_t qgb = ref_bytes(cx.b, A(9)), kgb = ref_bytes(cx.b, A(10));
+    const size_t qgb = ref_bytes(b, a[9]), kgb = ref_bytes(b, a[10]);
     if ((qgb && qgb < hd * 2u) || (kgb && kgb < hd * 2u)) return ERR("qk_rope_kv gamma shorter than head_dim");
-    State* s = state_kv(A(4), KVH * hd, err, errn);
-    if (!s) return -1;
-    const uint32_t si = A(4) & 0x1FFFu;
-    if ((uint64_t)s->count + n_tok > s->nslots)
-        return ERR("qk_rope_kv state %u count=%u + %u > nslots=%u", si, s->count, n_tok, s->nslots);
-    __half* q_out = reinterpret_cast<__half*>(temp_get(A(1), n_tok * H * hd * 2u));
-    __half* k_out = A(2) == WT_REF_NONE ? nullptr : reinterpret_cast<__half*>(temp_get(A(2), n_tok * KVH * hd * 2u));
-    __half* v_out = A(3) == WT_REF_NONE ? nullptr : reinterpret_cast<__half*>(temp_get(A(3), n_tok * KVH * hd * 2u));
-    if (!q_out || (A(2) != WT_REF_NONE && !k_out) || (A(3) != WT_REF_NONE && !v_out)) return ERR("qk_rope_kv out alloc");
-    const uint32_t pos = s->count;
-    s->count += n_tok;
-    for (uint32_t t = 0; t < n_tok; ++t) kv_mark(*s, pos + t);
-    CHECK_LAUNCH(launch_qk_rope_kv(qkv, n_tok, H, KVH, qg, kg, theta, q_out, k_out, v_out, s->dev, s->slot_bytes,
-                                   s->nslots, g.counters_dev + si, g.stream, g.counters_dev + WT_MAX_STATES + si));
+    r.s = state_kv(a[4], KVH * hd, err, errn);
+    if (!r.s) return -1;
+    r.si = a[4] & 0x1FFFu;
+    if ((uint64_t)r.s->count + n_tok > r.s->nslots)
+        return ERR("qk_rope_kv state %u count=%u + %u > nslots=%u", r.si, r.s->count, n_tok, r.s->nslots);
+    r.q_out = reinterpret_cast<__half*>(temp_get(a[1], n_tok * H * hd * 2u));
+    r.k_out = a[2] == WT_REF_NONE ? nullptr : reinterpret_cast<__half*>(temp_get(a[2], n_tok * KVH * hd * 2u));
+    r.v_out = a[3] == WT_REF_NONE ? nullptr : reinterpret_cast<__half*>(temp_get(a[3], n_tok * KVH * hd * 2u));
+    if (!r.q_out || (a[2] != WT_REF_NONE && !r.k_out) || (a[3] != WT_REF_NONE && !r.v_out))
+        return ERR("qk_rope_kv out alloc");
+    r.theta = f32_from_bits(a[11]);
+    r.n_tok = n_tok;
+    r.H = H;
+    r.KVH = KVH;
+    return 0;
+}
+// Host side of the op once its device work is queued: the positions it appends.
+void qk_rope_commit(const QkRope& r) {
+    const uint32_t pos = r.s->count;
+    r.s->count += r.n_tok;
+    for (uint32_t t = 0; t < r.n_tok; ++t) kv_mark(*r.s, pos + t);
+}
+
+int op_qk_rope_kv(Ctx& cx) {
+    char* err = cx.err; size_t errn = cx.errn;
+    if (g_rope_pre == cx.op) {   // the previous op's GEMM epilogue did it (op_w4g_fused)
+        g_rope_pre = nullptr;
+        return 0;
+    }
+    QkRope r;
+    if (qk_rope_prep(cx.b, cx.op, r, err, errn)) return -1;
+    CHECK_LAUNCH(launch_qk_rope_kv(r.qkv, r.n_tok, r.H, r.KVH, r.qg, r.kg, r.theta, r.q_out, r.k_out, r.v_out,
+                                   r.s->dev, r.s->slot_bytes, r.s->nslots, g.counters_dev + r.si, g.stream,
+                                   g.counters_dev + WT_MAX_STATES + r.si));
+    qk_rope_commit(r);
     return 0;
 }
 
@@ -1965,6 +2043,7 @@ int run_fused_attn(const wt_blob* b, const AttnChain& c, char* err, size_t errn)
 int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* err, size_t errn) {
     const wt_op* op = &b->ops[i];
     if (g_prenorm.op != op) g_prenorm = PreNorm{};   // only ever for the very next op
+    if (g_rope_pre != op) g_rope_pre = nullptr;
     if (g_fplan) {
         if (g_skip_until != kNone && i <= g_skip_until) return 0;   // part of a chain that ran fused
         const int32_t ci = g_fplan->head_of[i];
@@ -2046,6 +2125,7 @@ extern "C" {
 int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, uint32_t* engine_m,
                       int64_t* op_us, char* err, size_t errn) {
     g_prenorm = PreNorm{};
+    g_rope_pre = nullptr;
     char dummy_err[8];
     if (!err || !errn) { err = dummy_err; errn = sizeof dummy_err; }
     uint32_t dummy_m = 0;
@@ -2389,6 +2469,9 @@ void wt_exec_shutdown(void) {
     if (g.split_buf) dev_free(g.split_buf);
     g.split_buf = nullptr;
     g.split_cap = 0;
+    if (g.rope_buf) dev_free(g.rope_buf);
+    g.rope_buf = nullptr;
+    g.rope_cap = 0;
     if (g.w4_out) dev_free(g.w4_out);
     g.w4_out = nullptr;
     g.w4_out_cap = 0;
@@ -2465,6 +2548,8 @@ void wt_exec_fusion_stats(uint64_t* chains_found, uint64_t* fused_runs) {
     if (chains_found) *chains_found = g.chains_found;
     if (fused_runs) *fused_runs = g.fused_runs;
 }
+
+uint64_t wt_exec_qkv_rope_fused(void) { return g.qkv_rope_fused; }
 
 void wt_exec_set_hook(const char* spec) { g.hook = spec; }
 

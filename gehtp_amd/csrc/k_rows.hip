@@ -607,40 +607,10 @@ __global__ __launch_bounds__(256) void qk_rope_kv_rows_kernel(QkRopeKvArgs A, ui
         const uint32_t hr = grp + 32 * it, hc = min(hr, nrows - 1), tk = hc / nh, r = hc - tk * nh;
         const bool is_q = r < A.H;
         const u32x4 gl = is_q ? qgl : kgl, gh = is_q ? qgh : kgh;
-        float x[16];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            x[2 * k] = dev::bits_f((uint16_t)(xl[it][k] & 0xFFFFu));
-            x[2 * k + 1] = dev::bits_f((uint16_t)(xl[it][k] >> 16));
-            x[8 + 2 * k] = dev::bits_f((uint16_t)(xh[it][k] & 0xFFFFu));
-            x[8 + 2 * k + 1] = dev::bits_f((uint16_t)(xh[it][k] >> 16));
-        }
-        double ss = 0.0;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) ss += (double)x[k] * (double)x[k];
-        ss += dev::dpp<dev::kDppQuadSwap1>(ss);
-        ss += dev::dpp<dev::kDppQuadSwap2>(ss);
-        ss += dev::dpp<dev::kDppRowHalfMirror>(ss);
-        const float rms = (float)sqrt(ss / 128.0 + 1e-6);
-        const float y = __fdiv_rn(1.0f, rms);
-        uint32_t hw[8];   // normalized halves as f16 pairs: [0,4) low half, [4,8) high half
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t gw = k < 4 ? gl[k] : gh[k - 4];
-            const float h0 = __fadd_rn(__fmul_rn(dev::div_markstein(x[2 * k], rms, y), dev::bits_f((uint16_t)(gw & 0xFFFFu))), 0.0f);
-            const float h1 = __fadd_rn(__fmul_rn(dev::div_markstein(x[2 * k + 1], rms, y), dev::bits_f((uint16_t)(gw >> 16))), 0.0f);
-            hw[k] = h22u(h2v{(_Float16)h0, (_Float16)h1});
-        }
         const u32x4 cw = *reinterpret_cast<const u32x4*>(&s_cos[tk][8 * g]);
         const u32x4 sw = *reinterpret_cast<const u32x4*>(&s_sin[tk][8 * g]);
         u32x4 yl, yh;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const h2v a = u2h2(hw[k]), b = u2h2(hw[4 + k]), c = u2h2(cw[k]), sn = u2h2(sw[k]);
-            const h2v ac = a * c, bs = b * sn, bc = b * c, as = a * sn;
-            yl[k] = h22u(ac - bs);
-            yh[k] = h22u(bc + as);
-        }
+        dev::qk_row8_norm_rope(xl[it], xh[it], gl, gh, cw, sw, yl, yh);
         if (hr >= nrows) continue;
         const uint32_t tok = t0 + tk;
         if (is_q) {
@@ -680,6 +650,32 @@ __global__ __launch_bounds__(256) void qk_rope_kv_rows_kernel(QkRopeKvArgs A, ui
     }
 }
 constexpr uint32_t kQkRowsTok = 4;
+
+// RoPE table of one prefill call for the q|k|v GEMM's fused QK-norm/RoPE epilogue:
+// f16 cos and sin planes [n_tok][64] at positions *count + t (the entries the rows
+// kernel builds in LDS), the start position in hdr[0]; the last workgroup to finish
+// advances *count by n_tok, as the rows kernel does.
+__global__ __launch_bounds__(256) void rope_table_kernel(uint32_t* count, uint32_t* done, float theta,
+                                                         uint32_t n_tok, _Float16* cosp, _Float16* sinp,
+                                                         uint32_t* hdr) {
+    __shared__ uint32_t s_pos;
+    const uint32_t tid = threadIdx.x, e = blockIdx.x * 256 + tid;
+    if (tid == 0) s_pos = *count;
+    __syncthreads();
+    if (e < n_tok * 64) {
+        const uint32_t w = dev::rope_cs_bits(s_pos + (e >> 6), dev::rope_inv(e & 63, theta));
+        cosp[e] = __builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+        sinp[e] = __builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+    }
+    if (blockIdx.x == 0 && tid == 0) hdr[0] = s_pos;
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == gridDim.x - 1) {
+            *done = 0u;
+            *count = s_pos + n_tok;
+        }
+    }
+}
 
 // KV gather with GQA expansion (oplist_exec.c:2183-2231): kT[h][d][p], v[h][p][d].
 __global__ void kv_gather_kernel(const uint8_t* __restrict__ ring, uint32_t slot_bytes,
@@ -895,6 +891,15 @@ hipError_t launch_qk_rope_kv(const __half* qkv, uint32_t n_tok, uint32_t H, uint
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || n_tok == 1 || (rows && done_dev)) return e;
     hipLaunchKernelGGL(counter_add_kernel, dim3(1), dim3(1), 0, st, count_dev, n_tok);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_table(uint32_t* count_dev, uint32_t* done_dev, float theta, uint32_t n_tok, void* table,
+                             hipStream_t st) {
+    if (!n_tok || !count_dev || !done_dev || !table || ((uintptr_t)table & 15u)) return hipErrorInvalidValue;
+    _Float16* cosp = static_cast<_Float16*>(table);
+    hipLaunchKernelGGL(rope_table_kernel, dim3((n_tok * 64 + 255) / 256), dim3(256), 0, st, count_dev, done_dev, theta,
+                       n_tok, cosp, cosp + (size_t)n_tok * 64, reinterpret_cast<uint32_t*>(cosp + (size_t)n_tok * 128));
     return hipGetLastError();
 }
 

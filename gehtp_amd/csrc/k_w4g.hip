@@ -12,6 +12,7 @@
 // (k3,k7); activations are staged in the same pair order so each pair feeds one
 // v_dot2_f32_f16 (fp32 accumulate).
 #include "dev_reduce.h"
+#include "dev_rope.h"
 #include "kernels.h"
 
 #include <algorithm>
@@ -530,17 +531,87 @@ __device__ __forceinline__ void w4g_plain_tiles(const f16x_t (&acc)[WI][WJ], uin
         }
 }
 
+// Epilogue of the q|k|v GEMM that also performs OP_QK_ROPE_KV_F16 (W4gRope): the
+// workgroup's 128 x 128 tile is head n0 / 128 of tokens m0 .. m0 + 127. Its fp16 outputs
+// are staged in LDS (the A tiles' space) so that each 8-lane group holds one token's head
+// row as the rows kernel's groups do, then finished with that kernel's arithmetic
+// (dev::qk_row8_norm_rope, RoPE entries from the call's table): q heads to q_out, k
+// heads (normalized, rotated) and v heads (as they are) to the ring slot of the token's
+// position and to k_out / v_out; y is written as well, 16 bytes per store.
+constexpr uint32_t kRopeSR = 128 + 8;   // staging row stride (halves)
+__device__ __forceinline__ void w4g_rope_tile(const f16x_t (&acc)[WI][1], uint32_t tid, uint32_t m0, uint32_t n0,
+                                              uint32_t M, __half* __restrict__ y, uint32_t ldy, const W4gRope& R,
+                                              _Float16* __restrict__ st) {
+    const uint32_t lane = tid & 63, wave = tid >> 6, half = lane >> 5, l32 = lane & 31;
+    __syncthreads();   // every wave's last MFMAs have read the A tiles
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            st[(i * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) * kRopeSR + 32 * wave + l32] = (_Float16)acc[i][0][r];
+    const uint32_t grp = tid >> 3, g = tid & 7, hh = n0 >> 7;
+    const bool is_q = hh < R.H, is_k = !is_q && hh < R.H + R.KVH;
+    u32x4 gl = {0u, 0u, 0u, 0u}, gh = {0u, 0u, 0u, 0u};
+    if (is_q || is_k) {
+        const __half* gm = is_q ? R.q_gamma : R.k_gamma;
+        gl = *reinterpret_cast<const u32x4*>(gm + 8 * g);
+        gh = *reinterpret_cast<const u32x4*>(gm + 64 + 8 * g);
+    }
+    const _Float16* cosp = static_cast<const _Float16*>(R.table);
+    const _Float16* sinp = cosp + (size_t)M * 64;
+    const uint32_t pos0 = *reinterpret_cast<const uint32_t*>(cosp + (size_t)M * 128);
+    __syncthreads();
+#pragma unroll
+    for (uint32_t it = 0; it < 4; ++it) {
+        const uint32_t r = grp + 32 * it, tok = m0 + r;
+        if (tok >= M) break;   // the same for the 8 lanes of a group
+        const u32x4 xl = *reinterpret_cast<const u32x4*>(&st[r * kRopeSR + 8 * g]);
+        const u32x4 xh = *reinterpret_cast<const u32x4*>(&st[r * kRopeSR + 64 + 8 * g]);
+        __half* yr = y + (size_t)tok * ldy + n0;
+        *reinterpret_cast<u32x4*>(yr + 8 * g) = xl;
+        *reinterpret_cast<u32x4*>(yr + 64 + 8 * g) = xh;
+        __half* face = reinterpret_cast<__half*>(R.ring + (size_t)((pos0 + tok) % R.nslots) * R.slot_bytes);
+        __half *d0, *d1;   // ring / q_out row, k_out / v_out row
+        u32x4 ol = xl, oh = xh;
+        if (is_q || is_k) {
+            const u32x4 cw = *reinterpret_cast<const u32x4*>(cosp + (size_t)tok * 64 + 8 * g);
+            const u32x4 sw = *reinterpret_cast<const u32x4*>(sinp + (size_t)tok * 64 + 8 * g);
+            dev::qk_row8_norm_rope(xl, xh, gl, gh, cw, sw, ol, oh);
+        }
+        if (is_q) {
+            d0 = R.q_out + ((size_t)tok * R.H + hh) * 128;
+            d1 = nullptr;
+        } else if (is_k) {
+            const uint32_t kh = hh - R.H;
+            d0 = face + kh * 128;
+            d1 = R.k_out ? R.k_out + ((size_t)tok * R.KVH + kh) * 128 : nullptr;
+        } else {
+            const uint32_t vh = hh - R.H - R.KVH;
+            d0 = face + (R.KVH + vh) * 128;
+            d1 = R.v_out ? R.v_out + ((size_t)tok * R.KVH + vh) * 128 : nullptr;
+        }
+        *reinterpret_cast<u32x4*>(d0 + 8 * g) = ol;
+        *reinterpret_cast<u32x4*>(d0 + 64 + 8 * g) = oh;
+        if (d1) {
+            *reinterpret_cast<u32x4*>(d1 + 8 * g) = ol;
+            *reinterpret_cast<u32x4*>(d1 + 64 + 8 * g) = oh;
+        }
+    }
+}
+
 __device__ __forceinline__ u32x4 pair_order16(u32x4 v) {   // k0..k7 -> (k0,k4)(k1,k5)(k2,k6)(k3,k7)
     return u32x4{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
                  __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
 }
 
+template <bool ROPE>
 __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
     const __half* __restrict__ a, uint32_t lda, const uint8_t* __restrict__ wq,
     const __half* __restrict__ ws, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
     uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu, uint32_t mtiles, uint32_t ntiles,
-    uint32_t split_steps, float* __restrict__ part) {
+    uint32_t split_steps, float* __restrict__ part, W4gRope rope) {
     constexpr int CA = GB_M * (GB_K / 8) / 256;   // 16-byte A chunks per thread per K step
+    static_assert(GB_N == 128 && GB_M * kRopeSR <= 2 * GB_M * GB_LDS, "rope staging tile");
     __shared__ __align__(16) _Float16 As[2][GB_M * GB_LDS];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Workgroup -> (m tile, n tile, K part): m fastest, K part slowest. With `part`,
@@ -642,6 +713,10 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
     if (kb < nsteps) mfma(0, 0);   // odd step count: the last step is in buffer / set 0
 
     // Accumulator layout (32x32): lane l, reg r -> col l%32, row 8*(r/4) + 4*(l/32) + r%4.
+    if constexpr (ROPE) {   // launched only for an unsplit plain q|k|v GEMM
+        w4g_rope_tile(acc, tid, m0, n0, M, y, ldy, rope, &As[0][0]);
+        return;
+    }
     if (!part && swiglu) {
         w4g_swiglu_tiles<WJ>(acc, lane, m0, n0 + wn * 32 * WJ, M, N, y, ldy, res, ldr);
         return;
@@ -1064,6 +1139,19 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
                            hipStream_t st, const W4gEpilogue& epi) {
     if (M == 0 || N == 0) return hipSuccess;
     if (epi.gamma || (epi.swiglu && (N & 1))) return hipErrorInvalidValue;
+    if (epi.rope) {   // the q|k|v GEMM of OP_QK_ROPE_KV_F16: 128 x 128 tiles (one head each), unsplit
+        const W4gRope& R = *epi.rope;
+        auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+        if (epi.swiglu || epi.res || !R.H || !R.KVH || N != (R.H + 2 * R.KVH) * 128u || ldy % 8 || !al16(y) ||
+            !al16(R.q_gamma) || !al16(R.k_gamma) || !al16(R.table) || !al16(R.q_out) || !al16(R.k_out) ||
+            !al16(R.v_out) || !al16(R.ring) || R.slot_bytes % 16 || !R.nslots ||
+            R.slot_bytes < R.KVH * 128u * 4u)
+            return hipErrorInvalidValue;
+        const uint32_t mt = (M + GB_M - 1) / GB_M, nt = N / GB_N;
+        hipLaunchKernelGGL(w4g_gemm_kernel<true>, dim3(mt * nt), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K,
+                           nullptr, 0u, 0, mt, nt, K / GB_K, nullptr, R);
+        return hipGetLastError();
+    }
     if (epi.swiglu) {
         const hipError_t te = silu_table_ready(st);
         if (te != hipSuccess) return te;
@@ -1084,8 +1172,8 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
             hipLaunchKernelGGL(w4g_gemm_wide_kernel, dim3(mt * ntw * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq,
                                ws, y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, ntw, per, pw);
         else
-            hipLaunchKernelGGL(w4g_gemm_kernel, dim3(mt * nt * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq, ws,
-                               y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, nt, per, pw);
+            hipLaunchKernelGGL(w4g_gemm_kernel<false>, dim3(mt * nt * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq, ws,
+                               y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, nt, per, pw, W4gRope{});
     };
     if (split) {
         gemm(epi.split_ws);

@@ -14,6 +14,18 @@ namespace gehtp {
 int device_cu_count();
 
 // ---- W4G (int4, group 64, fp16 scales) ----
+// Outputs of OP_QK_ROPE_KV_F16 for a q|k|v GEMM that performs that op in its epilogue.
+struct W4gRope {
+    uint32_t H = 0, KVH = 0;
+    const __half* q_gamma = nullptr;
+    const __half* k_gamma = nullptr;
+    const void* table = nullptr;   // launch_rope_table's output for this call (n_tok = M)
+    __half* q_out = nullptr;
+    __half* k_out = nullptr;
+    __half* v_out = nullptr;
+    uint8_t* ring = nullptr;
+    uint32_t slot_bytes = 0, nslots = 0;
+};
 // Optional fused parts of a W4A16 linear (OP_W4G_FUSED_F16), each reproducing the
 // runlist op it replaces with that op's roundings:
 //   gamma  RMSNorm of the input rows first (RMSNORM2_F16 with a zero bias; GEMV only —
@@ -36,6 +48,12 @@ struct W4gEpilogue {
     const __half* norm_gamma = nullptr;
     __half* norm_out = nullptr;
     bool* norm_done = nullptr;
+    // GEMM only: the q|k|v GEMM of OP_QK_ROPE_KV_F16 (N = (H + 2 KVH) * 128, plain
+    // epilogue): when set, its epilogue also performs that op — per-head RMSNorm + RoPE
+    // of the q and k heads at the positions of a table built by launch_rope_table (which
+    // advances the counter), k and v appended to the ring, q_out [M][H*128] and the
+    // optional k_out / v_out [M][KVH*128] written — with the rows kernel's arithmetic.
+    const W4gRope* rope = nullptr;
 };
 // y[m*ldy + n] = f16( sum_k x[m*ldx + k] * fp16(q[n,k] * s[n, k/64]) ), m < M, n < N,
 // each dequantized weight rounded to fp16 as the reference does, fp32 accumulation
@@ -116,6 +134,13 @@ hipError_t launch_qk_rope_kv(const __half* qkv, uint32_t n_tok, uint32_t H, uint
                              __half* k_out, __half* v_out, uint8_t* ring, uint32_t slot_bytes,
                              uint32_t nslots, uint32_t* count_dev, hipStream_t st,
                              uint32_t* done_dev = nullptr);
+// RoPE table of an n_tok-token call at the counter's position for the fused q|k|v GEMM
+// epilogue: f16 cos [n_tok][64], f16 sin [n_tok][64], then the start position (uint32);
+// w4g_rope_table_bytes(n_tok) bytes, 16-byte aligned. Advances *count_dev by n_tok
+// (done_dev: a zero counter of the state, left zero).
+inline size_t w4g_rope_table_bytes(uint32_t n_tok) { return (size_t)n_tok * 256 + 16; }
+hipError_t launch_rope_table(uint32_t* count_dev, uint32_t* done_dev, float theta, uint32_t n_tok, void* table,
+                             hipStream_t st);
 // kT [H][hd][pstride], v [H][pstride][hd]; positions >= n_kv of the pstride are zero.
 hipError_t launch_kv_gather(const uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
                             __half* kT, __half* vo, uint32_t n_kv, uint32_t pstride, uint32_t H,

@@ -132,6 +132,11 @@ void wt_exec_graph_stats(uint32_t* captures, uint32_t* replays);
  * chain's intermediate temps (they were not computed). */
 int  wt_exec_set_fusion(int on);
 void wt_exec_fusion_stats(uint64_t* chains_found, uint64_t* fused_runs);
+/* Extension, under the same switch: an OP_W4G_FUSED_F16 q|k|v GEMM (GEMM path, plain
+ * epilogue) followed in the same run by the OP_QK_ROPE_KV_F16 that reads its output
+ * performs that op in its epilogue (same bits; the GEMM's own output is written too);
+ * this counts such executions. */
+uint64_t wt_exec_qkv_rope_fused(void);
 
 /* W3 inspect report: one JSON line per call of emit (reference wt_w3.c). */
 void wt_w3_report(const char* blob_name, const uint8_t* buf, size_t size,

@@ -131,6 +131,61 @@ def test_split_k_finish_normalizes_next_op(engine, oracle, mode):
     assert np.array_equal(fused.view(np.uint16), alone.view(np.uint16))
 
 
+@pytest.mark.parametrize("M,H,KVH,runs", [(256, 16, 8, 3), (200, 32, 8, 2), (2048, 32, 8, 1)])
+def test_qkv_gemm_performs_rope_op(engine, oracle, M, H, KVH, runs):
+    """OP_W4G_FUSED_F16 (RMSNorm + q|k|v GEMM) followed by the OP_QK_ROPE_KV_F16 reading
+    its output: with fusion on, the GEMM's epilogue performs that op (after a table
+    kernel that fixes the positions and advances the counter). Over `runs` prefill calls
+    in a row (positions continuing, later calls replayed from a HIP graph) the q / k / v
+    outputs, the GEMM output, the ring read back by KV_GATHER and the positions are
+    bit-identical to the op-by-op runs; a ragged M leaves a partial token tile. The q
+    output also matches the oracle's RMSNorm + RoPE of the GEMM output."""
+    rng = np.random.default_rng(90 + M + H)
+    K, hd, theta = 1024, 128, 1e6
+    N, kv = (H + 2 * KVH) * hd, KVH * hd
+    max_pos = runs * M
+    _, wq, ws = w4g_weights(rng, N, K)
+    gam = rng.uniform(0.8, 1.2, K).astype(np.float16)
+    qg = rng.uniform(0.8, 1.2, hd).astype(np.float16)
+    kg = rng.uniform(0.8, 1.2, hd).astype(np.float16)
+    bb = BlobBuilder()
+    st = bb.add_state(max_pos * kv * 4)
+    xs = bb.add_input_slot(M * K * 2)
+    sq, ss = bb.add_slot(wq, count=N * K), bb.add_slot(ws)
+    sg, sqg, skg = bb.add_slot(gam), bb.add_slot(qg), bb.add_slot(kg)
+    t_qkv, t_q, t_k, t_v, t_kT, t_vo = (bb.temp() for _ in range(6))
+    bb.op(OP.W4G_FUSED_F16, bb.slot_ref(xs), bb.slot_ref(sq), bb.slot_ref(ss), t_qkv, M, K, N, bb.slot_ref(sg),
+          WT_REF_NONE, 0, 2)
+    bb.op(OP.QK_ROPE_KV_F16, t_qkv, t_q, t_k, t_v, st, M, H, KVH, hd, bb.slot_ref(sqg), bb.slot_ref(skg),
+          f32_bits(theta))
+    bb.op(OP.KV_GATHER_F16, st, t_kT, t_vo, WT_KV_POS_AUTO, H, KVH, hd)
+    pb = engine.parse(bb.build())
+    xs_in = [normal_f16(rng, M, K) for _ in range(runs)]
+    got = {}
+    for fusion in (False, True):
+        prev = engine.set_fusion(fusion)
+        try:
+            engine.state_reset()
+            n0 = engine.qkv_rope_fused()
+            res = []
+            for x in xs_in:
+                engine.run_io(pb, x.tobytes(), t_q, out_bytes=M * H * hd * 2)
+                res.append([engine.temp(t) for t in (t_qkv, t_q, t_k, t_v, t_kT, t_vo)])
+            assert engine.qkv_rope_fused() - n0 == (runs if fusion else 0)
+            got[fusion] = res
+        finally:
+            engine.set_fusion(prev)
+    names = ("qkv", "q", "k", "v", "kT", "v gathered")
+    for r in range(runs):
+        for name, a, b in zip(names, got[False][r], got[True][r]):
+            assert a == b, f"call {r}: {name} differs between the fused and the op-by-op run"
+    qkv0 = _h(got[True][0][0], (M, N))
+    qn = oracle.rmsnorm2(np.ascontiguousarray(qkv0[:, :H * hd]).reshape(-1, hd), qg, np.zeros(hd, np.float16))
+    q_ref = oracle.rope(qn.reshape(M, -1), H, hd, 0, theta)
+    d = np.abs(_h(got[True][0][1]).view(np.int16).astype(np.int32) - q_ref.reshape(-1).view(np.int16).astype(np.int32))
+    assert d.max() <= 1 and (d == 0).mean() > 0.999   # RMSNorm's double sum order may flip 1 ulp
+
+
 def test_rmsnorm_then_w4g_gemm_runlist(engine, oracle):
     """Config 2 as a two-op runlist: RMSNORM2_F16 -> MATMUL_W4G_F16 (M=512)."""
     rng = np.random.default_rng(2)
