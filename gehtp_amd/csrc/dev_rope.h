@@ -48,7 +48,9 @@ __device__ __forceinline__ double rope_inv(uint32_t i, float theta) {
 }
 // The pair as f16 bits: cos in bits 0-15, sin in bits 16-31.
 __device__ __forceinline__ uint32_t rope_cs_bits(uint32_t pos, double inv) {
-    return (uint32_t)f64_to_f16_bits(cos((double)pos * inv)) | ((uint32_t)f64_to_f16_bits(sin((double)pos * inv)) << 16);
+    double s, c;
+    sincos((double)pos * inv, &s, &c);   // one argument reduction, the bits of cos() and sin()
+    return (uint32_t)f64_to_f16_bits(c) | ((uint32_t)f64_to_f16_bits(s) << 16);
 }
 __device__ __forceinline__ void rope_cs_inv(uint32_t pos, double inv, float& c, float& s) {
     const uint32_t w = rope_cs_bits(pos, inv);

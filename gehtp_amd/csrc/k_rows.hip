@@ -659,11 +659,13 @@ __global__ __launch_bounds__(256) void rope_table_kernel(uint32_t* count, uint32
                                                          uint32_t n_tok, _Float16* cosp, _Float16* sinp,
                                                          uint32_t* hdr) {
     __shared__ uint32_t s_pos;
+    __shared__ double s_inv[64];   // the 64 frequencies, once per workgroup
     const uint32_t tid = threadIdx.x, e = blockIdx.x * 256 + tid;
     if (tid == 0) s_pos = *count;
+    if (tid < 64) s_inv[tid] = dev::rope_inv(tid, theta);
     __syncthreads();
     if (e < n_tok * 64) {
-        const uint32_t w = dev::rope_cs_bits(s_pos + (e >> 6), dev::rope_inv(e & 63, theta));
+        const uint32_t w = dev::rope_cs_bits(s_pos + (e >> 6), s_inv[e & 63]);
         cosp[e] = __builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
         sinp[e] = __builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
     }
