@@ -131,15 +131,17 @@ def test_split_k_finish_normalizes_next_op(engine, oracle, mode):
     assert np.array_equal(fused.view(np.uint16), alone.view(np.uint16))
 
 
-@pytest.mark.parametrize("M,H,KVH,runs", [(256, 16, 8, 3), (200, 32, 8, 2), (2048, 32, 8, 1)])
-def test_qkv_gemm_performs_rope_op(engine, oracle, M, H, KVH, runs):
+@pytest.mark.parametrize("M,H,KVH,runs,kv_outs", [(256, 16, 8, 3, True), (200, 32, 8, 2, True),
+                                                  (2048, 32, 8, 1, True), (320, 16, 4, 2, False)])
+def test_qkv_gemm_performs_rope_op(engine, oracle, M, H, KVH, runs, kv_outs):
     """OP_W4G_FUSED_F16 (RMSNorm + q|k|v GEMM) followed by the OP_QK_ROPE_KV_F16 reading
     its output: with fusion on, the GEMM's epilogue performs that op (after a table
     kernel that fixes the positions and advances the counter). Over `runs` prefill calls
     in a row (positions continuing, later calls replayed from a HIP graph) the q / k / v
     outputs, the GEMM output, the ring read back by KV_GATHER and the positions are
     bit-identical to the op-by-op runs; a ragged M leaves a partial token tile. The q
-    output also matches the oracle's RMSNorm + RoPE of the GEMM output."""
+    output also matches the oracle's RMSNorm + RoPE of the GEMM output. Without k / v
+    outputs the ring alone receives them."""
     rng = np.random.default_rng(90 + M + H)
     K, hd, theta = 1024, 128, 1e6
     N, kv = (H + 2 * KVH) * hd, KVH * hd
@@ -156,8 +158,8 @@ def test_qkv_gemm_performs_rope_op(engine, oracle, M, H, KVH, runs):
     t_qkv, t_q, t_k, t_v, t_kT, t_vo = (bb.temp() for _ in range(6))
     bb.op(OP.W4G_FUSED_F16, bb.slot_ref(xs), bb.slot_ref(sq), bb.slot_ref(ss), t_qkv, M, K, N, bb.slot_ref(sg),
           WT_REF_NONE, 0, 2)
-    bb.op(OP.QK_ROPE_KV_F16, t_qkv, t_q, t_k, t_v, st, M, H, KVH, hd, bb.slot_ref(sqg), bb.slot_ref(skg),
-          f32_bits(theta))
+    bb.op(OP.QK_ROPE_KV_F16, t_qkv, t_q, t_k if kv_outs else WT_REF_NONE, t_v if kv_outs else WT_REF_NONE, st, M,
+          H, KVH, hd, bb.slot_ref(sqg), bb.slot_ref(skg), f32_bits(theta))
     bb.op(OP.KV_GATHER_F16, st, t_kT, t_vo, WT_KV_POS_AUTO, H, KVH, hd)
     pb = engine.parse(bb.build())
     xs_in = [normal_f16(rng, M, K) for _ in range(runs)]
@@ -170,12 +172,13 @@ def test_qkv_gemm_performs_rope_op(engine, oracle, M, H, KVH, runs):
             res = []
             for x in xs_in:
                 engine.run_io(pb, x.tobytes(), t_q, out_bytes=M * H * hd * 2)
-                res.append([engine.temp(t) for t in (t_qkv, t_q, t_k, t_v, t_kT, t_vo)])
+                temps = (t_qkv, t_q, t_k, t_v, t_kT, t_vo) if kv_outs else (t_qkv, t_q, t_kT, t_vo)
+                res.append([engine.temp(t) for t in temps])
             assert engine.qkv_rope_fused() - n0 == (runs if fusion else 0)
             got[fusion] = res
         finally:
             engine.set_fusion(prev)
-    names = ("qkv", "q", "k", "v", "kT", "v gathered")
+    names = ("qkv", "q", "k", "v", "kT", "v gathered") if kv_outs else ("qkv", "q", "kT", "v gathered")
     for r in range(runs):
         for name, a, b in zip(names, got[False][r], got[True][r]):
             assert a == b, f"call {r}: {name} differs between the fused and the op-by-op run"
