@@ -71,6 +71,52 @@ __global__ __launch_bounds__(256) void gemv_nk_kernel(const __half* __restrict__
     }
 }
 
+// The same GEMV for M = 1 when each lane owns NC = K / 512 16-byte chunks of a row (the
+// lm_head: K = 2560, NC = 5): the activation chunks are requested first, then every
+// weight chunk of the wave's 4 rows, and only then x is staged in LDS and the rows are
+// computed, so a wave waits on one memory round trip instead of one per row. Each lane
+// accumulates chunks lane, lane + 64, ... in the order of gemv_nk_kernel and the row sum
+// is the same wave reduction: the same bits.
+template <int NC>
+__global__ __launch_bounds__(256) void gemv_nk_pre_kernel(const __half* __restrict__ a,
+                                                          const __half* __restrict__ w,
+                                                          __half* __restrict__ y, uint32_t K,
+                                                          uint32_t N_full, uint32_t n0, uint32_t N) {
+    constexpr uint32_t kc = 64 * NC, XC = (kc + 255) / 256;
+    extern __shared__ u32x4 xs[];   // [K/8]
+    const uint32_t bb = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const u32x4* ab = reinterpret_cast<const u32x4*>(a + (size_t)bb * K);
+    const __half* wb = w + (size_t)bb * N_full * K;
+    __half* yb = y + (size_t)bb * N_full;
+    u32x4 xr[XC];
+#pragma unroll
+    for (uint32_t i = 0; i < XC; ++i) xr[i] = ab[min(tid + 256 * i, kc - 1)];
+    const uint32_t nb = blockIdx.x * 16 + wave * 4;
+    u32x4 wv[4][NC];
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {
+        const u32x4* wr = reinterpret_cast<const u32x4*>(wb + (size_t)(n0 + min(nb + r, N - 1)) * K);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) wv[r][j] = __builtin_nontemporal_load(&wr[lane + 64 * j]);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < XC; ++i)
+        if (tid + 256 * i < kc) xs[tid + 256 * i] = xr[i];
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const u32x4 xv = xs[lane + 64 * j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_fdot2(as_h2(wv[r][j][e]), as_h2(xv[e]), acc, false);
+        }
+        const float sum = wave_sum(acc);
+        if (lane == 0 && nb + r < N) yb[n0 + nb + r] = __float2half(sum);
+    }
+}
+
 // --- GEMV, w stored [K][N_full] --------------------------------------------------
 __global__ __launch_bounds__(256) void gemv_kn_kernel(const __half* __restrict__ a,
                                                       const __half* __restrict__ w,
@@ -172,6 +218,19 @@ hipError_t launch_matmul_f16(const __half* a, const __half* w, __half* y, uint32
     if (M <= 4 && t1 && !t0 && aligned && (size_t)M * K * 2 <= 65536) {
         const size_t lds = (size_t)M * K * 2;
         dim3 grid((N + 15) / 16, Bn);
+        if (M == 1 && K % 512 == 0 && K / 512 <= 8) {
+            switch (K / 512) {
+            case 1: hipLaunchKernelGGL(gemv_nk_pre_kernel<1>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N); break;
+            case 2: hipLaunchKernelGGL(gemv_nk_pre_kernel<2>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N); break;
+            case 3: hipLaunchKernelGGL(gemv_nk_pre_kernel<3>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N); break;
+            case 4: hipLaunchKernelGGL(gemv_nk_pre_kernel<4>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N); break;
+            case 5: hipLaunchKernelGGL(gemv_nk_pre_kernel<5>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N); break;
+            case 6: hipLaunchKernelGGL(gemv_nk_pre_kernel<6>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N); break;
+            case 7: hipLaunchKernelGGL(gemv_nk_pre_kernel<7>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N); break;
+            default: hipLaunchKernelGGL(gemv_nk_pre_kernel<8>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N); break;
+            }
+            return hipGetLastError();
+        }
         switch (M) {
         case 1: hipLaunchKernelGGL(gemv_nk_kernel<1>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N, M); break;
         case 2: hipLaunchKernelGGL(gemv_nk_kernel<2>, grid, dim3(256), lds, st, a, w, y, K, N_full, n0, N, M); break;

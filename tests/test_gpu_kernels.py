@@ -301,6 +301,31 @@ def test_matmul_f16_flags(lib, oracle, torch_dev):
     assert_close(got[:, 64:128], ref[:, 64:128], max_abs=3e-2, what="split")
 
 
+@pytest.mark.parametrize("K,N,n0", [(2560, 4099, 0), (1024, 3000, 0), (4096, 777, 0), (512, 96, 32)])
+def test_matmul_f16_gemv_m1_prefetch_form(lib, oracle, torch_dev, K, N, n0):
+    """M = 1, w stored [N, K], K a multiple of 512 (the lm_head): the GEMV form that
+    requests all of a wave's weight rows before computing. Its output equals row 0 of the
+    M = 2 form (the same per-lane order and wave reduction) bit for bit, and the oracle
+    within fp16 tolerance; with a SPLIT window only columns [n0, n0 + N) are written."""
+    import torch
+    rng = np.random.default_rng(K + N)
+    Nf = n0 + N + (16 if n0 else 0)
+    a = normal_f16(rng, K)
+    w = normal_f16(rng, Nf * K) * np.float16(0.25)
+    y1 = torch.zeros(Nf, dtype=torch.float16, device=torch_dev)
+    y2 = torch.zeros(2 * Nf, dtype=torch.float16, device=torch_dev)
+    ad, wd = to_dev(a, torch_dev), to_dev(np.concatenate([a, a]), torch_dev)
+    wdev = to_dev(w, torch_dev)
+    assert lib.gehtp_matmul_f16(ptr(ad), ptr(wdev), ptr(y1), 1, K, Nf, n0, N, 2, stream_ptr()) == 0
+    assert lib.gehtp_matmul_f16(ptr(wd), ptr(wdev), ptr(y2), 2, K, Nf, n0, N, 2, stream_ptr()) == 0
+    _sync()
+    got, two = from_dev(y1), from_dev(y2).reshape(2, Nf)
+    assert np.array_equal(got.view(np.uint16), two[0].view(np.uint16))
+    assert np.all(got[:n0] == 0) and np.all(got[n0 + N:] == 0)
+    ref = oracle.matmul_f16(a, w, 1, K, Nf, n0, N, 2)
+    assert_close(got[n0:n0 + N], ref[n0:n0 + N], max_abs=3e-2, what=f"gemv m1 {K}x{N}")
+
+
 # ---------------------------------------------------------------- attention --
 SCALE = float(np.float16(1.0 / math.sqrt(128)))
 
