@@ -430,6 +430,35 @@ def test_w4g_fused_gemv(lib, oracle, torch_dev, mode, use_norm, use_res):
     assert_close(from_dev(y), ref, what=f"w4g_fused mode={mode} norm={use_norm} res={use_res}")
 
 
+@pytest.mark.parametrize("M,N,use_res", [(1, 40, True), (1, 100, False), (2, 702, True), (1, 30000, False)])
+def test_w4g_fused_gemv_swiglu_odd_rows(lib, oracle, torch_dev, M, N, use_res):
+    """SwiGLU GEMV at K = 704 (22 threads per row, 23 rows per pass of a 512-thread
+    workgroup): a gate/up pair must not straddle workgroups, so the launcher makes each
+    workgroup's row count even (two passes instead of one when 46 <= N: N = 100, 702; 22
+    rows per pass when N < 46: N = 40; one pass fewer when the pass count is odd: N =
+    30000, three passes -> two), and no workgroup may span more than N rows (the last one
+    is moved back to end at row N). Against the oracle's MATMUL_W4G -> silu * up (-> ADD)."""
+    import torch
+    rng = np.random.default_rng(7 * N + M)
+    K = 704
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, M, K)
+    gamma = rng.uniform(0.8, 1.2, K).astype(np.float16)
+    n_out = N // 2
+    res = normal_f16(rng, M, n_out)
+    y = torch.empty((M, n_out), dtype=torch.float16, device=torch_dev)
+    rc = lib.gehtp_w4g_fused(ptr(to_dev(x, torch_dev)), K, ptr(to_dev(wq, torch_dev)), ptr(to_dev(ws, torch_dev)),
+                             ptr(y), n_out, M, N, K, ptr(to_dev(gamma, torch_dev)),
+                             ptr(to_dev(res, torch_dev)) if use_res else None, n_out, 1, stream_ptr())
+    assert rc == 0
+    _sync()
+    acc = oracle.matmul_w4g(oracle.rmsnorm2(x, gamma, np.zeros(K, np.float16)), wq, ws, threads=8)
+    ref = oracle.binary(oracle.unary(np.ascontiguousarray(acc[:, 0::2]), 12), np.ascontiguousarray(acc[:, 1::2]), 2)
+    if use_res:
+        ref = oracle.binary(ref, res, 0)
+    assert_close(from_dev(y), ref, what=f"swiglu gemv K=704 M={M} N={N}")
+
+
 def test_w4g_fused_gemm_epilogues(lib, oracle, torch_dev):
     """The GEMM path (M > 4) applies the same SwiGLU and residual epilogues."""
     import torch
