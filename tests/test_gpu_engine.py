@@ -189,6 +189,36 @@ def test_qkv_gemm_performs_rope_op(engine, oracle, M, H, KVH, runs, kv_outs):
     assert d.max() <= 1 and (d == 0).mean() > 0.999   # RMSNorm's double sum order may flip 1 ulp
 
 
+def test_qkv_gemm_rope_op_error_keeps_its_index(engine):
+    """A q|k|v GEMM + OP_QK_ROPE_KV_F16 pair whose state cannot take the call (256 tokens
+    into 64 slots) is not fused: the GEMM runs alone and the second op fails with its
+    own 1-based index and the reference's message."""
+    rng = np.random.default_rng(97)
+    M, H, KVH, K, hd = 256, 16, 8, 1024, 128
+    N = (H + 2 * KVH) * hd
+    _, wq, ws = w4g_weights(rng, N, K)
+    bb = BlobBuilder()
+    st = bb.add_state(64 * KVH * hd * 4)
+    xs = bb.add_input_slot(M * K * 2)
+    sq, ss = bb.add_slot(wq, count=N * K), bb.add_slot(ws)
+    sqg = bb.add_slot(rng.uniform(0.8, 1.2, hd).astype(np.float16))
+    t_qkv, t_q = bb.temp(), bb.temp()
+    bb.op(OP.W4G_FUSED_F16, bb.slot_ref(xs), bb.slot_ref(sq), bb.slot_ref(ss), t_qkv, M, K, N, WT_REF_NONE,
+          WT_REF_NONE, 0, 2)
+    bb.op(OP.QK_ROPE_KV_F16, t_qkv, t_q, WT_REF_NONE, WT_REF_NONE, st, M, H, KVH, hd, bb.slot_ref(sqg),
+          bb.slot_ref(sqg), f32_bits(1e6))
+    pb = engine.parse(bb.build())
+    prev = engine.set_fusion(True)
+    try:
+        n0 = engine.qkv_rope_fused()
+        with pytest.raises(WtExecError) as ei:
+            engine.run_io(pb, normal_f16(rng, M, K).tobytes(), t_q)
+        assert ei.value.rc == 2 and "nslots" in str(ei.value)
+        assert engine.qkv_rope_fused() == n0
+    finally:
+        engine.set_fusion(prev)
+
+
 def test_rmsnorm_then_w4g_gemm_runlist(engine, oracle):
     """Config 2 as a two-op runlist: RMSNORM2_F16 -> MATMUL_W4G_F16 (M=512)."""
     rng = np.random.default_rng(2)
