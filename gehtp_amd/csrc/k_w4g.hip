@@ -60,9 +60,9 @@ __device__ __forceinline__ void dequant_word(uint32_t w, h2_t s2, h2_t out[4]) {
 // A thread's activation slice stays in registers (pair order) for the whole kernel,
 // so the inner loop is global loads + dequant + v_dot2 with no LDS traffic. With up to
 // 4 passes all weight loads are issued up front and each pass is computed when its own
-// load lands; with more, loads for the next 4 passes are in flight while the current 4
-// are computed. Pass partials go to LDS and teams of 16, 32 or 64 lanes sum each row
-// before the epilogue.
+// load lands; with more, the passes run in batches (of 4, or 5 for 10 passes) with the
+// next batch's loads in flight while the current one is computed. Pass partials go to
+// LDS and teams of 16, 32 or 64 lanes sum each row before the epilogue.
 struct GemvArgs {
     const __half* x;
     uint32_t ldx;
