@@ -469,15 +469,15 @@ __device__ __forceinline__ void w4g_store_swiglu(__half* __restrict__ y, uint32_
 // q+1. All silu
 // lookups are issued before any store (a store through y could alias the table for the
 // compiler, which would otherwise wait for each store before the next lookup).
-template <int WJ>
-__device__ __forceinline__ void w4g_swiglu_tiles(f16x_t (&acc)[WI][WJ], uint32_t lane, uint32_t m0, uint32_t col0,
+template <int WI_, int WJ>
+__device__ __forceinline__ void w4g_swiglu_tiles(f16x_t (&acc)[WI_][WJ], uint32_t lane, uint32_t m0, uint32_t col0,
                                                  uint32_t M, uint32_t N, __half* __restrict__ y, uint32_t ldy,
                                                  const __half* __restrict__ res, uint32_t ldr) {
     const bool odd = lane & 1;
     const uint32_t half = lane >> 5, l32 = lane & 31;
-    uint16_t tb[WI][WJ][8];
+    uint16_t tb[WI_][WJ][8];
 #pragma unroll
-    for (int i = 0; i < WI; ++i)
+    for (int i = 0; i < WI_; ++i)
 #pragma unroll
         for (int j = 0; j < WJ; ++j)
 #pragma unroll
@@ -490,7 +490,7 @@ __device__ __forceinline__ void w4g_swiglu_tiles(f16x_t (&acc)[WI][WJ], uint32_t
                 tb[i][j][r / 2] = g_silu_tab[f2hb(gate)];
             }
 #pragma unroll
-    for (int i = 0; i < WI; ++i)
+    for (int i = 0; i < WI_; ++i)
 #pragma unroll
         for (int j = 0; j < WJ; ++j) {
             const uint32_t col = col0 + j * 32 + l32;
@@ -510,14 +510,14 @@ __device__ __forceinline__ void w4g_swiglu_tiles(f16x_t (&acc)[WI][WJ], uint32_t
 // Plain epilogue of a wave's WI x WJ accumulator tiles: fp16 outputs (plus the residual)
 // or, with `part`, fp32 split-K partials, one value per store (a lane-pair exchange that
 // stores two adjacent columns at once measured 3-5 % slower on the 4B shapes).
-template <int WJ>
-__device__ __forceinline__ void w4g_plain_tiles(const f16x_t (&acc)[WI][WJ], uint32_t lane, uint32_t m0,
+template <int WI_, int WJ>
+__device__ __forceinline__ void w4g_plain_tiles(const f16x_t (&acc)[WI_][WJ], uint32_t lane, uint32_t m0,
                                                 uint32_t col0, uint32_t M, uint32_t N, __half* __restrict__ y,
                                                 uint32_t ldy, const __half* __restrict__ res, uint32_t ldr,
                                                 float* __restrict__ part, uint32_t split) {
     const uint32_t half = lane >> 5, l32 = lane & 31;
 #pragma unroll
-    for (int i = 0; i < WI; ++i)
+    for (int i = 0; i < WI_; ++i)
 #pragma unroll
         for (int j = 0; j < WJ; ++j) {
             const uint32_t col = col0 + j * 32 + l32;
@@ -532,20 +532,21 @@ __device__ __forceinline__ void w4g_plain_tiles(const f16x_t (&acc)[WI][WJ], uin
 }
 
 // Epilogue of the q|k|v GEMM that also performs OP_QK_ROPE_KV_F16 (W4gRope): the
-// workgroup's 128 x 128 tile is head n0 / 128 of tokens m0 .. m0 + 127. Its fp16 outputs
+// workgroup's 32 WT x 128 tile is head n0 / 128 of tokens m0 .. m0 + 32 WT - 1. Its fp16 outputs
 // are staged in LDS (the A tiles' space) so that each 8-lane group holds one token's head
 // row as the rows kernel's groups do, then finished with that kernel's arithmetic
 // (dev::qk_row8_norm_rope, RoPE entries from the call's table): q heads to q_out, k
 // heads (normalized, rotated) and v heads (as they are) to the ring slot of the token's
 // position and to k_out / v_out; y is written as well, 16 bytes per store.
 constexpr uint32_t kRopeSR = 128 + 8;   // staging row stride (halves)
-__device__ __forceinline__ void w4g_rope_tile(const f16x_t (&acc)[WI][1], uint32_t tid, uint32_t m0, uint32_t n0,
+template <int WT>
+__device__ __forceinline__ void w4g_rope_tile(const f16x_t (&acc)[WT][1], uint32_t tid, uint32_t m0, uint32_t n0,
                                               uint32_t M, __half* __restrict__ y, uint32_t ldy, const W4gRope& R,
                                               _Float16* __restrict__ st) {
     const uint32_t lane = tid & 63, wave = tid >> 6, half = lane >> 5, l32 = lane & 31;
     __syncthreads();   // every wave's last MFMAs have read the A tiles
 #pragma unroll
-    for (int i = 0; i < WI; ++i)
+    for (int i = 0; i < WT; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
             st[(i * 32 + 8 * (r >> 2) + 4 * half + (r & 3)) * kRopeSR + 32 * wave + l32] = (_Float16)acc[i][0][r];
@@ -562,7 +563,7 @@ __device__ __forceinline__ void w4g_rope_tile(const f16x_t (&acc)[WI][1], uint32
     const uint32_t pos0 = *reinterpret_cast<const uint32_t*>(cosp + (size_t)M * 128);
     __syncthreads();
 #pragma unroll
-    for (uint32_t it = 0; it < 4; ++it) {
+    for (uint32_t it = 0; it < WT; ++it) {
         const uint32_t r = grp + 32 * it, tok = m0 + r;
         if (tok >= M) break;   // the same for the 8 lanes of a group
         const u32x4 xl = *reinterpret_cast<const u32x4*>(&st[r * kRopeSR + 8 * g]);
@@ -604,24 +605,25 @@ __device__ __forceinline__ u32x4 pair_order16(u32x4 v) {   // k0..k7 -> (k0,k4)(
                  __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
 }
 
-template <bool ROPE>
+template <bool ROPE, int WT>
 __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
     const __half* __restrict__ a, uint32_t lda, const uint8_t* __restrict__ wq,
     const __half* __restrict__ ws, __half* __restrict__ y, uint32_t ldy, uint32_t M, uint32_t N,
     uint32_t K, const __half* __restrict__ res, uint32_t ldr, int swiglu, uint32_t mtiles, uint32_t ntiles,
     uint32_t split_steps, float* __restrict__ part, W4gRope rope) {
-    constexpr int CA = GB_M * (GB_K / 8) / 256;   // 16-byte A chunks per thread per K step
-    static_assert(GB_N == 128 && GB_M * kRopeSR <= 2 * GB_M * GB_LDS, "rope staging tile");
-    __shared__ __align__(16) _Float16 As[2][GB_M * GB_LDS];
+    constexpr int BM = 32 * WT;                    // workgroup tile rows (WT MFMA tiles per wave)
+    constexpr int CA = BM * (GB_K / 8) / 256;      // 16-byte A chunks per thread per K step
+    static_assert(!ROPE || (GB_N == 128 && kRopeSR <= 2 * GB_LDS), "rope staging tile");
+    __shared__ __align__(16) _Float16 As[2][BM * GB_LDS];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Workgroup -> (m tile, n tile, K part): m fastest, K part slowest. With `part`,
     // K part s covers K steps [s*split_steps, (s+1)*split_steps) and its fp32 sums go to
     // part[s][M][N] for w4g_splitk_reduce_kernel; otherwise one part covers all of K.
-    const uint32_t m0 = (blockIdx.x % mtiles) * GB_M, n0 = (blockIdx.x / mtiles % ntiles) * GB_N;
+    const uint32_t m0 = (blockIdx.x % mtiles) * BM, n0 = (blockIdx.x / mtiles % ntiles) * GB_N;
     const uint32_t split = blockIdx.x / (mtiles * ntiles);
     const uint32_t G = K / 64, rowbytes = K / 2;
     const uint32_t kbase = split * split_steps, nsteps = min(split_steps, K / GB_K - kbase);
-    constexpr int WJ = 1;   // MFMA tiles per wave: WI (M) x WJ (N)
+    constexpr int WJ = 1;   // MFMA tiles per wave: WT (M) x WJ (N)
     const uint32_t wn = wave, half = lane >> 5, l32 = lane & 31;
     size_t wrow[WJ];
 #pragma unroll
@@ -662,9 +664,9 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
         }
     };
 
-    f16x_t acc[WI][WJ];
+    f16x_t acc[WT][WJ];
 #pragma unroll
-    for (int i = 0; i < WI; ++i)
+    for (int i = 0; i < WT; ++i)
 #pragma unroll
         for (int j = 0; j < WJ; ++j)
 #pragma unroll
@@ -673,12 +675,12 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
     auto mfma = [&](int buf, int set) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            h8_t af[WI];
+            h8_t af[WT];
 #pragma unroll
-            for (int i = 0; i < WI; ++i)
+            for (int i = 0; i < WT; ++i)
                 af[i] = *reinterpret_cast<const h8_t*>(&As[buf][(i * 32 + l32) * GB_LDS + 32 * half + 8 * q]);
 #pragma unroll
-            for (int i = 0; i < WI; ++i)
+            for (int i = 0; i < WT; ++i)
 #pragma unroll
                 for (int j = 0; j < WJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bop[set][j][q], acc[i][j], 0, 0, 0);
@@ -718,10 +720,10 @@ __global__ __launch_bounds__(256, 3) void w4g_gemm_kernel(
         return;
     }
     if (!part && swiglu) {
-        w4g_swiglu_tiles<WJ>(acc, lane, m0, n0 + wn * 32 * WJ, M, N, y, ldy, res, ldr);
+        w4g_swiglu_tiles(acc, lane, m0, n0 + wn * 32 * WJ, M, N, y, ldy, res, ldr);
         return;
     }
-    w4g_plain_tiles<WJ>(acc, lane, m0, n0 + wn * 32 * WJ, M, N, y, ldy, res, ldr, part, split);
+    w4g_plain_tiles(acc, lane, m0, n0 + wn * 32 * WJ, M, N, y, ldy, res, ldr, part, split);
 }
 
 // Wide variant for the wide-N shapes: a 128 x 256 workgroup tile, each wave 128 x 64
@@ -838,10 +840,10 @@ __global__ __launch_bounds__(256, 2) void w4g_gemm_wide_kernel(
     for (int u = 0; u < 5; ++u)
         if (kb + u < nsteps) step(u % 2, u % 3, (u + 2) % 3, kb + u);
     if (!part && swiglu) {
-        w4g_swiglu_tiles<WJ>(acc, lane, m0, n0 + wave * 32 * WJ, M, N, y, ldy, res, ldr);
+        w4g_swiglu_tiles(acc, lane, m0, n0 + wave * 32 * WJ, M, N, y, ldy, res, ldr);
         return;
     }
-    w4g_plain_tiles<WJ>(acc, lane, m0, n0 + wave * 32 * WJ, M, N, y, ldy, res, ldr, part, split);
+    w4g_plain_tiles(acc, lane, m0, n0 + wave * 32 * WJ, M, N, y, ldy, res, ldr, part, split);
 }
 
 // Split-K finish, vector form (N, ldy, ldr multiples of 8, 16-byte aligned rows): a
@@ -1134,6 +1136,18 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
     }
 }
 
+// MFMA row tiles per wave (rows per workgroup / 32) of the 128-column kernel, unsplit:
+// 128-row tiles while that grid covers the CUs, else 64-row tiles while their grid
+// reaches half of them, else 32-row tiles. Each output's K order and MFMA sequence do
+// not depend on the tile height, so all three give the same bits. Measured with idle
+// CUs (M x N x K, us for 128 / 64 / 32 rows): 512 x 3072 x 1024 16.0 / 10.0 / 12.3,
+// 512 x 4096 x 1024 16.0 / 10.0, 64 x 4096 x 1024 14.4 / 9.2 / 7.4.
+static uint32_t narrow_tile_wt(uint32_t M, uint32_t nt) {
+    const size_t cus = (size_t)device_cu_count();
+    if ((size_t)((M + 127) / 128) * nt >= cus) return 4u;
+    return (size_t)((M + 63) / 64) * nt * 2 >= cus ? 2u : 1u;
+}
+
 hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
                            hipStream_t st, const W4gEpilogue& epi) {
@@ -1147,9 +1161,11 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
             !al16(R.v_out) || !al16(R.ring) || R.slot_bytes % 16 || !R.nslots ||
             R.slot_bytes < R.KVH * 128u * 4u)
             return hipErrorInvalidValue;
-        const uint32_t mt = (M + GB_M - 1) / GB_M, nt = N / GB_N;
-        hipLaunchKernelGGL(w4g_gemm_kernel<true>, dim3(mt * nt), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K,
-                           nullptr, 0u, 0, mt, nt, K / GB_K, nullptr, R);
+        const uint32_t nt = N / GB_N, wt = narrow_tile_wt(M, nt);
+        const uint32_t mt = (M + 32 * wt - 1) / (32 * wt);
+        const auto kern = wt == 4 ? w4g_gemm_kernel<true, 4> : wt == 2 ? w4g_gemm_kernel<true, 2> : w4g_gemm_kernel<true, 1>;
+        hipLaunchKernelGGL(kern, dim3(mt * nt), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K, nullptr, 0u, 0, mt,
+                           nt, K / GB_K, nullptr, R);
         return hipGetLastError();
     }
     if (epi.swiglu) {
@@ -1167,13 +1183,22 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
     // fewer tiles, qkv N = 6144 and a two-part split of N = 2560, the 128 x 128 tile at
     // three per CU is 5-9 % faster) and for a three-part split, sized for it.
     const bool wide = (size_t)mt * ntw * (split ? parts : 1u) >= 4 * (size_t)device_cu_count() || (split && parts == 3);
+    const uint32_t wt = wide || split ? 4u : narrow_tile_wt(M, nt);
+    auto narrow = [&](auto kern, uint32_t rows, float* pw) {
+        const uint32_t mtn = (M + rows - 1) / rows;
+        hipLaunchKernelGGL(kern, dim3(mtn * nt * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K,
+                           epi.res, epi.ldr, epi.swiglu ? 1 : 0, mtn, nt, per, pw, W4gRope{});
+    };
     auto gemm = [&](float* pw) {
         if (wide)
             hipLaunchKernelGGL(w4g_gemm_wide_kernel, dim3(mt * ntw * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq,
                                ws, y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, ntw, per, pw);
+        else if (wt == 4)
+            narrow(w4g_gemm_kernel<false, 4>, 128u, pw);
+        else if (wt == 2)
+            narrow(w4g_gemm_kernel<false, 2>, 64u, pw);
         else
-            hipLaunchKernelGGL(w4g_gemm_kernel<false>, dim3(mt * nt * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq, ws,
-                               y, ldy, M, N, K, epi.res, epi.ldr, epi.swiglu ? 1 : 0, mt, nt, per, pw, W4gRope{});
+            narrow(w4g_gemm_kernel<false, 1>, 32u, pw);
     };
     if (split) {
         gemm(epi.split_ws);

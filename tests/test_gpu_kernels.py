@@ -523,6 +523,39 @@ def test_w4g_gemm_split_k(lib, oracle, torch_dev, mode, use_res, M, N, K):
     assert (a == b).mean() > 0.99
 
 
+@pytest.mark.parametrize("mode,use_res", [(0, False), (1, True)])
+def test_w4g_gemm_tile_heights(lib, oracle, torch_dev, mode, use_res):
+    """An unsplit GEMM whose grid of 128 x 128 tiles leaves CUs idle runs 64- or 32-row
+    tiles (on 256 CUs, N = 3072, K = 1024: M = 2048 keeps 128 rows, M = 512, the single
+    prefill GEMM shape of the benchmark's second config, takes 64, M = 40 takes 32 with a
+    partial tile). Each output's K order and MFMA sequence do not depend on the tile
+    height: the rows the three calls share are bit-identical, and M = 512 matches the
+    oracle."""
+    import torch
+    rng = np.random.default_rng(70 + mode + use_res)
+    N, K = 3072, 1024
+    n_out = N // 2 if mode else N
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = normal_f16(rng, 2048, K)
+    res = normal_f16(rng, 2048, n_out)
+    xd, wqd, wsd, resd = (to_dev(v, torch_dev) for v in (x, wq, ws, res))
+    outs = {}
+    for M in (2048, 512, 40):
+        assert lib.gehtp_w4g_split_bytes(M, N, K) == 0
+        y = torch.empty((M, n_out), dtype=torch.float16, device=torch_dev)
+        assert lib.gehtp_w4g_fused_ws(ptr(xd), K, ptr(wqd), ptr(wsd), ptr(y), n_out, M, N, K, None,
+                                      ptr(resd) if use_res else None, n_out, mode, None, 0, stream_ptr()) == 0
+        _sync()
+        outs[M] = from_dev(y)
+    assert np.array_equal(outs[512].view(np.uint16), outs[2048][:512].view(np.uint16))
+    assert np.array_equal(outs[40].view(np.uint16), outs[2048][:40].view(np.uint16))
+    acc = oracle.matmul_w4g(x[:512], wq, ws, threads=8)
+    ref = oracle.binary(oracle.unary(acc[:, 0::2].copy(), 12), acc[:, 1::2].copy(), 2) if mode else acc
+    if use_res:
+        ref = oracle.binary(ref, res[:512], 0)
+    assert_close(outs[512], ref, what=f"64-row tile gemm mode={mode} res={use_res}")
+
+
 @pytest.mark.parametrize("n_tok,H,KVH", [(1, 8, 2), (37, 8, 2), (130, 32, 8), (6, 16, 8), (3, 40, 24)])
 def test_qk_rope_kv(lib, oracle, torch_dev, n_tok, H, KVH):
     """OP_QK_ROPE_KV_F16 = per-head RMSNORM2 (q_norm / k_norm), ROPE at the counter
