@@ -464,7 +464,7 @@ def kernel_configs(args) -> int:
                                           H, KVH, HD_ATTN, scale, 1, sp) == 0
         t_rot = timed(c3p, copies, 5)
         t_res = timed(lambda i: c3p(0), 32, 5)
-        results["c3_attn_prefill"] = {"kernel": "attn_prefill_kernel<true>", "flops": flops, "copies": copies,
+        results["c3_attn_prefill"] = {"kernel": "attn_prefill_kernel<true, WPH>", "flops": flops, "copies": copies,
                                       "rotated_us": round(t_rot * 1e6, 3),
                                       "rotated_tflops": round(flops / t_rot / 1e12, 1),
                                       "resident_us": round(t_res * 1e6, 3),

@@ -24,7 +24,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int HD = 128;          // head dim this kernel is built for
-constexpr int QT = 128;          // queries per workgroup (4 waves x 32)
 constexpr int KT = 64;           // keys per LDS stage
 constexpr int KS = HD + 8;       // K tile row stride (halves)
 constexpr int VSR = HD + 32;     // V tile row stride (halves): 80 dwords, so the 4 rows x 64 bytes
@@ -41,15 +40,16 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const _Float16* p) {
     return __builtin_bit_cast(u32x2, r);
 }
 
-// Flash attention forward. A workgroup owns 128 queries of one head (wave w: queries
-// 32w..32w+31); per 64-key stage, K and V are staged row-major in LDS (the next stage's
+// Flash attention forward. A workgroup owns 32 WPH queries of one head (wave w of a
+// half: queries 32w..32w+31; WPH = 4 normally, 2 when 128-query tiles would leave CUs
+// idle); per 64-key stage, K and V are staged row-major in LDS (the next stage's
 // loads are in flight during the compute). Scores are computed transposed,
 // S^T = K Q^T (MFMA A = K rows, B = Q^T held in registers), so each lane owns one query
 // and its 32 scores of a stage; the online-softmax statistics need one exchange with
 // lane l^32. O^T = V^T P^T: the V^T operand comes from the row-major V tile through the
 // transposing LDS read, P^T straight from the score registers.
 //
-// Two halves of 4 waves split a tile's key stages: half p runs stages
+// Two halves of WPH waves split a tile's key stages: half p runs stages
 // [p*ns0, min(ns, (p+1)*ns0)) (ns0 = ceil(ns/2)) on its own LDS tiles, both halves in
 // lockstep (the shorter one idles through its last step), and half 1 hands its partial
 // (O, max, sum) to half 0 through LDS at the end. A causal tile then costs half its
@@ -57,13 +57,15 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const _Float16* p) {
 // tiles of every head first, one 8-wave workgroup per CU, the light ones behind them).
 constexpr uint32_t KV_HALF = KT * KS + KT * VSR;   // halves of one LDS K + V stage
 
-template <bool CAUSAL>
-__global__ __launch_bounds__(512) void attn_prefill_kernel(
+template <bool CAUSAL, int WPH>
+__global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
     const __half* __restrict__ q, uint32_t ldq, uint32_t qhs, const __half* __restrict__ k,
     const __half* __restrict__ v, uint32_t ldkv, uint32_t kvhs, __half* __restrict__ out, uint32_t ldo,
     uint32_t ohs, uint32_t S, uint32_t H, uint32_t KVH, float scale_log2) {
     __shared__ __align__(16) _Float16 kvbuf[2 * KV_HALF];
-    const uint32_t part = threadIdx.x >> 8, tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
+    constexpr uint32_t QT = 32 * WPH, NT = 64 * WPH;   // queries per tile, threads per half
+    constexpr int KR = KT * 16 / NT;                     // K / V rows per thread per stage
+    const uint32_t part = threadIdx.x / NT, tid = threadIdx.x % NT, lane = tid & 63, wave = tid >> 6;
     _Float16* const Ks = kvbuf + part * KV_HALF;
     _Float16* const Vs = Ks + KT * KS;
     const uint32_t n_qt = (S + QT - 1) / QT;
@@ -93,14 +95,14 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
     float m_run = -INFINITY, l_run = 0.0f;
 
     const uint32_t kend = CAUSAL ? min(S, q0 + QT) : S;
-    // K and V rows of this thread's 4 keys (stage-local key (tid>>4) + 16i, dims 8*ch..).
+    // K and V rows of this thread's KR keys (stage-local key (tid>>4) + (NT/16)i, dims 8*ch..).
     // Loads are unconditional (keys past S read row S-1; their scores are masked).
     const uint32_t ch = tid & 15;
-    u32x4 kv4[4], vv4[4];
+    u32x4 kv4[KR], vv4[KR];
     auto load_kv = [&](uint32_t kb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t key = min(kb + (tid >> 4) + 16 * i, S - 1);
+        for (int i = 0; i < KR; ++i) {
+            const uint32_t key = min(kb + (tid >> 4) + (NT / 16) * i, S - 1);
             const size_t off = (size_t)key * ldkv + (size_t)kvh * kvhs + ch * 8;
             kv4[i] = *reinterpret_cast<const u32x4*>(k + off);
             vv4[i] = *reinterpret_cast<const u32x4*>(v + off);
@@ -120,8 +122,8 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
         const uint32_t kb = (st0 + it) * KT;
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t key = (tid >> 4) + 16 * i;
+        for (int i = 0; i < KR; ++i) {
+            const uint32_t key = (tid >> 4) + (NT / 16) * i;
             *reinterpret_cast<u32x4*>(&Ks[key * KS + ch * 8]) = kv4[i];
             *reinterpret_cast<u32x4*>(&Vs[key * VSR + ch * 8]) = vv4[i];
         }
@@ -210,7 +212,7 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
     }
 
     // Half 1 hands (O, max, sum) to half 0 through the K/V tiles (lane-major floats: 66
-    // per lane, 64 lanes x 4 waves); half 0 rescales both to the common max.
+    // per lane, 64 lanes x WPH waves); half 0 rescales both to the common max.
     __syncthreads();
     float* xch = reinterpret_cast<float*>(kvbuf);
     const uint32_t xl = wave * 64 + lane;
@@ -218,21 +220,21 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) xch[(dt * 16 + r) * 256 + xl] = o[dt][r];
-        xch[64 * 256 + xl] = m_run;
-        xch[65 * 256 + xl] = l_run;
+            for (int r = 0; r < 16; ++r) xch[(dt * 16 + r) * NT + xl] = o[dt][r];
+        xch[64 * NT + xl] = m_run;
+        xch[65 * NT + xl] = l_run;
     }
     __syncthreads();
     if (part == 1) return;
     {
-        const float m1 = xch[64 * 256 + xl], l1 = xch[65 * 256 + xl];
+        const float m1 = xch[64 * NT + xl], l1 = xch[65 * NT + xl];
         const float m = fmaxf(m_run, m1);
         const float a0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m) * scale_log2);
         const float a1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m1 - m) * scale_log2);
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a0 + xch[(dt * 16 + r) * 256 + xl] * a1;
+            for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a0 + xch[(dt * 16 + r) * NT + xl] * a1;
         l_run = l_run * a0 + l1 * a1;
     }
     if (my_q < S) {
@@ -654,14 +656,16 @@ hipError_t launch_attn_prefill_hs(const __half* q, uint32_t ldq, uint32_t qhs, c
     if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
     if (!(scale > 0.0f && scale < INFINITY)) return hipErrorInvalidValue;   // the kernel's max needs scale > 0
     if (!S || !H) return hipSuccess;
-    dim3 grid(H, (S + QT - 1) / QT);   // heads fastest: the heavy tiles of every head go first
+    // 128-query tiles (8-wave workgroups) while they give every CU one; else 64-query
+    // tiles (4-wave workgroups), twice as many.
+    const uint32_t wph = (size_t)H * ((S + 127) / 128) >= (size_t)device_cu_count() ? 4u : 2u;
+    const uint32_t qt = 32 * wph;
+    dim3 grid(H, (S + qt - 1) / qt);   // heads fastest: the heavy tiles of every head go first
     const float sl2 = scale * kLog2e;
-    if (causal)
-        hipLaunchKernelGGL(attn_prefill_kernel<true>, grid, dim3(512), 0, st, q, ldq, qhs, k, v, ldkv, kvhs,
-                           out, ldo, ohs, S, H, KVH, sl2);
-    else
-        hipLaunchKernelGGL(attn_prefill_kernel<false>, grid, dim3(512), 0, st, q, ldq, qhs, k, v, ldkv, kvhs,
-                           out, ldo, ohs, S, H, KVH, sl2);
+    const auto kern = causal ? (wph == 4 ? attn_prefill_kernel<true, 4> : attn_prefill_kernel<true, 2>)
+                             : (wph == 4 ? attn_prefill_kernel<false, 4> : attn_prefill_kernel<false, 2>);
+    hipLaunchKernelGGL(kern, grid, dim3(4 * qt), 0, st, q, ldq, qhs, k, v, ldkv, kvhs, out, ldo, ohs, S, H, KVH,
+                       sl2);
     return hipGetLastError();
 }
 
