@@ -56,7 +56,7 @@ def parse_args():
                          "attention), operands rotated over copies totalling > 256 MB and, beside it, "
                          "one copy repeated (cache-resident); prints one JSON line")
     ap.add_argument("--only", default=None,
-                    help="with --kernel-configs: comma-separated subset of c1,c2,c3p,c3d")
+                    help="with --kernel-configs: comma-separated subset of c1,c2,c3p,c3d,c4")
     return ap.parse_args()
 
 
@@ -363,7 +363,12 @@ def kernel_configs(args) -> int:
       c3p causal GQA prefill S=1024, 16 Q / 8 KV heads, hd 128: flops 4*H*hd*S(S+1)/2
           = 4.30 G
       c3d decode over 4096 keys of the ring, 16 Q / 8 KV heads: bytes K + V =
-          4096*8*128*2*2 = 16,777,216 (the 4 KB query and output aside)"""
+          4096*8*128*2*2 = 16,777,216 (the 4 KB query and output aside)
+    and config 4 end to end through the runlist engine (not a single kernel): one
+    0.8B-class layer with its fp16 lm_head, a 512-token prefill (prompt embeddings
+    resident in HBM) then 128 greedy decode steps chained on the device
+    (wt_exec_run_steps), four times from reset state; the medians of runs 2-4 (run 1
+    uploads the weights) are reported, and every run must give the same tokens."""
     import numpy as np
     import torch
 
@@ -373,7 +378,7 @@ def kernel_configs(args) -> int:
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
-    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3p", "c3d"}
+    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3p", "c3d", "c4"}
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
     results = {}
@@ -499,6 +504,49 @@ def kernel_configs(args) -> int:
                                      "resident_gbs": round(nbytes / t_res / 1e9, 1)}
         log(f"c3 decode: rotated {t_rot * 1e6:.2f} us ({nbytes / t_rot / 1e9:.0f} GB/s), "
             f"resident {t_res * 1e6:.2f} us")
+    if "c4" in only:
+        from gehtp_amd import Engine
+        from gehtp_amd.qwen3 import CONFIG_08B_LAYER as c4cfg, Weights, emit_decode, emit_prefill
+        S4, n_dec, max_pos = 512, 128, 1024
+        w4 = Weights(c4cfg, seed=args.seed)
+        eng = Engine()
+        eng.set_ext_weights(w4.image.ctypes.data)
+        pre_blob, tp4 = emit_prefill(c4cfg, w4, S4, max_pos)
+        dec_blob, td4 = emit_decode(c4cfg, w4, max_pos, token_input=True)
+        pp4, pt4 = eng.parse(pre_blob), eng.parse(dec_blob)
+        ids = np.random.default_rng(args.seed + 1).integers(0, c4cfg.vocab, S4)
+        x_host = np.ascontiguousarray(w4.embed()[ids]).tobytes()
+        x4 = torch.from_numpy(np.frombuffer(x_host, np.uint8).copy()).to(dev)
+        torch.cuda.synchronize()
+        eng.set_input_device(x4.data_ptr(), x4.numel())
+        pre_t, dec_t, toks = [], [], None
+        try:
+            for _ in range(4):
+                eng.state_reset()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                out, _ = eng.run_io(pp4, None, tp4["tok"])
+                torch.cuda.synchronize()
+                t1 = time.perf_counter()
+                first = int(np.frombuffer(out, np.int32)[0])
+                run = [first] + np.frombuffer(eng.run_steps(pt4, n_dec, np.int32(first).tobytes(), td4["tok"]),
+                                              np.int32).tolist()
+                torch.cuda.synchronize()
+                pre_t.append(t1 - t0)
+                dec_t.append(time.perf_counter() - t1)
+                if toks is not None and run != toks:
+                    raise RuntimeError("config 4 runs from reset state give different tokens")
+                toks = run
+        finally:
+            eng.set_input_device(None)
+        t_pre, t_dec = sorted(pre_t[1:])[1], sorted(dec_t[1:])[1]
+        results["c4_layer_e2e"] = {"workload": "1 layer 0.8B-class + fp16 lm_head, prefill 512 + 128 greedy steps",
+                                   "prefill_ms": round(t_pre * 1e3, 3),
+                                   "prefill_tflops": round(c4cfg.prefill_flops(S4) / t_pre / 1e12, 1),
+                                   "decode_tok_s": round(n_dec / t_dec, 1),
+                                   "decode_ms_per_step": round(t_dec / n_dec * 1e3, 4),
+                                   "total_ms": round((t_pre + t_dec) * 1e3, 2), "tokens_head": toks[:8]}
+        log(f"c4: prefill {t_pre * 1e3:.3f} ms, decode {n_dec / t_dec:.0f} tok/s")
     print(json.dumps({"kernel_configs": True, **results}), flush=True)
     return 0
 
