@@ -1182,8 +1182,11 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
     // two workgroups per CU (measured at M = 2048: gate/up N = 19456 256 vs 263 us; with
     // fewer tiles, qkv N = 6144 and a two-part split of N = 2560, the 128 x 128 tile at
     // three per CU is 5-9 % faster) and for a three-part split, sized for it.
-    const bool wide = (size_t)mt * ntw * (split ? parts : 1u) >= 4 * (size_t)device_cu_count() || (split && parts == 3);
-    const uint32_t wt = wide || split ? 4u : narrow_tile_wt(M, nt);
+    const size_t cus = (size_t)device_cu_count();
+    const bool wide = (size_t)mt * ntw * (split ? parts : 1u) >= 4 * cus ||
+                      (split && parts == 3 && (size_t)6 * mt * ntw >= cus);
+    // A split on the 128 x 128 kernel counts its parts as further column tiles.
+    const uint32_t wt = wide ? 4u : narrow_tile_wt(M, split ? nt * parts : nt);
     auto narrow = [&](auto kern, uint32_t rows, float* pw) {
         const uint32_t mtn = (M + rows - 1) / rows;
         hipLaunchKernelGGL(kern, dim3(mtn * nt * (pw ? parts : 1u)), dim3(256), 0, st, a, lda, wq, ws, y, ldy, M, N, K,
@@ -1229,11 +1232,15 @@ hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, con
 
 // K is split when the 128 x 128 tile grid alone would give fewer than two workgroups
 // per CU (three fit at once): the narrow-N projections (N = hidden) otherwise run one
-// latency-bound workgroup on most CUs. Three parts of 16+ K steps on the 128 x 256 tile
-// when that grid fits one round at two workgroups per CU (M = 2048, N = 2560: 160 tiles,
-// 480 workgroups; the o- and down-projections measured 2.4 % faster per prefill than
-// two parts on the 128 x 128 tile, whose A reads from LDS take as long as its MFMAs);
-// otherwise two parts of 16+ steps on the 128 x 128 tile.
+// latency-bound workgroup on most CUs. Three parts of 16+ K steps when the 128 x 256
+// grid of three parts fits one round at two workgroups per CU: on that tile when it
+// also reaches half the CUs (M = 2048, N = 2560: 160 tiles, 480 workgroups; the o- and
+// down-projections measured 2.4 % faster per prefill than two parts on the 128 x 128
+// tile, whose A reads from LDS take as long as its MFMAs; M = 1024: 240 workgroups,
+// 74.1 against 75.4 us on 128-row narrow tiles), else on the 128 x 128 kernel's shorter
+// tiles (graph-timed, wide against narrow: M = 512, N = 1024, K = 3072 29.6 -> 15.0 us;
+// M = 128, N = 2560, K = 9728 58.2 -> 24.6 us);
+// otherwise two parts of 16+ steps on the 128 x 128 kernel.
 uint32_t w4g_gemm_split_parts(uint32_t M, uint32_t N, uint32_t K) {
     const size_t mt = (M + GB_M - 1) / GB_M, cus = (size_t)device_cu_count();
     if (mt * ((N + GB_N - 1) / GB_N) >= 2 * cus) return 1u;
