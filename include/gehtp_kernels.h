@@ -43,10 +43,11 @@ int gehtp_w4g_fused(const void* x, uint32_t ldx, const void* wq, const void* ws,
                     uint32_t ldy, uint32_t M, uint32_t N, uint32_t K, const void* gamma,
                     const void* res, uint32_t ldr, uint32_t mode, void* stream);
 /* gehtp_w4g_fused with an fp32 workspace (16-byte aligned) that lets the GEMM split K for
- * narrow-N shapes (fewer 128 x 128 tiles than two per CU): in three parts on 128 x 256
- * tiles when that grid fits one round at two workgroups per CU, else in two on 128 x 128
- * tiles; each part writes its sums there and a second pass adds them in part order and
- * applies the epilogue. Needs
+ * narrow-N shapes (fewer 128 x 128 tiles than two per CU): in three parts (K >= 48 * 64)
+ * when the 128 x 256 grid of three parts fits one round at two workgroups per CU (on
+ * that tile when the grid also reaches half the CUs, else on 128-column tiles of 128,
+ * 64 or 32 rows), else in two (K >= 32 * 64) on the 128-column tiles; each part writes
+ * its sums there and a second pass adds them in part order and applies the epilogue. Needs
  * gehtp_w4g_split_bytes(M, N, K) bytes (0: this shape does not split; work may be NULL
  * or smaller, and the GEMM then runs in one pass). Calls sharing a workspace must not
  * overlap. No counterpart in the reference (its matmul runs on the NPU's own engine). */
