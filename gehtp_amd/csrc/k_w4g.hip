@@ -1136,16 +1136,17 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
     }
 }
 
-// MFMA row tiles per wave (rows per workgroup / 32) of the 128-column kernel, unsplit:
-// 128-row tiles while that grid covers the CUs, else 64-row tiles while their grid
-// reaches half of them, else 32-row tiles. Each output's K order and MFMA sequence do
+// MFMA row tiles per wave (rows per workgroup / 32) of the 128-column kernel (nt counts
+// a split's parts as further column tiles): 128-row tiles while that grid covers the CUs, else 64-row tiles while their grid
+// exceeds half of them, else 32-row tiles. Each output's K order and MFMA sequence do
 // not depend on the tile height, so all three give the same bits. Measured with idle
 // CUs (M x N x K, us for 128 / 64 / 32 rows): 512 x 3072 x 1024 16.0 / 10.0 / 12.3,
-// 512 x 4096 x 1024 16.0 / 10.0, 64 x 4096 x 1024 14.4 / 9.2 / 7.4.
+// 512 x 4096 x 1024 16.0 / 10.0 / 12.3, 64 x 4096 x 1024 14.4 / 9.2 / 7.4; K in two
+// parts, 512 x 1024 x 2048 (128 or 256 workgroups at 64 or 32 rows): 13.2 / 11.6.
 static uint32_t narrow_tile_wt(uint32_t M, uint32_t nt) {
     const size_t cus = (size_t)device_cu_count();
     if ((size_t)((M + 127) / 128) * nt >= cus) return 4u;
-    return (size_t)((M + 63) / 64) * nt * 2 >= cus ? 2u : 1u;
+    return (size_t)((M + 63) / 64) * nt * 2 > cus ? 2u : 1u;
 }
 
 hipError_t launch_w4g_gemm(const __half* a, uint32_t lda, const uint8_t* wq, const __half* ws,
