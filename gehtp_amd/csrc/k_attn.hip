@@ -42,7 +42,7 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const _Float16* p) {
 
 // Flash attention forward. A workgroup owns 32 WPH queries of one head (wave w of a
 // half: queries 32w..32w+31; WPH = 4 normally, 2 when 128-query tiles would leave CUs
-// idle); per 64-key stage, K and V are staged row-major in LDS (the next stage's
+// idle, 1 when 64-query tiles would too); per 64-key stage, K and V are staged row-major in LDS (the next stage's
 // loads are in flight during the compute). Scores are computed transposed,
 // S^T = K Q^T (MFMA A = K rows, B = Q^T held in registers), so each lane owns one query
 // and its 32 scores of a stage; the online-softmax statistics need one exchange with
@@ -657,13 +657,18 @@ hipError_t launch_attn_prefill_hs(const __half* q, uint32_t ldq, uint32_t qhs, c
     if (!(scale > 0.0f && scale < INFINITY)) return hipErrorInvalidValue;   // the kernel's max needs scale > 0
     if (!S || !H) return hipSuccess;
     // 128-query tiles (8-wave workgroups) while they give every CU one; else 64-query
-    // tiles (4-wave workgroups), twice as many.
-    const uint32_t wph = (size_t)H * ((S + 127) / 128) >= (size_t)device_cu_count() ? 4u : 2u;
+    // tiles (4-wave workgroups) while those do; else 32-query tiles (2-wave workgroups).
+    const size_t cus = (size_t)device_cu_count();
+    const uint32_t wph = (size_t)H * ((S + 127) / 128) >= cus ? 4u : (size_t)H * ((S + 63) / 64) >= cus ? 2u : 1u;
     const uint32_t qt = 32 * wph;
     dim3 grid(H, (S + qt - 1) / qt);   // heads fastest: the heavy tiles of every head go first
     const float sl2 = scale * kLog2e;
-    const auto kern = causal ? (wph == 4 ? attn_prefill_kernel<true, 4> : attn_prefill_kernel<true, 2>)
-                             : (wph == 4 ? attn_prefill_kernel<false, 4> : attn_prefill_kernel<false, 2>);
+    const auto kern = causal ? (wph == 4   ? attn_prefill_kernel<true, 4>
+                                : wph == 2 ? attn_prefill_kernel<true, 2>
+                                           : attn_prefill_kernel<true, 1>)
+                             : (wph == 4   ? attn_prefill_kernel<false, 4>
+                                : wph == 2 ? attn_prefill_kernel<false, 2>
+                                           : attn_prefill_kernel<false, 1>);
     hipLaunchKernelGGL(kern, grid, dim3(4 * qt), 0, st, q, ldq, qhs, k, v, ldkv, kvhs, out, ldo, ohs, S, H, KVH,
                        sl2);
     return hipGetLastError();

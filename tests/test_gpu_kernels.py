@@ -353,19 +353,20 @@ def test_attn_prefill(lib, oracle, torch_dev, S, H, KVH, causal):
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_attn_prefill_tile_sizes(lib, oracle, torch_dev, causal):
-    """The prefill runs 128-query tiles when heads x tiles cover the CUs (256 on MI355X)
-    and 64-query tiles otherwise (config 3: 16 heads x 8 tiles). S = 512 with 64 heads
-    takes the 128-query tiles, its first 16 heads (over the first 2 KV heads, the same
-    grouping) the 64-query ones. Every query sums the same key stages in the same order
-    either way (with the mask too: a 64-query tile's two halves split its stages where
-    the enclosing 128-query tile's do, the extra stage of the latter being wholly masked
-    for the first 64 queries), so the outputs are bit-identical; both match the oracle."""
+    """The prefill runs 128-query tiles when heads x tiles cover the CUs (256 on MI355X),
+    else 64-query tiles when those do (config 3: 16 heads x 16 tiles), else 32-query
+    tiles. At S = 512, 64 heads take the 128-query tiles, their first 32 heads (over the
+    first 4 KV heads, the same grouping) the 64-query ones and their first 16 the
+    32-query ones. Every query sums the same key stages in the same order each time
+    (with the mask too: a tile's two halves split its stages where the enclosing larger
+    tile's do, the larger tile's extra stage being wholly masked for the queries before
+    it), so the outputs are bit-identical; they match the oracle."""
     import torch
     rng = np.random.default_rng(11 + causal)
     S, hd = 512, 128
     q, k, v = normal_f16(rng, S, 64, hd), normal_f16(rng, S, 8, hd), normal_f16(rng, S, 8, hd)
     outs = {}
-    for H, KVH in ((64, 8), (16, 2)):
+    for H, KVH in ((64, 8), (32, 4), (16, 2)):
         qs, ks, vs = (np.ascontiguousarray(t[:, :n]) for t, n in ((q, H), (k, KVH), (v, KVH)))
         out = torch.empty((S, H, hd), dtype=torch.float16, device=torch_dev)
         assert lib.gehtp_attn_prefill(ptr(to_dev(qs, torch_dev)), ptr(to_dev(ks, torch_dev)),
@@ -373,11 +374,12 @@ def test_attn_prefill_tile_sizes(lib, oracle, torch_dev, causal):
                                       stream_ptr()) == 0
         _sync()
         outs[H] = from_dev(out)
-    big, small = outs[64][:, :16], outs[16]
+    big, mid, small = outs[64][:, :16], outs[32][:, :16], outs[16]
     assert np.array_equal(big.view(np.uint16), small.view(np.uint16))
+    assert np.array_equal(mid.view(np.uint16), small.view(np.uint16))
     ref = oracle.attn_prefill(np.ascontiguousarray(q[:, :16]), np.ascontiguousarray(k[:, :2]),
                               np.ascontiguousarray(v[:, :2]), SCALE, causal)
-    assert_close(small, ref, what=f"64-query tiles causal={causal}")
+    assert_close(small, ref, what=f"32-query tiles causal={causal}")
     assert_close(big, ref, what=f"128-query tiles causal={causal}")
 
 
