@@ -44,6 +44,9 @@ class ParsedBlob:
                           C.byref(self.blob))
         if rc != 0:
             raise WtParseError(rc, lib.wt_err_str(rc).decode())
+        ins = [self.blob.slots[i].len for i in range(self.blob.n_slots)
+               if self.blob.slots[i].addr == abi.WT_SLOT_EXT_IN]
+        self._input_bytes = max(ins, default=0)
 
     @property
     def n_ops(self) -> int:
@@ -52,6 +55,12 @@ class ParsedBlob:
     @property
     def n_slots(self) -> int:
         return self.blob.n_slots
+
+    @property
+    def input_bytes(self) -> int:
+        """Bytes of the blob's EXT_IN input slot (the largest one; 0 if it has none): what
+        wt_exec_run_io and wt_exec_run_steps read from their host input pointer."""
+        return self._input_bytes
 
 
 class Engine:
@@ -87,6 +96,10 @@ class Engine:
         err = C.create_string_buffer(512)
         m = C.c_uint32(0)
         us = (C.c_int64 * max(pb.n_ops, 1))() if timing else None
+        # The library copies the input slot's length from in_ptr, whatever the caller
+        # passed: a shorter buffer would be read past its end.
+        if inp is not None and len(inp) < pb.input_bytes:
+            raise ValueError(f"run_io: input holds {len(inp)} bytes, the blob's input slot {pb.input_bytes}")
         ibuf = C.c_char_p(bytes(inp)) if inp is not None else None
         # run_io copies the output temp's last-written bytes into out_ptr, so the buffer
         # must hold the largest output the caller expects (out_bytes, default 64 MiB).
@@ -105,7 +118,13 @@ class Engine:
         become the next run's input); returns the steps' outputs concatenated."""
         err = C.create_string_buffer(512)
         m = C.c_uint32(0)
-        n = len(inp)
+        # The library reads the input slot's length from inp and writes steps times that
+        # many bytes to the output: both buffers are sized from the slot, not from inp.
+        n = pb.input_bytes
+        if len(inp) != n:
+            raise ValueError(f"run_steps: input holds {len(inp)} bytes, the blob's input slot {n}")
+        if steps * n > (64 << 20):
+            raise ValueError(f"run_steps: {steps} steps x {n} bytes exceed the 64 MiB output limit")
         obuf = C.create_string_buffer(max(steps * n, 1))
         rc = self.lib.wt_exec_run_steps(C.byref(pb.blob), steps, C.c_char_p(bytes(inp)), obuf, out_temp, C.byref(m),
                                         err, 512)

@@ -184,3 +184,24 @@ def test_builder_layout_rules():
     assert offs == [0, 128]
     woff = (16 + 32 + 4 + 127) // 128 * 128
     assert data[woff:woff + 3] == b"\x01" * 3 and data[woff + 128:woff + 328] == b"\x02" * 200
+
+
+def test_python_io_buffers_sized_from_the_input_slot():
+    """wt_exec_run_io / wt_exec_run_steps read the EXT_IN slot's length from the host input
+    and run_steps writes steps times that length: the Python mirror checks the caller's
+    bytes against the slot before any call (no GPU call is made: each raises first)."""
+    from gehtp_amd import Engine
+    bb = BlobBuilder()
+    x = bb.add_input_slot(64)
+    bb.op(OP.ARGMAX_F16, bb.slot_ref(x), 0, 32)
+    eng = Engine()
+    pb = eng.parse(bb.build())
+    assert pb.input_bytes == 64
+    with pytest.raises(ValueError, match="input slot 64"):
+        eng.run_steps(pb, 4, b"\0" * 4, 0)
+    with pytest.raises(ValueError, match="input slot 64"):
+        eng.run_steps(pb, 4, b"\0" * 128, 0)
+    with pytest.raises(ValueError, match="64 MiB"):
+        eng.run_steps(pb, (64 << 20) // 64 + 1, b"\0" * 64, 0)
+    with pytest.raises(ValueError, match="input slot 64"):
+        eng.run_io(pb, b"\0" * 32, 0)
