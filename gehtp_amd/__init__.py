@@ -189,6 +189,14 @@ class Engine:
         self.lib.wt_exec_fusion_stats(C.byref(f), C.byref(r))
         return f.value, r.value
 
+    def fusion_detail(self, pb: ParsedBlob) -> dict:
+        """The fusion plan of a blob after its first full run: chains found, chains the
+        observed run ruled out, chains whose output overlapped an input in that run, and
+        (process-wide) fused executions that wrote scratch because of such an overlap."""
+        n, blk, al, runs = C.c_uint32(0), C.c_uint32(0), C.c_uint32(0), C.c_uint64(0)
+        self.lib.wt_exec_fusion_detail(C.byref(pb.blob), C.byref(n), C.byref(blk), C.byref(al), C.byref(runs))
+        return {"chains": n.value, "blocked": blk.value, "aliased": al.value, "alias_runs": runs.value}
+
     def qkv_rope_fused(self) -> int:
         """QK-norm/RoPE/KV-append ops performed by their q|k|v GEMM's epilogue so far."""
         return int(self.lib.wt_exec_qkv_rope_fused())

@@ -153,6 +153,8 @@ EXPORTS = {
     "wt_exec_set_fusion": (_i, [_i]),
     "wt_exec_set_input_device": (None, [_vp, C.c_size_t]),
     "wt_exec_fusion_stats": (None, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "wt_exec_fusion_detail": (None, [C.POINTER(WtBlob), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                                     C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
     "wt_exec_qkv_rope_fused": (C.c_uint64, []),
     "wt_w3_report": (None, [C.c_char_p, _u8p, C.c_size_t, C.POINTER(WtBlob),
                             C.CFUNCTYPE(None, C.c_char_p, _vp), _vp]),

@@ -137,7 +137,9 @@ struct Engine {
     bool variant = false;   // an op of this run passed host-side step state to a kernel
     int graphs = -1;        // -1: not yet read from the environment; 0 off; 1 on
     int fusion = -1;        // attention-chain fusion: -1 not yet read from the environment
-    uint64_t chains_found = 0, fused_runs = 0;
+    uint64_t chains_found = 0, fused_runs = 0, fused_alias_runs = 0;
+    uint8_t* fuse_scratch = nullptr;       // fused attention output when it overlaps an input
+    uint64_t fuse_scratch_cap = 0;
     uint64_t qkv_rope_fused = 0;   // OP_QK_ROPE_KV_F16 ops performed by their GEMM's epilogue
     bool graphs_broken = false;
     uint32_t n_captures = 0, n_replays = 0;
@@ -157,17 +159,20 @@ struct Engine {
 
 Engine g;
 
-// ---- load-time fusion of the reference attention chain: observation hooks ----
-// The first full run of a blob runs its attention chains op by op and watches their
-// intermediate temps: a read of one after the chain (before it is written again), or a
-// read before any write in the run (a value carried over from the previous run), keeps
-// that chain unfused. ref_ptr reports reads, temp_get writes.
+// ---- load-time fusion of the reference attention chains: observation log ----
+// The first full run of a blob runs its attention chains op by op and logs, per op,
+// every temp it reads (with the op that last wrote that temp in this run) and every
+// temp it writes (with the device bytes written). A chain qualifies for fusion only if
+// the log shows that running it as one kernel at its last op gives what the op chain
+// gives (fusion_validate). ref_ptr reports reads, temp_get writes.
+struct ObsRead { uint32_t op, id, writer; uintptr_t p; uint64_t n; };
+struct ObsWrite { uint32_t op, id; uintptr_t p; uint64_t n; };
 struct FuseObs {
     bool on = false;
-    std::vector<int32_t> armed;      // temp id -> chain whose finished chain wrote it
-    std::vector<int32_t> inter_of;   // temp id -> chain it is an intermediate of
-    std::vector<uint8_t> written;    // temp written during this run
-    std::vector<uint8_t>* live = nullptr;
+    uint32_t op = 0;                  // op being run
+    std::vector<uint32_t> writer;     // temp id -> op that last wrote it in this run
+    std::vector<ObsRead> reads;
+    std::vector<ObsWrite> writes;
 };
 FuseObs g_obs;
 // Temps a fused chain left unwritten (its intermediates) since their last write:
@@ -180,14 +185,15 @@ inline void obs_read(uint32_t arg) {
     if (!g_obs.on || (arg & 0x8000u) || (arg & 0xE000u) == WT_REF_STATE_FLAG) return;
     const uint32_t t = arg & 0x3FFFu;
     if (t >= kMaxTemps) return;
-    int32_t c = g_obs.armed[t];
-    if (c < 0 && !g_obs.written[t]) c = g_obs.inter_of[t];
-    if (c >= 0) (*g_obs.live)[c] = 1;
+    const uint8_t* p = (arg & 0x4000u) ? (g.vtcm_pool && g.vtcm_off_arr[t] != kNone ? g.vtcm_pool + g.vtcm_off_arr[t]
+                                                                                   : nullptr)
+                                       : g.temps[t];
+    g_obs.reads.push_back({g_obs.op, t, g_obs.writer[t], reinterpret_cast<uintptr_t>(p), g.last_bytes[t]});
 }
-inline void obs_write(uint32_t id) {
-    if (!g_obs.on || id >= kMaxTemps) return;
-    g_obs.written[id] = 1;
-    g_obs.armed[id] = -1;
+inline void obs_write(uint32_t id, const uint8_t* p, uint64_t n) {
+    if (!g_obs.on || id >= kMaxTemps || !p) return;
+    g_obs.writer[id] = g_obs.op;
+    g_obs.writes.push_back({g_obs.op, id, reinterpret_cast<uintptr_t>(p), n});
 }
 
 #define ERR(...) (std::snprintf(err, errn, __VA_ARGS__), -1)
@@ -348,9 +354,8 @@ size_t ref_bytes(const wt_blob* b, uint32_t arg) {
 
 // Temp allocation (oplist_exec.c:257-335): VTCM-plan temps, static-plan temps, then
 // a 128-byte aligned bump that only grows; earlier pools are kept alive.
-uint8_t* temp_get(uint32_t id, uint32_t bytes) {
+uint8_t* temp_get_at(uint32_t id, uint32_t bytes) {
     if (id >= kMaxTemps) return nullptr;
-    obs_write(id);
     if (!g_unmat.empty()) g_unmat[id] = 0;
     if (g.vtcm_off_arr[id] != kNone) {
         const uint32_t off = g.vtcm_off_arr[id];
@@ -392,6 +397,12 @@ uint8_t* temp_get(uint32_t id, uint32_t bytes) {
     }
     g.last_bytes[id] = bytes;
     return g.temps[id];
+}
+
+uint8_t* temp_get(uint32_t id, uint32_t bytes) {
+    uint8_t* p = temp_get_at(id, bytes);
+    obs_write(id, p, bytes);
+    return p;
 }
 
 // TEMPOFF slot (oplist_exec.c:2012-2066): [cap][reserve: lo16 bump KB | hi16 VTCM KB][n][n x {tid,off,size}].
@@ -1727,34 +1738,64 @@ void keep_graph(const wt_blob* b, uint32_t first, uint32_t count, hipGraphExec_t
     g_graphs.push_back(std::move(r));
 }
 
-// ---- load-time fusion of the reference attention chain ----
-// The reference composes prefill attention from runlist ops (oplist_exec.c:1081-1194,
-// 1709-1813): batched MATMUL_F16 q.k^T (w stored [N,K]) -> BINARY mul by a constant
-// scale slot -> BINARY add of a causal mask slot (optional) -> SOFTMAX over rows ->
-// batched MATMUL_F16 p.v, heads in the batch dimension ([H, S, 128], K/V already
-// expanded to H heads). A chain whose shapes, scale and mask match, and whose
-// intermediates no later op reads (observed on the blob's first full run), runs as one
-// flash-attention launch on later runs; the other ops of the chain are skipped. Results
-// are within the fp16 tolerance of the chain, not its exact per-op roundings.
+// ---- load-time fusion of the reference attention chains ----
+// The reference composes attention from runlist ops (oplist_exec.c:1081-1194,
+// 1709-1813, 1876-1907, 2183-2231) in the forms its emitter writes
+// (compiler/tools/wtop_ops/op_matmul.cpp:36-98, op_eltwise_binary.cpp:9-67,
+// op_softmax.cpp:9-21, op_decode_state.cpp:66-80):
+//   prefill: [q = BINARY mul(q0, scale)] -> MATMUL_F16 q.k^T with the heads in the batch
+//     dimension ([H, S, 128]; k given with flags bit1, or as k^T [H, 128, S] written by
+//     a TRANSPOSE_GEN of k; one unbatched head likewise) -> [BINARY mul by a scale] ->
+//     [BINARY add or ADD_F16 of an additive mask: causal 0 / -inf, or all zero] ->
+//     SOFTMAX over rows -> MATMUL_F16 p.v;
+//   decode (scripts/surgery_decode_graph.py:143-168): KV_GATHER of a state (one op with
+//     both faces, or one op per face: kT [H, hd, P], v [H, P, hd]) -> [pre-scale] ->
+//     MATMUL_F16 q.kT -> [BINARY mul by a scale] -> [add of a mask operand of H rows of
+//     P, or of one row BROADCAST over the heads] -> SOFTMAX -> MATMUL_F16 p.v.
+// A scale is a constant slot of equal positive values or a BROADCAST of one; a prefill
+// mask is a constant slot or a BROADCAST of one over the heads. BROADCAST and
+// TRANSPOSE_GEN ops that feed the chain are members of it. Members are found by
+// dataflow (for each operand, the op that last wrote it), not by adjacency: other ops
+// may stand between them, and temp ids the emitter recycles are followed
+// (compiler/tools/wtop_ops/wtop_ops.hpp:131-146). The chain runs as one kernel at its
+// last member (the flash prefill kernel, or the split-KV decode kernel reading the ring
+// in place), each input's device pointer taken where the member reading it stands; the
+// other members are skipped.
 //
-// The decode form (scripts/surgery_decode_graph.py:143-168, oplist_exec.c:2183-2231):
-// KV_GATHER of a state (kT [H, hd, P], v [H, P, hd]; P = the ring's slots with the
-// automatic count, whose tail it zero-fills) -> batched MATMUL_F16 q.kT -> [BINARY mul
-// by a constant scale] -> [BINARY add of a mask operand [H, P], e.g. the step input's
-// -inf tail] -> SOFTMAX -> batched MATMUL_F16 p.v runs as the split-KV decode kernel
-// reading the ring in place, with the mask applied as the chain adds it (positions past
-// the count score the mask value alone). The gather's count travels as the state's
-// device counter, so the fused step stays graph-capturable.
+// A blob's first full run executes every chain op by op and logs reads and writes; a
+// chain is fused on later runs only if the log shows (fusion_validate):
+//  - each member read the value the matcher expects (nothing rewrote it in between);
+//  - no other op read an intermediate of the chain (inside its window, or after it
+//    before the temp is written again, or as run_io's output), and no member read one
+//    carried over from a previous run; a BROADCAST, TRANSPOSE_GEN or KV_GATHER member
+//    whose output other ops read still runs (it is kept, not skipped);
+//  - no other op that still runs wrote over an input's bytes between the member's read
+//    and the last member (under a TEMPOFF plan, temps of other ids may share them).
+// When the output's bytes overlap an input's at run time (a plan may place the output
+// over k, dead after the first matmul in op order), the kernel writes engine scratch
+// and the result is copied to the output. Fused results are within the fp16 tolerance
+// of the chain, not its per-op roundings.
+constexpr uint32_t kChainMax = 12;   // member ops of one chain
+constexpr uint32_t kWindow = 48;     // ops searched before / after a member for its neighbours
+
+struct ChainEdge { uint32_t op, id, from; };   // member `op` reads temp `id` last written by op `from` (kNone: an input)
+
 struct AttnChain {
-    uint32_t head = 0, len = 0, S = 0, H = 0;
-    float scale = 0.0f;
+    uint32_t mem[kChainMax] = {};
+    uint32_t n_mem = 0;
+    uint32_t head = 0, last = 0;          // first and last member (the kernel runs at `last`)
+    uint32_t S = 0, H = 0;
+    float scale = 1.0f;
     bool causal = false;
-    uint32_t q = 0, k = 0, v = 0, out = 0;
-    uint32_t inter[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    uint32_t n_inter = 0;
     bool decode = false;
-    uint32_t state = 0, KVH = 0, P = 0, n_kv = 0;   // decode: gather's state, kv heads, layout, n_kv arg
-    uint32_t mask = kNone;                           // decode: mask operand, or kNone
+    // Kernel inputs: each reference and the member op where its pointer is taken.
+    uint32_t q = 0, k = 0, v = 0, mask = kNone;
+    uint32_t q_at = 0, k_at = 0, v_at = 0, mask_at = 0;
+    bool mask_shared = false;             // decode: one mask row for every head
+    uint32_t out = 0;                     // the last member's output temp
+    uint32_t state = 0, KVH = 0, P = 0, n_kv = 0;   // decode: gathered state, kv heads, layout, n_kv arg
+    ChainEdge edge[2 * kChainMax] = {};
+    uint32_t n_edge = 0;
 };
 struct FusionPlan {
     const wt_blob* b = nullptr;
@@ -1762,16 +1803,21 @@ struct FusionPlan {
     uint64_t parse_epoch = 0;
     bool observed = false;
     std::vector<AttnChain> chains;
-    std::vector<uint8_t> live;             // per chain: an intermediate is read outside it
-    std::vector<int32_t> head_of, end_of;  // op index -> chain index (-1: none)
+    std::vector<uint8_t> blocked;          // per chain: the observed run ruled fusion out
+    std::vector<uint32_t> keep;            // per chain: members (bit k = mem[k]) that run when fused
+    std::vector<uint8_t> aliased;          // per chain: observed output bytes overlapping an input's
+    std::vector<int32_t> member_of;        // op index -> chain index (-1: none)
     uint64_t used = 0;
 };
+struct FusedIn { const uint8_t* q = nullptr; const uint8_t* k = nullptr; const uint8_t* v = nullptr;
+                 const uint8_t* mask = nullptr; };
 constexpr size_t kMaxPlans = 8;
 std::vector<FusionPlan> g_plans;
 uint64_t g_plan_tick = 0;
 const FusionPlan* g_fplan = nullptr;   // plan applied to the current run (observed, fusion on)
 FusionPlan* g_obs_plan = nullptr;      // plan being observed during the current run
-uint32_t g_skip_until = kNone;         // ops up to here belong to a chain that ran fused
+std::vector<uint8_t> g_active;         // per chain of g_fplan: running fused in the current run
+std::vector<FusedIn> g_fin;            // per chain: input pointers taken so far in the current run
 uint32_t g_run_end = 0;                // one past the current run's last op
 
 bool fusion_on() {
@@ -1785,6 +1831,7 @@ bool fusion_on() {
 bool is_temp_ref(uint32_t r) {
     return !(r & 0x8000u) && (r & 0xE000u) != WT_REF_STATE_FLAG && (r & 0x3FFFu) < kMaxTemps;
 }
+bool same_temp(uint32_t a, uint32_t b) { return is_temp_ref(a) && is_temp_ref(b) && (a & 0x3FFFu) == (b & 0x3FFFu); }
 
 // Host bytes of a constant slot reference (in-blob or external weights), or null.
 const uint16_t* slot_host_f16(const wt_blob* b, uint32_t ref, uint64_t n) {
@@ -1803,68 +1850,265 @@ const uint16_t* slot_host_f16(const wt_blob* b, uint32_t ref, uint64_t n) {
     return (p && (reinterpret_cast<uintptr_t>(p) & 1u) == 0) ? reinterpret_cast<const uint16_t*>(p) : nullptr;
 }
 
-bool match_attn_chain(const wt_blob* b, uint32_t i, AttnChain& c) {
-    if ((uint64_t)i + 4 > b->n_ops) return false;
+// Whether op o writes temp ref t, for the opcodes a chain is made of.
+bool writes_temp(const wt_op& o, uint32_t t) {
+    switch (o.opcode) {
+    case OP_MATMUL_F16: case OP_BINARY_F16: case OP_ADD_F16:
+        return o.n_args >= 3 && same_temp(o.args[2], t);
+    case OP_BROADCAST_F16: case OP_TRANSPOSE_GEN_F16: case OP_SOFTMAX_F16:
+        return o.n_args >= 2 && same_temp(o.args[1], t);
+    case OP_KV_GATHER_F16:
+        return o.n_args >= 3 && ((o.args[1] && same_temp(o.args[1], t)) || (o.args[2] && same_temp(o.args[2], t)));
+    default:
+        return false;
+    }
+}
+
+// The latest op in [lo, y) of those opcodes that writes temp t (kNone if none). Other
+// ops that may write t in between are found by the observed run's log.
+uint32_t writer_before(const wt_blob* b, uint32_t y, uint32_t t, uint32_t lo) {
+    if (!is_temp_ref(t)) return kNone;
+    for (uint32_t j = y; j-- > lo;)
+        if (writes_temp(b->ops[j], t)) return j;
+    return kNone;
+}
+
+// The first op in (x, x + kWindow] of those opcodes that reads temp t as an input;
+// *pos = the argument position.
+bool next_reader(const wt_blob* b, uint32_t x, uint32_t t, uint32_t* at, uint32_t* pos) {
+    const uint32_t hi = (uint32_t)std::min<uint64_t>((uint64_t)x + kWindow, b->n_ops - 1u);
+    for (uint32_t j = x + 1; j <= hi; ++j) {
+        const wt_op& o = b->ops[j];
+        uint32_t np = 0;
+        switch (o.opcode) {
+        case OP_MATMUL_F16: case OP_BINARY_F16: case OP_ADD_F16: np = 2; break;
+        case OP_SOFTMAX_F16: case OP_BROADCAST_F16: case OP_TRANSPOSE_GEN_F16: np = 1; break;
+        default: break;
+        }
+        for (uint32_t p = 0; p < np && p < o.n_args; ++p)
+            if (same_temp(o.args[p], t)) { *at = j; *pos = p; return true; }
+    }
+    return false;
+}
+
+// A BROADCAST that repeats its n_in-element input `reps` times back to back (numpy
+// broadcast of one leading axis of 1; dims of 4, left- or right-aligned).
+bool bcast_tiles(const wt_op& B, uint64_t n_in, uint32_t reps) {
+    if (B.n_args < 12 || B.args[3] != n_in || (uint64_t)B.args[2] != n_in * reps) return false;
+    const uint32_t* id = &B.args[4];
+    const uint32_t* od = &B.args[8];
+    uint32_t j = 0;
+    while (j < 4 && id[j] == od[j]) ++j;
+    if (j == 4) return reps == 1;
+    uint64_t outer = 1;
+    for (uint32_t i = 0; i < j; ++i) outer *= od[i];
+    if (outer != 1 || id[j] != 1 || od[j] != reps) return false;
+    for (uint32_t i = j + 1; i < 4; ++i)
+        if (id[i] != od[i]) return false;
+    return true;
+}
+
+struct Matcher {
+    const wt_blob* b;
+    const std::vector<int32_t>& member_of;   // ops claimed by earlier chains
+    AttnChain c;
+    uint32_t lo = 0;                         // lowest op index searched for a member
+
+    bool add(uint32_t op) {
+        for (uint32_t k = 0; k < c.n_mem; ++k)
+            if (c.mem[k] == op) return true;
+        if (c.n_mem >= kChainMax || member_of[op] >= 0) return false;
+        c.mem[c.n_mem++] = op;
+        return true;
+    }
+    bool edge(uint32_t op, uint32_t ref, uint32_t from) {
+        if (!is_temp_ref(ref)) return true;
+        if (c.n_edge >= 2 * kChainMax) return false;
+        c.edge[c.n_edge++] = {op, ref & 0x3FFFu, from};
+        return true;
+    }
+    // A BROADCAST written into operand `ref` of op `at`: made a member (if no earlier
+    // chain holds it) and recorded as the operand's writer.
+    bool bcast_member(uint32_t at, uint32_t ref, uint32_t j) {
+        if (member_of[j] < 0 && !add(j)) return false;
+        return edge(at, ref, j);
+    }
+    // The positive scale of operand `ref` (n elements) of op `at`: a slot of n equal
+    // values, or a BROADCAST of a slot of equal values.
+    bool scale_source(uint32_t at, uint32_t ref, uint64_t n, float* sc) {
+        const uint16_t* p = nullptr;
+        uint64_t m = n;
+        uint32_t j = kNone;
+        if (ref & 0x8000u) {
+            p = slot_host_f16(b, ref, n);
+        } else if (is_temp_ref(ref)) {
+            j = writer_before(b, at, ref, lo);
+            if (j == kNone) return false;
+            const wt_op& B = b->ops[j];
+            if (B.opcode != OP_BROADCAST_F16 || B.n_args < 12 || B.args[2] != n || !B.args[3]) return false;
+            m = B.args[3];
+            p = slot_host_f16(b, B.args[0], m);
+        }
+        if (!p) return false;
+        for (uint64_t e = 1; e < m; ++e)
+            if (p[e] != p[0]) return false;
+        const float v = (float)__builtin_bit_cast(_Float16, p[0]);
+        if (!(v > 0.0f && v < INFINITY)) return false;
+        *sc = v;
+        return j == kNone || bcast_member(at, ref, j);
+    }
+    // q, or a pre-scaled q: BINARY mul of q0 by a constant scale (written before `at`).
+    bool query(uint32_t at, uint32_t qref, uint64_t nq, bool* pre) {
+        *pre = false;
+        c.q = qref;
+        c.q_at = at;
+        const uint32_t j = writer_before(b, at, qref, lo);
+        if (j != kNone && member_of[j] < 0) {
+            const wt_op& P = b->ops[j];
+            if (P.opcode == OP_BINARY_F16 && P.n_args >= 5 && P.args[4] == 2u && P.args[3] == nq) {
+                for (uint32_t side = 0; side < 2 && !*pre; ++side) {
+                    const uint32_t q0 = P.args[side], sref = P.args[1 - side];
+                    if (!is_temp_ref(q0) && !(q0 & 0x8000u)) continue;
+                    const uint32_t n0 = c.n_mem, e0 = c.n_edge;
+                    float sc;
+                    if (scale_source(j, sref, nq, &sc)) {
+                        *pre = true;
+                        c.scale = sc;
+                        c.q = q0;
+                        c.q_at = j;
+                        if (!add(j) || !edge(j, q0, kNone)) return false;
+                    } else {
+                        c.n_mem = n0;
+                        c.n_edge = e0;
+                    }
+                }
+            }
+        }
+        return edge(at, qref, *pre ? j : kNone);
+    }
+    // Window bounds and ops that would invalidate the chain's inputs unseen by the log.
+    bool finish() {
+        c.head = c.last = c.mem[0];
+        for (uint32_t k = 1; k < c.n_mem; ++k) {
+            c.head = std::min(c.head, c.mem[k]);
+            c.last = std::max(c.last, c.mem[k]);
+        }
+        // The kernel reads the ring at the last member; the gathers read it where they
+        // stand: no op between them may append to a ring.
+        uint32_t ring0 = c.last;
+        for (uint32_t k = 0; k < c.n_mem; ++k)
+            if (b->ops[c.mem[k]].opcode == OP_KV_GATHER_F16) ring0 = std::min(ring0, c.mem[k]);
+        for (uint32_t o = c.head; o <= c.last; ++o) {
+            const uint16_t oc = b->ops[o].opcode;
+            if (oc == OP_DMA || oc == OP_SPILL || oc == OP_FILL) return false;
+            if (c.decode && o > ring0 && (oc == OP_KV_APPEND_F16 || oc == OP_KV_APPEND_N_F16 ||
+                                          oc == OP_QK_ROPE_KV_F16 || oc == OP_ATTN_DECODE_QKV_F16))
+                return false;
+        }
+        return true;
+    }
+};
+
+// Prefill chain whose q.k^T MATMUL_F16 is op i.
+bool match_attn_chain(Matcher& m, uint32_t i) {
+    const wt_blob* b = m.b;
+    AttnChain& c = m.c;
     const wt_op& A = b->ops[i];
     if (A.opcode != OP_MATMUL_F16 || A.n_args < 7) return false;
-    const uint32_t S = A.args[3], fl = A.args[6], H = fl >> 16;
-    if (S == 0 || A.args[4] != 128 || A.args[5] != S || (fl & 0xFFFFu) != 6u || H == 0) return false;
+    const uint32_t S = A.args[3], fl = A.args[6];
+    const bool batched = (fl & 4u) != 0;
+    const uint32_t H = batched ? fl >> 16 : 1u;
+    if (!S || A.args[4] != 128 || A.args[5] != S || !H || (fl & 1u) || (!batched && (fl >> 16))) return false;
     const uint64_t n = (uint64_t)H * S * S;
     if (n > 0xFFFFFFFFull || !is_temp_ref(A.args[2])) return false;
     c = AttnChain{};
-    c.head = i; c.S = S; c.H = H;
-    c.q = A.args[0]; c.k = A.args[1];
-    c.inter[c.n_inter++] = A.args[2];
-    // BINARY mul by a slot holding one positive finite value n times
-    uint32_t j = i + 1;
-    const wt_op& B = b->ops[j];
-    if (B.opcode != OP_BINARY_F16 || B.n_args < 5 || B.args[4] != 2u || B.args[0] != A.args[2] ||
-        B.args[3] != n || !is_temp_ref(B.args[2]))
-        return false;
-    const uint16_t* sc = slot_host_f16(b, B.args[1], n);
-    if (!sc) return false;
-    for (uint64_t e = 1; e < n; ++e)
-        if (sc[e] != sc[0]) return false;
-    c.scale = (float)__builtin_bit_cast(_Float16, sc[0]);
-    if (!(c.scale > 0.0f && c.scale < INFINITY)) return false;
-    uint32_t prev = B.args[2];
-    c.inter[c.n_inter++] = prev;
-    ++j;
-    // optional BINARY add of a mask slot: causal (0 where key <= query, -inf above), or all 0
-    const wt_op& C = b->ops[j];
-    if (C.opcode == OP_BINARY_F16 && C.n_args >= 5 && C.args[4] == 0u && C.args[0] == prev && C.args[3] == n &&
-        is_temp_ref(C.args[2])) {
-        const uint16_t* mk = slot_host_f16(b, C.args[1], n);
-        if (!mk) return false;
-        bool causal = true, zeros = true;
-        for (uint64_t e = 0; e < n && (causal || zeros); ++e) {
-            const uint32_t row = (uint32_t)((e / S) % S), col = (uint32_t)(e % S);
-            const bool zero = (mk[e] & 0x7FFFu) == 0;
-            zeros = zeros && zero;
-            causal = causal && (col <= row ? zero : mk[e] == 0xFC00u);
-        }
-        if (!causal && !zeros) return false;
-        c.causal = causal && S > 1;
-        prev = C.args[2];
-        c.inter[c.n_inter++] = prev;
-        ++j;
+    c.S = S; c.H = H;
+    m.lo = i > kWindow ? i - kWindow : 0;
+    if (!m.add(i)) return false;
+    // k: [H, S, 128] read transposed (flags bit1), or k^T [H, 128, S] from a TRANSPOSE_GEN
+    if (fl & 2u) {
+        if (!is_temp_ref(A.args[1]) && !(A.args[1] & 0x8000u)) return false;
+        c.k = A.args[1];
+        c.k_at = i;
+        if (!m.edge(i, A.args[1], kNone)) return false;
+    } else {
+        const uint32_t j = writer_before(b, i, A.args[1], m.lo);
+        if (j == kNone) return false;
+        const wt_op& T = b->ops[j];
+        if (T.opcode != OP_TRANSPOSE_GEN_F16 || T.n_args < 8) return false;
+        const uint32_t rk = T.args[2], perm = T.args[7];
+        const bool ok3 = rk == 3 && T.args[3] == H && T.args[4] == S && T.args[5] == 128 &&
+                         (perm & 0xFFFFFFu) == (0u | (2u << 8) | (1u << 16));
+        const bool ok2 = rk == 2 && H == 1 && T.args[3] == S && T.args[4] == 128 && (perm & 0xFFFFu) == (1u | (0u << 8));
+        if (!(ok3 || ok2) || (!is_temp_ref(T.args[0]) && !(T.args[0] & 0x8000u))) return false;
+        if (!m.add(j) || !m.edge(j, T.args[0], kNone) || !m.edge(i, A.args[1], j)) return false;
+        c.k = T.args[0];
+        c.k_at = j;
     }
-    if ((uint64_t)j + 2 > b->n_ops) return false;
+    bool pre = false;
+    if (!is_temp_ref(A.args[0]) && !(A.args[0] & 0x8000u)) return false;
+    if (!m.query(i, A.args[0], (uint64_t)H * S * 128u, &pre)) return false;
+    // scale and mask, in either order, then SOFTMAX
+    uint32_t prev = A.args[2], at = i, j = 0, pos = 0;
+    bool post = false, masked = false;
+    for (;;) {
+        if (!next_reader(b, at, prev, &j, &pos)) return false;
+        const wt_op& X = b->ops[j];
+        if (X.opcode == OP_SOFTMAX_F16) break;
+        if (pos > 1 || X.args[3] != n || !is_temp_ref(X.args[2])) return false;
+        const uint32_t other = X.args[1 - pos];
+        if (X.opcode == OP_BINARY_F16 && X.n_args >= 5 && X.args[4] == 2u && !post && !pre) {
+            if (!m.scale_source(j, other, n, &c.scale)) return false;
+            post = true;
+        } else if (((X.opcode == OP_BINARY_F16 && X.n_args >= 5 && X.args[4] == 0u) ||
+                    (X.opcode == OP_ADD_F16 && X.n_args >= 4)) && !masked) {
+            // additive mask [H, S, S]: a slot, or a BROADCAST of an [S, S] slot over the heads
+            const uint16_t* mk = nullptr;
+            if (other & 0x8000u) {
+                mk = slot_host_f16(b, other, n);
+            } else {
+                const uint32_t bj = writer_before(b, j, other, m.lo);
+                if (bj == kNone || b->ops[bj].opcode != OP_BROADCAST_F16 || !bcast_tiles(b->ops[bj], (uint64_t)S * S, H))
+                    return false;
+                mk = slot_host_f16(b, b->ops[bj].args[0], (uint64_t)S * S);
+                if (mk && !m.bcast_member(j, other, bj)) return false;
+            }
+            if (!mk) return false;
+            const uint64_t nm = (other & 0x8000u) ? n : (uint64_t)S * S;
+            bool causal = true, zeros = true;
+            for (uint64_t e = 0; e < nm && (causal || zeros); ++e) {
+                const uint32_t row = (uint32_t)((e / S) % S), col = (uint32_t)(e % S);
+                const bool zero = (mk[e] & 0x7FFFu) == 0;
+                zeros = zeros && zero;
+                causal = causal && (col <= row ? zero : mk[e] == 0xFC00u);
+            }
+            if (!causal && !zeros) return false;
+            c.causal = causal && S > 1;
+            masked = true;
+        } else {
+            return false;
+        }
+        if (!m.add(j) || !m.edge(j, prev, at)) return false;
+        prev = X.args[2];
+        at = j;
+    }
     const wt_op& D = b->ops[j];
-    if (D.opcode != OP_SOFTMAX_F16 || D.n_args < 4 || D.args[0] != prev || D.args[2] != H * S || D.args[3] != S ||
-        !is_temp_ref(D.args[1]))
+    if (D.n_args < 4 || D.args[0] != prev || D.args[2] != H * S || D.args[3] != S || !is_temp_ref(D.args[1]))
         return false;
-    c.inter[c.n_inter++] = D.args[1];
-    const wt_op& E = b->ops[j + 1];
-    if (E.opcode != OP_MATMUL_F16 || E.n_args < 7 || E.args[0] != D.args[1] || E.args[3] != S || E.args[4] != S ||
-        E.args[5] != 128 || E.args[6] != ((H << 16) | 4u) || !is_temp_ref(E.args[2]))
+    if (!m.add(j) || !m.edge(j, prev, at)) return false;
+    prev = D.args[1];
+    at = j;
+    if (!next_reader(b, at, prev, &j, &pos)) return false;
+    const wt_op& E = b->ops[j];
+    if (E.opcode != OP_MATMUL_F16 || E.n_args < 7 || pos != 0 || E.args[3] != S || E.args[4] != S ||
+        E.args[5] != 128 || E.args[6] != (batched ? ((H << 16) | 4u) : 0u) || !is_temp_ref(E.args[2]) ||
+        (!is_temp_ref(E.args[1]) && !(E.args[1] & 0x8000u)))
         return false;
+    if (!m.add(j) || !m.edge(j, prev, at) || !m.edge(j, E.args[1], kNone)) return false;
     c.v = E.args[1];
+    c.v_at = j;
     c.out = E.args[2];
-    c.len = j + 2 - i;
-    for (uint32_t t = 0; t < c.n_inter; ++t)   // inputs must come from outside the chain
-        if (c.inter[t] == c.q || c.inter[t] == c.k || c.inter[t] == c.v) return false;
-    return true;
+    return m.finish() && c.last == j;
 }
 
 // Bytes of state idx in the blob's STATE table (0 if absent).
@@ -1883,81 +2127,121 @@ uint32_t blob_state_bytes(const wt_blob* b, uint32_t idx) {
     return 0;
 }
 
-bool match_decode_chain(const wt_blob* b, uint32_t i, AttnChain& c) {
-    if ((uint64_t)i + 4 > b->n_ops) return false;
-    const wt_op& G = b->ops[i];
-    if (G.opcode != OP_KV_GATHER_F16 || G.n_args < 7) return false;
-    const uint32_t st = G.args[0], kT = G.args[1], vv = G.args[2], n_kv = G.args[3];
-    const uint32_t H = G.args[4], KVH = G.args[5], hd = G.args[6];
-    if ((st & 0xE000u) != WT_REF_STATE_FLAG || hd != 128 || !KVH || !H || H % KVH || H > 0xFFFFu) return false;
+// Decode chain whose q.kT MATMUL_F16 (one query row) is op i.
+bool match_decode_chain(Matcher& m, uint32_t i) {
+    const wt_blob* b = m.b;
+    AttnChain& c = m.c;
+    const wt_op& A = b->ops[i];
+    if (A.opcode != OP_MATMUL_F16 || A.n_args < 7 || A.args[3] != 1u || A.args[4] != 128u) return false;
+    const uint32_t P = A.args[5], H = A.args[6] >> 16, hd = 128;
+    if (!P || !H || A.args[6] != ((H << 16) | 4u) || !is_temp_ref(A.args[1]) || !is_temp_ref(A.args[2])) return false;
+    c = AttnChain{};
+    c.decode = true;
+    c.S = 1; c.H = H; c.P = P;
+    m.lo = i > kWindow ? i - kWindow : 0;
+    if (!m.add(i)) return false;
+    // the kT face: a KV_GATHER of a state
+    const uint32_t gk = writer_before(b, i, A.args[1], m.lo);
+    if (gk == kNone) return false;
+    const wt_op& G = b->ops[gk];
+    if (G.opcode != OP_KV_GATHER_F16 || G.n_args < 7 || !G.args[1] || !same_temp(G.args[1], A.args[1])) return false;
+    const uint32_t st = G.args[0], n_kv = G.args[3], KVH = G.args[5];
+    if ((st & 0xE000u) != WT_REF_STATE_FLAG || G.args[4] != H || G.args[6] != hd || !KVH || H % KVH ||
+        H > 0xFFFFu)
+        return false;
     const uint32_t rep = H / KVH;
     if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return false;
-    if (!kT || !vv || !is_temp_ref(kT) || !is_temp_ref(vv) || (kT & 0x3FFFu) == (vv & 0x3FFFu)) return false;
-    uint32_t P = n_kv;
+    uint32_t Pg = n_kv;
     if (n_kv == WT_KV_POS_AUTO) {
         const uint32_t bytes = blob_state_bytes(b, st & 0x1FFFu), slot = KVH * hd * 4u;
         if (!bytes || bytes % slot) return false;
-        P = bytes / slot;
+        Pg = bytes / slot;
     }
-    if (!P) return false;
+    if (Pg != P) return false;
+    c.state = st; c.KVH = KVH; c.n_kv = n_kv;
+    if (!m.add(gk) || !m.edge(i, A.args[1], gk)) return false;
     const uint64_t n = (uint64_t)H * P;
-    c = AttnChain{};
-    c.decode = true;
-    c.head = i; c.H = H; c.KVH = KVH; c.P = P; c.n_kv = n_kv; c.state = st; c.S = 1;
-    c.inter[c.n_inter++] = kT;
-    c.inter[c.n_inter++] = vv;
-    uint32_t j = i + 1;
-    const wt_op& A = b->ops[j];
-    if (A.opcode != OP_MATMUL_F16 || A.n_args < 7 || A.args[1] != kT || A.args[3] != 1u || A.args[4] != hd ||
-        A.args[5] != P || A.args[6] != ((H << 16) | 4u) || !is_temp_ref(A.args[2]))
-        return false;
-    c.q = A.args[0];
-    uint32_t prev = A.args[2];
-    c.inter[c.n_inter++] = prev;
-    ++j;
-    c.scale = 1.0f;
-    if ((uint64_t)j + 3 > b->n_ops) return false;
-    const wt_op& B = b->ops[j];   // optional: BINARY mul by a constant slot
-    if (B.opcode == OP_BINARY_F16 && B.n_args >= 5 && B.args[4] == 2u && B.args[0] == prev && B.args[3] == n &&
-        is_temp_ref(B.args[2])) {
-        const uint16_t* sc = slot_host_f16(b, B.args[1], n);
-        if (!sc) return false;
-        for (uint64_t e = 1; e < n; ++e)
-            if (sc[e] != sc[0]) return false;
-        c.scale = (float)__builtin_bit_cast(_Float16, sc[0]);
-        if (!(c.scale > 0.0f && c.scale < INFINITY)) return false;
-        prev = B.args[2];
-        c.inter[c.n_inter++] = prev;
-        ++j;
+    bool pre = false;
+    if (!is_temp_ref(A.args[0]) && !(A.args[0] & 0x8000u)) return false;
+    if (!m.query(i, A.args[0], (uint64_t)H * hd, &pre)) return false;
+    uint32_t prev = A.args[2], at = i, j = 0, pos = 0;
+    bool post = false, masked = false;
+    for (;;) {
+        if (!next_reader(b, at, prev, &j, &pos)) return false;
+        const wt_op& X = b->ops[j];
+        if (X.opcode == OP_SOFTMAX_F16) break;
+        if (pos > 1 || X.args[3] != n || !is_temp_ref(X.args[2])) return false;
+        const uint32_t other = X.args[1 - pos];
+        if (X.opcode == OP_BINARY_F16 && X.n_args >= 5 && X.args[4] == 2u && !post && !pre) {
+            if (!m.scale_source(j, other, n, &c.scale)) return false;
+            post = true;
+        } else if (((X.opcode == OP_BINARY_F16 && X.n_args >= 5 && X.args[4] == 0u) ||
+                    (X.opcode == OP_ADD_F16 && X.n_args >= 4)) && !masked) {
+            // the mask: one row of P BROADCAST over the heads after q.kT (read in place), or
+            // H rows (a broadcast written earlier, e.g. once for every layer, is read as it
+            // stands: its input row need not outlive it)
+            const uint32_t bj = is_temp_ref(other) ? writer_before(b, j, other, m.lo) : kNone;
+            if (bj != kNone && bj > i && m.member_of[bj] < 0 && b->ops[bj].opcode == OP_BROADCAST_F16 &&
+                bcast_tiles(b->ops[bj], P, H) && (is_temp_ref(b->ops[bj].args[0]) || (b->ops[bj].args[0] & 0x8000u))) {
+                if (!m.bcast_member(j, other, bj) || !m.edge(bj, b->ops[bj].args[0], kNone)) return false;
+                c.mask = b->ops[bj].args[0];
+                c.mask_at = bj;
+                c.mask_shared = true;
+            } else {
+                if (!is_temp_ref(other) && !(other & 0x8000u)) return false;
+                if (!m.edge(j, other, kNone)) return false;
+                c.mask = other;
+                c.mask_at = j;
+            }
+            masked = true;
+        } else {
+            return false;
+        }
+        if (!m.add(j) || !m.edge(j, prev, at)) return false;
+        prev = X.args[2];
+        at = j;
     }
-    const wt_op& C = b->ops[j];   // optional: BINARY add of a mask operand [H, P]
-    if (C.opcode == OP_BINARY_F16 && C.n_args >= 5 && C.args[4] == 0u && C.args[0] == prev && C.args[3] == n &&
-        is_temp_ref(C.args[2])) {
-        c.mask = C.args[1];
-        prev = C.args[2];
-        c.inter[c.n_inter++] = prev;
-        ++j;
-    } else if (n_kv == WT_KV_POS_AUTO && P > 1) {
-        return false;   // without a mask the zero-filled tail takes part in the softmax
-    }
-    if ((uint64_t)j + 2 > b->n_ops) return false;
+    if (n_kv == WT_KV_POS_AUTO && P > 1 && !masked) return false;   // the zero-filled tail would take part
     const wt_op& D = b->ops[j];
-    if (D.opcode != OP_SOFTMAX_F16 || D.n_args < 4 || D.args[0] != prev || D.args[2] != H || D.args[3] != P ||
-        !is_temp_ref(D.args[1]))
+    if (D.n_args < 4 || D.args[0] != prev || D.args[2] != H || D.args[3] != P || !is_temp_ref(D.args[1]))
         return false;
-    c.inter[c.n_inter++] = D.args[1];
-    const wt_op& E = b->ops[j + 1];
-    if (E.opcode != OP_MATMUL_F16 || E.n_args < 7 || E.args[0] != D.args[1] || E.args[1] != vv || E.args[3] != 1u ||
-        E.args[4] != P || E.args[5] != hd || E.args[6] != ((H << 16) | 4u) || !is_temp_ref(E.args[2]))
+    if (!m.add(j) || !m.edge(j, prev, at)) return false;
+    prev = D.args[1];
+    at = j;
+    if (!next_reader(b, at, prev, &j, &pos)) return false;
+    const wt_op& E = b->ops[j];
+    if (E.opcode != OP_MATMUL_F16 || E.n_args < 7 || pos != 0 || E.args[3] != 1u || E.args[4] != P ||
+        E.args[5] != hd || E.args[6] != ((H << 16) | 4u) || !is_temp_ref(E.args[2]) || !is_temp_ref(E.args[1]))
         return false;
+    // the v face: the same gather, or a second KV_GATHER of the same state and layout
+    const uint32_t gv = writer_before(b, j, E.args[1], m.lo);
+    if (gv == kNone) return false;
+    const wt_op& V = b->ops[gv];
+    if (V.opcode != OP_KV_GATHER_F16 || V.n_args < 7 || !V.args[2] || !same_temp(V.args[2], E.args[1]) ||
+        V.args[0] != st || V.args[3] != n_kv || V.args[4] != H || V.args[5] != KVH || V.args[6] != hd)
+        return false;
+    if (!m.add(gv) || !m.edge(j, E.args[1], gv) || !m.add(j) || !m.edge(j, prev, at)) return false;
+    c.v = E.args[1];
+    c.v_at = j;
     c.out = E.args[2];
-    c.len = j + 2 - i;
-    for (uint32_t t = 0; t < c.n_inter; ++t)   // inputs must come from outside the chain
-        if ((c.q & 0x3FFFu) == (c.inter[t] & 0x3FFFu) && is_temp_ref(c.q)) return false;
-    if (c.mask != kNone && is_temp_ref(c.mask))
-        for (uint32_t t = 0; t < c.n_inter; ++t)
-            if ((c.mask & 0x3FFFu) == (c.inter[t] & 0x3FFFu)) return false;
-    return true;
+    return m.finish() && c.last == j;
+}
+
+// The attention chains of a blob, in op order (each op a member of at most one chain).
+std::vector<AttnChain> scan_chains(const wt_blob* b, std::vector<int32_t>& member_of) {
+    std::vector<AttnChain> chains;
+    member_of.assign(b->n_ops, -1);
+    for (uint32_t i = 0; i < b->n_ops; ++i) {
+        Matcher m{b, member_of, AttnChain{}};
+        if (!match_attn_chain(m, i)) {
+            Matcher d{b, member_of, AttnChain{}};
+            if (!match_decode_chain(d, i)) continue;
+            m.c = d.c;
+        }
+        for (uint32_t k = 0; k < m.c.n_mem; ++k) member_of[m.c.mem[k]] = (int32_t)chains.size();
+        chains.push_back(m.c);
+    }
+    return chains;
 }
 
 // The plan of a blob (created, with its chains detected, on first sight of the blob as
@@ -1977,23 +2261,114 @@ FusionPlan* fusion_plan(const wt_blob* b) {
     drop_graphs();
     FusionPlan p;
     p.b = b; p.n_ops = b->n_ops; p.parse_epoch = ep; p.used = ++g_plan_tick;
-    p.head_of.assign(b->n_ops, -1);
-    p.end_of.assign(b->n_ops, -1);
-    for (uint32_t i = 0; i < b->n_ops; ++i) {
-        AttnChain c;
-        if (!match_attn_chain(b, i, c) && !match_decode_chain(b, i, c)) continue;
-        p.head_of[i] = (int32_t)p.chains.size();
-        p.end_of[i + c.len - 1] = (int32_t)p.chains.size();
-        p.chains.push_back(c);
-        i += c.len - 1;
-    }
-    p.live.assign(p.chains.size(), 0);
+    p.chains = scan_chains(b, p.member_of);
+    p.blocked.assign(p.chains.size(), 0);
+    p.keep.assign(p.chains.size(), 0);
+    p.aliased.assign(p.chains.size(), 0);
     g.chains_found += p.chains.size();
     g_plans.push_back(std::move(p));
     return &g_plans.back();
 }
 
-int run_fused_decode(const wt_blob* b, const AttnChain& c, char* err, size_t errn) {
+int member_index(const AttnChain& c, uint32_t op) {
+    for (uint32_t k = 0; k < c.n_mem; ++k)
+        if (c.mem[k] == op) return (int)k;
+    return -1;
+}
+
+bool ranges_overlap(uintptr_t a, uint64_t na, uintptr_t b, uint64_t nb) {
+    return na && nb && a < b + nb && b < a + na;
+}
+
+// Decides, from the observed run's log, which chains may run fused and which of their
+// members still run then (the rules above fusion's matchers).
+void fusion_validate(FusionPlan& p) {
+    for (size_t ci = 0; ci < p.chains.size(); ++ci) {
+        const AttnChain& c = p.chains[ci];
+        bool blocked = false;
+        uint32_t keep = 0;
+        // 1. each member read what the matcher expects
+        for (const ObsRead& r : g_obs.reads) {
+            if (r.op < c.head || r.op > c.last || member_index(c, r.op) < 0) continue;
+            const ChainEdge* e = nullptr;
+            for (uint32_t k = 0; k < c.n_edge && !e; ++k)
+                if (c.edge[k].op == r.op && c.edge[k].id == r.id) e = &c.edge[k];
+            if (!e) { blocked = true; break; }
+            if (e->from != kNone ? r.writer != e->from : (r.writer != kNone && member_index(c, r.writer) >= 0)) {
+                blocked = true;
+                break;
+            }
+        }
+        // 2. members' outputs read elsewhere (the last member's output excepted)
+        for (const ObsRead& r : g_obs.reads) {
+            if (blocked) break;
+            if (r.writer == kNone || r.writer == c.last) continue;
+            const int mw = member_index(c, r.writer);
+            if (mw < 0 || member_index(c, r.op) >= 0) continue;
+            const uint16_t oc = p.b->ops[r.writer].opcode;
+            if (oc == OP_BROADCAST_F16 || oc == OP_TRANSPOSE_GEN_F16 || oc == OP_KV_GATHER_F16) keep |= 1u << mw;
+            else blocked = true;
+        }
+        // 3. inputs' bytes intact from their read to the last member, and the output's
+        //    overlap with them (then the kernel writes scratch)
+        bool aliased = false;
+        for (uint32_t k = 0; k < c.n_edge && !blocked; ++k) {
+            const ChainEdge& e = c.edge[k];
+            if (e.from != kNone) continue;
+            const ObsRead* r = nullptr;
+            for (const ObsRead& x : g_obs.reads)
+                if (x.op == e.op && x.id == e.id) { r = &x; break; }
+            if (!r || !r->p) { blocked = true; break; }
+            for (const ObsWrite& w : g_obs.writes) {
+                if (w.op <= e.op || w.op > c.last || !ranges_overlap(w.p, w.n, r->p, r->n)) continue;
+                if (w.op == c.last) { aliased = true; continue; }
+                const int mw = member_index(c, w.op);
+                if (mw >= 0 && !((keep >> mw) & 1u)) continue;   // a skipped member writes nothing when fused
+                blocked = true;
+                break;
+            }
+        }
+        p.blocked[ci] = blocked;
+        p.keep[ci] = keep;
+        p.aliased[ci] = aliased;
+    }
+}
+
+// The fused kernel's output: the chain's output temp, or, when its bytes overlap an
+// input's, engine scratch copied to it after the kernel.
+struct FusedOut { __half* dst = nullptr; __half* kernel = nullptr; uint64_t bytes = 0; };
+int fused_out(const AttnChain& c, uint64_t bytes, const std::pair<const uint8_t*, uint64_t>* in, int n_in,
+              FusedOut& o, char* err, size_t errn) {
+    if (bytes > 0xFFFFFFFFull) return ERR("fused attention output too large");
+    o.dst = reinterpret_cast<__half*>(temp_get(c.out, (uint32_t)bytes));
+    if (!o.dst) return ERR("fused attention output alloc");
+    o.kernel = o.dst;
+    o.bytes = bytes;
+    bool alias = false;
+    for (int k = 0; k < n_in; ++k)
+        alias = alias || ranges_overlap(reinterpret_cast<uintptr_t>(o.dst), bytes,
+                                        reinterpret_cast<uintptr_t>(in[k].first), in[k].second);
+    if (!alias) return 0;
+    if (g.fuse_scratch_cap < bytes) {
+        if (g.fuse_scratch) dev_free(g.fuse_scratch);
+        g.fuse_scratch = nullptr;
+        g.fuse_scratch_cap = 0;
+        if (dev_malloc(reinterpret_cast<void**>(&g.fuse_scratch), bytes) != hipSuccess)
+            return ERR("fused attention scratch alloc");
+        g.fuse_scratch_cap = bytes;
+    }
+    o.kernel = reinterpret_cast<__half*>(g.fuse_scratch);
+    g.fused_alias_runs++;
+    return 0;
+}
+
+int fused_out_done(const FusedOut& o, char* err, size_t errn) {
+    if (o.kernel == o.dst) return 0;
+    if (copy_d2d(o.dst, o.kernel, o.bytes) != hipSuccess) return ERR("fused attention output copy");
+    return 0;
+}
+
+int run_fused_decode(const wt_blob* b, const AttnChain& c, const FusedIn& in, char* err, size_t errn) {
     const uint32_t H = c.H, KVH = c.KVH, hd = 128, P = c.P;
     State* s = state_kv(c.state, KVH * hd, err, errn);
     if (!s) return -1;
@@ -2009,34 +2384,81 @@ int run_fused_decode(const wt_blob* b, const AttnChain& c, char* err, size_t err
         return ERR("kv gather n_kv %u > nslots %u", n_kv, s->nslots);
     }
     if (kv_check(*s, n_kv, err, errn)) return -1;
-    const __half* q = reinterpret_cast<const __half*>(ref_ptr(b, c.q));
-    const __half* mask = c.mask != kNone ? reinterpret_cast<const __half*>(ref_ptr(b, c.mask)) : nullptr;
-    __half* o = reinterpret_cast<__half*>(temp_get(c.out, H * hd * 2u));
-    if (!q || !o || (c.mask != kNone && !mask)) return ERR("fused decode attention ref fail");
+    const __half* q = reinterpret_cast<const __half*>(in.q);
+    const __half* mask = c.mask != kNone ? reinterpret_cast<const __half*>(in.mask) : nullptr;
+    if (!q || (c.mask != kNone && !mask)) return ERR("fused decode attention ref fail");
+    const uint64_t qn = (uint64_t)H * hd * 2u, mn = c.mask != kNone ? (uint64_t)(c.mask_shared ? 1u : H) * P * 2u : 0;
     const size_t qb = ref_bytes(b, c.q), mb = c.mask != kNone ? ref_bytes(b, c.mask) : 0;
-    if ((qb && qb < (uint64_t)H * hd * 2u) || (mb && mb < (uint64_t)H * P * 2u))
-        return ERR("fused decode attention operand too small");
+    if ((qb && qb < qn) || (mb && mb < mn)) return ERR("fused decode attention operand too small");
+    const std::pair<const uint8_t*, uint64_t> ins[2] = {{in.q, qn}, {in.mask, mn}};
     if (attn_workspace(attn_decode_work_floats(autopos ? s->nslots : n_kv, H, hd), err, errn)) return -1;
-    CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o, autopos ? 0u : n_kv,
+    FusedOut o;
+    if (fused_out(c, (uint64_t)H * hd * 2u, ins, 2, o, err, errn)) return -1;
+    CHECK_LAUNCH(launch_attn_decode(q, s->dev, s->slot_bytes, s->nslots, o.kernel, autopos ? 0u : n_kv,
                                     autopos ? g.counters_dev + si : nullptr, H, KVH, hd, c.scale, g.attn_work,
-                                    g.attn_work_floats, g.stream, mask, mask ? P : 0u, n_kv));
-    return 0;
+                                    g.attn_work_floats, g.stream, mask, mask ? P : 0u, n_kv, c.mask_shared));
+    return fused_out_done(o, err, errn);
 }
 
-int run_fused_attn(const wt_blob* b, const AttnChain& c, char* err, size_t errn) {
-    if (c.decode) return run_fused_decode(b, c, err, errn);
+int run_fused_attn(const wt_blob* b, const AttnChain& c, const FusedIn& in, char* err, size_t errn) {
+    if (c.decode) return run_fused_decode(b, c, in, err, errn);
     const uint32_t S = c.S, H = c.H;
     const uint64_t bytes = (uint64_t)S * H * 128u * 2u;
-    const __half* q = reinterpret_cast<const __half*>(ref_ptr(b, c.q));
-    const __half* k = reinterpret_cast<const __half*>(ref_ptr(b, c.k));
-    const __half* v = reinterpret_cast<const __half*>(ref_ptr(b, c.v));
-    __half* o = reinterpret_cast<__half*>(temp_get(c.out, (uint32_t)bytes));
-    if (!q || !k || !v || !o) return ERR("fused attention ref fail");
+    const __half* q = reinterpret_cast<const __half*>(in.q);
+    const __half* k = reinterpret_cast<const __half*>(in.k);
+    const __half* v = reinterpret_cast<const __half*>(in.v);
+    if (!q || !k || !v) return ERR("fused attention ref fail");
     const size_t qb = ref_bytes(b, c.q), kb = ref_bytes(b, c.k), vb = ref_bytes(b, c.v);
     if ((qb && qb < bytes) || (kb && kb < bytes) || (vb && vb < bytes)) return ERR("fused attention operand too small");
-    CHECK_LAUNCH(launch_attn_prefill_hs(q, 128, S * 128, k, v, 128, S * 128, o, 128, S * 128, S, H, H, 128, c.scale,
-                                        c.causal, g.stream));
-    return 0;
+    const std::pair<const uint8_t*, uint64_t> ins[3] = {{in.q, bytes}, {in.k, bytes}, {in.v, bytes}};
+    FusedOut o;
+    if (fused_out(c, bytes, ins, 3, o, err, errn)) return -1;
+    CHECK_LAUNCH(launch_attn_prefill_hs(q, 128, S * 128, k, v, 128, S * 128, o.kernel, 128, S * 128, S, H, H, 128,
+                                        c.scale, c.causal, g.stream));
+    return fused_out_done(o, err, errn);
+}
+
+// Marks the outputs of a skipped member as not materialized.
+void unmat_member(const wt_op& o, const AttnChain& c) {
+    if (g_unmat.empty()) g_unmat.assign(kMaxTemps, 0);
+    uint32_t outs[2] = {kNone, kNone};
+    switch (o.opcode) {
+    case OP_MATMUL_F16: case OP_BINARY_F16: case OP_ADD_F16: outs[0] = o.args[2]; break;
+    case OP_BROADCAST_F16: case OP_TRANSPOSE_GEN_F16: case OP_SOFTMAX_F16: outs[0] = o.args[1]; break;
+    case OP_KV_GATHER_F16: outs[0] = o.args[1] ? o.args[1] : kNone; outs[1] = o.args[2] ? o.args[2] : kNone; break;
+    default: break;
+    }
+    for (uint32_t t : outs)
+        if (t != kNone && is_temp_ref(t) && !same_temp(t, c.out)) g_unmat[t & 0x3FFFu] = 1;
+}
+
+// Fused-run handling of op i of a chain: returns 1 when the op is done (skipped, or the
+// chain's kernel launched at its last member: *rc holds the status), 0 to run it.
+int fused_member(const wt_blob* b, uint32_t i, int* rc, char* err, size_t errn) {
+    const int32_t ci = g_fplan->member_of[i];
+    if (ci < 0) return 0;
+    const AttnChain& c = g_fplan->chains[ci];
+    if (i == c.head) {
+        g_active[ci] = !g_fplan->blocked[ci] && c.last < g_run_end;
+        g_fin[ci] = FusedIn{};
+    }
+    if (!g_active[ci]) return 0;
+    FusedIn& in = g_fin[ci];
+    if (i == c.q_at) in.q = ref_ptr(b, c.q);
+    if (i == c.k_at && !c.decode) in.k = ref_ptr(b, c.k);
+    if (i == c.v_at && !c.decode) in.v = ref_ptr(b, c.v);
+    if (c.mask != kNone && i == c.mask_at) in.mask = ref_ptr(b, c.mask);
+    if (i == c.last) {
+        *rc = run_fused_attn(b, c, in, err, errn);
+        g.fused_runs++;
+        g.stats.ops++;
+        return 1;
+    }
+    const int mk = member_index(c, i);
+    if (mk >= 0 && ((g_fplan->keep[ci] >> mk) & 1u)) return 0;
+    unmat_member(b->ops[i], c);
+    *rc = 0;
+    return 1;
 }
 
 // One op through its handler; returns the handler's status.
@@ -2045,20 +2467,10 @@ int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* 
     if (g_prenorm.op != op) g_prenorm = PreNorm{};   // only ever for the very next op
     if (g_rope_pre != op) g_rope_pre = nullptr;
     if (g_fplan) {
-        if (g_skip_until != kNone && i <= g_skip_until) return 0;   // part of a chain that ran fused
-        const int32_t ci = g_fplan->head_of[i];
-        if (ci >= 0 && !g_fplan->live[ci] && i + g_fplan->chains[ci].len <= g_run_end) {
-            const AttnChain& c = g_fplan->chains[ci];
-            const int rc = run_fused_attn(b, c, err, errn);
-            if (g_unmat.empty()) g_unmat.assign(kMaxTemps, 0);
-            for (uint32_t t = 0; t < c.n_inter; ++t)
-                if ((c.inter[t] & 0x3FFFu) != (c.out & 0x3FFFu)) g_unmat[c.inter[t] & 0x3FFFu] = 1;
-            g_skip_until = i + c.len - 1;
-            g.fused_runs++;
-            g.stats.ops++;
-            return rc;
-        }
+        int frc = 0;
+        if (fused_member(b, i, &frc, err, errn)) return frc;
     }
+    if (g_obs.on) g_obs.op = i;
     Ctx cx{b, op, engine_m, err, errn};
     const int rc = op->opcode < 64 ? kTable.fn[op->opcode](cx) : op_unsupported(cx);
     if (g.trace)
@@ -2066,16 +2478,6 @@ int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* 
                      op->args[0], op->args[1], op->args[2], op->args[3], rc, g.pool_used,
                      g.replay ? " (graph)" : "");
     g.stats.ops++;
-    if (g_obs.on && rc == 0) {
-        const int32_t ce = g_obs_plan->end_of[i];
-        if (ce >= 0) {   // the chain has run: watch its intermediates (not its output)
-            const AttnChain& c = g_obs_plan->chains[ce];
-            for (uint32_t t = 0; t < c.n_inter; ++t) {
-                const uint32_t id = c.inter[t] & 0x3FFFu;
-                if (id != (c.out & 0x3FFFu)) g_obs.armed[id] = ce;
-            }
-        }
-    }
     return rc;
 }
 
@@ -2153,24 +2555,21 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
     // hooks see every op's output, so they run without fusion.
     g_fplan = nullptr;
     g_obs_plan = nullptr;
-    g_skip_until = kNone;
     g_run_end = first + count;
     bool observing = false;
     if (fusion_on() && !hooked) {
         FusionPlan* fp = fusion_plan(b);
         if (fp->observed) {
             g_fplan = fp;
+            g_active.assign(fp->chains.size(), 0);
+            g_fin.assign(fp->chains.size(), FusedIn{});
         } else if (!fp->chains.empty() && first == 0 && count == b->n_ops) {
             observing = true;
             g_obs_plan = fp;
-            std::fill(fp->live.begin(), fp->live.end(), 0);
-            g_obs.armed.assign(kMaxTemps, -1);
-            g_obs.inter_of.assign(kMaxTemps, -1);
-            g_obs.written.assign(kMaxTemps, 0);
-            for (size_t c = 0; c < fp->chains.size(); ++c)
-                for (uint32_t t = 0; t < fp->chains[c].n_inter; ++t)
-                    g_obs.inter_of[fp->chains[c].inter[t] & 0x3FFFu] = (int32_t)c;
-            g_obs.live = &fp->live;
+            g_obs.writer.assign(kMaxTemps, kNone);
+            g_obs.reads.clear();
+            g_obs.writes.clear();
+            g_obs.op = 0;
             g_obs.on = true;
         }
     }
@@ -2208,10 +2607,15 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
         if (rc) fail = (int)i + 1;
     }
     if (observing) {
-        if (g_run_out_temp != kNone) obs_read(g_run_out_temp);   // copied to the host next
+        g_obs.op = b->n_ops;   // run_io's output copy reads after every op
+        if (g_run_out_temp != kNone) obs_read(g_run_out_temp);
         g_obs.on = false;
-        g_obs.live = nullptr;
-        if (!fail) g_obs_plan->observed = true;
+        if (!fail) {
+            fusion_validate(*g_obs_plan);
+            g_obs_plan->observed = true;
+        }
+        g_obs.reads.clear();
+        g_obs.writes.clear();
         g_obs_plan = nullptr;
     }
     if (capture) {
@@ -2463,6 +2867,9 @@ void wt_exec_shutdown(void) {
     if (g.attn_work) dev_free(g.attn_work);
     g.attn_work = nullptr;
     g.attn_work_floats = 0;
+    if (g.fuse_scratch) dev_free(g.fuse_scratch);
+    g.fuse_scratch = nullptr;
+    g.fuse_scratch_cap = 0;
     if (g.norm_buf) dev_free(g.norm_buf);
     g.norm_buf = nullptr;
     g.norm_cap = 0;
@@ -2547,6 +2954,30 @@ int wt_exec_set_fusion(int on) {
 void wt_exec_fusion_stats(uint64_t* chains_found, uint64_t* fused_runs) {
     if (chains_found) *chains_found = g.chains_found;
     if (fused_runs) *fused_runs = g.fused_runs;
+}
+
+void wt_exec_fusion_detail(const struct wt_blob* b, uint32_t* chains, uint32_t* blocked, uint32_t* aliased,
+                           uint64_t* alias_runs) {
+    uint32_t n = 0, nb = 0, na = 0;
+    bool planned = false;
+    const uint64_t ep = g_parse_epoch.load(std::memory_order_relaxed);
+    for (const FusionPlan& p : g_plans) {
+        if (!b || p.b != b || p.n_ops != b->n_ops || p.parse_epoch != ep) continue;
+        planned = true;
+        n = (uint32_t)p.chains.size();
+        for (size_t c = 0; c < p.chains.size(); ++c) {
+            nb += p.observed && p.blocked[c];
+            na += p.observed && p.aliased[c];
+        }
+    }
+    if (!planned && b && b->n_ops) {   // not run yet: the chains the matchers find (no device work)
+        std::vector<int32_t> member_of;
+        n = (uint32_t)scan_chains(b, member_of).size();
+    }
+    if (chains) *chains = n;
+    if (blocked) *blocked = nb;
+    if (aliased) *aliased = na;
+    if (alias_runs) *alias_runs = g.fused_alias_runs;
 }
 
 uint64_t wt_exec_qkv_rope_fused(void) { return g.qkv_rope_fused; }

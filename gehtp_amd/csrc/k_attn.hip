@@ -297,11 +297,13 @@ struct DecodeArgs {
     float* part;             // partials [KVH][max_chunks][REP][PS]
     uint32_t max_chunks;
     uint32_t* ws;            // fused: workspace head (snapshot, RoPE records)
-    // Additive mask (plain op only, may be null): row h (query head) at mask + h * P,
-    // one value per position of a gathered layout of P positions; positions [n_kv, P)
-    // hold zero K/V there, so they score the mask value alone (added by the merge pass).
+    // Additive mask (plain op only, may be null): row h (query head) at mask + h * mask_hs
+    // (mask_hs = P, or 0 for one row shared by every head), one value per position of a
+    // gathered layout of P positions; positions [n_kv, P) hold zero K/V there, so they
+    // score the mask value alone (added by the merge pass).
     const __half* mask;
     uint32_t P;
+    uint32_t mask_hs;
     uint32_t spec_chunks;    // chunks whose keys are known to lie below the count
 };
 
@@ -474,7 +476,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
         for (int i = 0; i < 4; ++i) {
             const uint32_t key = c * DC + 16 * t + 4 * lr + i;
             float mk = 0.0f;
-            if (!FUSED && A.mask) mk = __half2float(A.mask[(size_t)(g * REP + qh) * A.P + min(key, n_kv - 1u)]) * kLog2e;
+            if (!FUSED && A.mask) mk = __half2float(A.mask[(size_t)(g * REP + qh) * A.mask_hs + min(key, n_kv - 1u)]) * kLog2e;
             x[t][i] = key < n_kv ? sa[t][i] * A.scale_log2 + mk : -INFINITY;
         }
     float mx = -INFINITY;   // scores are finite or -inf: v_max3 without NaN quieting
@@ -537,7 +539,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
 __global__ __launch_bounds__(256) void attn_merge_kernel(
     const float* __restrict__ part, uint32_t n_kv_host, uint32_t* __restrict__ count, int advance,
     uint32_t rep, uint32_t max_chunks, __half* __restrict__ out, uint32_t* __restrict__ ws, float theta,
-    const __half* __restrict__ mask, uint32_t P) {
+    const __half* __restrict__ mask, uint32_t P, uint32_t mask_hs) {
     __shared__ __align__(16) float4 s_o[256];
     __shared__ float s_m[8], s_l[8], s_t[4];
     const uint32_t h = blockIdx.x, g = h / rep, r = h % rep;
@@ -604,7 +606,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
     float tm = -INFINITY, tl = 0.0f;
     const bool tail = mask && P > n_kv;
     if (tail) {
-        const __half* mrow = mask + (size_t)h * P;
+        const __half* mrow = mask + (size_t)h * mask_hs;
         for (uint32_t j = n_kv + tid; j < P; j += 256) tm = fmaxf(tm, __half2float(mrow[j]) * kLog2e);
         tm = dev::wave_max(tm);
         if ((tid & 63) == 0) s_t[tid >> 6] = tm;
@@ -696,7 +698,7 @@ hipError_t decode_launch(const DecodeArgs& A, uint32_t rep, int advance, __half*
     }
     hipLaunchKernelGGL(attn_merge_kernel, dim3(A.H + (advance ? 1 : 0)), dim3(256), 0, st, A.part, A.n_kv_host,
                        A.count, advance, rep, A.max_chunks, out, reinterpret_cast<uint32_t*>(work), A.theta,
-                       A.mask, A.P);
+                       A.mask, A.P, A.mask_hs);
     return hipGetLastError();
 }
 
@@ -706,7 +708,7 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
                               uint32_t nslots, __half* out, uint32_t n_kv_host,
                               const uint32_t* count_dev, uint32_t H, uint32_t KVH, uint32_t hd,
                               float scale, float* work, uint32_t work_floats, hipStream_t st,
-                              const __half* mask, uint32_t P, uint32_t n_kv_known) {
+                              const __half* mask, uint32_t P, uint32_t n_kv_known, bool mask_shared) {
     if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
     if (mask && (P == 0 || P > nslots || (!count_dev && n_kv_host > P))) return hipErrorInvalidValue;
     const uint32_t rep = H / KVH;
@@ -719,7 +721,8 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
     if (!max_chunks) return hipSuccess;
     DecodeArgs A{q, nullptr, nullptr, nullptr, 0.0f, const_cast<uint8_t*>(ring), slot_bytes, nslots, KVH, H,
                  n_kv_host, const_cast<uint32_t*>(count_dev), scale * kLog2e, work + kWsHead, max_chunks, nullptr,
-                 mask, mask ? P : 0u, (count_dev ? std::min(n_kv_known, nslots) : n_kv_host) / DC};
+                 mask, mask ? P : 0u, mask && !mask_shared ? P : 0u,
+                 (count_dev ? std::min(n_kv_known, nslots) : n_kv_host) / DC};
     return decode_launch<false>(A, rep, 0, out, work, st);
 }
 
@@ -735,7 +738,7 @@ hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, cons
     if (attn_decode_work_floats(nslots, H, HD) > work_floats) return hipErrorInvalidValue;
     DecodeArgs A{nullptr, qkv, q_gamma, k_gamma, theta, ring, slot_bytes, nslots, KVH, H,
                  0u, count_dev, scale * kLog2e, work + kWsHead, max_chunks,
-                 reinterpret_cast<uint32_t*>(work), nullptr, 0u, std::min(n_kv_known, nslots) / DC};
+                 reinterpret_cast<uint32_t*>(work), nullptr, 0u, 0u, std::min(n_kv_known, nslots) / DC};
     return decode_launch<true>(A, rep, 1, out, work, st);
 }
 

@@ -161,7 +161,8 @@ hipError_t launch_attn_prefill_hs(const __half* q, uint32_t ldq, uint32_t qhs, c
                                   uint32_t H, uint32_t KVH, uint32_t hd, float scale, bool causal, hipStream_t st);
 // Split-KV decode: q [H][hd]; K/V read from the ring for positions [0, n_kv) where
 // n_kv = n_kv_host, or *count_dev when count_dev is non-null. mask (optional): additive
-// fp16 mask rows [H][P] over a gathered layout of P >= n_kv positions (P <= nslots) whose
+// fp16 mask rows [H][P] (mask_shared: one row [P] for every head) over a gathered layout
+// of P >= n_kv positions (P <= nslots) whose
 // positions past n_kv hold zero K and V, as KV_GATHER with an automatic count lays out
 // (those positions then score their mask value alone). n_kv_known: a count the device
 // counter is known to have reached (K/V of the chunks below it are requested before the
@@ -170,7 +171,8 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
                               uint32_t nslots, __half* out, uint32_t n_kv_host,
                               const uint32_t* count_dev, uint32_t H, uint32_t KVH, uint32_t hd,
                               float scale, float* work, uint32_t work_floats, hipStream_t st,
-                              const __half* mask = nullptr, uint32_t P = 0, uint32_t n_kv_known = 0);
+                              const __half* mask = nullptr, uint32_t P = 0, uint32_t n_kv_known = 0,
+                              bool mask_shared = false);
 // Fused decode step (OP_ATTN_DECODE_QKV_F16): QK-RMSNorm + RoPE of the raw [q | k | v]
 // row at position *count_dev, k/v appended to the ring, attention over positions
 // 0..*count_dev, then *count_dev += 1. work's leading counter must be zero before the

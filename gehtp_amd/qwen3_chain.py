@@ -29,6 +29,22 @@ the additive mask over the P = max_pos ring positions (0 up to the token's posit
 -inf after). The embedding row is gathered in-graph (GATHER, 20) and the face is carved
 with STRIDED_SLICE. The prefill blob's input is the prompt's token ids (int32 [S]).
 
+`lowering` selects how the attention chain is written:
+  "chain"    : as above (scale and mask as full-size constant slots, one KV_GATHER with
+               both faces, fresh temp ids);
+  "ref_post" : the forms the reference emitter writes for a scale after q.k^T
+               (test_models/transformer32: MatMul -> BROADCAST -> BINARY mul): k^T by
+               TRANSPOSE_GEN and MATMUL_F16 flags 4, the scale a 1-value slot BROADCAST
+               to the scores' shape and multiplied, the mask a BROADCAST of one [S, S] (or,
+               in decode, the step input's [P] row) over the heads added with ADD_F16,
+               one KV_GATHER per face (compiler/tools/wtop_ops/op_decode_state.cpp:66-80);
+  "ref_pre"  : the same with the scale applied to q before the matmul and k read
+               transposed (flags 6) (qwen35_08b manifest ops 2722-2728: BROADCAST, BINARY,
+               MATMUL, BROADCAST, ADD_F16, SOFTMAX, MATMUL).
+`recycle` renumbers temps with the reference emitter's free list (gehtp_amd.tempplan),
+and `tempoff` adds a static temp plan (TEMPOFF slot) whose temps share bytes wherever
+their spans do not meet.
+
 Weights are the same external image as gehtp_amd.qwen3.Weights: q/k/v are contiguous
 row ranges of the stored q|k|v matrix; gate/up stay interleaved in one matrix and are
 separated by two strided slices after the linear.
@@ -138,6 +154,11 @@ class _ChainEmitter:
         self.bb.op(OP.BINARY_F16, a, b, y, n, sub)
         return y
 
+    def add_f16(self, a, b, n):
+        y = self.T()
+        self.bb.op(OP.ADD_F16, a, b, y, n)
+        return y
+
     def unary(self, x, n, sub):
         y = self.T()
         self.bb.op(OP.UNARY_F16, x, y, n, sub)
@@ -200,23 +221,54 @@ class _ChainEmitter:
         return x
 
 
-def emit_decode_chain(cfg: Qwen3Config, w: Weights, max_pos: int):
+LOWERINGS = ("chain", "ref_post", "ref_pre")
+
+
+def _finish(bb, keep, recycle: bool, tempoff: bool):
+    """Renumber temps (reference free list) and add a TEMPOFF plan, as asked; returns
+    the renumbered ids of `keep`."""
+    from .tempplan import recycle as _recycle, tempoff_plan
+    ids = list(keep)
+    if recycle:
+        m = _recycle(bb, keep=ids)
+        ids = [m[t] for t in ids]
+    if tempoff:
+        cap, entries = tempoff_plan(bb, keep=ids)
+        bb.set_tempoff(cap, entries)
+    return ids
+
+
+def _scale_ref(e, lowering, n, dims):
+    """The scale operand for a BINARY mul over n values: a full-size slot ("chain") or
+    a 1-value slot BROADCAST to `dims`."""
+    c, bb = e.cfg, e.bb
+    if lowering == "chain":
+        return bb.slot_ref(bb.add_slot(np.full(n, np.float16(c.scale), np.float16)))
+    if not hasattr(e, "scale1"):
+        e.scale1 = bb.slot_ref(bb.add_slot(np.array([c.scale], np.float16)))
+    return e.broadcast(e.scale1, [1] * len(dims), dims)
+
+
+def emit_decode_chain(cfg: Qwen3Config, w: Weights, max_pos: int, lowering: str = "chain",
+                      recycle: bool = False, tempoff: bool = False):
     """(blob, temps) of one decode step in the reference op chain. Input: the step body
     of decode_input(); KV rings of max_pos positions (one STATE per layer)."""
+    if lowering not in LOWERINGS:
+        raise ValueError(f"lowering {lowering!r} not in {LOWERINGS}")
     e = _ChainEmitter(cfg, w)
     c, bb = cfg, e.bb
     H, KVH, hd, P, D = c.heads, c.kv_heads, c.head_dim, max_pos, c.hidden
     nface = face_elems(cfg, max_pos)
     face = bb.slot_ref(bb.add_input_slot(nface * 2))
     states = [bb.add_state(max_pos * c.kv_dim * 4) for _ in range(c.layers)]
-    scale = bb.add_slot(np.full(H * P, np.float16(c.scale), np.float16))
+    scale_full = _scale_ref(e, "chain", H * P, None) if lowering == "chain" else None
     x = e.gather_rows(face, 1)
     cos = e.slice1(face, nface, 2, 2 + hd)
     sin = e.slice1(face, nface, 2 + hd, 2 + 2 * hd)
     mask = e.slice1(face, nface, 2 + 2 * hd, 2 + 2 * hd + P)
     cos_q, sin_q = e.broadcast(cos, [1, hd], [H, hd]), e.broadcast(sin, [1, hd], [H, hd])
     cos_k, sin_k = e.broadcast(cos, [1, hd], [KVH, hd]), e.broadcast(sin, [1, hd], [KVH, hd])
-    mask_h = e.broadcast(mask, [1, P], [H, P])
+    mask_h = e.broadcast(mask, [1, P], [H, P]) if lowering == "chain" else None
     for l in range(c.layers):
         h = e.rmsnorm(x, e.ref(f"{l}.g_attn"), e.zero_d, D)
         q = e.w4g(h, l, "wq", 1, D, c.q_dim)
@@ -225,11 +277,24 @@ def emit_decode_chain(cfg: Qwen3Config, w: Weights, max_pos: int):
         qr = e.rope(e.rmsnorm(q, e.ref(f"{l}.q_norm"), e.zero_hd, c.q_dim), H, cos_q, sin_q)
         kr = e.rope(e.rmsnorm(k, e.ref(f"{l}.k_norm"), e.zero_hd, c.kv_dim), KVH, cos_k, sin_k)
         bb.op(OP.KV_APPEND_F16, kr, v, states[l], WT_KV_POS_AUTO)
-        kT, vv = e.T(), e.T()
-        bb.op(OP.KV_GATHER_F16, states[l], kT, vv, WT_KV_POS_AUTO, H, KVH, hd)
-        s = e.T()
-        bb.op(OP.MATMUL_F16, qr, kT, s, 1, hd, P, 4 | (H << 16))
-        s2 = e.binary(e.binary(s, bb.slot_ref(scale), H * P, MUL), mask_h, H * P, ADD)
+        if lowering == "chain":
+            kT, vv = e.T(), e.T()
+            bb.op(OP.KV_GATHER_F16, states[l], kT, vv, WT_KV_POS_AUTO, H, KVH, hd)
+            s = e.T()
+            bb.op(OP.MATMUL_F16, qr, kT, s, 1, hd, P, 4 | (H << 16))
+            s2 = e.binary(e.binary(s, scale_full, H * P, MUL), mask_h, H * P, ADD)
+        else:
+            kT = e.T()
+            bb.op(OP.KV_GATHER_F16, states[l], kT, 0, WT_KV_POS_AUTO, H, KVH, hd)
+            vv = e.T()
+            bb.op(OP.KV_GATHER_F16, states[l], 0, vv, WT_KV_POS_AUTO, H, KVH, hd)
+            if lowering == "ref_pre":
+                qr = e.binary(qr, _scale_ref(e, lowering, H * hd, [H, hd]), H * hd, MUL)
+            s = e.T()
+            bb.op(OP.MATMUL_F16, qr, kT, s, 1, hd, P, 4 | (H << 16))
+            if lowering == "ref_post":
+                s = e.binary(s, _scale_ref(e, lowering, H * P, [H, P]), H * P, MUL)
+            s2 = e.add_f16(s, e.broadcast(mask, [1, P], [H, P]), H * P)
         p, a = e.T(), e.T()
         bb.op(OP.SOFTMAX_F16, s2, p, H, P)
         bb.op(OP.MATMUL_F16, p, vv, a, 1, P, hd, 4 | (H << 16))
@@ -238,13 +303,17 @@ def emit_decode_chain(cfg: Qwen3Config, w: Weights, max_pos: int):
         bb.op(OP.ADD_F16, x, o, x1, D)
         x = e.ffn(x1, l, 1)
     logits, tok = e.head(x, 1)
+    logits, tok = _finish(bb, [logits, tok], recycle, tempoff)
     return bb.build(), {"logits": logits, "tok": tok}
 
 
-def emit_prefill_chain(cfg: Qwen3Config, w: Weights, S: int):
+def emit_prefill_chain(cfg: Qwen3Config, w: Weights, S: int, lowering: str = "chain", recycle: bool = False,
+                       tempoff: bool = False):
     """(blob, temps) of a causal prefill of S tokens in the reference op chain (no KV
     state: the reference serves a prompt through its decode graph). Input: the prompt's
     token ids, int32 [S]."""
+    if lowering not in LOWERINGS:
+        raise ValueError(f"lowering {lowering!r} not in {LOWERINGS}")
     e = _ChainEmitter(cfg, w)
     c, bb = cfg, e.bb
     H, KVH, hd, D = c.heads, c.kv_heads, c.head_dim, c.hidden
@@ -253,9 +322,12 @@ def emit_prefill_chain(cfg: Qwen3Config, w: Weights, S: int):
     cos_t, sin_t = rope_tables(np.arange(S), hd, c.theta)
     cos_s, sin_s = bb.slot_ref(bb.add_slot(cos_t)), bb.slot_ref(bb.add_slot(sin_t))
     n = H * S * S
-    scale = bb.add_slot(np.full(n, np.float16(c.scale), np.float16))
     causal = np.where(np.arange(S)[None, :] <= np.arange(S)[:, None], np.float16(0), np.float16(-np.inf))
-    mask = bb.add_slot(np.broadcast_to(causal, (H, S, S)).astype(np.float16))
+    if lowering == "chain":
+        scale = _scale_ref(e, lowering, n, None)
+        mask = bb.slot_ref(bb.add_slot(np.broadcast_to(causal, (H, S, S)).astype(np.float16)))
+    else:
+        mask_ss = bb.slot_ref(bb.add_slot(causal.astype(np.float16)))
     x = e.gather_rows(ids, S)
     cos_q, sin_q = e.broadcast(cos_s, [S, 1, hd], [S, H, hd]), e.broadcast(sin_s, [S, 1, hd], [S, H, hd])
     cos_k, sin_k = e.broadcast(cos_s, [S, 1, hd], [S, KVH, hd]), e.broadcast(sin_s, [S, 1, hd], [S, KVH, hd])
@@ -270,8 +342,18 @@ def emit_prefill_chain(cfg: Qwen3Config, w: Weights, S: int):
         kh = e.broadcast(e.transpose3(kr, (S, KVH, hd), (1, 0, 2)), [KVH, 1, S, hd], [KVH, rep, S, hd])
         vh = e.broadcast(e.transpose3(v, (S, KVH, hd), (1, 0, 2)), [KVH, 1, S, hd], [KVH, rep, S, hd])
         s = e.T()
-        bb.op(OP.MATMUL_F16, qh, kh, s, S, hd, S, 6 | (H << 16))
-        s2 = e.binary(e.binary(s, bb.slot_ref(scale), n, MUL), bb.slot_ref(mask), n, ADD)
+        if lowering == "chain":
+            bb.op(OP.MATMUL_F16, qh, kh, s, S, hd, S, 6 | (H << 16))
+            s2 = e.binary(e.binary(s, scale, n, MUL), mask, n, ADD)
+        elif lowering == "ref_post":
+            kT = e.transpose3(kh, (H, S, hd), (0, 2, 1))
+            bb.op(OP.MATMUL_F16, qh, kT, s, S, hd, S, 4 | (H << 16))
+            s1 = e.binary(s, _scale_ref(e, lowering, n, [H, S, S]), n, MUL)
+            s2 = e.add_f16(s1, e.broadcast(mask_ss, [1, S, S], [H, S, S]), n)
+        else:
+            qs = e.binary(qh, _scale_ref(e, lowering, H * S * hd, [H, S, hd]), H * S * hd, MUL)
+            bb.op(OP.MATMUL_F16, qs, kh, s, S, hd, S, 6 | (H << 16))
+            s2 = e.add_f16(s, e.broadcast(mask_ss, [1, S, S], [H, S, S]), n)
         p, ah = e.T(), e.T()
         bb.op(OP.SOFTMAX_F16, s2, p, H * S, S)
         bb.op(OP.MATMUL_F16, p, vh, ah, S, S, hd, 4 | (H << 16))
@@ -281,4 +363,5 @@ def emit_prefill_chain(cfg: Qwen3Config, w: Weights, S: int):
         bb.op(OP.ADD_F16, x, o, x1, S * D)
         x = e.ffn(x1, l, S)
     logits, tok = e.head(x, S)
+    logits, tok = _finish(bb, [logits, tok], recycle, tempoff)
     return bb.build(), {"logits": logits, "tok": tok}

@@ -120,18 +120,34 @@ void wt_exec_set_hook(const char* spec);
 int  wt_exec_set_graphs(int on);
 void wt_exec_graph_stats(uint32_t* captures, uint32_t* replays);
 
-/* Extension: load-time fusion of the reference attention op chain. A batched
- * MATMUL_F16 q.k^T (w stored [N,K], head dim 128) -> BINARY mul by a constant scale slot
- * -> optional BINARY add of a causal (0 / -inf) or all-zero mask slot -> SOFTMAX ->
- * batched MATMUL_F16 p.v, heads in the batch dimension, runs as one flash-attention
- * kernel once the blob's first full run has shown that no other op reads the chain's
- * intermediate temps. Results are within the fp16 tolerance of the op-by-op chain.
- * Default on unless the environment sets GEHTP_NO_FUSE=1; wt_exec_set_fusion returns
- * the previous setting; wt_exec_fusion_stats reports chains found in the blobs seen
- * and chain executions run fused. After a fused run, wt_exec_temp returns NULL for the
- * chain's intermediate temps (they were not computed). */
+/* Extension: load-time fusion of the reference attention op chains. Prefill: [BINARY
+ * mul of q by a constant scale] -> MATMUL_F16 q.k^T (heads in the batch dimension, head
+ * dim 128; k read transposed, or k^T written by a TRANSPOSE_GEN of k) -> [BINARY mul by
+ * a constant scale] -> [BINARY add or ADD_F16 of a causal (0 / -inf) or all-zero mask]
+ * -> SOFTMAX -> MATMUL_F16 p.v runs as one flash-attention kernel; decode: KV_GATHER of
+ * a state (one op, or one per face) -> [pre-scale] -> MATMUL_F16 q.kT -> [scale] ->
+ * [mask add: H rows, or one row BROADCAST over the heads] -> SOFTMAX -> MATMUL_F16 p.v
+ * runs as the split-KV decode kernel on the ring. Scales and masks may be constant
+ * slots or BROADCASTs of them. Members are found by dataflow (other ops may stand
+ * between them; recycled temp ids are followed); the kernel runs at the last member.
+ * A blob's first full run executes the chains op by op and logs reads and writes; a
+ * chain is fused on later runs only if no other op read its intermediates and no op
+ * that still runs wrote over its inputs' bytes before the kernel's turn. Results are
+ * within the fp16 tolerance of the op-by-op chain. Default on unless the environment
+ * sets GEHTP_NO_FUSE=1; wt_exec_set_fusion returns the previous setting;
+ * wt_exec_fusion_stats reports chains found in the blobs seen and chain executions run
+ * fused. After a fused run, wt_exec_temp returns NULL for the chain's intermediate
+ * temps (they were not computed). */
 int  wt_exec_set_fusion(int on);
 void wt_exec_fusion_stats(uint64_t* chains_found, uint64_t* fused_runs);
+/* Extension: the fusion plan of a parsed blob (after its first full run): attention
+ * chains found in it, those its observed run ruled out of fusion, those whose output
+ * bytes overlapped an input's in that run; and, process-wide, fused executions whose
+ * output overlapped an input (the kernel then writes engine scratch, copied to the
+ * output after it). For a blob not yet run, chains is what the matchers find in it
+ * (host work only, no device call) and the other counts 0. */
+void wt_exec_fusion_detail(const struct wt_blob* b, uint32_t* chains, uint32_t* blocked, uint32_t* aliased,
+                           uint64_t* alias_runs);
 /* Extension, under the same switch: an OP_W4G_FUSED_F16 q|k|v GEMM (GEMM path, plain
  * epilogue) followed in the same run by the OP_QK_ROPE_KV_F16 that reads its output
  * performs that op in its epilogue (same bits; the GEMM's own output is written too);

@@ -38,8 +38,15 @@ def _check_rows(got, ref, what):
         assert int(np.argmax(gf)) == int(np.argmax(rf)), f"{what} step {t}: top-1 (ref margin {top[1] - top[0]:.3g})"
 
 
-def _chain_decode(engine, cfg, w, ids, max_pos, fusion):
-    blob, t = emit_decode_chain(cfg, w, max_pos)
+# (lowering, recycled temp ids, TEMPOFF plan): this build's chain form, and the
+# reference emitter's post- and pre-scale forms (gehtp_amd.qwen3_chain)
+FORMS = [("chain", False, False), ("ref_post", True, True), ("ref_pre", True, False)]
+FORM_IDS = ["chain", "ref-post-recycled-tempoff", "ref-pre-recycled"]
+
+
+def _chain_decode(engine, cfg, w, ids, max_pos, fusion, form=FORMS[0]):
+    lowering, recycle, tempoff = form
+    blob, t = emit_decode_chain(cfg, w, max_pos, lowering=lowering, recycle=recycle, tempoff=tempoff)
     prev = engine.set_fusion(fusion)
     f0, r0 = engine.fusion_stats()
     try:
@@ -53,9 +60,12 @@ def _chain_decode(engine, cfg, w, ids, max_pos, fusion):
             rows.append(np.frombuffer(engine.temp(t["logits"]), np.float16)[:cfg.vocab].copy())
             assert int(np.frombuffer(out, np.int32)[0]) == int(np.argmax(rows[-1].astype(np.float32)))
         f1, r1 = engine.fusion_stats()
+        detail = engine.fusion_detail(pd)
         engine.shutdown()
     finally:
         engine.set_fusion(prev)
+    if fusion:
+        assert detail["chains"] == cfg.layers and detail["blocked"] == 0, detail
     return rows, (f1 - f0, r1 - r0)
 
 
@@ -66,20 +76,22 @@ def _oracle_decode(cfg, w, ids, max_pos):
     return [ref.decode(emb[int(t)]) for t in ids]
 
 
+@pytest.mark.parametrize("form", FORMS, ids=FORM_IDS)
 @pytest.mark.parametrize("cfg,n,max_pos,seed", [(SMALL, 40, 64, 21), (CONFIG_08B_LAYER, 24, 96, 22)],
                          ids=["small-2layer", "config4-geometry"])
-def test_chain_decode_vs_oracle(engine, cfg, n, max_pos, seed):
-    """Prompt and generation one token per step through the chain-form decode blob,
+def test_chain_decode_vs_oracle(engine, cfg, n, max_pos, seed, form):
+    """Prompt and generation one token per step through the chain-form decode blob in each
+    lowering (the reference forms with recycled temp ids, one with a TEMPOFF plan),
     fusion off and on, every step against the oracle; with fusion on every layer's
     decode chain is found and runs fused (after the blob's first, observed run)."""
     w = Weights(cfg, seed=seed)
     ids = np.random.default_rng(seed + 1).integers(0, cfg.vocab, n)
     ref = _oracle_decode(cfg, w, ids, max_pos)
-    plain, (found0, runs0) = _chain_decode(engine, cfg, w, ids, max_pos, fusion=False)
-    _check_rows(plain, ref, "chain, fusion off")
+    plain, (found0, runs0) = _chain_decode(engine, cfg, w, ids, max_pos, fusion=False, form=form)
+    _check_rows(plain, ref, f"{form[0]}, fusion off")
     assert runs0 == 0
-    fused, (found, runs) = _chain_decode(engine, cfg, w, ids, max_pos, fusion=True)
-    _check_rows(fused, ref, "chain, fusion on")
+    fused, (found, runs) = _chain_decode(engine, cfg, w, ids, max_pos, fusion=True, form=form)
+    _check_rows(fused, ref, f"{form[0]}, fusion on")
     assert found >= cfg.layers and runs == cfg.layers * (n - 1), (found, runs)
 
 
@@ -125,17 +137,19 @@ def test_chain_decode_graph_replay(engine):
         assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"step {t}"
 
 
+@pytest.mark.parametrize("form", FORMS, ids=FORM_IDS)
 @pytest.mark.parametrize("cfg,S,seed", [(SMALL, 40, 51), (CONFIG_08B_LAYER, 64, 52)],
                          ids=["small-2layer", "config4-geometry"])
-def test_chain_prefill_vs_oracle(engine, cfg, S, seed):
-    """The chain-form prefill blob (ids in, GQA by TRANSPOSE_GEN + BROADCAST, causal mask
-    slot) against the oracle's prefill, fusion off and on (the prefill chains as the
-    flash kernel)."""
+def test_chain_prefill_vs_oracle(engine, cfg, S, seed, form):
+    """The chain-form prefill blob (ids in, GQA by TRANSPOSE_GEN + BROADCAST, causal mask)
+    in each lowering against the oracle's prefill, fusion off and on (the prefill chains
+    as the flash kernel)."""
     from oracle.qwen3_ref import RefModel
     w = Weights(cfg, seed=seed)
     ids = np.random.default_rng(seed + 1).integers(0, cfg.vocab, S).astype(np.int32)
     ref = RefModel(cfg, w, S + 8).prefill(np.ascontiguousarray(w.embed()[ids]))
-    blob, t = emit_prefill_chain(cfg, w, S)
+    lowering, recycle, tempoff = form
+    blob, t = emit_prefill_chain(cfg, w, S, lowering=lowering, recycle=recycle, tempoff=tempoff)
     for fusion in (False, True):
         prev = engine.set_fusion(fusion)
         try:
@@ -146,9 +160,12 @@ def test_chain_prefill_vs_oracle(engine, cfg, S, seed):
             for _ in range(2):   # the first run is observed, the second runs the chains fused
                 out, _ = engine.run_io(pb, ids.tobytes(), t["tok"])
                 got = np.frombuffer(engine.temp(t["logits"]), np.float16)[:cfg.vocab].copy()
-                _check_rows([got], [ref], f"prefill chain, fusion {'on' if fusion else 'off'}")
+                _check_rows([got], [ref], f"prefill {lowering}, fusion {'on' if fusion else 'off'}")
                 assert int(np.frombuffer(out, np.int32)[0]) == int(np.argmax(got.astype(np.float32)))
             f1, r1 = engine.fusion_stats()
+            if fusion:
+                d = engine.fusion_detail(pb)
+                assert d["chains"] == cfg.layers and d["blocked"] == 0, d
             engine.shutdown()
         finally:
             engine.set_fusion(prev)

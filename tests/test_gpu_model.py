@@ -185,8 +185,14 @@ def test_run_steps_errors(engine):
     pt = engine.parse(dect)
     engine.state_reset()
     first = np.int32(5).tobytes()
-    with pytest.raises(RuntimeError, match="output limit"):
+    with pytest.raises(ValueError, match="64 MiB"):   # the Python mirror checks first
         engine.run_steps(pt, 20_000_000, first, tdt["tok"])
+    # the library's own check, called directly: it refuses before writing any output
+    import ctypes as C
+    err, m, obuf = C.create_string_buffer(256), C.c_uint32(0), C.create_string_buffer(16)
+    rc = engine.lib.wt_exec_run_steps(C.byref(pt.blob), 20_000_000, C.c_char_p(first), obuf, tdt["tok"],
+                                      C.byref(m), err, 256)
+    assert rc != 0 and b"output limit" in err.value, (rc, err.value)
     with pytest.raises(RuntimeError, match="output temp"):
         engine.run_steps(pt, 2, first, tdt["logits"])
     ids = np.frombuffer(engine.run_steps(pt, 3, first, tdt["tok"]), np.int32)
