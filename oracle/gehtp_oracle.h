@@ -51,6 +51,12 @@ int go_matmul_f16_nk_ref(const uint16_t* a, const uint16_t* w, uint16_t* y,
  * scalar forms, go_fast_disable(0) re-enables detection. */
 int go_fast_available(void);
 void go_fast_disable(int off);
+/* Summation order of the vector forms (linears, attention): 0 = the scalar restatement's
+ * sequential order (default); 1 = 32-wide slices combined pairwise; 2 = 16-wide slices
+ * combined in sequence (attention's P.V: 64-key chunks). Same products and f16 rounding
+ * points; for measuring order-only spread. Returns -1 for an unknown mode or when the
+ * vector forms are unavailable. */
+int go_set_order(int mode);
 
 /* ---- row ops ---- */
 int  go_rmsnorm2(const uint16_t* x, const uint16_t* gamma, const uint16_t* beta,

@@ -3,8 +3,9 @@
  * Loaded only by tests/, the smoke check and bench.py's cpu_baseline leg; the HIP
  * engine never links or calls it.
  *
- * Every function here computes what a scalar restatement in gehtp_oracle.c computes,
- * with the same per-output arithmetic: each output keeps its own sequential
+ * Every function here computes what a scalar restatement in gehtp_oracle.c computes
+ * (in summation order 0, the default; go_set_order below), with the same per-output
+ * arithmetic: each output keeps its own sequential
  * accumulation order (k = 0, 1, 2, ... for the linears, d for attention scores, j for
  * attention values), with an f32 product rounded before the f32 add (no FMA: the file
  * is built with -ffp-contract=off), and the same f16 rounding points. Only the
@@ -45,6 +46,36 @@ int go_fast_available(void) {
 
 /* Force the scalar forms (1) or allow the vector forms again (0); for tests. */
 void go_fast_disable(int off) { g_fast = off ? 0 : -1; }
+
+/* Summation order of the vector forms' long sums (go_set_order). Mode 0 is the scalar
+ * restatement's sequential order, bit-identical to it. Modes 1 and 2 are other valid
+ * fp32 orders of the same products, with the same f16 rounding points, used only to
+ * measure how far a correct implementation's results may move with the order alone:
+ *   1: each sum cut into 32-wide slices (linears: k; attention scores: d), each slice
+ *      summed in sequence from zero, the slice sums combined pairwise (a tree:
+ *      (s0 + s1) + (s2 + s3) ...); attention's P.V sum over keys in 64-key chunks,
+ *      combined pairwise;
+ *   2: 16-wide slices summed from zero, their sums added in sequence
+ *      (((s0 + s1) + s2) + ...); P.V in 64-key chunks added in sequence. */
+static int g_order = 0;
+
+int go_set_order(int mode) {
+    if (mode < 0 || mode > 2 || (mode && !go_fast_available())) return -1;
+    g_order = mode;
+    return 0;
+}
+
+static inline uint32_t order_width(void) { return g_order == 1 ? 32u : 16u; }
+
+/* Combine n slice sums (vectors at stride st) into v[0] in the mode's order. */
+static inline void combine_slices(v8f* v, uint32_t n, uint32_t st) {
+    if (g_order == 1) {
+        for (uint32_t w = 1; w < n; w *= 2)
+            for (uint32_t i = 0; i + w < n; i += 2 * w) v[(size_t)i * st] = v[(size_t)i * st] + v[(size_t)(i + w) * st];
+    } else {
+        for (uint32_t i = 1; i < n; i++) v[0] = v[0] + v[(size_t)i * st];
+    }
+}
 
 TGT static inline v8f ld8(const float* p) { v8f v; memcpy(&v, p, sizeof v); return v; }
 TGT static inline void st8(float* p, v8f v) { memcpy(p, &v, sizeof v); }
@@ -158,6 +189,31 @@ TGT static void mm_block(const float* af, uint32_t M, uint32_t K, const float* b
     }
 }
 
+/* mm_block in the order of g_order (1 or 2): per row, the two 8-column accumulators
+ * restart at each slice of order_width() k values; part holds 2 * ceil(K / width)
+ * vectors. */
+TGT static void mm_block_ordered(const float* af, uint32_t M, uint32_t K, const float* blk, uint16_t* y,
+                                 uint32_t ldy, uint32_t n0, uint32_t nb, v8f* part) {
+    const uint32_t W = order_width(), ns = (K + W - 1) / W;
+    for (uint32_t m = 0; m < M; m++) {
+        const float* a0 = af + (size_t)m * K;
+        for (uint32_t sl = 0; sl < ns; sl++) {
+            v8f c0 = bc8(0.0f), c1 = c0;
+            const uint32_t ke = (sl + 1) * W < K ? (sl + 1) * W : K;
+            for (uint32_t k = sl * W; k < ke; k++) {
+                const v8f x0 = bc8(a0[k]);
+                c0 = c0 + x0 * ld8(blk + (size_t)k * NB);
+                c1 = c1 + x0 * ld8(blk + (size_t)k * NB + 8);
+            }
+            part[2 * sl] = c0;
+            part[2 * sl + 1] = c1;
+        }
+        combine_slices(part, ns, 2);
+        combine_slices(part + 1, ns, 2);
+        store_row(y + (size_t)m * ldy + n0, part[0], part[1], nb);
+    }
+}
+
 TGT static float* to_f32(const uint16_t* a, size_t n) {
     float* f = (float*)malloc(n * sizeof(float) + 32);
     if (!f) return NULL;
@@ -180,7 +236,8 @@ TGT static int linear_fast(const uint16_t* a, const uint8_t* wq, const uint16_t*
     {
         float* blk = (float*)malloc((size_t)K * NB * sizeof(float));
         float* tmp = (float*)malloc((size_t)K * sizeof(float) + 64);
-        if (!blk || !tmp) {
+        v8f* part = (v8f*)aligned_alloc(32, ((size_t)2 * (K / 16 + 1) * sizeof(v8f) + 31) / 32 * 32);
+        if (!blk || !tmp || !part) {
 #pragma omp atomic write
             fail = 1;
         } else {
@@ -189,11 +246,13 @@ TGT static int linear_fast(const uint16_t* a, const uint8_t* wq, const uint16_t*
                 const uint32_t n0 = b * NB, nb = N - n0 < NB ? N - n0 : NB;
                 if (wq) block_w4g(wq, ws, K, group, n0, nb, blk, tmp);
                 else block_f16(w, K, n0, nb, blk, tmp);
-                mm_block(af, M, K, blk, y, N, n0, nb);
+                if (g_order) mm_block_ordered(af, M, K, blk, y, N, n0, nb, part);
+                else mm_block(af, M, K, blk, y, N, n0, nb);
             }
         }
         free(blk);
         free(tmp);
+        free(part);
     }
     free(af);
     return fail ? -1 : 0;
@@ -226,6 +285,21 @@ TGT static void attn_scores(const float* qrow, const float* kt, uint32_t ldk, ui
                             uint32_t jn, float sc, float* srow) {
     const v8f vsc = bc8(sc), zero = bc8(0.0f);
     uint32_t j0 = 0;
+    if (g_order) {   /* d in slices of order_width(), combined in the mode's order */
+        const uint32_t W = order_width(), ns = (hd + W - 1) / W;
+        v8f part[256 / 16];
+        for (; j0 < jn; j0 += 8) {   /* kt rows are padded to a multiple of 8 keys */
+            for (uint32_t sl = 0; sl < ns; sl++) {
+                v8f c0 = zero;
+                const uint32_t de = (sl + 1) * W < hd ? (sl + 1) * W : hd;
+                for (uint32_t d = sl * W; d < de; d++) c0 = c0 + bc8(qrow[d]) * ld8(kt + (size_t)d * ldk + j0);
+                part[sl] = c0;
+            }
+            combine_slices(part, ns, 1);
+            st8(srow + j0, rt16(rt16(rt16(part[0]) * vsc) + zero));
+        }
+        return;
+    }
     for (; j0 + 32 <= jn; j0 += 32) {
         v8f c0 = zero, c1 = zero, c2 = zero, c3 = zero;
         for (uint32_t d = 0; d < hd; d++) {
@@ -275,6 +349,28 @@ static void attn_softmax(const float* s, float* p, uint32_t jn, uint32_t rows, u
 TGT static void attn_values(const float* p, const float* vf, uint32_t hd, uint32_t jn, uint16_t* out) {
     v8f acc[32];
     const uint32_t nv = hd / 8;
+    if (g_order) {   /* keys in 64-key chunks, each from zero, combined in the mode's order */
+        const uint32_t nc = (jn + 63) / 64;
+        v8f* part = (v8f*)aligned_alloc(32, (size_t)(nc ? nc : 1) * nv * sizeof(v8f));
+        if (part) {
+            for (uint32_t c = 0; c < nc; c++) {
+                for (uint32_t i = 0; i < nv; i++) acc[i] = bc8(0.0f);
+                const uint32_t je = (c + 1) * 64 < jn ? (c + 1) * 64 : jn;
+                for (uint32_t j = c * 64; j < je; j++) {
+                    const v8f pb = bc8(p[j]);
+                    const float* vr = vf + (size_t)j * hd;
+                    for (uint32_t i = 0; i < nv; i++) acc[i] = acc[i] + pb * ld8(vr + 8 * i);
+                }
+                for (uint32_t i = 0; i < nv; i++) part[(size_t)c * nv + i] = acc[i];
+            }
+            for (uint32_t i = 0; i < nv; i++) {
+                if (nc) combine_slices(part + i, nc, nv);
+                f2h8(out + 8 * i, nc ? part[i] : bc8(0.0f));
+            }
+            free(part);
+            return;
+        }
+    }
     for (uint32_t i = 0; i < nv; i++) acc[i] = bc8(0.0f);
     for (uint32_t j = 0; j < jn; j++) {
         const v8f pb = bc8(p[j]);

@@ -46,6 +46,7 @@ def lib():
             "go_matmul_f16_nk_ref": (C.c_int, [_p, _p, _p, u, u, u, C.c_int]),
             "go_fast_available": (C.c_int, []),
             "go_fast_disable": (None, [C.c_int]),
+            "go_set_order": (C.c_int, [C.c_int]),
             "go_attn_prefill_mt": (C.c_int, [_p, _p, _p, _p, u, u, u, u, C.c_float, C.c_int, C.c_int]),
             "go_attn_prefill_ref": (C.c_int, [_p, _p, _p, _p, u, u, u, u, C.c_float, C.c_int]),
             "go_attn_decode_ring": (C.c_int, [_p, _p, u, u, _p, _p, u, u, u, u, C.c_float]),
@@ -169,6 +170,26 @@ def matmul_f16_nk(a, w, threads: int = 1, form: str = "fast") -> np.ndarray:
 
 def fast_available() -> bool:
     return bool(lib().go_fast_available())
+
+
+class summation_order:
+    """Context manager: run the vector forms in fp32 summation order `mode` (0 = the
+    scalar restatement's sequential order; 1 = 32-wide slices combined pairwise; 2 =
+    16-wide slices combined in sequence; attention's P.V in 64-key chunks) with the same
+    f16 rounding points, to measure how far a correct implementation may move with the
+    order alone. Raises when the vector forms are unavailable."""
+
+    def __init__(self, mode: int):
+        self.mode = mode
+
+    def __enter__(self):
+        if lib().go_set_order(self.mode):
+            raise RuntimeError(f"summation order {self.mode} unavailable (needs the AVX2/F16C forms)")
+        return self
+
+    def __exit__(self, *exc):
+        lib().go_set_order(0)
+        return False
 
 
 # ---- rows ----

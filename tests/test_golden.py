@@ -47,3 +47,21 @@ def test_w4g_oracle_fixture(oracle):
     K = d["x"].shape[1]
     assert np.array_equal(oracle.w4g_dequant(d["wq"], d["ws"], K).view(np.uint16), d["w"].view(np.uint16))
     assert np.array_equal(oracle.matmul_w4g(d["x"], d["wq"], d["ws"]).view(np.uint16), d["y"].view(np.uint16))
+
+
+def test_e2e_fixture_order_band():
+    """The config-5 fixture carries, per row, the order-only band (largest top-64 move
+    when the oracle sums in its two other fp32 orders) and each order's own leader: the
+    band is positive and below the logits' scale, and wherever the golden margin exceeds
+    twice the band both other orders pick the golden top-1 (the property the GPU gate's
+    tie rule rests on)."""
+    import numpy as np
+    from pathlib import Path
+    fx = np.load(Path(__file__).resolve().parent / "golden" / "e2e_4b_seed0.npz")
+    band, top2, am, alt = fx["band"], fx["top2"], fx["argmax"], fx["alt_argmax"]
+    assert list(fx["orders"]) == [1, 2] and alt.shape == (2, len(am))
+    assert (band > 0).all() and (band < 0.02 * np.abs(top2[:, 0])).all()
+    margin = top2[:, 0] - top2[:, 1]
+    clear = margin > 2 * band
+    assert clear.sum() >= len(am) - 6
+    assert (alt[:, clear] == am[clear]).all()

@@ -8,15 +8,17 @@ the reference's own decode gate (scripts/judge_logits.py:1-30: cosine >= 0.9999 
 same top-1):
   - the prompt's last-token logits and every decode step the fixture holds: cosine
     >= 0.9999 over every 8th logit, and the 64 largest logits within max(2e-2, 1 % of
-    |ref|) of the oracle's (36 layers of fp16 rounding in another summation order move
-    logits of ~220 by up to ~1, i.e. 8 ulps; 1 % is the relative error a cosine of
-    0.9999 allows); top-1 identical at every step whose golden margin exceeds twice that
-    step's largest top-64 logit error, and at the remaining near-tie steps (random-init
-    logits put a few leaders within 2-3 ulps of each other) the engine's top-1 must be
-    one of the golden's leaders within that band; a top-1 that differs from the golden's
-    is allowed only where the golden margin is at most 4 fp16 ulps of its leading logit
-    (the logits' own rounding step), and at no more than 3 of the sampled steps;
-    margins and ties are reported;
+    |ref|) of the oracle's;
+  - top-1: the fixture also holds, per step, the order-only band: how far the oracle's
+    own logits move (largest change over the 64 leaders) when its fp32 sums run in two
+    other valid orders with the same roundings (32-wide slices combined pairwise, the
+    decode GEMV's shape; 16-deep slices added in sequence, the GEMM's K steps). Two
+    leaders each moving by up to the band can swap only when their golden margin is at
+    most twice it, so wherever the margin exceeds twice the band the engine's top-1
+    must be the golden's, with no allowance; at the remaining steps (ties at the
+    precision fixed by the summation order, not by the engine) it must be one of the
+    golden leaders within twice the band of the first. Every such step is reported with
+    its margin and band;
   - the decode steps are teacher forced: the engine consumes the fixture's ids, which are
     the oracle's own greedy choices, so with top-1 identical it runs the same greedy path;
   - every one of the 256 steps: finite logits, and the token the blob's ARGMAX op returns
@@ -101,7 +103,9 @@ def test_config5_e2e_vs_cpu_golden(engine, model4b):
         assert tok == int(np.argmax(f)), f"step {t}: ARGMAX op gave {tok}, logits' first max {int(np.argmax(f))}"
 
     stride = int(fx["stride"])
-    margins, worst_rel, exact, ties = [], 0.0, 0, []
+    band = fx["band"].astype(np.float64)
+    assert band.shape == (len(fx["argmax"]),) and (band > 0).all(), "fixture without its order-only band"
+    margins, worst_rel, exact, ties, ratio = [], 0.0, 0, [], []
     for t in range(len(fx["argmax"])):
         g = rows[t].astype(np.float32)
         want = int(fx["argmax"][t])
@@ -115,28 +119,21 @@ def test_config5_e2e_vs_cpu_golden(engine, model4b):
         err = np.abs(g[ti].astype(np.float64) - tv)
         assert (err <= tol).all(), f"step {t}: top-64 logit off by {err.max():.4g}"
         worst_rel = max(worst_rel, float((err / np.maximum(np.abs(tv), 1e-3)).max()))
-        # Top-1: identical whenever the golden margin exceeds twice this step's largest
-        # top-64 logit error (the two leaders cannot swap within that error); below it
-        # the step is a tie at the logits' precision, and the engine's choice must be
-        # one of the golden's candidates within that band.
-        noise = 2.0 * float(err.max())
+        ratio.append(float(err.max()) / band[t])
+        tie = 2.0 * band[t]
         got = int(np.argmax(g))
-        if margin > noise:
-            assert got == want, f"step {t}: top-1 {got} vs golden {want} (golden margin {margin:.4g} > {noise:.4g})"
+        if margin > tie:
+            assert got == want, (f"step {t}: top-1 {got} vs golden {want} at a golden margin of {margin:.4g}, "
+                                 f"above twice the order-only band ({tie:.4g})")
             exact += 1
         else:
-            cand = {int(i) for i, v in zip(ti, tv) if v >= tv[0] - noise}
-            assert got in cand, f"step {t}: near-tie (margin {margin:.4g} <= {noise:.4g}), top-1 {got} not in {cand}"
-            ties.append((t, margin, got == want))
-    print(f"config 5: {exact} of {len(margins)} golden rows top-1 identical with a margin above twice the logit "
-          f"error; near ties (step, margin, same top-1) {ties}; margins min {min(margins):.4g} median "
-          f"{float(np.median(margins)):.4g}; top-64 worst relative error {worst_rel:.3g}; {STEPS} greedy steps")
-    flips = [(t, m) for t, m, same in ties if not same]
-    for t, m in flips:
-        lead = float(np.abs(fx["top2"][t][0]))
-        ulp = 2.0 ** (np.floor(np.log2(max(lead, 2.0 ** -14))) - 10)
-        assert m <= 4 * ulp, f"step {t}: top-1 differs at a golden margin of {m:.4g} (> 4 fp16 ulps = {4 * ulp:.4g})"
-    assert len(flips) <= 3, f"top-1 differs from the golden at {len(flips)} of {len(margins)} sampled steps: {flips}"
+            cand = {int(i) for i, v in zip(ti, tv) if v >= tv[0] - tie}
+            assert got in cand, f"step {t}: tie (margin {margin:.4g} <= {tie:.4g}), top-1 {got} not in {cand}"
+            ties.append((t, round(margin, 4), round(float(band[t]), 4), got == want))
+    print(f"config 5: {exact} of {len(margins)} golden rows above twice the order-only band, all top-1 "
+          f"identical; ties within it (step, margin, band, same top-1): {ties}; margins min {min(margins):.4g} "
+          f"median {float(np.median(margins)):.4g}; engine top-64 error / band: max {max(ratio):.3g} median "
+          f"{float(np.median(ratio)):.3g}; top-64 worst relative error {worst_rel:.3g}; {STEPS} greedy steps")
 
     direct, dtoks = _generate(engine, model4b, graphs=False)
     assert dtoks == toks

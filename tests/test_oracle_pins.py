@@ -306,3 +306,105 @@ def test_scalar_fallback_equals_vector_forms(oracle):
         oracle.lib().go_fast_disable(0)
     for f, s in zip(fast, slow):
         assert np.array_equal(_bits(f), _bits(s))
+
+
+def _ordered_sum(prod: np.ndarray, width: int, mode: int) -> np.ndarray:
+    """float32 sum over the last axis of `prod` in summation order `mode`: slices of
+    `width` summed from zero in sequence, the slice sums combined pairwise (mode 1) or
+    in sequence (mode 2); every add one float32 rounding (numpy float32 arrays)."""
+    n = prod.shape[-1]
+    parts = []
+    for s0 in range(0, n, width):
+        acc = np.zeros(prod.shape[:-1], np.float32)
+        for k in range(s0, min(s0 + width, n)):
+            acc = acc + prod[..., k]
+        parts.append(acc)
+    if mode == 1:
+        w = 1
+        while w < len(parts):
+            for i in range(0, len(parts) - w, 2 * w):
+                parts[i] = parts[i] + parts[i + w]
+            w *= 2
+        return parts[0]
+    acc = parts[0]
+    for p in parts[1:]:
+        acc = acc + p
+    return acc
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_summation_orders_are_the_stated_fp32_orders(oracle, mode):
+    """go_set_order's modes (used to measure order-only spread for the end-to-end gate)
+    compute exactly the stated fp32 order of the same products: the W4G linear (K = 200:
+    a ragged last slice; 7 slices of 32 in mode 1, an odd count for the pairwise tree)
+    and the fp16 [N, K] linear against float32 numpy sums in that order, bit for bit;
+    mode 0 stays the sequential order."""
+    if not oracle.fast_available():
+        pytest.skip("vector forms unavailable")
+    rng = np.random.default_rng(11 + mode)
+    M, K, N = 3, 200, 21
+    q = rng.integers(-8, 8, (N, K)).astype(np.int8)
+    wq = oracle.w4g_pack(q)
+    ws = rng.uniform(0.005, 0.02, (N, K // 8)).astype(np.float16)   # group 8
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    wf = rng.standard_normal((N, K)).astype(np.float16)
+    # Row 0 x column 0 tells the orders apart: products 1, then 2^-25 each (below half an
+    # ulp of 1, lost one by one in sequence, kept as 32- / 16-term slice sums), then -1:
+    # the sequential sum is 0, a sliced one 2^-25 times the kept terms.
+    a[0] = np.float16(2.0 ** -12)
+    a[0, 0], a[0, -1] = 1, -1
+    wf[0] = np.float16(2.0 ** -13)
+    wf[0, 0] = wf[0, -1] = 1
+    width = 32 if mode == 1 else 16
+    wdq = oracle.w4g_dequant(wq, ws, K, 8).astype(np.float32)
+
+    def ordered(w):
+        prod = a.astype(np.float32)[:, None, :] * w.astype(np.float32)[None, :, :]
+        return _ordered_sum(prod, width, mode).astype(np.float16)
+
+    seq_w4g = oracle.lib()
+    y0 = np.empty((M, N), np.float16)
+    assert seq_w4g.go_matmul_w4g(O._p(a), O._p(wq), O._p(ws), O._p(y0), M, K, N, 8, 2) == 0
+    with oracle.summation_order(mode):
+        y = np.empty((M, N), np.float16)
+        assert seq_w4g.go_matmul_w4g(O._p(a), O._p(wq), O._p(ws), O._p(y), M, K, N, 8, 2) == 0
+        yf = oracle.matmul_f16_nk(a, wf, 2)
+    assert yf[0, 0] > 0 and oracle.matmul_f16_nk(a, wf, 2)[0, 0] == 0
+    assert np.array_equal(_bits(y), _bits(ordered(wdq)))
+    assert np.array_equal(_bits(yf), _bits(ordered(wf)))
+    seq = np.zeros((M, N), np.float32)
+    for k in range(K):
+        seq = seq + a.astype(np.float32)[:, k:k + 1] * wdq[None, :, k][0]
+    assert np.array_equal(_bits(y0), _bits(seq.astype(np.float16)))
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_attention_summation_orders(oracle, mode):
+    """Causal prefill attention in mode 1 / 2: the q.k scores summed over d in 32- / 16-wide
+    slices (pairwise / in sequence), rounded through the chain's f16 points (score, times
+    f16 scale, plus a zero mask), the oracle's softmax row, then P.V over keys in 64-key
+    chunks combined pairwise / in sequence, against float32 numpy in those orders (S = 150:
+    three chunks, the last ragged)."""
+    if not oracle.fast_available():
+        pytest.skip("vector forms unavailable")
+    rng = np.random.default_rng(21 + mode)
+    S, H, KVH, hd, scale = 150, 2, 1, 64, 0.125
+    qa = rng.standard_normal((S, H, hd)).astype(np.float16)
+    ka = rng.standard_normal((S, KVH, hd)).astype(np.float16)
+    va = rng.standard_normal((S, KVH, hd)).astype(np.float16)
+    with oracle.summation_order(mode):
+        got = oracle.attn_prefill(qa, ka, va, scale, True, threads=2)
+    width = 32 if mode == 1 else 16
+    sc = np.float32(np.float16(scale))
+    want = np.empty((S, H, hd), np.float16)
+    for h in range(H):
+        qf, kf, vf = qa[:, h].astype(np.float32), ka[:, 0].astype(np.float32), va[:, 0].astype(np.float32)
+        t = _ordered_sum(qf[:, None, :] * kf[None, :, :], width, mode).astype(np.float16)
+        t = (t.astype(np.float32) * sc).astype(np.float16)
+        s = (t.astype(np.float32) + np.float32(0)).astype(np.float16)
+        s[np.triu_indices(S, 1)] = np.float16(-np.inf)
+        p = oracle.softmax(s, S, S).astype(np.float32)
+        for i in range(S):
+            prod = (p[i, :i + 1, None] * vf[:i + 1]).T   # [hd, keys]
+            want[i, h] = _ordered_sum(prod, 64, mode).astype(np.float16)
+    assert np.array_equal(_bits(got), _bits(want))
