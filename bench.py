@@ -685,13 +685,24 @@ def cpu_prefill(cfg, w, threads):
 
 
 def _cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo gives it: the model name (a virtual machine may show
+    only the vendor line), with the family / model / stepping numbers that identify the
+    core generation, and the logical CPUs visible to this process."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (t.strip() for t in line.split(":", 1))
+                if k in ("model name", "cpu family", "model", "stepping") and k not in info:
+                    info[k] = v
+            if not line.strip() and info:
+                break
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    ids = ", ".join(f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info)
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return f"{name} ({ids}; {n} logical CPUs visible)" if ids else name
 
 
 if __name__ == "__main__":
