@@ -62,12 +62,14 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
     const __half* __restrict__ q, uint32_t ldq, uint32_t qhs, const __half* __restrict__ k,
     const __half* __restrict__ v, uint32_t ldkv, uint32_t kvhs, __half* __restrict__ out, uint32_t ldo,
     uint32_t ohs, uint32_t S, uint32_t H, uint32_t KVH, float scale_log2) {
-    __shared__ __align__(16) _Float16 kvbuf[2 * KV_HALF];
+    // 8-wave tiles double-buffer the stages (one workgroup per CU either way); smaller
+    // workgroups keep one buffer, so that two of them still fit a CU's LDS.
+    constexpr bool DB = WPH == 4;
+    __shared__ __align__(16) _Float16 kvbuf[(DB ? 2 : 1) * 2 * KV_HALF];   // [stage buffer][half]
     constexpr uint32_t QT = 32 * WPH, NT = 64 * WPH;   // queries per tile, threads per half
     constexpr int KR = KT * 16 / NT;                     // K / V rows per thread per stage
     const uint32_t part = threadIdx.x / NT, tid = threadIdx.x % NT, lane = tid & 63, wave = tid >> 6;
-    _Float16* const Ks = kvbuf + part * KV_HALF;
-    _Float16* const Vs = Ks + KT * KS;
+    _Float16* const Ks0 = kvbuf + part * KV_HALF;   // stage buffer b at + 2 * b * KV_HALF
     const uint32_t n_qt = (S + QT - 1) / QT;
     const uint32_t qtile = n_qt - 1 - blockIdx.y;      // heaviest causal tiles first
     const uint32_t h = blockIdx.x;
@@ -117,21 +119,23 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
     const uint32_t ns = (kend + KT - 1) / KT, ns0 = (ns + 1) / 2;
     const uint32_t st0 = part * ns0, st1 = min(ns, st0 + ns0);   // this half's stages
     const uint32_t klast = st1 > st0 ? min(st1 * KT, kend) - 1 : kend - 1;
-    load_kv(min(st0 * KT, kend - 1));
-    for (uint32_t it = 0; it < ns0; ++it) {
-        const uint32_t kb = (st0 + it) * KT;
-        __syncthreads();
+    // With two LDS stage buffers, stage it is computed from buffer it % 2 while the
+    // registers hold stage it + 1, written to the other buffer after the compute: one
+    // barrier per stage (the other buffer was last read in stage it - 1, before the
+    // previous barrier). With one buffer, a barrier before the write as well.
+    auto stage_kv = [&](uint32_t b) __attribute__((always_inline)) {
+        _Float16* const Kd = Ks0 + 2 * b * KV_HALF;
+        _Float16* const Vd = Kd + KT * KS;
 #pragma unroll
         for (int i = 0; i < KR; ++i) {
             const uint32_t key = (tid >> 4) + (NT / 16) * i;
-            *reinterpret_cast<u32x4*>(&Ks[key * KS + ch * 8]) = kv4[i];
-            *reinterpret_cast<u32x4*>(&Vs[key * VSR + ch * 8]) = vv4[i];
+            *reinterpret_cast<u32x4*>(&Kd[key * KS + ch * 8]) = kv4[i];
+            *reinterpret_cast<u32x4*>(&Vd[key * VSR + ch * 8]) = vv4[i];
         }
-        __syncthreads();
-        load_kv(min(kb + KT, klast));
-        if (st0 + it >= st1) continue;          // the shorter half's idle step
-        if (CAUSAL && kb > qw + 31) continue;   // the whole stage is masked for this wave
-
+    };
+    load_kv(min(st0 * KT, kend - 1));
+    // One stage of this wave: keys kb .. kb + KT - 1 from the K / V tiles at Ks / Vs.
+    auto stage_compute = [&](const _Float16* Ks, const _Float16* Vs, uint32_t kb) __attribute__((always_inline)) {
         // Scores of the stage's two 32-key halves: two independent MFMA chains, all K
         // fragments read first.
         f16x_t s0, s1;
@@ -208,6 +212,32 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
                 const u32x4 packed = {lo[0], lo[1], hi[0], hi[1]};
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, packed), pb[j], o[dt], 0, 0, 0);
             }
+        }
+    };
+    // A stage runs unless it is the shorter half's idle step or wholly masked for this wave.
+    auto active = [&](uint32_t it, uint32_t kb) { return st0 + it < st1 && !(CAUSAL && kb > qw + 31); };
+    if constexpr (DB) {
+        stage_kv(0);
+        load_kv(min(st0 * KT + KT, klast));
+        __syncthreads();
+        for (uint32_t it = 0; it < ns0; ++it) {
+            const uint32_t kb = (st0 + it) * KT;
+            const _Float16* const Ks = Ks0 + 2 * (it & 1) * KV_HALF;
+            if (active(it, kb)) stage_compute(Ks, Ks + KT * KS, kb);
+            if (it + 1 < ns0) {
+                stage_kv((it + 1) & 1);
+                load_kv(min(kb + 2 * KT, klast));
+            }
+            __syncthreads();
+        }
+    } else {
+        for (uint32_t it = 0; it < ns0; ++it) {
+            const uint32_t kb = (st0 + it) * KT;
+            __syncthreads();
+            stage_kv(0);
+            __syncthreads();
+            load_kv(min(kb + KT, klast));
+            if (active(it, kb)) stage_compute(Ks0, Ks0 + KT * KS, kb);
         }
     }
 
