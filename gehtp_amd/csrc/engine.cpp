@@ -76,6 +76,8 @@ struct Engine {
     bool pool_owned = false;
     std::vector<void*> retired_pools;   // earlier bump pools stay valid until shutdown
     const uint32_t* static_offsets = nullptr;
+    bool plan_from_blob = false;          // static_offsets come from a blob's TEMPOFF slot
+    std::vector<uint8_t> plan_payload;    // that slot's bytes
     uint32_t static_off_arr[kMaxTemps];
     uint8_t* vtcm_pool = nullptr;
     uint32_t vtcm_pool_size = 0;
@@ -405,15 +407,63 @@ uint8_t* temp_get(uint32_t id, uint32_t bytes) {
     return p;
 }
 
-// TEMPOFF slot (oplist_exec.c:2012-2066): [cap][reserve: lo16 bump KB | hi16 VTCM KB][n][n x {tid,off,size}].
-int load_tempoff(const wt_blob* b, char* err, size_t errn) {
-    if (g.static_offsets) return 0;
+// Drops a static plan loaded from a blob's TEMPOFF slot: the temps living in its pools
+// are forgotten (a later write allocates them again), the pools are freed once the
+// stream is idle, and captured graphs (which hold their addresses) are dropped.
+void drop_graphs();
+void drop_blob_plan() {
+    if (g.stream) hipStreamSynchronize(g.stream);
+    drop_graphs();
+    auto inside = [](const uint8_t* p, const uint8_t* base, uint64_t n) { return base && p >= base && p < base + n; };
+    for (uint32_t t = 0; t < kMaxTemps; ++t)
+        if (g.temps[t] && (inside(g.temps[t], g.pool, g.pool_cap) || inside(g.temps[t], g.vtcm_pool, g.vtcm_pool_size))) {
+            g.temps[t] = nullptr;
+            g.temp_bytes[t] = 0;
+        }
+    if (g.pool && g.pool_owned) dev_free(g.pool);
+    if (g.vtcm_pool) dev_free(g.vtcm_pool);
     std::fill(std::begin(g.static_off_arr), std::end(g.static_off_arr), kNone);
     std::fill(std::begin(g.vtcm_off_arr), std::end(g.vtcm_off_arr), kNone);
-    for (uint32_t s = 0; s < b->n_slots; ++s) {
-        if (b->slots[s].addr != WT_SLOT_TEMPOFF) continue;
-        const uint8_t* p = b->weight_base + b->slots[s].offset;
-        const uint32_t len = b->slots[s].len;
+    g.pool = nullptr;
+    g.pool_cap = g.pool_used = 0;
+    g.pool_owned = false;
+    g.vtcm_pool = nullptr;
+    g.vtcm_pool_size = 0;
+    g.static_offsets = nullptr;
+    g.plan_payload.clear();
+    g.plan_from_blob = false;
+    ++g.epoch;
+}
+
+// TEMPOFF slot (oplist_exec.c:2012-2066): [cap][reserve: lo16 bump KB | hi16 VTCM KB][n][n x {tid,off,size}].
+// The reference parses the first TEMPOFF slot it meets and keeps that plan until
+// shutdown, so a second blob with another plan (a model's decode blob after its prefill
+// blob) would run on the first blob's offsets, whose sizes and sharing belong to other
+// temps. Here each blob runs with its own plan: a different TEMPOFF payload replaces the
+// loaded one, a blob without one drops it (bump allocation); a plan installed by the
+// caller through wt_exec_pool_init is kept, as in the reference.
+int load_tempoff(const wt_blob* b, char* err, size_t errn) {
+    const uint8_t* tp = nullptr;
+    uint32_t tlen = 0;
+    for (uint32_t s = 0; s < b->n_slots; ++s)
+        if (b->slots[s].addr == WT_SLOT_TEMPOFF) {
+            tp = b->weight_base + b->slots[s].offset;
+            tlen = b->slots[s].len;
+            break;
+        }
+    if (g.static_offsets && !g.plan_from_blob) return 0;   // the caller's plan
+    if (!tp) {
+        if (g.plan_from_blob) drop_blob_plan();
+        return 0;
+    }
+    if (g.plan_from_blob && g.plan_payload.size() == tlen && std::memcmp(g.plan_payload.data(), tp, tlen) == 0)
+        return 0;   // this blob's plan is loaded
+    if (g.plan_from_blob) drop_blob_plan();
+    std::fill(std::begin(g.static_off_arr), std::end(g.static_off_arr), kNone);
+    std::fill(std::begin(g.vtcm_off_arr), std::end(g.vtcm_off_arr), kNone);
+    {
+        const uint8_t* p = tp;
+        const uint32_t len = tlen;
         if (len < 12u) return ERR("tempoff slot short");
         uint32_t cap, reserve, n;
         std::memcpy(&cap, p, 4);
@@ -459,7 +509,8 @@ int load_tempoff(const wt_blob* b, char* err, size_t errn) {
             g.vtcm_pool = static_cast<uint8_t*>(vp);
             g.vtcm_pool_size = vtcm_cap;
         }
-        break;
+        g.plan_payload.assign(tp, tp + tlen);
+        g.plan_from_blob = true;
     }
     return 0;
 }
@@ -2853,6 +2904,8 @@ void wt_exec_shutdown(void) {
     g.pool_cap = g.pool_used = 0;
     g.pool_owned = false;
     g.static_offsets = nullptr;
+    g.plan_from_blob = false;
+    g.plan_payload.clear();
     if (g.vtcm_pool) dev_free(g.vtcm_pool);
     g.vtcm_pool = nullptr;
     g.vtcm_pool_size = 0;
@@ -2902,6 +2955,7 @@ void wt_exec_state_reset(void) {
 
 void wt_exec_pool_init(uint8_t* base, uint32_t total_cap, uint32_t static_cap, const uint32_t* offsets) {
     ++g.epoch;
+    if (g.plan_from_blob) drop_blob_plan();   // the caller's plan replaces a blob's
     if (base) {
         if (g.pool && g.pool_owned) g.retired_pools.push_back(g.pool);
         g.pool = base;

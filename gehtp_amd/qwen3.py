@@ -237,7 +237,23 @@ class _Emitter:
         bb.op(OP.MATMUL_F16, src, self.ref("embed"), t["logits"], 1, c.hidden, c.vocab, 2)
         bb.op(OP.ARGMAX_F16, t["logits"], t["tok"], c.vocab)
 
-    def emit(self, S: int, decode: bool, token_input: bool = False) -> bytes:
+    def finish(self, recycle: bool, tempoff: bool) -> bytes:
+        """Build the blob; with `recycle` its temps renumbered by the reference emitter's
+        free list, with `tempoff` a TEMPOFF static plan added (gehtp_amd.tempplan). The
+        logits and token temps are kept live to the end (read after the run)."""
+        from .tempplan import recycle as _recycle, tempoff_plan
+        keep = [self.t["logits"], self.t["tok"]]
+        if recycle:
+            m = _recycle(self.bb, keep=keep)
+            self.t = {k: m[v] for k, v in self.t.items() if v in m}
+            keep = [self.t["logits"], self.t["tok"]]
+        if tempoff:
+            cap, entries = tempoff_plan(self.bb, keep=keep)
+            self.bb.set_tempoff(cap, entries)
+        return self.bb.build()
+
+    def emit(self, S: int, decode: bool, token_input: bool = False, recycle: bool = False,
+             tempoff: bool = False) -> bytes:
         c, bb = self.cfg, self.bb
         if token_input:   # int32 token ids in; the embedding rows gathered in-graph
             ids = bb.add_input_slot(S * 4)
@@ -251,20 +267,25 @@ class _Emitter:
         for l in range(c.layers):
             self.layer(l, S, x_in if l == 0 else self.t["x"], decode)
         self.head(S)
-        return bb.build()
+        return self.finish(recycle, tempoff)
 
 
-def emit_prefill(cfg: Qwen3Config, w: Weights, S: int, max_pos: int):
-    """(blob bytes, temp ids): a prefill of S tokens; input = embeddings [S, hidden] fp16."""
+def emit_prefill(cfg: Qwen3Config, w: Weights, S: int, max_pos: int, recycle: bool = False,
+                 tempoff: bool = False):
+    """(blob bytes, temp ids): a prefill of S tokens; input = embeddings [S, hidden] fp16.
+    recycle / tempoff: temp ids from the reference emitter's free list / a TEMPOFF plan."""
     e = _Emitter(cfg, w, max_pos)
-    return e.emit(S, decode=False), dict(e.t)
+    blob = e.emit(S, decode=False, recycle=recycle, tempoff=tempoff)
+    return blob, dict(e.t)
 
 
-def emit_decode(cfg: Qwen3Config, w: Weights, max_pos: int, fused: bool = True, token_input: bool = False):
+def emit_decode(cfg: Qwen3Config, w: Weights, max_pos: int, fused: bool = True, token_input: bool = False,
+                recycle: bool = False, tempoff: bool = False):
     """(blob bytes, temp ids): one decode step; input = the token's embedding [hidden],
     or with token_input its int32 id (the row gathered in-graph from the lm_head / embedding
     table, so the step's ARGMAX output can feed the next step: wt_exec_run_steps).
     fused: attention as one OP_ATTN_DECODE_QKV_F16 per layer instead of
-    OP_QK_ROPE_KV_F16 + OP_ATTN_DECODE_F16."""
+    OP_QK_ROPE_KV_F16 + OP_ATTN_DECODE_F16. recycle / tempoff as for emit_prefill."""
     e = _Emitter(cfg, w, max_pos, fused_decode=fused)
-    return e.emit(1, decode=True, token_input=token_input), dict(e.t)
+    blob = e.emit(1, decode=True, token_input=token_input, recycle=recycle, tempoff=tempoff)
+    return blob, dict(e.t)

@@ -37,14 +37,21 @@ _ROLES = {
     OP.BROADCAST_F16: ((0,), (1,)),
     OP.TRANSPOSE_GEN_F16: ((0,), (1,)),
     OP.MATMUL_W4G_F16: ((0,), (3,)),
+    # this build's fused opcodes (include/oplist_parse.h)
+    OP.W4G_FUSED_F16: ((0, 8), (3,)),
+    OP.QK_ROPE_KV_F16: ((0,), (1, 2, 3)),
+    OP.ATTN_DECODE_QKV_F16: ((0,), (2,)),
+    OP.ATTN_F16: ((0, 1, 2), (3,)),
+    OP.ATTN_DECODE_F16: ((0,), (2,)),
 }
 
 
-def _is_temp(a: int) -> bool:
+def _is_temp(a: int) -> bool:   # WT_REF_NONE (0xFFFFFFFF) carries bit 15: no temp
     return not (a & 0x8000) and (a & 0xE000) != WT_REF_STATE_FLAG
 
 
-def _roles(opc: int, args):
+def _positions(opc: int, args):
+    """(input, output) argument positions holding temps."""
     if opc not in _ROLES:
         raise ValueError(f"recycle: no temp roles for opcode {opc}")
     ins, outs = _ROLES[opc]
@@ -52,54 +59,79 @@ def _roles(opc: int, args):
         outs = tuple(p for p in outs if args[p] != 0)
     if opc == OP.CONCAT_F16:
         ins = tuple(p for p in range(8) if p < 2 or args[p] != 0)
-    return ([args[p] for p in ins if _is_temp(args[p])], [args[p] for p in outs if _is_temp(args[p])])
+    return (tuple(p for p in ins if _is_temp(args[p])), tuple(p for p in outs if _is_temp(args[p])))
+
+
+def _roles(opc: int, args):
+    ins, outs = _positions(opc, args)
+    return ([args[p] for p in ins], [args[p] for p in outs])
 
 
 def recycle(bb, keep=()) -> dict:
-    """Renumber the temps of bb's ops in place with the reference emitter's free list;
-    temps in `keep` (read after the run, e.g. logits) are never released. Returns the
-    map old id -> new id."""
-    last = {}
-    for i, (opc, args) in enumerate(bb.ops):
-        for t in _roles(opc, args)[0]:
-            last[t] = i
-    for t in keep:
-        last[t] = len(bb.ops)
-    # Ids start at 1: a KV_GATHER face argument of 0 means "no face", so id 0 could not
-    # name a gathered face.
-    free, nxt, new = [], 1, {}
+    """Renumber the temps of bb's ops in place with the reference emitter's free list.
+    Every write of a temp starts a new value (an emitter may write one id once per layer);
+    a value's id returns to the list after its last read. Temps in `keep` (read after the
+    run, e.g. logits) keep their last value to the end. Returns the map old id -> the new
+    id of its last value."""
+    # values: one per write; last read of each
+    cur, last, n_val = {}, {}, 0
+    vals_in, vals_out = [], []
     for i, (opc, args) in enumerate(bb.ops):
         ins, outs = _roles(opc, args)
-        ins_new = [new[t] for t in ins]   # an input is always written before it is read
-        for t in outs:
-            if t in new and last.get(t, -1) > i:
-                raise ValueError(f"recycle: temp {t} written again while live (op {i})")
-            if free:
-                new[t] = free.pop()
-            else:
-                new[t] = nxt
-                nxt += 1
-        amap = dict(zip(ins, ins_new))
-        amap.update({t: new[t] for t in outs})
-        p_ins, p_outs = _ROLES[opc]
-        for p in set(p_ins) | set(p_outs):
-            if p < len(args) and _is_temp(args[p]) and args[p] in amap:
-                args[p] = amap[args[p]]
-        released = []
+        vin = []
         for t in ins:
-            if last.get(t) == i and t not in released:
-                released.append(t)
-                free.append(new[t])
+            if t not in cur:
+                raise ValueError(f"recycle: op {i} reads temp {t} before any write")
+            vin.append(cur[t])
+            last[cur[t]] = i
+        vout = []
+        for t in outs:
+            cur[t] = n_val
+            last.setdefault(n_val, i)
+            vout.append(n_val)
+            n_val += 1
+        vals_in.append(vin)
+        vals_out.append(vout)
+    for t in keep:
+        last[cur[t]] = len(bb.ops)
+    # Ids start at 1: a KV_GATHER face argument of 0 means "no face", so id 0 could not
+    # name a gathered face.
+    free, nxt, vid = [], 1, {}
+    for i, (opc, args) in enumerate(bb.ops):
+        ins, outs = _roles(opc, args)
+        amap = {t: vid[v] for t, v in zip(ins, vals_in[i])}
+        for t, v in zip(outs, vals_out[i]):
+            if free:
+                vid[v] = free.pop()
+            else:
+                vid[v] = nxt
+                nxt += 1
+        omap = {t: vid[v] for t, v in zip(outs, vals_out[i])}
+        p_in, p_out = _positions(opc, args)
+        for p in p_in:
+            args[p] = amap[args[p]]
+        for p in p_out:
+            args[p] = omap[args[p]]
+        released = []
+        for v in vals_in[i]:
+            if last[v] == i and v not in released:
+                released.append(v)
+                free.append(vid[v])
+        for v in vals_out[i]:   # written, never read (and not kept): free at once
+            if last[v] == i and v not in vals_in[i] and v not in released:
+                released.append(v)
+                free.append(vid[v])
     bb.next_temp = nxt
-    return new
+    return {t: vid[v] for t, v in cur.items()}
 
 
 def _state_slots(bb, st_ref: int, kv_elems: int) -> int:
     return bb.state_bytes[st_ref & 0x1FFF] // (kv_elems * 4)
 
 
-def out_bytes(bb, opc: int, args) -> int:
-    """Bytes an op writes to its output temp(s) (per face for KV_GATHER)."""
+def out_bytes(bb, opc: int, args, pos: int | None = None) -> int:
+    """Bytes an op writes to its output temp at argument position `pos` (default: its
+    first output; every KV_GATHER face has the same size)."""
     a = args
     if opc in (OP.ADD_F16, OP.BINARY_F16):
         return a[3] * 2
@@ -127,6 +159,17 @@ def out_bytes(bb, opc: int, args) -> int:
     if opc == OP.KV_GATHER_F16:
         P = a[3] if a[3] != WT_KV_POS_AUTO else _state_slots(bb, a[0], a[5] * a[6])
         return a[4] * a[6] * P * 2
+    if opc == OP.W4G_FUSED_F16:   # [a, wq, ws, y, M, K, N, gamma, res, swiglu, flags]
+        return a[4] * (a[6] // 2 if a[9] else a[6]) * 2
+    if opc == OP.QK_ROPE_KV_F16:  # [qkv, q_out, k_out, v_out, state, S, H, KVH, hd, ...]
+        heads = a[6] if (pos or 1) == 1 else a[7]
+        return a[5] * heads * a[8] * 2
+    if opc == OP.ATTN_DECODE_QKV_F16:   # [qkv, state, out, H, KVH, hd, ...]
+        return a[3] * a[5] * 2
+    if opc == OP.ATTN_F16:        # [q, k, v, out, S, H, KVH, hd, ...]
+        return a[4] * a[5] * a[7] * 2
+    if opc == OP.ATTN_DECODE_F16:  # [q, state, out, n_kv, H, KVH, hd, scale]
+        return a[4] * a[6] * 2
     return 0
 
 
@@ -137,13 +180,13 @@ def tempoff_plan(bb, keep=(), align: int = 128):
     no id busy at the same time holds."""
     spans, size = {}, {}
     for i, (opc, args) in enumerate(bb.ops):
-        ins, outs = _roles(opc, args)
-        for t in ins:
-            spans[t][-1][1] = i
-        nb = out_bytes(bb, opc, args)
-        for t in outs:
+        pin, pout = _positions(opc, args)
+        for p in pin:
+            spans[args[p]][-1][1] = i
+        for p in pout:
+            t = args[p]
             spans.setdefault(t, []).append([i, i])
-            size[t] = max(size.get(t, 0), nb)
+            size[t] = max(size.get(t, 0), out_bytes(bb, opc, args, p))
     for t in keep:
         spans[t][-1][1] = len(bb.ops)
 

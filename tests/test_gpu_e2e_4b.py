@@ -139,3 +139,30 @@ def test_config5_e2e_vs_cpu_golden(engine, model4b):
     assert dtoks == toks
     for t, (a, b) in enumerate(zip(rows, direct)):
         assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"step {t}: graph replay and direct runs differ"
+
+
+def test_config5_with_a_static_temp_plan(engine, model4b):
+    """The 36-layer model's prefill (2048 tokens) and 8 decode steps with a TEMPOFF static
+    plan (the SwiGLU activation sharing bytes with the attention tensors) give the bits of
+    the bump-allocated blobs at every step."""
+    from gehtp_amd.qwen3 import CONFIG_4B, emit_decode, emit_prefill
+    cfg, w, fx, pre, tp, dec, td = model4b
+    S, max_pos = int(fx["prompt"]), int(fx["prompt"]) + STEPS + 64
+    pre2, tp2 = emit_prefill(CONFIG_4B, w, S, max_pos, tempoff=True)
+    dec2, td2 = emit_decode(CONFIG_4B, w, max_pos, tempoff=True)
+    emb = w.embed()
+    runs = []
+    for (p_, tp_, d_, td_) in ((pre, tp, dec, td), (pre2, tp2, dec2, td2)):
+        engine.shutdown()
+        engine.set_ext_weights(w.image.ctypes.data)
+        pp, pd = engine.parse(p_), engine.parse(d_)
+        engine.state_reset()
+        engine.run_io(pp, np.ascontiguousarray(emb[fx["prompt_ids"]]).tobytes(), tp_["tok"])
+        rows = [np.frombuffer(engine.temp(tp_["logits"]), np.float16)[:cfg.vocab].copy()]
+        for t in range(8):
+            engine.run_io(pd, emb[int(fx["decode_ids"][t])].tobytes(), td_["tok"])
+            rows.append(np.frombuffer(engine.temp(td_["logits"]), np.float16)[:cfg.vocab].copy())
+        engine.shutdown()
+        runs.append(rows)
+    for t, (a, b) in enumerate(zip(*runs)):
+        assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"step {t}"

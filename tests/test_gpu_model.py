@@ -198,3 +198,48 @@ def test_run_steps_errors(engine):
     ids = np.frombuffer(engine.run_steps(pt, 3, first, tdt["tok"]), np.int32)
     assert ids.shape == (3,) and (ids >= 0).all() and (ids < cfg.vocab).all()
     engine.shutdown()
+
+
+def _run_plain_vs_planned(engine, cfg, S, n_dec, seed, max_pos, **plan):
+    """Prompt + teacher-forced decode steps through this build's blobs, plain and with
+    `plan` (recycle / tempoff); returns the logits rows of both."""
+    w = Weights(cfg, seed=seed)
+    ids = np.random.default_rng(seed + 1).integers(0, cfg.vocab, S + n_dec)
+    emb = w.embed()
+    out = []
+    for kw in ({}, plan):
+        engine.shutdown()
+        engine.set_ext_weights(w.image.ctypes.data)
+        pre, tp = emit_prefill(cfg, w, S, max_pos, **kw)
+        dec, td = emit_decode(cfg, w, max_pos, **kw)
+        pp, pd = engine.parse(pre), engine.parse(dec)
+        engine.state_reset()
+        engine.run_io(pp, np.ascontiguousarray(emb[ids[:S]]).tobytes(), tp["tok"])
+        rows = [np.frombuffer(engine.temp(tp["logits"]), np.float16)[:cfg.vocab].copy()]
+        for t in range(n_dec):
+            engine.run_io(pd, emb[ids[S + t]].tobytes(), td["tok"])
+            rows.append(np.frombuffer(engine.temp(td["logits"]), np.float16)[:cfg.vocab].copy())
+        # the prefill blob again after the decode blob (with plans: back to its own plan)
+        engine.state_reset()
+        engine.run_io(pp, np.ascontiguousarray(emb[ids[:S]]).tobytes(), tp["tok"])
+        again = np.frombuffer(engine.temp(tp["logits"]), np.float16)[:cfg.vocab]
+        assert np.array_equal(again.view(np.uint16), rows[0].view(np.uint16)), "prefill after decode"
+        engine.shutdown()
+        out.append(rows)
+    return out
+
+
+@pytest.mark.parametrize("plan", [{"tempoff": True}, {"recycle": True, "tempoff": True}],
+                         ids=["tempoff", "recycled-tempoff"])
+@pytest.mark.parametrize("cfg,S,n_dec,max_pos", [(SMALL, 40, 12, 96), (CONFIG_08B_LAYER, 512, 24, 600)],
+                         ids=["small-2layer", "config4"])
+def test_static_temp_plan_gives_the_same_bits(engine, cfg, S, n_dec, max_pos, plan):
+    """The model's prefill and decode blobs with a TEMPOFF static plan (temps whose values
+    never meet share bytes: the SwiGLU activation over the attention tensors), with and
+    without recycled temp ids, give the bits of the same blobs with bump-allocated temps,
+    at every step (graph replay on, as by default). Each blob runs on its own plan: the
+    decode blob's replaces the prefill blob's, and the prefill blob run again afterwards
+    gets its own back."""
+    plain, planned = _run_plain_vs_planned(engine, cfg, S, n_dec, 61, max_pos, **plan)
+    for t, (a, b) in enumerate(zip(plain, planned)):
+        assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"step {t}"
