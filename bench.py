@@ -55,6 +55,9 @@ def parse_args():
                     help="BASELINE configs 1-3 kernel by kernel (GEMV, RMSNorm + GEMM, prefill and decode "
                          "attention), operands rotated over copies totalling > 256 MB and, beside it, "
                          "one copy repeated (cache-resident); prints one JSON line")
+    ap.add_argument("--gemm-operands", action="store_true",
+                    help="the four 4B prefill GEMM shapes (M = 2048) with random and with constant operands: "
+                         "this build's W4A16 GEMM and torch's fp16 GEMM side by side; prints one JSON line")
     ap.add_argument("--only", default=None,
                     help="with --kernel-configs: comma-separated subset of c1,c2,c3p,c3d,c4")
     return ap.parse_args()
@@ -87,6 +90,8 @@ def main() -> int:
         return roofline_only(args)
     if args.kernel_configs:
         return kernel_configs(args)
+    if args.gemm_operands:
+        return gemm_operands(args)
     import numpy as np
     import torch
 
@@ -346,6 +351,99 @@ def roofline_only(args) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"roofline_only": True, "avg_launch_us": avg_s * 1e6, "bytes_per_launch": bpl,
                       "achieved_gbs": gbs, "copy_bytes": 256 << 20}), flush=True)
+    return 0
+
+
+def gemm_operands(args) -> int:
+    """The 4B prefill GEMM shapes (M = 2048 tokens; q|k|v N 6144 K 2560, o-proj N 2560
+    K 4096 with its residual, gate/up N 19456 K 2560 with SwiGLU, down N 2560 K 9728 with
+    its residual) through gehtp_w4g_fused_ws (o-proj and down split K through the
+    workspace; the time includes the finishing pass), once with random operands (int4
+    codes uniform over all 16 values, scales U[0.005, 0.02], activations N(0, 1)) and
+    once with constant ones (every weight byte 0x77, every scale 2^-6, every activation
+    1/16), the same launches on the same buffers. Beside each, torch's fp16 GEMM
+    (hipBLASLt) of the same M x N x K with N(0, 1) / N(0, 0.02) operands and with
+    constants. Each time is the mean over back-to-back launches between two HIP events
+    on the launch stream, after warm-up launches."""
+    import torch
+
+    from gehtp_amd import load_library, lib_path
+    lib = load_library(lib_path)
+    assert torch.cuda.is_available(), "needs a GPU"
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    M = 2048
+    shapes = [("qkv", 6144, 2560, False, 0), ("o_proj", 2560, 4096, True, 0), ("gate_up", 19456, 2560, False, 1),
+              ("down", 2560, 9728, True, 0)]
+    reps = 20
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+    out = {}
+    for name, N, K, has_res, mode in shapes:
+        flops = 2.0 * M * N * K
+        n_out = N // 2 if mode else N
+        wq = torch.empty((N, K // 2), dtype=torch.uint8, device=dev)
+        ws = torch.empty((N, K // 64), dtype=torch.float16, device=dev)
+        x = torch.empty((M, K), dtype=torch.float16, device=dev)
+        res = torch.randn((M, n_out), device=dev, generator=gen).half() if has_res else None
+        y = torch.empty((M, n_out), dtype=torch.float16, device=dev)
+        need = int(lib.gehtp_w4g_split_bytes(M, N, K))
+        work = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+
+        def w4(_x=x, _wq=wq, _ws=ws, _y=y, _res=res, _n_out=n_out, _N=N, _K=K, _mode=mode, _need=need, _work=work):
+            assert lib.gehtp_w4g_fused_ws(_x.data_ptr(), _K, _wq.data_ptr(), _ws.data_ptr(), _y.data_ptr(), _n_out, M,
+                                          _N, _K, None, _res.data_ptr() if _res is not None else None, _n_out, _mode,
+                                          _work.data_ptr() if _need else None, _need, sp) == 0
+        row = {"M": M, "N": N, "K": K, "flops": flops}
+        for kind in ("random", "constant"):
+            if kind == "random":
+                wq.copy_(torch.randint(0, 256, wq.shape, dtype=torch.uint8, device=dev, generator=gen))
+                ws.copy_((torch.rand(ws.shape, device=dev, generator=gen) * 0.015 + 0.005).half())
+                x.copy_(torch.randn(x.shape, device=dev, generator=gen).half())
+            else:
+                wq.fill_(0x77)
+                ws.fill_(2.0 ** -6)
+                x.fill_(1.0 / 16)
+            t = timed(w4)
+            row[f"w4a16_{kind}_us"] = round(t * 1e6, 1)
+            row[f"w4a16_{kind}_tflops"] = round(flops / t / 1e12, 1)
+        del wq, ws, work
+        if mode:
+            y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        for kind in ("random", "constant"):
+            if kind == "random":
+                a = torch.randn((M, K), device=dev, generator=gen).half()
+                b = (torch.randn((N, K), device=dev, generator=gen) * 0.02).half()
+            else:
+                a = torch.full((M, K), 1.0 / 16, dtype=torch.float16, device=dev)
+                b = torch.full((N, K), 2.0 ** -6, dtype=torch.float16, device=dev)
+            bt = b.t()
+            t = timed(lambda: torch.matmul(a, bt, out=y))
+            row[f"torch_fp16_{kind}_us"] = round(t * 1e6, 1)
+            row[f"torch_fp16_{kind}_tflops"] = round(flops / t / 1e12, 1)
+            del a, b, bt
+        out[name] = row
+        log(f"{name:8s} M {M} N {N:5d} K {K:4d}: W4A16 random {row['w4a16_random_us']:.1f} us "
+            f"({row['w4a16_random_tflops']:.0f} TF), constant {row['w4a16_constant_us']:.1f} us "
+            f"({row['w4a16_constant_tflops']:.0f} TF); torch fp16 random {row['torch_fp16_random_us']:.1f} us "
+            f"({row['torch_fp16_random_tflops']:.0f} TF), constant {row['torch_fp16_constant_us']:.1f} us "
+            f"({row['torch_fp16_constant_tflops']:.0f} TF)")
+    print(json.dumps({"metric": "prefill GEMM time by operand values, 4B shapes", "unit": "us", "shapes": out,
+                      "peak_tflops": FP16_PEAK_TFLOPS}), flush=True)
     return 0
 
 
