@@ -394,6 +394,186 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// GEMV for M = 1 with whole rows inside a wave. P = 16 or 32 lanes share a row, each
+// owning C of its 16-byte slices (lane p: slices p, p + P, ...; K = 32 * C * P, so each
+// load instruction reads P consecutive slices of a row), and a wave holds RW = 64 / P
+// rows per pass and a row's partial sums meet in DPP / row-swap steps inside the wave:
+// no workgroup barrier follows the passes, and each wave stores its rows as soon as its
+// own loads have landed (w4g_gemv_kernel waits at a barrier for the workgroup's slowest
+// wave before its LDS row sums). Every weight load is issued up front, slice-major (the
+// order the arithmetic consumes them), behind the activation loads. The workgroup stages
+// x once in LDS, in the dequant's pair order, normalized first when gamma is given (the
+// RMSNorm prologue of w4g_gemv_kernel: same arithmetic and bits), chunk i at slot
+// i ^ ((i >> 4) & 3) so that the 16 lanes of a read hit 16 distinct bank groups. Per row
+// the C slices of a lane are summed in order, then the P lanes by the butterfly of
+// dev::row_sum16 (and dev::pair_row_sum for P = 32).
+struct GemvRwArgs {
+    const __half* x;
+    const uint8_t* wq;
+    const __half* ws;
+    __half* y;
+    uint32_t N, K;
+    const __half* gamma;
+    const __half* res;
+    int swiglu;
+};
+
+template <int C, int P, int NP>
+__global__ __launch_bounds__(512) void w4g_gemv_rw_kernel(GemvRwArgs A) {
+    constexpr int RW = 64 / P;
+    static_assert(P == 16 || P == 32, "lanes per row");
+    extern __shared__ __align__(16) float lds_rw[];   // x in pair order, padded layout
+    __shared__ double s_ss[8];
+    const uint32_t nt = blockDim.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t p = lane % P, g = lane / P;
+    const uint32_t R = (nt / 64) * RW, rows_wg = R * NP;
+    // As in w4g_gemv_kernel: N >= rows_wg, and the last workgroup is moved back to end at
+    // row N, recomputing (not storing) the rows its predecessor covers.
+    const uint32_t r0n = blockIdx.x * rows_wg;
+    const uint32_t r0 = min(r0n, A.N - rows_wg);
+    const uint32_t skip = r0n - r0;
+    const uint32_t rowbytes = A.K / 2, G = A.K / 64, K8 = A.K / 8;
+    const uint32_t lrow = wave * RW + g;   // this lane's row within a pass
+    auto slice = [&](int c) -> uint32_t { return (uint32_t)c * P + p; };   // this lane's slices
+
+    // x (and gamma) chunks this thread stages: t, t + nt (clamped; K8 <= 2 nt is checked
+    // on the host).
+    constexpr int PRE = 2;
+    u32x4 xv[PRE], gv[PRE];
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+        const uint32_t i = min(t + k * nt, K8 - 1);
+        xv[k] = reinterpret_cast<const u32x4*>(A.x)[i];
+        if (A.gamma) gv[k] = reinterpret_cast<const u32x4*>(A.gamma)[i];
+    }
+    uint16_t resv[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const uint32_t r = r0 + i * R + lrow;
+        resv[i] = A.res ? __builtin_bit_cast(uint16_t, A.res[A.swiglu ? r / 2 : r]) : (uint16_t)0;
+    }
+    const uint8_t* wq0 = A.wq + (size_t)r0 * rowbytes;
+    const uint16_t* ws0 = reinterpret_cast<const uint16_t*>(A.ws) + (size_t)r0 * G;
+    u32x4 w[C][NP];
+    uint16_t sc[C][NP];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const uint32_t lr = i * R + lrow;
+            w[c][i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(wq0 + (size_t)(lr * rowbytes + slice(c) * 16)));
+            sc[c][i] = ws0[(size_t)lr * G + (slice(c) >> 1)];
+        }
+
+    float rms = 1.0f, rcp = 1.0f;
+    if (A.gamma) {
+        // RMSNorm of w4g_gemv_kernel (M = 1): sum of squares in double over the row.
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < PRE; ++k) {
+            if (t + k * nt >= K8) break;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double lo = (double)h2f((uint16_t)(xv[k][e] & 0xFFFFu));
+                const double hi = (double)h2f((uint16_t)(xv[k][e] >> 16));
+                ss = __builtin_fma(lo, lo, ss);
+                ss = __builtin_fma(hi, hi, ss);
+            }
+        }
+        {
+            const double wsum = dev::wave_sum(ss);
+            if (lane == 0) s_ss[wave] = wsum;
+        }
+        __syncthreads();
+        double tot = 0.0;
+        for (uint32_t v = 0; v < nt / 64; ++v) tot += s_ss[v];
+        rms = (float)sqrt(tot / (double)A.K + 1e-6);
+        rcp = __fdiv_rn(1.0f, rms);
+    }
+    auto div_rms = [&](float a) {
+        const float q = a * rcp;
+        return __builtin_fmaf(__builtin_fmaf(-q, rms, a), rcp, q);
+    };
+    u32x4* xn = reinterpret_cast<u32x4*>(lds_rw);
+    auto xslot = [](uint32_t i) -> uint32_t { return i ^ ((i >> 4) & 3u); };
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+        const uint32_t i = t + k * nt;
+        if (i >= K8) break;
+        u32x4 o = xv[k];
+        if (A.gamma) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float lo = div_rms(h2f((uint16_t)(o[e] & 0xFFFFu)));
+                float hi = div_rms(h2f((uint16_t)(o[e] >> 16)));
+                lo = __fadd_rn(__fmul_rn(lo, h2f((uint16_t)(gv[k][e] & 0xFFFFu))), 0.0f);
+                hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(gv[k][e] >> 16))), 0.0f);
+                o[e] = (uint32_t)f2hb(lo) | ((uint32_t)f2hb(hi) << 16);
+            }
+        }
+        // pair order (x0,x4) (x1,x5) (x2,x6) (x3,x7)
+        xn[xslot(i)] = u32x4{(o[0] & 0xFFFFu) | (o[2] << 16), (o[0] >> 16) | (o[2] & 0xFFFF0000u),
+                             (o[1] & 0xFFFFu) | (o[3] << 16), (o[1] >> 16) | (o[3] & 0xFFFF0000u)};
+    }
+    __syncthreads();
+
+    float acc[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        u32x4 xp[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xp[e] = xn[xslot(4 * slice(c) + e)];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const _Float16 sh = __builtin_bit_cast(_Float16, sc[c][i]);
+            const h2_t s2 = {sh, sh};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h2_t d[4];
+                dequant_word(w[c][i][e], s2, d);
+                acc[i] = __builtin_amdgcn_fdot2(d[0], as_h2(xp[e][0]), acc[i], false);
+                acc[i] = __builtin_amdgcn_fdot2(d[1], as_h2(xp[e][1]), acc[i], false);
+                acc[i] = __builtin_amdgcn_fdot2(d[2], as_h2(xp[e][2]), acc[i], false);
+                acc[i] = __builtin_amdgcn_fdot2(d[3], as_h2(xp[e][3]), acc[i], false);
+            }
+        }
+        // one slice's x pairs in registers at a time (the compiler would otherwise hoist
+        // every slice's LDS reads and hold them all)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        float sum = dev::row_sum16(acc[i]);
+        if constexpr (P == 32) sum = dev::pair_row_sum(sum);
+        const uint32_t lr = i * R + lrow;
+        if (!A.swiglu) {
+            if (p == 0 && lr >= skip) {
+                uint16_t v = f2hb(sum);
+                if (A.res) v = f2hb(__fadd_rn(h2f(v), h2f(resv[i])));
+                reinterpret_cast<uint16_t*>(A.y)[r0 + lr] = v;
+            }
+        } else {
+            // gate = row 2k (group g even), up = row 2k + 1 (group g + 1): the partner's
+            // sum arrives in the even group's lanes through the row swap pairing them.
+            uint32_t a = __builtin_bit_cast(uint32_t, sum), b = a;
+            if constexpr (P == 16) dev::permlane16_swap(a, b);
+            else dev::permlane32_swap(a, b);
+            const float up = __builtin_bit_cast(float, b);
+            if (p == 0 && !(g & 1) && lr >= skip) {
+                const float gvf = h2f(f2hb(sum)), uv = h2f(f2hb(up));
+                const float act = h2f(silu_f16_expr(f2hb(gvf)));
+                uint16_t v = f2hb(__fmul_rn(act, uv));
+                if (A.res) v = f2hb(__fadd_rn(h2f(v), h2f(resv[i])));
+                reinterpret_cast<uint16_t*>(A.y)[(r0 + lr) >> 1] = v;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Bit-exact dequant: one thread per 32 weights (16 bytes in, 64 bytes out).
 __global__ __launch_bounds__(256) void w4g_dequant_kernel(const uint4* __restrict__ wq,
                                                           const __half* __restrict__ ws,
@@ -1084,6 +1264,55 @@ hipError_t gemv_dispatch(dim3 g3, dim3 b3, size_t lds, hipStream_t st, const Gem
 
 bool w4g_gemv_supported(uint32_t M, uint32_t K) { return gemv_plan(M, K).ok; }
 
+// Row-in-wave GEMV (M = 1): lanes per row P and slices per lane C for K, and the launch.
+// Returns false (nothing launched) for the shapes it does not take.
+template <int C, int P>
+hipError_t gemv_rw_dispatch(uint32_t np, dim3 g3, dim3 b3, size_t lds, hipStream_t st, const GemvRwArgs& A) {
+    if (np == 1) hipLaunchKernelGGL((w4g_gemv_rw_kernel<C, P, 1>), g3, b3, lds, st, A);
+    else hipLaunchKernelGGL((w4g_gemv_rw_kernel<C, P, 2>), g3, b3, lds, st, A);
+    return hipGetLastError();
+}
+
+bool gemv_rw_launch(const GemvRwArgs& A, hipStream_t st, hipError_t* err) {
+    if (A.K % 32) return false;
+    const uint32_t S = A.K / 32, K8 = A.K / 8;
+    uint32_t C, P;
+    if (S % 16 == 0 && (S / 16 == 2 || S / 16 == 4 || S / 16 == 5)) { C = S / 16; P = 16; }
+    else if (S % 32 == 0 && (S / 32 == 3 || S / 32 == 4)) { C = S / 32; P = 32; }
+    else return false;
+    // Workgroups of W waves (W = 5 and 7 leave one SIMD with an extra wave) running NP
+    // passes of W * RW rows. The busiest CU sets the time, so the choice minimizes the
+    // rows on the busiest CU (workgroups spread evenly), then the workgroup count (each
+    // stages x, and normalizes it). Graph-timed on the 4B decode shapes against the
+    // cross-wave kernel: q|k|v (N 6144, K 2560, RMSNorm; 256 workgroups of 3 waves, 2
+    // passes) 4.31 against 5.43 us, o-proj (N 2560, K 4096, residual; 214 of 6 waves)
+    // 3.58 against 3.90 us, gate/up (N 19456, K 2560, RMSNorm + SwiGLU; 1216 of 4 waves)
+    // 8.89 against 10.09 us.
+    const uint32_t RW = 64 / P, cus = (uint32_t)device_cu_count();
+    uint32_t bW = 0, bNP = 0;
+    uint64_t best_cu = ~0ull, best_wg = ~0ull;
+    for (uint32_t W : {2u, 3u, 4u, 6u, 8u})
+        for (uint32_t np = 1; np <= 2; ++np) {
+            const uint32_t rows = W * RW * np;
+            if (rows > A.N || K8 > 2 * 64 * W) continue;   // each thread stages at most 2 chunks of x
+            const uint64_t nwg = (A.N + rows - 1) / rows, per_cu = (nwg + cus - 1) / cus * rows;
+            if (per_cu < best_cu || (per_cu == best_cu && nwg < best_wg)) {
+                best_cu = per_cu; best_wg = nwg; bW = W; bNP = np;
+            }
+        }
+    if (!bW) return false;
+    const uint32_t rows_wg = bW * RW * bNP;
+    const size_t lds = (size_t)K8 * 16;
+    const dim3 g3((A.N + rows_wg - 1) / rows_wg), b3(64 * bW);
+    if (P == 16)
+        *err = C == 2 ? gemv_rw_dispatch<2, 16>(bNP, g3, b3, lds, st, A)
+             : C == 4 ? gemv_rw_dispatch<4, 16>(bNP, g3, b3, lds, st, A)
+                      : gemv_rw_dispatch<5, 16>(bNP, g3, b3, lds, st, A);
+    else
+        *err = C == 3 ? gemv_rw_dispatch<3, 32>(bNP, g3, b3, lds, st, A) : gemv_rw_dispatch<4, 32>(bNP, g3, b3, lds, st, A);
+    return true;
+}
+
 hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, const __half* ws,
                            __half* y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
                            hipStream_t st, const W4gEpilogue& epi) {
@@ -1096,6 +1325,10 @@ hipError_t launch_w4g_gemv(const __half* x, uint32_t ldx, const uint8_t* wq, con
     }
     // The kernel addresses weights by 32-bit offsets from a workgroup's first row.
     if ((uint64_t)N * (K / 2) >= (1ull << 32)) return hipErrorInvalidValue;
+    if (M == 1) {
+        hipError_t e = hipSuccess;
+        if (gemv_rw_launch(GemvRwArgs{x, wq, ws, y, N, K, epi.gamma, epi.res, epi.swiglu ? 1 : 0}, st, &e)) return e;
+    }
     // Rows per workgroup: about two workgroups per CU (three when one workgroup holds a
     // single row per pass, as for K = 9728: measured 11 % faster there, slower for the
     // multi-row shapes), partial sums within 32 KiB.

@@ -462,6 +462,41 @@ def test_w4g_fused_gemv(lib, oracle, torch_dev, mode, use_norm, use_res):
     assert_close(from_dev(y), ref, what=f"w4g_fused mode={mode} norm={use_norm} res={use_res}")
 
 
+@pytest.mark.parametrize("K", [1024, 2048, 2560, 3072, 4096])
+@pytest.mark.parametrize("N,mode,use_norm,use_res", [(6144, 0, True, False), (2562, 0, False, True),
+                                                      (19456, 1, True, False), (1002, 1, True, True),
+                                                      (14, 0, False, False), (26, 1, True, True)])
+def test_w4g_gemv_row_in_wave(lib, oracle, torch_dev, K, N, mode, use_norm, use_res):
+    """The M = 1 GEMV whose rows sit inside one wave: 16 lanes per row with 2 / 4 / 5 slices
+    each (K = 1024 / 2048 / 2560) and 32 lanes with 3 / 4 (K = 3072 / 4096); RMSNorm,
+    SwiGLU (the gate/up partner through a row swap) and residual epilogues; N = 2562 and
+    1002 leave a last workgroup moved back to end at row N, N = 14 / 26 fit only small
+    workgroups. Against the oracle's RMSNORM2 -> MATMUL_W4G (-> silu * up) (-> ADD). The
+    activations are scaled (x by 1/4, gamma U[0.2, 0.3]) so that outputs stay below 16,
+    where the 2e-2 bound is above the fp16 spacing that the summation order can move."""
+    import torch
+    rng = np.random.default_rng(K + 3 * N + mode)
+    _, wq, ws = w4g_weights(rng, N, K)
+    x = (normal_f16(rng, 1, K) * np.float16(0.25)).astype(np.float16)
+    gamma = rng.uniform(0.2, 0.3, K).astype(np.float16)
+    n_out = N // 2 if mode else N
+    res = normal_f16(rng, 1, n_out)
+    y = torch.empty((1, n_out), dtype=torch.float16, device=torch_dev)
+    rc = lib.gehtp_w4g_fused(ptr(to_dev(x, torch_dev)), K, ptr(to_dev(wq, torch_dev)), ptr(to_dev(ws, torch_dev)),
+                             ptr(y), n_out, 1, N, K, ptr(to_dev(gamma, torch_dev)) if use_norm else None,
+                             ptr(to_dev(res, torch_dev)) if use_res else None, n_out, mode, stream_ptr())
+    assert rc == 0
+    _sync()
+    h = oracle.rmsnorm2(x, gamma, np.zeros(K, np.float16)) if use_norm else x
+    acc = oracle.matmul_w4g(h, wq, ws, threads=8)
+    ref = oracle.binary(oracle.unary(np.ascontiguousarray(acc[:, 0::2]), 12), np.ascontiguousarray(acc[:, 1::2]),
+                        2) if mode else acc
+    if use_res:
+        ref = oracle.binary(ref, res, 0)
+    assert np.abs(ref.astype(np.float32)).max() < 16.0
+    assert_close(from_dev(y), ref, what=f"row-in-wave gemv K={K} N={N} mode={mode} norm={use_norm} res={use_res}")
+
+
 @pytest.mark.parametrize("M,N,use_res", [(1, 40, True), (1, 100, False), (2, 702, True), (1, 30000, False)])
 def test_w4g_fused_gemv_swiglu_odd_rows(lib, oracle, torch_dev, M, N, use_res):
     """SwiGLU GEMV at K = 704 (22 threads per row, 23 rows per pass of a 512-thread
