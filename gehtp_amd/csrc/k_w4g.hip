@@ -418,7 +418,7 @@ struct GemvRwArgs {
     int swiglu;
 };
 
-template <int C, int P, int NP>
+template <int C, int P, int NP, int PRE>
 __global__ __launch_bounds__(512) void w4g_gemv_rw_kernel(GemvRwArgs A) {
     constexpr int RW = 64 / P;
     static_assert(P == 16 || P == 32, "lanes per row");
@@ -436,9 +436,8 @@ __global__ __launch_bounds__(512) void w4g_gemv_rw_kernel(GemvRwArgs A) {
     const uint32_t lrow = wave * RW + g;   // this lane's row within a pass
     auto slice = [&](int c) -> uint32_t { return (uint32_t)c * P + p; };   // this lane's slices
 
-    // x (and gamma) chunks this thread stages: t, t + nt (clamped; K8 <= 2 nt is checked
-    // on the host).
-    constexpr int PRE = 2;
+    // x (and gamma) chunks this thread stages: t, t + nt, ... (clamped; K8 <= PRE nt is
+    // checked on the host).
     u32x4 xv[PRE], gv[PRE];
 #pragma unroll
     for (int k = 0; k < PRE; ++k) {
@@ -1266,10 +1265,16 @@ bool w4g_gemv_supported(uint32_t M, uint32_t K) { return gemv_plan(M, K).ok; }
 
 // Row-in-wave GEMV (M = 1): lanes per row P and slices per lane C for K, and the launch.
 // Returns false (nothing launched) for the shapes it does not take.
-template <int C, int P>
+template <int C, int P, int PRE = 2>
 hipError_t gemv_rw_dispatch(uint32_t np, dim3 g3, dim3 b3, size_t lds, hipStream_t st, const GemvRwArgs& A) {
-    if (np == 1) hipLaunchKernelGGL((w4g_gemv_rw_kernel<C, P, 1>), g3, b3, lds, st, A);
-    else hipLaunchKernelGGL((w4g_gemv_rw_kernel<C, P, 2>), g3, b3, lds, st, A);
+    if constexpr (C > 5) {   // one pass: two would not fit the registers
+        if (np != 1) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((w4g_gemv_rw_kernel<C, P, 1, PRE>), g3, b3, lds, st, A);
+    } else if (np == 1) {
+        hipLaunchKernelGGL((w4g_gemv_rw_kernel<C, P, 1, PRE>), g3, b3, lds, st, A);
+    } else {
+        hipLaunchKernelGGL((w4g_gemv_rw_kernel<C, P, 2, PRE>), g3, b3, lds, st, A);
+    }
     return hipGetLastError();
 }
 
@@ -1277,9 +1282,12 @@ bool gemv_rw_launch(const GemvRwArgs& A, hipStream_t st, hipError_t* err) {
     if (A.K % 32) return false;
     const uint32_t S = A.K / 32, K8 = A.K / 8;
     uint32_t C, P;
+    // (K = 9728 as 19 slices on 16 lanes ran the 4B down-projection in 6.50 us against
+    // 5.87 us for the cross-wave kernel's three single-row workgroups per CU.)
     if (S % 16 == 0 && (S / 16 == 2 || S / 16 == 4 || S / 16 == 5)) { C = S / 16; P = 16; }
     else if (S % 32 == 0 && (S / 32 == 3 || S / 32 == 4)) { C = S / 32; P = 32; }
     else return false;
+    const uint32_t pre = 2;   // chunks of x each thread stages
     // Workgroups of W waves (W = 5 and 7 leave one SIMD with an extra wave) running NP
     // passes of W * RW rows. The busiest CU sets the time, so the choice minimizes the
     // rows on the busiest CU (workgroups spread evenly), then the workgroup count (each
@@ -1292,9 +1300,9 @@ bool gemv_rw_launch(const GemvRwArgs& A, hipStream_t st, hipError_t* err) {
     uint32_t bW = 0, bNP = 0;
     uint64_t best_cu = ~0ull, best_wg = ~0ull;
     for (uint32_t W : {2u, 3u, 4u, 6u, 8u})
-        for (uint32_t np = 1; np <= 2; ++np) {
+        for (uint32_t np = 1; np <= (C > 5 ? 1u : 2u); ++np) {
             const uint32_t rows = W * RW * np;
-            if (rows > A.N || K8 > 2 * 64 * W) continue;   // each thread stages at most 2 chunks of x
+            if (rows > A.N || K8 > pre * 64 * W) continue;
             const uint64_t nwg = (A.N + rows - 1) / rows, per_cu = (nwg + cus - 1) / cus * rows;
             if (per_cu < best_cu || (per_cu == best_cu && nwg < best_wg)) {
                 best_cu = per_cu; best_wg = nwg; bW = W; bNP = np;
