@@ -265,7 +265,7 @@ def main() -> int:
                              "tokens_equal_value_run": True},
         "decode_weight_bytes_per_token": cfg.decode_weight_bytes(),
         "decode_ideal_tok_s_at_hbm_peak": round(HBM_PEAK_GBS * 1e9 / cfg.decode_weight_bytes(), 1),
-        "roofline": {"bound": "hbm", "kernel": "w4g_gemv_kernel<1, NP> (decode W4A16 GEMV; NP = passes per thread: 3 and 4 straight-line, 10 as two unrolled batches of 5)",
+        "roofline": {"bound": "hbm", "kernel": "decode W4A16 GEMV: w4g_gemv_rw_kernel (q|k|v, o-proj, gate/up: whole rows inside a wave) and w4g_gemv_kernel<1, 4> (down, K = 9728)",
                      "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": round(bytes_per_launch), "avg_launch_us": round(avg_s * 1e6, 3)},
@@ -512,7 +512,7 @@ def kernel_configs(args) -> int:
                                       K, sp) == 0
         t_rot = timed(c1, copies, 10)
         t_res = timed(lambda i: c1(0), 64, 10)
-        results["c1_gemv"] = {"kernel": "w4g_gemv_kernel<1, NP>", "bytes": nbytes, "copies": copies,
+        results["c1_gemv"] = {"kernel": "w4g_gemv_rw_kernel<2, 16, NP, 2>", "bytes": nbytes, "copies": copies,
                               "rotated_us": round(t_rot * 1e6, 3), "rotated_gbs": round(nbytes / t_rot / 1e9, 1),
                               "resident_us": round(t_res * 1e6, 3), "resident_gbs": round(nbytes / t_res / 1e9, 1)}
         log(f"c1 gemv: rotated {t_rot * 1e6:.2f} us ({nbytes / t_rot / 1e9:.0f} GB/s), "
