@@ -401,11 +401,53 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
             vr[s] = *reinterpret_cast<const u32x4*>(kb + A.slot_bytes / 2 + 64 * s);
         }
     };
+    // Load order = wait order (loads return in order): the counter first, then the new
+    // token's q rows (and its k / v rows and gammas, FUSED), the plain op's q, and only
+    // then the K/V rows of the chunks below spec_chunks. Waiting for the counter and the
+    // q rows does not wait for the K/V rows, so the queries' norm + RoPE run while those
+    // are in flight.
+    const uint32_t cnt = (FUSED || A.count) ? *A.count : A.n_kv_host;
+    constexpr int QW = (REP + 3) / 4;   // query heads per wave
+    const uint32_t kwave = (REP < 4 ? (uint32_t)REP : 0u) % 4;   // the wave that handles k of head g
+    uint16_t qx1[QW] = {}, qx2[QW] = {}, kx1 = 0, kx2 = 0, kg1 = 0, kg2 = 0, vx1 = 0, vx2 = 0, qg1 = 0, qg2 = 0;
+    u32x4 vn[4] = {};
+    h8_t qpl[4] = {};
+    const uint32_t qh = min(lc, (uint32_t)REP - 1u);
+    if constexpr (FUSED) {
+#pragma unroll
+        for (int j = 0; j < QW; ++j) {
+            const uint32_t r = wave + 4 * j;
+            if (r < (uint32_t)REP) {
+                const __half* src = A.qkv + (size_t)(g * REP + r) * HD;
+                qx1[j] = __half_as_ushort(src[lane]);
+                qx2[j] = __half_as_ushort(src[lane + 64]);
+            }
+        }
+        qg1 = __half_as_ushort(A.qg[lane]);
+        qg2 = __half_as_ushort(A.qg[lane + 64]);
+        if (wave == kwave) {
+            const __half* ksrc = A.qkv + (size_t)(A.H + g) * HD;
+            const __half* vsrc = A.qkv + (size_t)(A.H + A.KVH + g) * HD;
+            kx1 = __half_as_ushort(ksrc[lane]);
+            kx2 = __half_as_ushort(ksrc[lane + 64]);
+            kg1 = __half_as_ushort(A.kg[lane]);
+            kg2 = __half_as_ushort(A.kg[lane + 64]);
+            vx1 = __half_as_ushort(vsrc[lane]);
+            vx2 = __half_as_ushort(vsrc[lane + 64]);
+        }
+        const __half* vnew = A.qkv + (size_t)(A.H + A.KVH + g) * HD + 8 * lr;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) vn[s] = *reinterpret_cast<const u32x4*>(vnew + 32 * s);
+    } else if (wave == 0) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            qpl[s] = *reinterpret_cast<const h8_t*>(A.q + (size_t)(g * REP + qh) * HD + 32 * s + 8 * lr);
+    }
     const bool early = c < A.spec_chunks;
     if (early) load_kv(0xFFFFFFFFu);
     asm volatile("" ::: "memory");
-    const uint32_t pos = FUSED ? *A.count : 0u;   // position of the new token
-    const uint32_t n_kv = FUSED ? pos + 1 : (A.count ? *A.count : A.n_kv_host);
+    const uint32_t pos = FUSED ? cnt : 0u;   // position of the new token
+    const uint32_t n_kv = FUSED ? pos + 1 : cnt;
     if (c * DC >= n_kv) return;
     if (FUSED && c == 0 && g == 0 && tid == 0) A.ws[kWsSnap] = n_kv;
     if (!early) load_kv(n_kv);
@@ -422,29 +464,28 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
         } else {
             dev::rope_cs_inv(pos, dev::rope_inv(lane, A.theta), cr, sr);
         }
-        for (uint32_t r = wave; r < (uint32_t)REP; r += 4) {
-            const __half* src = A.qkv + (size_t)(g * REP + r) * HD;
+        auto hf = [](uint16_t b) { return __half2float(__ushort_as_half(b)); };
+#pragma unroll
+        for (int j = 0; j < QW; ++j) {
+            const uint32_t r = wave + 4 * j;
+            if (r >= (uint32_t)REP) break;
             float y1, y2;
-            dev::head_norm_rope(__half2float(src[lane]), __half2float(src[lane + 64]), __half2float(A.qg[lane]),
-                                __half2float(A.qg[lane + 64]), cr, sr, y1, y2);
+            dev::head_norm_rope(hf(qx1[j]), hf(qx2[j]), hf(qg1), hf(qg2), cr, sr, y1, y2);
             s_q[r][lane] = (_Float16)y1;
             s_q[r][lane + 64] = (_Float16)y2;
         }
-        if (owns_new && wave == (REP < 4 ? (uint32_t)REP : 0u) % 4) {
+        if (owns_new && wave == kwave) {
             // k of head g: norm + RoPE; v raw. Written to the ring; k kept for this chunk.
-            const __half* ksrc = A.qkv + (size_t)(A.H + g) * HD;
-            const __half* vsrc = A.qkv + (size_t)(A.H + A.KVH + g) * HD;
             float y1, y2;
-            dev::head_norm_rope(__half2float(ksrc[lane]), __half2float(ksrc[lane + 64]), __half2float(A.kg[lane]),
-                                __half2float(A.kg[lane + 64]), cr, sr, y1, y2);
+            dev::head_norm_rope(hf(kx1), hf(kx2), hf(kg1), hf(kg2), cr, sr, y1, y2);
             s_k[lane] = (_Float16)y1;
             s_k[lane + 64] = (_Float16)y2;
             _Float16* kface = reinterpret_cast<_Float16*>(A.ring + (size_t)(pos % A.nslots) * A.slot_bytes);
             _Float16* vface = kface + A.KVH * HD;
             kface[g * HD + lane] = (_Float16)y1;
             kface[g * HD + lane + 64] = (_Float16)y2;
-            vface[g * HD + lane] = __builtin_bit_cast(_Float16, __half_as_ushort(vsrc[lane]));
-            vface[g * HD + lane + 64] = __builtin_bit_cast(_Float16, __half_as_ushort(vsrc[lane + 64]));
+            vface[g * HD + lane] = __builtin_bit_cast(_Float16, vx1);
+            vface[g * HD + lane + 64] = __builtin_bit_cast(_Float16, vx2);
         }
     }
     // K and V tiles. The new token's V row comes from the QKV row (its ring slot was read
@@ -453,11 +494,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     // value would reach the sums; their scores are -inf whatever K holds.
     {
         const uint32_t kl = 16 * wave + lc, key = c * DC + kl;
-        const __half* vnew = FUSED ? A.qkv + (size_t)(A.H + A.KVH + g) * HD + 8 * lr : nullptr;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             u32x4 v = vr[s];
-            if (FUSED && key == pos) v = *reinterpret_cast<const u32x4*>(vnew + 32 * s);
+            if (FUSED && key == pos) v = vn[s];
             if (key >= n_kv) v = u32x4{0u, 0u, 0u, 0u};
             *reinterpret_cast<u32x4*>(&s_v[kl * VSD + 32 * s + 8 * lr]) = v;
             *reinterpret_cast<u32x4*>(&s_kt[kl * KSD + 32 * s + 8 * lr]) = kr[s];
@@ -469,11 +509,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     // Queries as B columns; K rows as A tiles (key 16t + lc), the new token's k in place
     // of its stale ring row.
     h8_t qb[4];
-    const uint32_t qh = min(lc, (uint32_t)REP - 1u);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const h8_t v = FUSED ? *reinterpret_cast<const h8_t*>(&s_q[qh][32 * s + 8 * lr])
-                             : *reinterpret_cast<const h8_t*>(A.q + (size_t)(g * REP + qh) * HD + 32 * s + 8 * lr);
+        const h8_t v = FUSED ? *reinterpret_cast<const h8_t*>(&s_q[qh][32 * s + 8 * lr]) : qpl[s];
         qb[s] = lc < (uint32_t)REP ? v : h8_t{};
     }
     u32x4 kf[4][4];
