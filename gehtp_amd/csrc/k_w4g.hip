@@ -264,8 +264,10 @@ __global__ __launch_bounds__(512) void w4g_gemv_kernel(GemvArgs A) {
                 for (int e = 0; e < 4; ++e) {
                     float lo = div_rms(h2f((uint16_t)(v[e] & 0xFFFFu)), m);
                     float hi = div_rms(h2f((uint16_t)(v[e] >> 16)), m);
-                    lo = __fadd_rn(__fmul_rn(lo, h2f((uint16_t)(g4[e] & 0xFFFFu))), 0.0f);
-                    hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(g4[e] >> 16))), 0.0f);
+                    // RN(y * g) with -0 -> +0 as one fma with a +0 addend (see below)
+                    lo = __builtin_fmaf(lo, h2f((uint16_t)(g4[e] & 0xFFFFu)), 0.0f);
+                    hi = __builtin_fmaf(hi, h2f((uint16_t)(g4[e] >> 16)), 0.0f);
+                    asm volatile("" : "+v"(lo), "+v"(hi));
                     o[e] = (uint32_t)f2hb(lo) | ((uint32_t)f2hb(hi) << 16);
                 }
                 xn[m * K8 + xslot(i)] = o;
@@ -506,8 +508,13 @@ __global__ __launch_bounds__(512) void w4g_gemv_rw_kernel(GemvRwArgs A) {
             for (int e = 0; e < 4; ++e) {
                 float lo = div_rms(h2f((uint16_t)(o[e] & 0xFFFFu)));
                 float hi = div_rms(h2f((uint16_t)(o[e] >> 16)));
-                lo = __fadd_rn(__fmul_rn(lo, h2f((uint16_t)(gv[k][e] & 0xFFFFu))), 0.0f);
-                hi = __fadd_rn(__fmul_rn(hi, h2f((uint16_t)(gv[k][e] >> 16))), 0.0f);
+                // RN(y * g + 0) in one fma: the exact product plus +0 rounded once is the
+                // separate multiply's rounding, with -0 mapped to +0 as by the "+ 0". The
+                // empty asm keeps the f32 result as it is before the fp16 conversion (a
+                // mixed-precision fma rounding straight to fp16 would skip that rounding).
+                lo = __builtin_fmaf(lo, h2f((uint16_t)(gv[k][e] & 0xFFFFu)), 0.0f);
+                hi = __builtin_fmaf(hi, h2f((uint16_t)(gv[k][e] >> 16)), 0.0f);
+                asm volatile("" : "+v"(lo), "+v"(hi));
                 o[e] = (uint32_t)f2hb(lo) | ((uint32_t)f2hb(hi) << 16);
             }
         }
