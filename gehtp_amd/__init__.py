@@ -201,5 +201,9 @@ class Engine:
         """QK-norm/RoPE/KV-append ops performed by their q|k|v GEMM's epilogue so far."""
         return int(self.lib.wt_exec_qkv_rope_fused())
 
+    def qkv_attn_fused(self) -> int:
+        """Decode attention ops run in their q|k|v GEMV's launch so far."""
+        return int(self.lib.wt_exec_qkv_attn_fused())
+
 
 WT_ERR = WT_ERR

@@ -156,6 +156,7 @@ EXPORTS = {
     "wt_exec_fusion_detail": (None, [C.POINTER(WtBlob), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
                                      C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
     "wt_exec_qkv_rope_fused": (C.c_uint64, []),
+    "wt_exec_qkv_attn_fused": (C.c_uint64, []),
     "wt_w3_report": (None, [C.c_char_p, _u8p, C.c_size_t, C.POINTER(WtBlob),
                             C.CFUNCTYPE(None, C.c_char_p, _vp), _vp]),
     # gehtp_kernels.h
@@ -177,6 +178,9 @@ EXPORTS = {
     "gehtp_attn_decode_noalloc": (_i, [_vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32, C.c_float, _vp]),
     "gehtp_attn_decode_qkv": (_i, [_vp, _u32, _u32, _vp, _vp, C.c_float, C.c_float, _vp, _u32, _vp, _vp, _vp,
                                    _u32, _vp]),
+    "gehtp_attn_qkv_fused_work_floats": (_u32, [_u32, _u32, _u32]),
+    "gehtp_qkv_attn_decode": (_i, [_vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, C.c_float, C.c_float, _vp,
+                                   _u32, _vp, _vp, _vp, _u32, _vp]),
     "gehtp_kv_append": (_i, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _vp]),
     "gehtp_rope": (_i, [_vp, _vp, _u32, _u32, _u32, _u32, C.c_float, _u32, _vp]),
     "gehtp_argmax": (_i, [_vp, _u32, _vp, _vp]),

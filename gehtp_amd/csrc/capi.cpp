@@ -182,6 +182,28 @@ int gehtp_attn_decode_qkv(const void* qkv, uint32_t Hh, uint32_t KVH, const void
                                      scale, static_cast<float*>(work), work_floats, S(stream)));
 }
 
+uint32_t gehtp_attn_qkv_fused_work_floats(uint32_t nslots, uint32_t Hh, uint32_t KVH) {
+    return attn_qkv_fused_work_floats(nslots, Hh, KVH);
+}
+
+int gehtp_qkv_attn_decode(const void* x, const void* wq, const void* ws, const void* gamma, uint32_t K, void* qkv,
+                          uint32_t Hh, uint32_t KVH, const void* q_gamma, const void* k_gamma, float theta,
+                          float scale, void* ring, uint32_t state_bytes, void* count_dev, void* out, void* work,
+                          uint32_t work_floats, void* stream) {
+    const uint32_t slot_bytes = KVH * 128u * 4u;
+    if (!x || !wq || !ws || !qkv || !q_gamma || !k_gamma || !ring || !count_dev || !out || !work || !KVH ||
+        Hh % KVH || !K || K % 64 || state_bytes % slot_bytes || !state_bytes || !al16(x) || !al16(wq) ||
+        (gamma && !al16(gamma)) || (reinterpret_cast<uintptr_t>(ws) & 1u) || !al16(ring) || !al16(work) ||
+        (reinterpret_cast<uintptr_t>(out) & 7u))
+        return GEHTP_EINVAL;
+    const hipError_t e = launch_qkv_attn_decode(H(x), static_cast<const uint8_t*>(wq), H(ws), H(gamma), K, Hm(qkv),
+                                                H(q_gamma), H(k_gamma), theta, static_cast<uint8_t*>(ring),
+                                                slot_bytes, state_bytes / slot_bytes,
+                                                static_cast<uint32_t*>(count_dev), Hm(out), Hh, KVH, scale,
+                                                static_cast<float*>(work), work_floats, S(stream));
+    return e == hipErrorNotSupported ? GEHTP_ENOTSUP : rc(e);
+}
+
 int gehtp_attn_decode_noalloc(const void* q, const void* ring, uint32_t state_bytes, void* out, uint32_t n_kv,
                               uint32_t Hh, uint32_t KVH, uint32_t hd, float scale, void* stream) {
     const uint32_t slot_bytes = KVH * hd * 4u;

@@ -143,6 +143,7 @@ struct Engine {
     uint8_t* fuse_scratch = nullptr;       // fused attention output when it overlaps an input
     uint64_t fuse_scratch_cap = 0;
     uint64_t qkv_rope_fused = 0;   // OP_QK_ROPE_KV_F16 ops performed by their GEMM's epilogue
+    uint64_t qkv_attn_fused = 0;   // OP_ATTN_DECODE_QKV_F16 ops performed in their GEMV's launch
     bool graphs_broken = false;
     uint32_t n_captures = 0, n_replays = 0;
 
@@ -1036,6 +1037,20 @@ struct QkRope {
 };
 int qk_rope_prep(const wt_blob* b, const wt_op* op, QkRope& r, char* err, size_t errn);
 void qk_rope_commit(const QkRope& r);
+// An OP_ATTN_DECODE_QKV_F16 that the q|k|v GEMV before it performed in the same launch.
+const wt_op* g_attn_pre = nullptr;
+// OP_ATTN_DECODE_QKV_F16's operands, checked, with its output and workspace allocated.
+struct AttnQkv {
+    const __half* qkv = nullptr;
+    const __half* qg = nullptr;
+    const __half* kg = nullptr;
+    float theta = 0.0f, scale = 0.0f;
+    uint32_t H = 0, KVH = 0, si = 0;
+    State* s = nullptr;
+    __half* o = nullptr;
+};
+int attn_qkv_prep(const wt_blob* b, const wt_op* op, AttnQkv& r, char* err, size_t errn);
+void attn_qkv_commit(const AttnQkv& r);
 bool fusion_on();
 extern uint32_t g_run_end;
 
@@ -1081,6 +1096,40 @@ int op_w4g_fused(Ctx& cx) {
     const bool gemv_fits = w4g_gemv_supported(M, K);
     if (gemv_fits) {
         epi.gamma = gamma;
+        // The OP_ATTN_DECODE_QKV_F16 that reads this q|k|v row next, in the same run:
+        // one launch runs the GEMV and that op's chunk pass side by side (the chunk
+        // workgroups' K/V loads overlap the GEMV), then its merge pass; that op then finds
+        // its work done. Shapes the launch does not take leave the op to run alone.
+        const wt_op* rx = cx.op + 1;
+        if (fusion_on() && M == 1 && !swiglu && !res && ldy == N && (uint32_t)(rx - cx.b->ops) < g_run_end &&
+            rx->opcode == OP_ATTN_DECODE_QKV_F16 && rx->n_args >= 10 && rx->args[0] == A(3) && rx->args[5] == 128 &&
+            rx->args[4] && rx->args[3] % rx->args[4] == 0 &&
+            (uint64_t)(rx->args[3] + 2ull * rx->args[4]) * 128u == N) {
+            AttnQkv r;
+            char rerr[8];
+            if (attn_qkv_prep(cx.b, rx, r, rerr, sizeof rerr) == 0) {
+                // The launch's GEMV reads x while its chunk workgroups write the ring, and
+                // writes y while they read the ring: both must be apart.
+                const uint8_t* rb = r.s->dev;
+                const uint64_t rn = (uint64_t)r.s->nslots * r.s->slot_bytes;
+                auto apart = [&](const void* p, uint64_t n) {
+                    const uint8_t* q = static_cast<const uint8_t*>(p);
+                    return q + n <= rb || q >= rb + rn;
+                };
+                auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+                if (apart(a, (uint64_t)K * 2u) && apart(y, (uint64_t)N * 2u) && apart(gamma ? gamma : a, K * 2u) &&
+                    al16(g.attn_work) && qkv_attn_decode_supported(K, r.H, r.KVH, r.s->nslots)) {
+                    CHECK_LAUNCH(launch_qkv_attn_decode(a, wq, ws, gamma, K, y, r.qg, r.kg, r.theta, r.s->dev,
+                                                        r.s->slot_bytes, r.s->nslots, g.counters_dev + r.si, r.o,
+                                                        r.H, r.KVH, r.scale, g.attn_work, g.attn_work_floats,
+                                                        g.stream, r.s->count + 1));
+                    attn_qkv_commit(r);
+                    g_attn_pre = rx;
+                    g.qkv_attn_fused++;
+                    return 0;
+                }
+            }
+        }
         CHECK_LAUNCH(launch_w4g_gemv(a, K, wq, ws, y, ldy, M, N, K, g.stream, epi));
         return 0;
     }
@@ -1226,34 +1275,62 @@ int attn_workspace(uint32_t need, char* err, size_t errn) {
 
 int op_attn_decode_qkv(Ctx& cx) {
     char* err = cx.err; size_t errn = cx.errn;
-    const uint32_t H = A(3), KVH = A(4), hd = A(5);
-    const float theta = f32_from_bits(A(8)), scale = f32_from_bits(A(9));
+    if (g_attn_pre == cx.op) {   // the q|k|v GEMV before it ran it in its own launch (op_w4g_fused)
+        g_attn_pre = nullptr;
+        return 0;
+    }
+    AttnQkv r;
+    if (attn_qkv_prep(cx.b, cx.op, r, err, errn)) return -1;
+    attn_qkv_commit(r);
+    CHECK_LAUNCH(launch_attn_decode_qkv(r.qkv, r.qg, r.kg, r.theta, r.s->dev, r.s->slot_bytes, r.s->nslots,
+                                        g.counters_dev + r.si, r.o, r.H, r.KVH, r.scale, g.attn_work,
+                                        g.attn_work_floats, g.stream, r.s->count));
+    return 0;
+}
+
+int attn_qkv_prep(const wt_blob* b, const wt_op* op, AttnQkv& r, char* err, size_t errn) {
+    const uint32_t* a = op->args;
+    const uint32_t H = a[3], KVH = a[4], hd = a[5];
+    const float theta = f32_from_bits(a[8]), scale = f32_from_bits(a[9]);
     if (hd != 128) return ERR("attn_decode_qkv head_dim %u unsupported (128 only)", hd);
     if (!KVH || H % KVH) return ERR("attn_decode_qkv heads %u not a multiple of kv heads %u", H, KVH);
     const uint32_t rep = H / KVH;
     if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return ERR("attn_decode_qkv group size %u unsupported", rep);
-    const __half* qkv = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(0)));
-    const __half* qg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(6)));
-    const __half* kg = reinterpret_cast<const __half*>(ref_ptr(cx.b, A(7)));
+    const __half* qkv = reinterpret_cast<const __half*>(ref_ptr(b, a[0]));
+    const __half* qg = reinterpret_cast<const __half*>(ref_ptr(b, a[6]));
+    const __half* kg = reinterpret_cast<const __half*>(ref_ptr(b, a[7]));
     if (!qkv || !qg || !kg) return ERR("attn_decode_qkv ref fail");
-    const size_t xb = ref_bytes(cx.b, A(0));
+    const size_t xb = ref_bytes(b, a[0]);
     if (xb && xb < (uint64_t)(H + 2 * KVH) * hd * 2u) return ERR("attn_decode_qkv input smaller than one qkv row");
-    const size_t qgb = ref_bytes(cx.b, A(6)), kgb = ref_bytes(cx.b, A(7));
+    const size_t qgb = ref_bytes(b, a[6]), kgb = ref_bytes(b, a[7]);
     if ((qgb && qgb < hd * 2u) || (kgb && kgb < hd * 2u)) return ERR("attn_decode_qkv gamma shorter than head_dim");
-    State* s = state_kv(A(1), KVH * hd, err, errn);
+    State* s = state_kv(a[1], KVH * hd, err, errn);
     if (!s) return -1;
-    const uint32_t si = A(1) & 0x1FFFu;
+    const uint32_t si = a[1] & 0x1FFFu;
     if (s->count >= s->nslots)
         return ERR("attn_decode_qkv state %u count=%u >= nslots=%u (context too long)", si, s->count, s->nslots);
     if (kv_check(*s, s->count, err, errn)) return -1;
-    __half* o = reinterpret_cast<__half*>(temp_get(A(2), H * hd * 2u));
+    __half* o = reinterpret_cast<__half*>(temp_get(a[2], H * hd * 2u));
     if (!o) return ERR("attn_decode_qkv out alloc");
-    if (attn_workspace(attn_decode_work_floats(s->nslots, H, hd), err, errn)) return -1;
-    kv_mark(*s, s->count);
-    s->count += 1;
-    CHECK_LAUNCH(launch_attn_decode_qkv(qkv, qg, kg, theta, s->dev, s->slot_bytes, s->nslots, g.counters_dev + si,
-                                        o, H, KVH, scale, g.attn_work, g.attn_work_floats, g.stream, s->count));
+    // sized for the one-launch form too (launch_qkv_attn_decode), which the plain form
+    // shares
+    if (attn_workspace(attn_qkv_fused_work_floats(s->nslots, H, KVH), err, errn)) return -1;
+    r.qkv = qkv;
+    r.qg = qg;
+    r.kg = kg;
+    r.theta = theta;
+    r.scale = scale;
+    r.H = H;
+    r.KVH = KVH;
+    r.si = si;
+    r.s = s;
+    r.o = o;
     return 0;
+}
+
+void attn_qkv_commit(const AttnQkv& r) {
+    kv_mark(*r.s, r.s->count);
+    r.s->count += 1;
 }
 
 // Host bytes of constant slot s (in-blob weights or the external image), or null.
@@ -2517,6 +2594,7 @@ int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* 
     const wt_op* op = &b->ops[i];
     if (g_prenorm.op != op) g_prenorm = PreNorm{};   // only ever for the very next op
     if (g_rope_pre != op) g_rope_pre = nullptr;
+    if (g_attn_pre != op) g_attn_pre = nullptr;
     if (g_fplan) {
         int frc = 0;
         if (fused_member(b, i, &frc, err, errn)) return frc;
@@ -2579,6 +2657,7 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
                       int64_t* op_us, char* err, size_t errn) {
     g_prenorm = PreNorm{};
     g_rope_pre = nullptr;
+    g_attn_pre = nullptr;
     char dummy_err[8];
     if (!err || !errn) { err = dummy_err; errn = sizeof dummy_err; }
     uint32_t dummy_m = 0;
@@ -3035,6 +3114,7 @@ void wt_exec_fusion_detail(const struct wt_blob* b, uint32_t* chains, uint32_t* 
 }
 
 uint64_t wt_exec_qkv_rope_fused(void) { return g.qkv_rope_fused; }
+uint64_t wt_exec_qkv_attn_fused(void) { return g.qkv_attn_fused; }
 
 void wt_exec_set_hook(const char* spec) { g.hook = spec; }
 

@@ -9,8 +9,10 @@
 #include "kernels.h"
 #include "dev_reduce.h"
 #include "dev_rope.h"
+#include "dev_w4g.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 
 namespace gehtp {
@@ -307,11 +309,16 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
 constexpr int DC = 64;          // keys per chunk
 constexpr int MAX_REP = 8;
 constexpr int PS = HD + 4;      // partial record: O[HD], m, l, 2 pad (16-byte aligned)
-// Workspace head (uint32 words): [1] n_kv of the last fused call; RoPE records j = 0, 1:
-// [4 + j] position + 1 (0 = empty), [6 + j] theta bits, [8 + 64j + i] pair i as
-// f16 cos | f16 sin << 16. Partials follow the head.
-constexpr uint32_t kWsSnap = 1, kWsRopeTag = 4, kWsRopeTheta = 6, kWsRope = 8;
+// Workspace head (uint32 words): [1] n_kv of the last fused call; [2] call sequence
+// number of the fused calls (advanced by their merge pass; tags the q|k|v hand-off
+// records, see qkv_attn_decode_kernel); [3] nonzero once a hand-off wait gave up;
+// RoPE records j = 0, 1: [4 + j] position + 1 (0 = empty), [6 + j] theta bits,
+// [8 + 64j + i] pair i as f16 cos | f16 sin << 16. Partials follow the head.
+constexpr uint32_t kWsSnap = 1, kWsSeq = 2, kWsErr = 3, kWsRopeTag = 4, kWsRopeTheta = 6, kWsRope = 8;
 constexpr uint32_t kWsHead = kWsRope + HD;
+// Polls of one hand-off record before the wait gives up (sets kWsErr and goes on), so
+// that every wave ends even if a record never arrives: ~1 us per poll, so tens of ms.
+constexpr uint32_t kHandoffSpins = 1u << 15;
 
 struct DecodeArgs {
     const __half* q;         // [H, HD] ready queries (plain op)
@@ -366,13 +373,28 @@ __device__ __forceinline__ float cross_row_max(float v) {
     return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
-template <int REP, bool FUSED>
-__global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
-    __shared__ __align__(16) _Float16 s_v[DC * VSD];
-    __shared__ __align__(16) _Float16 s_kt[DC * KSD];
-    __shared__ __align__(16) _Float16 s_q[REP][HD];
-    __shared__ __align__(16) _Float16 s_k[HD];
-    const uint32_t c = blockIdx.x, g = blockIdx.y;
+// LDS of one chunk workgroup. raw: the new token's REP q rows, then its k and v rows of
+// head g, as f16 pairs (hand-off form only).
+template <int REP>
+struct DecodeSmem {
+    __align__(16) _Float16 v[DC * VSD];
+    __align__(16) _Float16 kt[DC * KSD];
+    __align__(16) _Float16 q[REP][HD];
+    __align__(16) _Float16 k[HD];
+    __align__(16) uint32_t raw[(REP + 2) * HD / 2];
+};
+
+// Chunk c of kv head g. HO (hand-off, FUSED only): the new token's q|k|v row is not read
+// from A.qkv but from the row-pair records rec[] that the q|k|v GEMV workgroups of the
+// same launch publish with the call's tag (workspace word kWsSeq + 1).
+template <int REP, bool FUSED, bool HO>
+__device__ __forceinline__ void attn_decode_body(const DecodeArgs& A, uint32_t c, uint32_t g, DecodeSmem<REP>& sm,
+                                                 const unsigned long long* rec) {
+    static_assert(FUSED || !HO, "the hand-off form is the fused op's");
+    _Float16* const s_v = sm.v;
+    _Float16* const s_kt = sm.kt;
+    auto& s_q = sm.q;
+    _Float16* const s_k = sm.k;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t lc = lane & 15, lr = lane >> 4;
     uint32_t rtag[2] = {0u, 0u}, rtheta[2] = {0u, 0u}, rw[2] = {0u, 0u};
@@ -407,13 +429,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     // q rows does not wait for the K/V rows, so the queries' norm + RoPE run while those
     // are in flight.
     const uint32_t cnt = (FUSED || A.count) ? *A.count : A.n_kv_host;
+    uint32_t tag = 0u;
+    if constexpr (HO) tag = A.ws[kWsSeq] + 1u;
     constexpr int QW = (REP + 3) / 4;   // query heads per wave
     const uint32_t kwave = (REP < 4 ? (uint32_t)REP : 0u) % 4;   // the wave that handles k of head g
     uint16_t qx1[QW] = {}, qx2[QW] = {}, kx1 = 0, kx2 = 0, kg1 = 0, kg2 = 0, vx1 = 0, vx2 = 0, qg1 = 0, qg2 = 0;
     u32x4 vn[4] = {};
     h8_t qpl[4] = {};
     const uint32_t qh = min(lc, (uint32_t)REP - 1u);
-    if constexpr (FUSED) {
+    if constexpr (HO) {   // the rows themselves arrive through the records, below
+        qg1 = __half_as_ushort(A.qg[lane]);
+        qg2 = __half_as_ushort(A.qg[lane + 64]);
+        if (wave == kwave) {
+            kg1 = __half_as_ushort(A.kg[lane]);
+            kg2 = __half_as_ushort(A.kg[lane + 64]);
+        }
+    } else if constexpr (FUSED) {
 #pragma unroll
         for (int j = 0; j < QW; ++j) {
             const uint32_t r = wave + 4 * j;
@@ -452,6 +483,46 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     if (FUSED && c == 0 && g == 0 && tid == 0) A.ws[kWsSnap] = n_kv;
     if (!early) load_kv(n_kv);
     const bool owns_new = FUSED && pos / DC == c;
+    if constexpr (HO) {
+        // Wait for the records of this group's q rows and of k and v of head g (record i
+        // of row block b: rows 2i, 2i + 1 of head b), then take the values from LDS as
+        // the other form takes them from the q|k|v row.
+        constexpr uint32_t NREC = (REP + 2) * HD / 2;
+        for (uint32_t i = tid; i < NREC; i += 256) {
+            const uint32_t b = i / (HD / 2);
+            const uint32_t head = b < (uint32_t)REP ? g * REP + b : b == (uint32_t)REP ? A.H + g : A.H + A.KVH + g;
+            const unsigned long long* rp = rec + (size_t)head * (HD / 2) + i % (HD / 2);
+            unsigned long long v = __hip_atomic_load(rp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (uint32_t spin = 0; (uint32_t)(v >> 32) != tag; ++spin) {
+                if (spin == kHandoffSpins) {
+                    A.ws[kWsErr] = 1u;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                v = __hip_atomic_load(rp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sm.raw[i] = (uint32_t)v;
+        }
+        __syncthreads();
+        const uint16_t* raw16 = reinterpret_cast<const uint16_t*>(sm.raw);
+#pragma unroll
+        for (int j = 0; j < QW; ++j) {
+            const uint32_t r = wave + 4 * j;
+            if (r < (uint32_t)REP) {
+                qx1[j] = raw16[r * HD + lane];
+                qx2[j] = raw16[r * HD + lane + 64];
+            }
+        }
+        if (wave == kwave) {
+            kx1 = raw16[REP * HD + lane];
+            kx2 = raw16[REP * HD + lane + 64];
+            vx1 = raw16[(REP + 1) * HD + lane];
+            vx2 = raw16[(REP + 1) * HD + lane + 64];
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            vn[s] = *reinterpret_cast<const u32x4*>(&raw16[(REP + 1) * HD + 32 * s + 8 * lr]);
+    }
 
     if constexpr (FUSED) {
         float cr, sr;
@@ -594,6 +665,42 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
     }
 }
 
+template <int REP, bool FUSED>
+__global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs A) {
+    __shared__ DecodeSmem<REP> sm;
+    attn_decode_body<REP, FUSED, false>(A, blockIdx.x, blockIdx.y, sm, nullptr);
+}
+
+// The fused op's q|k|v GEMV and its chunk pass in one launch. Workgroups [0, n_gemv)
+// run the row-in-wave GEMV (gemv_rw_body: 4 waves, one pass, C slices of P lanes per
+// row) and, besides writing the q|k|v row, publish it as tagged row-pair records; the
+// chunk workgroups (c, g) behind them request their K/V rows at once and take the new
+// token's q, k and v from the records when they arrive, so the K/V stream of the chunk
+// pass overlaps the GEMV instead of following it. Waits go one way only, chunk
+// workgroups on GEMV workgroups, which never wait; the host launches this only when
+// the whole grid fits on the device at once, so every waited-for workgroup is running.
+// Tags are the workspace's call sequence number + 1 (the merge pass advances it after
+// each call), so a record left by an earlier call never matches.
+struct QkvAttnArgs {
+    GemvRwArgs G;
+    DecodeArgs D;
+    unsigned long long* rec;   // (H + 2 KVH) * HD / 2 records
+    uint32_t n_gemv;
+};
+
+template <int REP, int C, int P>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void qkv_attn_decode_kernel(QkvAttnArgs QA) {
+    __shared__ DecodeSmem<REP> sm;
+    __shared__ double s_ss[8];
+    if (blockIdx.x < QA.n_gemv) {
+        const uint32_t tag = QA.D.ws[kWsSeq] + 1u;
+        gemv_rw_body<C, P, 1, 2, true>(QA.G, blockIdx.x, 256u, reinterpret_cast<u32x4*>(sm.v), s_ss, QA.rec, tag);
+        return;
+    }
+    const uint32_t b = blockIdx.x - QA.n_gemv;
+    attn_decode_body<REP, true, true>(QA.D, b % QA.D.max_chunks, b / QA.D.max_chunks, sm, QA.rec);
+}
+
 // Decode, pass 2: one workgroup per query head h = g*rep + r merges its chunks:
 // M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c - M) / L, in one pass:
 // thread (grp, d4) merges chunks grp, grp+8, ... of dims 4*d4..4*d4+3 online (running
@@ -613,6 +720,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
     const uint32_t h = blockIdx.x, g = h / rep, r = h % rep;
     const uint32_t tid = threadIdx.x;
     if (advance && h == gridDim.x - 1) {
+        if (tid == 0) ws[kWsSeq] = ws[kWsSeq] + 1u;   // this call's records are all read
         const uint32_t n_kv = ws[kWsSnap];
         // RoPE records for positions n_kv - 1 (wave 0) and n_kv (wave 1).
         const uint32_t j = tid >> 6, i = tid & 63;
@@ -808,6 +916,118 @@ hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, cons
                  0u, count_dev, scale * kLog2e, work + kWsHead, max_chunks,
                  reinterpret_cast<uint32_t*>(work), nullptr, 0u, 0u, std::min(n_kv_known, nslots) / DC};
     return decode_launch<true>(A, rep, 1, out, work, st);
+}
+
+namespace {
+
+// Workgroups per CU of the one-launch kernel (0 if unknown), once per instance.
+template <int REP, int C, int P>
+int qkv_attn_occupancy() {
+    static std::atomic<int> occ{-1};
+    int o = occ.load(std::memory_order_relaxed);
+    if (o < 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, qkv_attn_decode_kernel<REP, C, P>, 256, 0) !=
+            hipSuccess)
+            nb = 0;
+        occ.store(nb, std::memory_order_relaxed);
+        o = nb;
+    }
+    return o;
+}
+
+// The instance for (rep, C, P): its occupancy query (launch == false) or its launch.
+template <int REP>
+int qkv_attn_instance(uint32_t C, uint32_t P, bool launch, const QkvAttnArgs* QA, uint32_t grid, hipStream_t st) {
+#define GEHTP_QKV_ATTN(CC, PP)                                                                     \
+    if (C == CC && P == PP) {                                                                     \
+        if (!launch) return qkv_attn_occupancy<REP, CC, PP>();                                    \
+        hipLaunchKernelGGL((qkv_attn_decode_kernel<REP, CC, PP>), dim3(grid), dim3(256), 0, st, *QA); \
+        return 1;                                                                                 \
+    }
+    GEHTP_QKV_ATTN(2, 16)
+    GEHTP_QKV_ATTN(4, 16)
+    GEHTP_QKV_ATTN(5, 16)
+    GEHTP_QKV_ATTN(3, 32)
+    GEHTP_QKV_ATTN(4, 32)
+#undef GEHTP_QKV_ATTN
+    return 0;
+}
+
+int qkv_attn_call(uint32_t rep, uint32_t C, uint32_t P, bool launch, const QkvAttnArgs* QA, uint32_t grid,
+                  hipStream_t st) {
+    switch (rep) {
+    case 1: return qkv_attn_instance<1>(C, P, launch, QA, grid, st);
+    case 2: return qkv_attn_instance<2>(C, P, launch, QA, grid, st);
+    case 4: return qkv_attn_instance<4>(C, P, launch, QA, grid, st);
+    case 8: return qkv_attn_instance<8>(C, P, launch, QA, grid, st);
+    default: return 0;
+    }
+}
+
+struct QkvAttnPlan {
+    bool ok = false;
+    uint32_t C = 0, P = 0, rep = 0, N = 0, n_gemv = 0, max_chunks = 0, grid = 0;
+};
+
+// Shape rules of the one-launch form; ok only when the whole grid fits on the device at
+// once (the waits need every GEMV workgroup resident or done while a chunk workgroup
+// waits, which holds in any dispatch order when all are resident together; at most
+// 128 VGPRs, amdgpu_waves_per_eu(4), gives four 4-wave workgroups per CU).
+QkvAttnPlan qkv_attn_plan(uint32_t K, uint32_t H, uint32_t KVH, uint32_t nslots) {
+    QkvAttnPlan pl;
+    if (!KVH || H % KVH || !nslots) return pl;
+    pl.rep = H / KVH;
+    if (pl.rep != 1 && pl.rep != 2 && pl.rep != 4 && pl.rep != 8) return pl;
+    if (K % 512 == 0 && (K / 512 == 2 || K / 512 == 4 || K / 512 == 5)) { pl.C = K / 512; pl.P = 16; }
+    else if (K % 1024 == 0 && (K / 1024 == 3 || K / 1024 == 4)) { pl.C = K / 1024; pl.P = 32; }
+    else return pl;
+    pl.N = (H + 2 * KVH) * HD;
+    if ((uint64_t)pl.N * (K / 2) >= (1ull << 32)) return pl;   // 32-bit row offsets
+    const uint32_t rows_wg = 4u * (64u / pl.P);               // 4 waves, one pass
+    pl.n_gemv = (pl.N + rows_wg - 1) / rows_wg;
+    pl.max_chunks = (nslots + DC - 1) / DC;
+    const uint64_t grid = (uint64_t)pl.n_gemv + (uint64_t)pl.max_chunks * KVH;
+    const int occ = qkv_attn_call(pl.rep, pl.C, pl.P, false, nullptr, 0, nullptr);
+    if (occ <= 0 || grid > (uint64_t)occ * (uint64_t)device_cu_count()) return pl;
+    pl.grid = (uint32_t)grid;
+    pl.ok = true;
+    return pl;
+}
+
+uint32_t qkv_rec_offset(uint32_t nslots, uint32_t H) { return (attn_decode_work_floats(nslots, H, HD) + 1u) & ~1u; }
+
+}  // namespace
+
+uint32_t attn_qkv_fused_work_floats(uint32_t nslots, uint32_t H, uint32_t KVH) {
+    return qkv_rec_offset(nslots, H) + (H + 2 * KVH) * HD;   // 8-byte records of 2 values
+}
+
+bool qkv_attn_decode_supported(uint32_t K, uint32_t H, uint32_t KVH, uint32_t nslots) {
+    return qkv_attn_plan(K, H, KVH, nslots).ok;
+}
+
+hipError_t launch_qkv_attn_decode(const __half* x, const uint8_t* wq, const __half* wsc, const __half* gamma,
+                                  uint32_t K, __half* qkv, const __half* q_gamma, const __half* k_gamma,
+                                  float theta, uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
+                                  uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH, float scale,
+                                  float* work, uint32_t work_floats, hipStream_t st, uint32_t n_kv_known) {
+    if (!KVH || H % KVH || !count_dev || !nslots || slot_bytes != KVH * HD * 4) return hipErrorInvalidValue;
+    if (attn_qkv_fused_work_floats(nslots, H, KVH) > work_floats) return hipErrorInvalidValue;
+    if (((uintptr_t)x | (uintptr_t)wq | (uintptr_t)gamma | (uintptr_t)work) % 16) return hipErrorInvalidValue;
+    const QkvAttnPlan pl = qkv_attn_plan(K, H, KVH, nslots);
+    if (!pl.ok) return hipErrorNotSupported;
+    QkvAttnArgs QA;
+    QA.G = GemvRwArgs{x, wq, wsc, qkv, pl.N, K, gamma, nullptr, 0};
+    QA.D = DecodeArgs{nullptr, qkv, q_gamma, k_gamma, theta, ring, slot_bytes, nslots, KVH, H,
+                      0u, count_dev, scale * kLog2e, work + kWsHead, pl.max_chunks,
+                      reinterpret_cast<uint32_t*>(work), nullptr, 0u, 0u, std::min(n_kv_known, nslots) / DC};
+    QA.rec = reinterpret_cast<unsigned long long*>(work + qkv_rec_offset(nslots, H));
+    QA.n_gemv = pl.n_gemv;
+    qkv_attn_call(pl.rep, pl.C, pl.P, true, &QA, pl.grid, st);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(H + 1), dim3(256), 0, st, QA.D.part, 0u, count_dev, 1, pl.rep,
+                       pl.max_chunks, out, reinterpret_cast<uint32_t*>(work), theta, nullptr, 0u, 0u);
+    return hipGetLastError();
 }
 
 }  // namespace gehtp

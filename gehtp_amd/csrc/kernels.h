@@ -175,8 +175,8 @@ hipError_t launch_attn_decode(const __half* q, const uint8_t* ring, uint32_t slo
                               bool mask_shared = false);
 // Fused decode step (OP_ATTN_DECODE_QKV_F16): QK-RMSNorm + RoPE of the raw [q | k | v]
 // row at position *count_dev, k/v appended to the ring, attention over positions
-// 0..*count_dev, then *count_dev += 1. work's leading counter must be zero before the
-// first call (every call leaves it zero).
+// 0..*count_dev, then *count_dev += 1. work's head must be zero before the first call
+// (the engine clears a new workspace).
 hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, const __half* k_gamma,
                                   float theta, uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
                                   uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH,
@@ -184,6 +184,23 @@ hipError_t launch_attn_decode_qkv(const __half* qkv, const __half* q_gamma, cons
                                   uint32_t n_kv_known = 0);
 // Floats of workspace launch_attn_decode needs for n_kv positions.
 uint32_t attn_decode_work_floats(uint32_t max_kv, uint32_t H, uint32_t hd);
+// OP_W4G_FUSED_F16's GEMV (M = 1; RMSNorm gamma optional; no residual, no SwiGLU) that
+// writes the [q | k | v] row qkv (N = (H + 2 KVH) * 128 rows of K) and the
+// OP_ATTN_DECODE_QKV_F16 reading it next, in one launch plus the merge pass: the bits of
+// launch_w4g_gemv followed by launch_attn_decode_qkv. Returns hipErrorNotSupported and
+// launches nothing for what it does not take (K = 512 C with C in {2, 4, 5} or K = 1024 C
+// with C in {3, 4}; group size 1, 2, 4 or 8; a grid that does not fit on the device at
+// once; invalid arguments give hipErrorInvalidValue). work:
+// attn_qkv_fused_work_floats(nslots, H, KVH) floats, head zero before the first call,
+// shared with launch_attn_decode_qkv.
+hipError_t launch_qkv_attn_decode(const __half* x, const uint8_t* wq, const __half* wsc, const __half* gamma,
+                                  uint32_t K, __half* qkv, const __half* q_gamma, const __half* k_gamma,
+                                  float theta, uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
+                                  uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH, float scale,
+                                  float* work, uint32_t work_floats, hipStream_t st, uint32_t n_kv_known = 0);
+uint32_t attn_qkv_fused_work_floats(uint32_t nslots, uint32_t H, uint32_t KVH);
+// Whether launch_qkv_attn_decode takes this shape (16-byte aligned operands aside).
+bool qkv_attn_decode_supported(uint32_t K, uint32_t H, uint32_t KVH, uint32_t nslots);
 
 // ---- crouton16_row4 surfaces, opcode 1 / 2, data ops (k_data.hip) ----
 hipError_t launch_crouton_encode(const uint16_t* lin, uint16_t* surf, uint32_t rows, uint32_t cols,

@@ -9,7 +9,8 @@
  * Conventions: every pointer is a DEVICE pointer; `stream` is a hipStream_t
  * (NULL = the legacy default stream); the call only enqueues work. Return 0 on
  * success, GEHTP_EINVAL for a rejected shape/alignment, GEHTP_E2BIG for a request beyond
- * a fixed scratch, or a positive hipError_t.
+ * a fixed scratch, GEHTP_ENOTSUP for a form an entry point does not take, or a positive
+ * hipError_t.
  */
 #ifndef GEHTP_KERNELS_H
 #define GEHTP_KERNELS_H
@@ -113,6 +114,21 @@ int gehtp_attn_decode_qkv(const void* qkv, uint32_t H, uint32_t KVH, const void*
                           const void* k_gamma, float theta, float scale, void* ring,
                           uint32_t state_bytes, void* count_dev, void* out, void* work,
                           uint32_t work_floats, void* stream);
+/* OP_W4G_FUSED_F16's GEMV (M = 1; gamma = RMSNorm weights or NULL; no residual, no
+ * SwiGLU) writing qkv ((H + 2*KVH)*128 rows of K) followed by gehtp_attn_decode_qkv on
+ * that row, in one launch plus the merge pass, with the bits of the two calls. Returns
+ * GEHTP_ENOTSUP, launching nothing, for what the one-launch form does not take (K = 512 C
+ * with C in {2, 4, 5} or 1024 C with C in {3, 4}; H / KVH in {1, 2, 4, 8}; a grid the
+ * device cannot hold at once). work: 16-byte aligned,
+ * gehtp_attn_qkv_fused_work_floats(ring slots, H, KVH) floats, zeroed before its first
+ * use; gehtp_attn_decode_qkv may share it. No counterpart in the reference: the engine
+ * performs its OP_W4G_FUSED_F16 -> OP_ATTN_DECODE_QKV_F16 pairs this way. */
+#define GEHTP_ENOTSUP (-95)
+uint32_t gehtp_attn_qkv_fused_work_floats(uint32_t nslots, uint32_t H, uint32_t KVH);
+int gehtp_qkv_attn_decode(const void* x, const void* wq, const void* ws, const void* gamma, uint32_t K,
+                          void* qkv, uint32_t H, uint32_t KVH, const void* q_gamma, const void* k_gamma,
+                          float theta, float scale, void* ring, uint32_t state_bytes, void* count_dev,
+                          void* out, void* work, uint32_t work_floats, void* stream);
 /* Append n_tok tokens (k/v [n_tok, KVH*hd]) at positions pos..pos+n_tok-1 of the ring. */
 int gehtp_kv_append(void* ring, uint32_t state_bytes, const void* k, const void* v,
                     uint32_t kv_elems, uint32_t n_tok, uint32_t pos, void* stream);

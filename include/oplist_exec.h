@@ -153,6 +153,11 @@ void wt_exec_fusion_detail(const struct wt_blob* b, uint32_t* chains, uint32_t* 
  * performs that op in its epilogue (same bits; the GEMM's own output is written too);
  * this counts such executions. */
 uint64_t wt_exec_qkv_rope_fused(void);
+/* Extension, under the same switch: an OP_W4G_FUSED_F16 q|k|v GEMV (M = 1, no residual,
+ * no SwiGLU) followed in the same run by the OP_ATTN_DECODE_QKV_F16 that reads its
+ * output runs in one launch with that op's chunk pass (same bits; the GEMV's own output
+ * is written too), where the shape allows; this counts such executions. */
+uint64_t wt_exec_qkv_attn_fused(void);
 
 /* W3 inspect report: one JSON line per call of emit (reference wt_w3.c). */
 void wt_w3_report(const char* blob_name, const uint8_t* buf, size_t size,
