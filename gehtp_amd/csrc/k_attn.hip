@@ -342,6 +342,7 @@ struct DecodeArgs {
     uint32_t P;
     uint32_t mask_hs;
     uint32_t spec_chunks;    // chunks whose keys are known to lie below the count
+    uint32_t kv_naps;        // hand-off form: s_sleep(4) steps before the K/V rows are requested
 };
 
 // MFMA operand layouts of v_mfma_f32_16x16x32_f16 (lane l, column lc = l % 16, row group
@@ -383,6 +384,23 @@ struct DecodeSmem {
     __align__(16) _Float16 k[HD];
     __align__(16) uint32_t raw[(REP + 2) * HD / 2];
 };
+
+// The low half of a q|k|v hand-off record (see qkv_attn_decode_kernel) once its high
+// half carries tag. Polls with s_sleep(NAP) between agent-scope atomic loads; gives up
+// after kHandoffSpins polls (setting the workspace's error word) so that every wave ends.
+template <int NAP>
+__device__ __forceinline__ uint32_t rec_wait(const unsigned long long* p, uint32_t tag, uint32_t* ws) {
+    unsigned long long v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t spin = 0; (uint32_t)(v >> 32) != tag; ++spin) {
+        if (spin == kHandoffSpins) {
+            ws[kWsErr] = 1u;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(NAP);
+        v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return (uint32_t)v;
+}
 
 // Chunk c of kv head g. HO (hand-off, FUSED only): the new token's q|k|v row is not read
 // from A.qkv but from the row-pair records rec[] that the q|k|v GEMV workgroups of the
@@ -475,6 +493,12 @@ __device__ __forceinline__ void attn_decode_body(const DecodeArgs& A, uint32_t c
             qpl[s] = *reinterpret_cast<const h8_t*>(A.q + (size_t)(g * REP + qh) * HD + 32 * s + 8 * lr);
     }
     const bool early = c < A.spec_chunks;
+    if constexpr (HO) {
+        // The K/V rows are not needed before the GEMV's records arrive: requested ~1 us in
+        // (for the 4B q|k|v weights), they leave the memory system to the GEMV's weight
+        // stream first (the 4B layer 13.5 -> 13.05 us; 2 us in: 13.8).
+        for (uint32_t k = 0; k < A.kv_naps; ++k) __builtin_amdgcn_s_sleep(4);
+    }
     if (early) load_kv(0xFFFFFFFFu);
     asm volatile("" ::: "memory");
     const uint32_t pos = FUSED ? cnt : 0u;   // position of the new token
@@ -483,26 +507,40 @@ __device__ __forceinline__ void attn_decode_body(const DecodeArgs& A, uint32_t c
     if (FUSED && c == 0 && g == 0 && tid == 0) A.ws[kWsSnap] = n_kv;
     if (!early) load_kv(n_kv);
     const bool owns_new = FUSED && pos / DC == c;
+    // K and V tiles. The new token's V row comes from the QKV row (its ring slot was read
+    // before this launch wrote it; its K row is replaced below). V rows past n_kv are
+    // zero, since slots not yet written may hold anything and p = 0 times a non-finite
+    // value would reach the sums; their scores are -inf whatever K holds. In the
+    // hand-off form the tiles are staged before the records are waited for (the K/V
+    // loads are the older ones in flight), the new token's V row once its record is in.
+    const uint32_t trow = 16 * wave + lc, tkey = c * DC + trow;   // this lane's tile row
+    auto stage_tiles = [&]() {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            u32x4 v = vr[s];
+            if (!HO && FUSED && tkey == pos) v = vn[s];
+            if (tkey >= n_kv) v = u32x4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(&s_v[trow * VSD + 32 * s + 8 * lr]) = v;
+            *reinterpret_cast<u32x4*>(&s_kt[trow * KSD + 32 * s + 8 * lr]) = kr[s];
+        }
+    };
     if constexpr (HO) {
+        stage_tiles();
         // Wait for the records of this group's q rows and of k and v of head g (record i
         // of row block b: rows 2i, 2i + 1 of head b), then take the values from LDS as
-        // the other form takes them from the q|k|v row.
+        // the other form takes them from the q|k|v row. One thread first waits for the
+        // last v record (the v rows are the GEMV's last row blocks), then every thread
+        // reads and checks its own records, so that the polls do not load the memory
+        // system while the GEMV streams its weights.
         constexpr uint32_t NREC = (REP + 2) * HD / 2;
-        for (uint32_t i = tid; i < NREC; i += 256) {
+        auto rec_at = [&](uint32_t i) {
             const uint32_t b = i / (HD / 2);
             const uint32_t head = b < (uint32_t)REP ? g * REP + b : b == (uint32_t)REP ? A.H + g : A.H + A.KVH + g;
-            const unsigned long long* rp = rec + (size_t)head * (HD / 2) + i % (HD / 2);
-            unsigned long long v = __hip_atomic_load(rp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            for (uint32_t spin = 0; (uint32_t)(v >> 32) != tag; ++spin) {
-                if (spin == kHandoffSpins) {
-                    A.ws[kWsErr] = 1u;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-                v = __hip_atomic_load(rp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            sm.raw[i] = (uint32_t)v;
-        }
+            return rec + (size_t)head * (HD / 2) + i % (HD / 2);
+        };
+        if (tid == 0) rec_wait<2>(rec_at(NREC - 1), tag, A.ws);
+        __syncthreads();
+        for (uint32_t i = tid; i < NREC; i += 256) sm.raw[i] = rec_wait<1>(rec_at(i), tag, A.ws);
         __syncthreads();
         const uint16_t* raw16 = reinterpret_cast<const uint16_t*>(sm.raw);
 #pragma unroll
@@ -519,9 +557,12 @@ __device__ __forceinline__ void attn_decode_body(const DecodeArgs& A, uint32_t c
             vx1 = raw16[(REP + 1) * HD + lane];
             vx2 = raw16[(REP + 1) * HD + lane + 64];
         }
+        if (tkey == pos) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-            vn[s] = *reinterpret_cast<const u32x4*>(&raw16[(REP + 1) * HD + 32 * s + 8 * lr]);
+            for (int s = 0; s < 4; ++s)
+                *reinterpret_cast<u32x4*>(&s_v[trow * VSD + 32 * s + 8 * lr]) =
+                    *reinterpret_cast<const u32x4*>(&raw16[(REP + 1) * HD + 32 * s + 8 * lr]);
+        }
     }
 
     if constexpr (FUSED) {
@@ -559,21 +600,7 @@ __device__ __forceinline__ void attn_decode_body(const DecodeArgs& A, uint32_t c
             vface[g * HD + lane + 64] = __builtin_bit_cast(_Float16, vx2);
         }
     }
-    // K and V tiles. The new token's V row comes from the QKV row (its ring slot was read
-    // before this launch wrote it; its K row is replaced below). V rows past n_kv are
-    // zero, since slots not yet written may hold anything and p = 0 times a non-finite
-    // value would reach the sums; their scores are -inf whatever K holds.
-    {
-        const uint32_t kl = 16 * wave + lc, key = c * DC + kl;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            u32x4 v = vr[s];
-            if (FUSED && key == pos) v = vn[s];
-            if (key >= n_kv) v = u32x4{0u, 0u, 0u, 0u};
-            *reinterpret_cast<u32x4*>(&s_v[kl * VSD + 32 * s + 8 * lr]) = v;
-            *reinterpret_cast<u32x4*>(&s_kt[kl * KSD + 32 * s + 8 * lr]) = kr[s];
-        }
-    }
+    if constexpr (!HO) stage_tiles();
     __syncthreads();
     if (wave != 0) return;
 
@@ -973,7 +1000,9 @@ struct QkvAttnPlan {
 // Shape rules of the one-launch form; ok only when the whole grid fits on the device at
 // once (the waits need every GEMV workgroup resident or done while a chunk workgroup
 // waits, which holds in any dispatch order when all are resident together; at most
-// 128 VGPRs, amdgpu_waves_per_eu(4), gives four 4-wave workgroups per CU).
+// 128 VGPRs, amdgpu_waves_per_eu(4), gives four 4-wave workgroups per CU). (GEMV
+// workgroups of three working waves and 12 rows, two per CU, ran the 4B layer slower:
+// 14.2 against 13.6 us, each of the 512 workgroups staging and normalizing x.)
 QkvAttnPlan qkv_attn_plan(uint32_t K, uint32_t H, uint32_t KVH, uint32_t nslots) {
     QkvAttnPlan pl;
     if (!KVH || H % KVH || !nslots) return pl;
@@ -1019,9 +1048,11 @@ hipError_t launch_qkv_attn_decode(const __half* x, const uint8_t* wq, const __ha
     if (!pl.ok) return hipErrorNotSupported;
     QkvAttnArgs QA;
     QA.G = GemvRwArgs{x, wq, wsc, qkv, pl.N, K, gamma, nullptr, 0};
+    // ~1.07 us of s_sleep(4) steps (256 clocks each) per 7.9 MB of q|k|v weights
+    const uint32_t naps = (uint32_t)std::min<uint64_t>(20u, ((uint64_t)pl.N * (K / 2) * 10u + 3932160u) / 7864320u);
     QA.D = DecodeArgs{nullptr, qkv, q_gamma, k_gamma, theta, ring, slot_bytes, nslots, KVH, H,
                       0u, count_dev, scale * kLog2e, work + kWsHead, pl.max_chunks,
-                      reinterpret_cast<uint32_t*>(work), nullptr, 0u, 0u, std::min(n_kv_known, nslots) / DC};
+                      reinterpret_cast<uint32_t*>(work), nullptr, 0u, 0u, std::min(n_kv_known, nslots) / DC, naps};
     QA.rec = reinterpret_cast<unsigned long long*>(work + qkv_rec_offset(nslots, H));
     QA.n_gemv = pl.n_gemv;
     qkv_attn_call(pl.rep, pl.C, pl.P, true, &QA, pl.grid, st);

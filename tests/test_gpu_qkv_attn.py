@@ -28,6 +28,7 @@ def _sync():
 
 @pytest.mark.parametrize("H,KVH,K,nslots,pos0", [
     (32, 8, 2560, 4096, 2059),   # the 4B decode shape at ~2k keys (spec chunks, 33 active)
+    (32, 8, 2560, 4608, 3000),   # a grid too large for GEMV workgroups of three waves
     (32, 8, 2560, 256, 0),       # first position
     (16, 8, 1024, 256, 62),      # 0.8B-class; crosses a 64-key chunk boundary
     (16, 8, 4096, 512, 127),     # 32 lanes per row, 4 slices
