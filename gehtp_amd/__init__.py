@@ -205,5 +205,9 @@ class Engine:
         """Decode attention ops run in their q|k|v GEMV's launch so far."""
         return int(self.lib.wt_exec_qkv_attn_fused())
 
+    def merge_oproj_fused(self) -> int:
+        """o-proj GEMVs run in one launch with the decode attention's merge pass so far."""
+        return int(self.lib.wt_exec_merge_oproj_fused())
+
 
 WT_ERR = WT_ERR

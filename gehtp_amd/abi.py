@@ -157,6 +157,7 @@ EXPORTS = {
                                      C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
     "wt_exec_qkv_rope_fused": (C.c_uint64, []),
     "wt_exec_qkv_attn_fused": (C.c_uint64, []),
+    "wt_exec_merge_oproj_fused": (C.c_uint64, []),
     "wt_w3_report": (None, [C.c_char_p, _u8p, C.c_size_t, C.POINTER(WtBlob),
                             C.CFUNCTYPE(None, C.c_char_p, _vp), _vp]),
     # gehtp_kernels.h

@@ -75,6 +75,36 @@ __device__ __forceinline__ uint16_t silu_f16_expr(uint16_t hb) {
 // store: a reader on any XCD that polls rec[i] with agent-scope atomic loads until it
 // sees the tag has both values, with no fence on either side (a kernel that runs this
 // body next to the rows' readers hands them over that way).
+//
+// With XREC, x is not read from A.x but from such records, xrec[i] = x[2i] | x[2i + 1] <<
+// 16 | xtag << 32, which other workgroups of the same launch publish: the weight loads
+// are issued first, then one thread waits for the last record and every thread reads
+// (and checks) its own.
+
+// Bound on the polls of one hand-off record: a wait that reaches it writes 1 to *err and
+// goes on (with whatever the record holds), so that every wave ends. ~1 us per poll, so
+// tens of ms.
+constexpr uint32_t kHandoffSpins = 1u << 15;
+
+// The low 32 bits of record p once its high half carries tag: agent-scope atomic loads,
+// s_sleep(NAP) between them.
+template <int NAP>
+__device__ __forceinline__ uint32_t handoff_wait(const unsigned long long* p, uint32_t tag, uint32_t* err) {
+    unsigned long long v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t spin = 0; (uint32_t)(v >> 32) != tag; ++spin) {
+        if (spin == kHandoffSpins) {
+            *err = 1u;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(NAP);
+        v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return (uint32_t)v;
+}
+__device__ __forceinline__ void handoff_store(unsigned long long* p, uint32_t tag, uint32_t v) {
+    __hip_atomic_store(p, (unsigned long long)tag << 32 | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct GemvRwArgs {
     const __half* x;
     const uint8_t* wq;
@@ -88,10 +118,11 @@ struct GemvRwArgs {
 
 // Workgroup wg of the launch, nt threads (nt / 64 waves); xn: K / 8 16-byte LDS slots
 // (x in pair order, padded layout), s_ss: 8 doubles of LDS.
-template <int C, int P, int NP, int PRE, bool REC = false>
+template <int C, int P, int NP, int PRE, bool REC = false, bool XREC = false>
 __device__ __forceinline__ void gemv_rw_body(const GemvRwArgs& A, uint32_t wg, uint32_t nt, u32x4* xn,
                                              double* s_ss, unsigned long long* rec = nullptr,
-                                             uint32_t tag = 0u) {
+                                             uint32_t tag = 0u, const unsigned long long* xrec = nullptr,
+                                             uint32_t xtag = 0u, uint32_t* err = nullptr) {
     constexpr int RW = 64 / P;
     static_assert(P == 16 || P == 32, "lanes per row");
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -112,7 +143,7 @@ __device__ __forceinline__ void gemv_rw_body(const GemvRwArgs& A, uint32_t wg, u
 #pragma unroll
     for (int k = 0; k < PRE; ++k) {
         const uint32_t i = min(t + k * nt, K8 - 1);
-        xv[k] = reinterpret_cast<const u32x4*>(A.x)[i];
+        if constexpr (!XREC) xv[k] = reinterpret_cast<const u32x4*>(A.x)[i];
         if (A.gamma) gv[k] = reinterpret_cast<const u32x4*>(A.gamma)[i];
     }
     uint16_t resv[NP];
@@ -134,6 +165,16 @@ __device__ __forceinline__ void gemv_rw_body(const GemvRwArgs& A, uint32_t wg, u
                 reinterpret_cast<const u32x4*>(wq0 + (size_t)(lr * rowbytes + slice(c) * 16)));
             sc[c][i] = ws0[(size_t)lr * G + (slice(c) >> 1)];
         }
+    if constexpr (XREC) {
+        if (t == 0) handoff_wait<2>(xrec + (K8 * 4 - 1), xtag, err);
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < PRE; ++k) {
+            const uint32_t i = min(t + k * nt, K8 - 1);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[k][e] = handoff_wait<1>(xrec + 4 * i + e, xtag, err);
+        }
+    }
 
     float rms = 1.0f, rcp = 1.0f;
     if (A.gamma) {

@@ -144,6 +144,7 @@ struct Engine {
     uint64_t fuse_scratch_cap = 0;
     uint64_t qkv_rope_fused = 0;   // OP_QK_ROPE_KV_F16 ops performed by their GEMM's epilogue
     uint64_t qkv_attn_fused = 0;   // OP_ATTN_DECODE_QKV_F16 ops performed in their GEMV's launch
+    uint64_t merge_oproj_fused = 0;   // o-proj GEMVs run in one launch with the merge pass before them
     bool graphs_broken = false;
     uint32_t n_captures = 0, n_replays = 0;
 
@@ -1051,6 +1052,17 @@ struct AttnQkv {
 };
 int attn_qkv_prep(const wt_blob* b, const wt_op* op, AttnQkv& r, char* err, size_t errn);
 void attn_qkv_commit(const AttnQkv& r);
+// The merge pass that such a launch left to the o-proj GEMV op after it (op), which runs
+// both in one launch; any other next op, or the end of the run, runs it alone first.
+struct MergePending {
+    const wt_op* op = nullptr;
+    uint32_t* count = nullptr;
+    __half* out = nullptr;
+    uint32_t H = 0, KVH = 0, nslots = 0;
+    float theta = 0.0f;
+};
+MergePending g_merge_pending;
+int flush_merge_pending(char* err, size_t errn);
 bool fusion_on();
 extern uint32_t g_run_end;
 
@@ -1094,6 +1106,18 @@ int op_w4g_fused(Ctx& cx) {
     epi.ldr = n_out;
     epi.swiglu = swiglu;
     const bool gemv_fits = w4g_gemv_supported(M, K);
+    if (g_merge_pending.op == cx.op) {   // left by the q|k|v GEMV two ops back
+        const MergePending mp = g_merge_pending;
+        g_merge_pending = MergePending{};
+        if (gemv_fits && M == 1 && a == mp.out && !gamma && !swiglu && ldy == N && ((uintptr_t)ws & 1u) == 0) {
+            CHECK_LAUNCH(launch_merge_oproj(mp.count, mp.out, mp.H, mp.KVH, mp.nslots, mp.theta, g.attn_work,
+                                            g.attn_work_floats, wq, ws, y, N, res, g.stream));
+            g.merge_oproj_fused++;
+            return 0;
+        }
+        CHECK_LAUNCH(launch_attn_merge_deferred(mp.count, mp.out, mp.H, mp.KVH, mp.nslots, mp.theta, g.attn_work,
+                                                g.stream));
+    }
     if (gemv_fits) {
         epi.gamma = gamma;
         // The OP_ATTN_DECODE_QKV_F16 that reads this q|k|v row next, in the same run:
@@ -1118,11 +1142,21 @@ int op_w4g_fused(Ctx& cx) {
                 };
                 auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
                 if (apart(a, (uint64_t)K * 2u) && apart(y, (uint64_t)N * 2u) && apart(gamma ? gamma : a, K * 2u) &&
-                    al16(g.attn_work) && qkv_attn_decode_supported(K, r.H, r.KVH, r.s->nslots)) {
+                    al16(g.attn_work) && al16(r.o) && qkv_attn_decode_supported(K, r.H, r.KVH, r.s->nslots)) {
+                    // The o-proj GEMV reading the attention output right after (M = 1, no
+                    // RMSNorm, no SwiGLU, output stride N) takes the merge pass into its
+                    // own launch, where its weight loads overlap the merge.
+                    const wt_op* ox = cx.op + 2;
+                    const bool defer = (uint32_t)(ox - cx.b->ops) < g_run_end && ox->opcode == OP_W4G_FUSED_F16 &&
+                                       ox->n_args >= 11 && ox->args[0] == rx->args[2] && ox->args[4] == 1 &&
+                                       ox->args[5] == r.H * 128u && ox->args[7] == WT_REF_NONE && ox->args[9] == 0 &&
+                                       ox->args[10] == 2u && merge_oproj_supported(r.H, ox->args[6]);
                     CHECK_LAUNCH(launch_qkv_attn_decode(a, wq, ws, gamma, K, y, r.qg, r.kg, r.theta, r.s->dev,
                                                         r.s->slot_bytes, r.s->nslots, g.counters_dev + r.si, r.o,
                                                         r.H, r.KVH, r.scale, g.attn_work, g.attn_work_floats,
-                                                        g.stream, r.s->count + 1));
+                                                        g.stream, r.s->count + 1, defer));
+                    if (defer)
+                        g_merge_pending = MergePending{ox, g.counters_dev + r.si, r.o, r.H, r.KVH, r.s->nslots, r.theta};
                     attn_qkv_commit(r);
                     g_attn_pre = rx;
                     g.qkv_attn_fused++;
@@ -1331,6 +1365,15 @@ int attn_qkv_prep(const wt_blob* b, const wt_op* op, AttnQkv& r, char* err, size
 void attn_qkv_commit(const AttnQkv& r) {
     kv_mark(*r.s, r.s->count);
     r.s->count += 1;
+}
+
+int flush_merge_pending(char* err, size_t errn) {
+    if (!g_merge_pending.op) return 0;
+    const MergePending mp = g_merge_pending;
+    g_merge_pending = MergePending{};
+    CHECK_LAUNCH(launch_attn_merge_deferred(mp.count, mp.out, mp.H, mp.KVH, mp.nslots, mp.theta, g.attn_work,
+                                            g.stream));
+    return 0;
 }
 
 // Host bytes of constant slot s (in-blob weights or the external image), or null.
@@ -2595,6 +2638,8 @@ int run_op(const wt_blob* b, uint32_t i, uint32_t ii, uint32_t* engine_m, char* 
     if (g_prenorm.op != op) g_prenorm = PreNorm{};   // only ever for the very next op
     if (g_rope_pre != op) g_rope_pre = nullptr;
     if (g_attn_pre != op) g_attn_pre = nullptr;
+    if (g_merge_pending.op && g_merge_pending.op != op && g_attn_pre != op && flush_merge_pending(err, errn))
+        return -1;
     if (g_fplan) {
         int frc = 0;
         if (fused_member(b, i, &frc, err, errn)) return frc;
@@ -2633,6 +2678,7 @@ int replay_graph(RunGraph& r, const wt_blob* b, uint32_t first, uint32_t count, 
     int fail = 0;
     for (uint32_t ii = 0; ii < count && !fail; ++ii)
         if (run_op(b, first + ii, ii, engine_m, err, errn)) fail = (int)(first + ii) + 1;
+    if (flush_merge_pending(err, errn) && !fail) fail = (int)(first + count);
     g.replay = false;
     const hipError_t e = g_defer_wait && !fail ? hipSuccess : end_run_sync();
     if (e != hipSuccess) return ERR("device error: %s", hipGetErrorString(e));
@@ -2658,6 +2704,7 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
     g_prenorm = PreNorm{};
     g_rope_pre = nullptr;
     g_attn_pre = nullptr;
+    g_merge_pending = MergePending{};
     char dummy_err[8];
     if (!err || !errn) { err = dummy_err; errn = sizeof dummy_err; }
     uint32_t dummy_m = 0;
@@ -2736,6 +2783,8 @@ int wt_exec_run_range(const struct wt_blob* b, uint32_t first, uint32_t count, u
         if (rc == 0) hook_dump(ii);
         if (rc) fail = (int)i + 1;
     }
+    // a merge pass still left over (its GEMV op failed or lies past the run) runs alone
+    if (flush_merge_pending(err, errn) && !fail) fail = (int)(first + count);
     if (observing) {
         g_obs.op = b->n_ops;   // run_io's output copy reads after every op
         if (g_run_out_temp != kNone) obs_read(g_run_out_temp);
@@ -3115,6 +3164,7 @@ void wt_exec_fusion_detail(const struct wt_blob* b, uint32_t* chains, uint32_t* 
 
 uint64_t wt_exec_qkv_rope_fused(void) { return g.qkv_rope_fused; }
 uint64_t wt_exec_qkv_attn_fused(void) { return g.qkv_attn_fused; }
+uint64_t wt_exec_merge_oproj_fused(void) { return g.merge_oproj_fused; }
 
 void wt_exec_set_hook(const char* spec) { g.hook = spec; }
 

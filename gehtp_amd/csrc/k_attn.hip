@@ -309,16 +309,15 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
 constexpr int DC = 64;          // keys per chunk
 constexpr int MAX_REP = 8;
 constexpr int PS = HD + 4;      // partial record: O[HD], m, l, 2 pad (16-byte aligned)
-// Workspace head (uint32 words): [1] n_kv of the last fused call; [2] call sequence
-// number of the fused calls (advanced by their merge pass; tags the q|k|v hand-off
-// records, see qkv_attn_decode_kernel); [3] nonzero once a hand-off wait gave up;
+// Workspace head (uint32 words): [0] second call sequence number of the fused calls
+// (advanced by qkv_attn_decode_kernel; tags the attention-output records of
+// merge_oproj_kernel); [1] n_kv of the last fused call; [2] call sequence number of the
+// fused calls (advanced by their merge pass; tags the q|k|v hand-off records, see
+// qkv_attn_decode_kernel); [3] nonzero once a hand-off wait gave up;
 // RoPE records j = 0, 1: [4 + j] position + 1 (0 = empty), [6 + j] theta bits,
 // [8 + 64j + i] pair i as f16 cos | f16 sin << 16. Partials follow the head.
-constexpr uint32_t kWsSnap = 1, kWsSeq = 2, kWsErr = 3, kWsRopeTag = 4, kWsRopeTheta = 6, kWsRope = 8;
+constexpr uint32_t kWsSeqB = 0, kWsSnap = 1, kWsSeq = 2, kWsErr = 3, kWsRopeTag = 4, kWsRopeTheta = 6, kWsRope = 8;
 constexpr uint32_t kWsHead = kWsRope + HD;
-// Polls of one hand-off record before the wait gives up (sets kWsErr and goes on), so
-// that every wave ends even if a record never arrives: ~1 us per poll, so tens of ms.
-constexpr uint32_t kHandoffSpins = 1u << 15;
 
 struct DecodeArgs {
     const __half* q;         // [H, HD] ready queries (plain op)
@@ -384,23 +383,6 @@ struct DecodeSmem {
     __align__(16) _Float16 k[HD];
     __align__(16) uint32_t raw[(REP + 2) * HD / 2];
 };
-
-// The low half of a q|k|v hand-off record (see qkv_attn_decode_kernel) once its high
-// half carries tag. Polls with s_sleep(NAP) between agent-scope atomic loads; gives up
-// after kHandoffSpins polls (setting the workspace's error word) so that every wave ends.
-template <int NAP>
-__device__ __forceinline__ uint32_t rec_wait(const unsigned long long* p, uint32_t tag, uint32_t* ws) {
-    unsigned long long v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (uint32_t spin = 0; (uint32_t)(v >> 32) != tag; ++spin) {
-        if (spin == kHandoffSpins) {
-            ws[kWsErr] = 1u;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(NAP);
-        v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return (uint32_t)v;
-}
 
 // Chunk c of kv head g. HO (hand-off, FUSED only): the new token's q|k|v row is not read
 // from A.qkv but from the row-pair records rec[] that the q|k|v GEMV workgroups of the
@@ -538,9 +520,9 @@ __device__ __forceinline__ void attn_decode_body(const DecodeArgs& A, uint32_t c
             const uint32_t head = b < (uint32_t)REP ? g * REP + b : b == (uint32_t)REP ? A.H + g : A.H + A.KVH + g;
             return rec + (size_t)head * (HD / 2) + i % (HD / 2);
         };
-        if (tid == 0) rec_wait<2>(rec_at(NREC - 1), tag, A.ws);
+        if (tid == 0) handoff_wait<2>(rec_at(NREC - 1), tag, A.ws + kWsErr);
         __syncthreads();
-        for (uint32_t i = tid; i < NREC; i += 256) sm.raw[i] = rec_wait<1>(rec_at(i), tag, A.ws);
+        for (uint32_t i = tid; i < NREC; i += 256) sm.raw[i] = handoff_wait<1>(rec_at(i), tag, A.ws + kWsErr);
         __syncthreads();
         const uint16_t* raw16 = reinterpret_cast<const uint16_t*>(sm.raw);
 #pragma unroll
@@ -721,6 +703,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void q
     __shared__ double s_ss[8];
     if (blockIdx.x < QA.n_gemv) {
         const uint32_t tag = QA.D.ws[kWsSeq] + 1u;
+        // merge_oproj_kernel's tags: no workgroup of this launch reads that word
+        if (blockIdx.x == 0 && threadIdx.x == 0) QA.D.ws[kWsSeqB] = QA.D.ws[kWsSeqB] + 1u;
         gemv_rw_body<C, P, 1, 2, true>(QA.G, blockIdx.x, 256u, reinterpret_cast<u32x4*>(sm.v), s_ss, QA.rec, tag);
         return;
     }
@@ -738,15 +722,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void q
 // With a mask over a gathered layout of P > n_kv positions, positions [n_kv, P) (zero K
 // and V) add their mask values to the softmax denominator: one more partial (m, l) with
 // O = 0, reduced over the workgroup.
-__global__ __launch_bounds__(256) void attn_merge_kernel(
-    const float* __restrict__ part, uint32_t n_kv_host, uint32_t* __restrict__ count, int advance,
-    uint32_t rep, uint32_t max_chunks, __half* __restrict__ out, uint32_t* __restrict__ ws, float theta,
-    const __half* __restrict__ mask, uint32_t P, uint32_t mask_hs) {
-    __shared__ __align__(16) float4 s_o[256];
-    __shared__ float s_m[8], s_l[8], s_t[4];
-    const uint32_t h = blockIdx.x, g = h / rep, r = h % rep;
+// Workgroup h of the pass (rope_wg: the extra one). With orec, the head's output is also
+// published as tagged row-pair records orec[h * HD / 2 + i] (see merge_oproj_kernel).
+struct MergeSmem {
+    __align__(16) float4 o[256];
+    float m[8], l[8], t[4];
+};
+__device__ __forceinline__ void attn_merge_body(const float* __restrict__ part, uint32_t n_kv_host,
+                                                uint32_t* __restrict__ count, int advance, uint32_t rep,
+                                                uint32_t max_chunks, __half* __restrict__ out,
+                                                uint32_t* __restrict__ ws, float theta,
+                                                const __half* __restrict__ mask, uint32_t P, uint32_t mask_hs,
+                                                uint32_t h, bool rope_wg, MergeSmem& lds,
+                                                unsigned long long* orec, uint32_t otag) {
+    float4* const s_o = lds.o;
+    float* const s_m = lds.m;
+    float* const s_l = lds.l;
+    float* const s_t = lds.t;
+    const uint32_t g = h / rep, r = h % rep;
     const uint32_t tid = threadIdx.x;
-    if (advance && h == gridDim.x - 1) {
+    if (rope_wg) {
         if (tid == 0) ws[kWsSeq] = ws[kWsSeq] + 1u;   // this call's records are all read
         const uint32_t n_kv = ws[kWsSnap];
         // RoPE records for positions n_kv - 1 (wave 0) and n_kv (wave 1).
@@ -842,8 +837,56 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
         h4_t hv = {(_Float16)(L > 0.0f ? o.x / L : 0.0f), (_Float16)(L > 0.0f ? o.y / L : 0.0f),
                    (_Float16)(L > 0.0f ? o.z / L : 0.0f), (_Float16)(L > 0.0f ? o.w / L : 0.0f)};
         *reinterpret_cast<h4_t*>(out + (size_t)h * HD + 4 * tid) = hv;
+        if (orec) {
+            const u32x2 w = __builtin_bit_cast(u32x2, hv);
+            handoff_store(orec + (size_t)h * (HD / 2) + 2 * tid, otag, w[0]);
+            handoff_store(orec + (size_t)h * (HD / 2) + 2 * tid + 1, otag, w[1]);
+        }
     }
     if (advance && h == 0 && tid == 0) *count = n_kv;
+}
+
+__global__ __launch_bounds__(256) void attn_merge_kernel(
+    const float* __restrict__ part, uint32_t n_kv_host, uint32_t* __restrict__ count, int advance,
+    uint32_t rep, uint32_t max_chunks, __half* __restrict__ out, uint32_t* __restrict__ ws, float theta,
+    const __half* __restrict__ mask, uint32_t P, uint32_t mask_hs) {
+    __shared__ MergeSmem sm;
+    attn_merge_body(part, n_kv_host, count, advance, rep, max_chunks, out, ws, theta, mask, P, mask_hs, blockIdx.x,
+                    advance && blockIdx.x == gridDim.x - 1, sm, nullptr, 0u);
+}
+
+// The fused op's merge pass and the o-proj GEMV reading its output (an OP_W4G_FUSED_F16
+// with M = 1, no RMSNorm, no SwiGLU) in one launch. Workgroups [0, H) merge a query
+// head each and, besides writing the attention output, publish it as tagged row-pair
+// records (tag: workspace word kWsSeqB + 1); workgroup H writes the RoPE records; the
+// GEMV workgroups behind them (gemv_rw_body, 4 waves, 2 passes) request their weights
+// at once and take x from those records. Waits go one way (GEMV on merge workgroups,
+// which never wait) and the host launches this only when the grid fits on the device
+// at once.
+struct MergeOprojArgs {
+    const float* part;
+    uint32_t* count;
+    uint32_t rep, max_chunks, H;
+    __half* out;
+    uint32_t* ws;
+    float theta;
+    GemvRwArgs G;               // the o-proj; x = out
+    unsigned long long* xrec;   // H * HD / 2 records of out
+};
+
+template <int C, int P>
+__global__ __launch_bounds__(256) void merge_oproj_kernel(MergeOprojArgs M) {
+    __shared__ MergeSmem ms;
+    __shared__ __align__(16) u32x4 xs[C * P * 4];   // x in pair order (K / 8 slots)
+    __shared__ double s_ss[8];
+    const uint32_t tag = M.ws[kWsSeqB] + 1u;
+    if (blockIdx.x <= M.H) {
+        attn_merge_body(M.part, 0u, M.count, 1, M.rep, M.max_chunks, M.out, M.ws, M.theta, nullptr, 0u, 0u,
+                        blockIdx.x, blockIdx.x == M.H, ms, M.xrec, tag);
+        return;
+    }
+    gemv_rw_body<C, P, 2, 2, false, true>(M.G, blockIdx.x - (M.H + 1), 256u, xs, s_ss, nullptr, 0u, M.xrec, tag,
+                                          M.ws + kWsErr);
 }
 
 }  // namespace
@@ -1028,8 +1071,98 @@ uint32_t qkv_rec_offset(uint32_t nslots, uint32_t H) { return (attn_decode_work_
 
 }  // namespace
 
+// Records (8 bytes, 2 values each) after the partials: the q|k|v row, then the attention
+// output (merge_oproj_kernel).
 uint32_t attn_qkv_fused_work_floats(uint32_t nslots, uint32_t H, uint32_t KVH) {
-    return qkv_rec_offset(nslots, H) + (H + 2 * KVH) * HD;   // 8-byte records of 2 values
+    return qkv_rec_offset(nslots, H) + (H + 2 * KVH) * HD + H * HD;
+}
+
+namespace {
+
+unsigned long long* out_recs(float* work, uint32_t nslots, uint32_t H, uint32_t KVH) {
+    return reinterpret_cast<unsigned long long*>(work + qkv_rec_offset(nslots, H) + (H + 2 * KVH) * HD);
+}
+
+template <int C, int P>
+int merge_oproj_occupancy() {
+    static std::atomic<int> occ{-1};
+    int o = occ.load(std::memory_order_relaxed);
+    if (o < 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, merge_oproj_kernel<C, P>, 256, 0) != hipSuccess) nb = 0;
+        occ.store(nb, std::memory_order_relaxed);
+        o = nb;
+    }
+    return o;
+}
+
+struct MergeOprojPlan {
+    bool ok = false;
+    uint32_t C = 0, P = 0, n_gemv = 0;
+};
+
+// The o-proj GEMV of merge_oproj_kernel: K = H * 128 as 16 lanes x {2, 4, 5} or 32 lanes
+// x {3, 4} slices per row, 4 waves of 2 passes per workgroup; the grid must fit at once.
+MergeOprojPlan merge_oproj_plan(uint32_t H, uint32_t N) {
+    MergeOprojPlan pl;
+    const uint32_t K = H * HD;
+    if (K % 512 == 0 && (K / 512 == 2 || K / 512 == 4 || K / 512 == 5)) { pl.C = K / 512; pl.P = 16; }
+    else if (K % 1024 == 0 && (K / 1024 == 3 || K / 1024 == 4)) { pl.C = K / 1024; pl.P = 32; }
+    else return pl;
+    const uint32_t rows_wg = 4u * (64u / pl.P) * 2u;
+    if (N < rows_wg || (uint64_t)N * (K / 2) >= (1ull << 32)) return pl;
+    pl.n_gemv = (N + rows_wg - 1) / rows_wg;
+    int occ = 0;
+    if (pl.P == 16) occ = pl.C == 2 ? merge_oproj_occupancy<2, 16>() : pl.C == 4 ? merge_oproj_occupancy<4, 16>()
+                                                                             : merge_oproj_occupancy<5, 16>();
+    else occ = pl.C == 3 ? merge_oproj_occupancy<3, 32>() : merge_oproj_occupancy<4, 32>();
+    if (occ <= 0 || (uint64_t)H + 1 + pl.n_gemv > (uint64_t)occ * (uint64_t)device_cu_count()) return pl;
+    pl.ok = true;
+    return pl;
+}
+
+}  // namespace
+
+bool merge_oproj_supported(uint32_t H, uint32_t N) { return merge_oproj_plan(H, N).ok; }
+
+hipError_t launch_attn_merge_deferred(uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH, uint32_t nslots,
+                                      float theta, float* work, hipStream_t st) {
+    if (!KVH || H % KVH || !nslots) return hipErrorInvalidValue;
+    const uint32_t max_chunks = (nslots + DC - 1) / DC;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(H + 1), dim3(256), 0, st, work + kWsHead, 0u, count_dev, 1, H / KVH,
+                       max_chunks, out, reinterpret_cast<uint32_t*>(work), theta, nullptr, 0u, 0u);
+    return hipGetLastError();
+}
+
+hipError_t launch_merge_oproj(uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH, uint32_t nslots,
+                              float theta, float* work, uint32_t work_floats, const uint8_t* wq, const __half* wsc,
+                              __half* y, uint32_t N, const __half* res, hipStream_t st) {
+    if (!KVH || H % KVH || !nslots || attn_qkv_fused_work_floats(nslots, H, KVH) > work_floats)
+        return hipErrorInvalidValue;
+    if (((uintptr_t)wq | (uintptr_t)work | (uintptr_t)out) % 16) return hipErrorInvalidValue;
+    const MergeOprojPlan pl = merge_oproj_plan(H, N);
+    if (!pl.ok) return hipErrorNotSupported;
+    MergeOprojArgs M;
+    M.part = work + kWsHead;
+    M.count = count_dev;
+    M.rep = H / KVH;
+    M.max_chunks = (nslots + DC - 1) / DC;
+    M.H = H;
+    M.out = out;
+    M.ws = reinterpret_cast<uint32_t*>(work);
+    M.theta = theta;
+    M.G = GemvRwArgs{out, wq, wsc, y, N, H * HD, nullptr, res, 0};
+    M.xrec = out_recs(work, nslots, H, KVH);
+    const dim3 grid(H + 1 + pl.n_gemv), blk(256);
+    if (pl.P == 16) {
+        if (pl.C == 2) hipLaunchKernelGGL((merge_oproj_kernel<2, 16>), grid, blk, 0, st, M);
+        else if (pl.C == 4) hipLaunchKernelGGL((merge_oproj_kernel<4, 16>), grid, blk, 0, st, M);
+        else hipLaunchKernelGGL((merge_oproj_kernel<5, 16>), grid, blk, 0, st, M);
+    } else {
+        if (pl.C == 3) hipLaunchKernelGGL((merge_oproj_kernel<3, 32>), grid, blk, 0, st, M);
+        else hipLaunchKernelGGL((merge_oproj_kernel<4, 32>), grid, blk, 0, st, M);
+    }
+    return hipGetLastError();
 }
 
 bool qkv_attn_decode_supported(uint32_t K, uint32_t H, uint32_t KVH, uint32_t nslots) {
@@ -1040,7 +1173,8 @@ hipError_t launch_qkv_attn_decode(const __half* x, const uint8_t* wq, const __ha
                                   uint32_t K, __half* qkv, const __half* q_gamma, const __half* k_gamma,
                                   float theta, uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
                                   uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH, float scale,
-                                  float* work, uint32_t work_floats, hipStream_t st, uint32_t n_kv_known) {
+                                  float* work, uint32_t work_floats, hipStream_t st, uint32_t n_kv_known,
+                                  bool defer_merge) {
     if (!KVH || H % KVH || !count_dev || !nslots || slot_bytes != KVH * HD * 4) return hipErrorInvalidValue;
     if (attn_qkv_fused_work_floats(nslots, H, KVH) > work_floats) return hipErrorInvalidValue;
     if (((uintptr_t)x | (uintptr_t)wq | (uintptr_t)gamma | (uintptr_t)work) % 16) return hipErrorInvalidValue;
@@ -1056,6 +1190,7 @@ hipError_t launch_qkv_attn_decode(const __half* x, const uint8_t* wq, const __ha
     QA.rec = reinterpret_cast<unsigned long long*>(work + qkv_rec_offset(nslots, H));
     QA.n_gemv = pl.n_gemv;
     qkv_attn_call(pl.rep, pl.C, pl.P, true, &QA, pl.grid, st);
+    if (defer_merge) return hipGetLastError();
     hipLaunchKernelGGL(attn_merge_kernel, dim3(H + 1), dim3(256), 0, st, QA.D.part, 0u, count_dev, 1, pl.rep,
                        pl.max_chunks, out, reinterpret_cast<uint32_t*>(work), theta, nullptr, 0u, 0u);
     return hipGetLastError();

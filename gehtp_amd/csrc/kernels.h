@@ -197,8 +197,20 @@ hipError_t launch_qkv_attn_decode(const __half* x, const uint8_t* wq, const __ha
                                   uint32_t K, __half* qkv, const __half* q_gamma, const __half* k_gamma,
                                   float theta, uint8_t* ring, uint32_t slot_bytes, uint32_t nslots,
                                   uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH, float scale,
-                                  float* work, uint32_t work_floats, hipStream_t st, uint32_t n_kv_known = 0);
+                                  float* work, uint32_t work_floats, hipStream_t st, uint32_t n_kv_known = 0,
+                                  bool defer_merge = false);
 uint32_t attn_qkv_fused_work_floats(uint32_t nslots, uint32_t H, uint32_t KVH);
+// After launch_qkv_attn_decode(defer_merge = true): its merge pass and the o-proj GEMV that
+// reads the attention output (OP_W4G_FUSED_F16, M = 1, K = H * 128, N rows, optional
+// residual res, no RMSNorm, no SwiGLU; y = its output) in one launch, the bits of the
+// merge pass followed by launch_w4g_gemv. hipErrorNotSupported (nothing launched) where
+// merge_oproj_supported is false; then launch_attn_merge_deferred runs the merge alone.
+bool merge_oproj_supported(uint32_t H, uint32_t N);
+hipError_t launch_merge_oproj(uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH, uint32_t nslots,
+                              float theta, float* work, uint32_t work_floats, const uint8_t* wq, const __half* wsc,
+                              __half* y, uint32_t N, const __half* res, hipStream_t st);
+hipError_t launch_attn_merge_deferred(uint32_t* count_dev, __half* out, uint32_t H, uint32_t KVH, uint32_t nslots,
+                                      float theta, float* work, hipStream_t st);
 // Whether launch_qkv_attn_decode takes this shape (16-byte aligned operands aside).
 bool qkv_attn_decode_supported(uint32_t K, uint32_t H, uint32_t KVH, uint32_t nslots);
 

@@ -158,6 +158,10 @@ uint64_t wt_exec_qkv_rope_fused(void);
  * output runs in one launch with that op's chunk pass (same bits; the GEMV's own output
  * is written too), where the shape allows; this counts such executions. */
 uint64_t wt_exec_qkv_attn_fused(void);
+/* Extension, same switch: after such a launch, the o-proj OP_W4G_FUSED_F16 GEMV that reads
+ * the attention output next (M = 1, no RMSNorm, no SwiGLU) runs in one launch with the
+ * attention op's merge pass (same bits); this counts such executions. */
+uint64_t wt_exec_merge_oproj_fused(void);
 
 /* W3 inspect report: one JSON line per call of emit (reference wt_w3.c). */
 void wt_w3_report(const char* blob_name, const uint8_t* buf, size_t size,

@@ -161,6 +161,73 @@ def test_engine_runs_decode_pair_in_one_launch(engine, torch_dev, H, KVH, K, nsl
         assert got[False][s][1] == got[True][s][1], f"step {s}: attention output differs"
 
 
+def _decode_block_blob(rng, H, KVH, K, nslots, res_kind):
+    """q|k|v GEMV -> ATTN_DECODE_QKV -> o-proj GEMV (res_kind: 'x' = the block input as the
+    residual, 'none'), then a second GEMV reading the o-proj output."""
+    hd = 128
+    N, kv, Ko = (H + 2 * KVH) * hd, KVH * hd, H * hd
+    _, wq, ws = w4g_weights(rng, N, K)
+    _, woq, wos = w4g_weights(rng, K, Ko)
+    bb = BlobBuilder()
+    st = bb.add_state(nslots * kv * 4)
+    xs = bb.add_input_slot(K * 2)
+    sq, ss = bb.add_slot(wq, count=N * K), bb.add_slot(ws)
+    soq, sos = bb.add_slot(woq, count=K * Ko), bb.add_slot(wos)
+    sg = bb.add_slot(rng.uniform(0.2, 0.3, K).astype(np.float16))
+    sqg = bb.add_slot(rng.uniform(0.8, 1.2, hd).astype(np.float16))
+    skg = bb.add_slot(rng.uniform(0.8, 1.2, hd).astype(np.float16))
+    t_qkv, t_a, t_o, t_y = bb.temp(), bb.temp(), bb.temp(), bb.temp()
+    bb.op(OP.W4G_FUSED_F16, bb.slot_ref(xs), bb.slot_ref(sq), bb.slot_ref(ss), t_qkv, 1, K, N, bb.slot_ref(sg),
+          WT_REF_NONE, 0, 2)
+    bb.op(OP.ATTN_DECODE_QKV_F16, t_qkv, st, t_a, H, KVH, hd, bb.slot_ref(sqg), bb.slot_ref(skg), f32_bits(1e6),
+          f32_bits(SCALE))
+    bb.op(OP.W4G_FUSED_F16, t_a, bb.slot_ref(soq), bb.slot_ref(sos), t_o, 1, Ko, K, WT_REF_NONE,
+          bb.slot_ref(xs) if res_kind == "x" else WT_REF_NONE, 0, 2)
+    bb.op(OP.W4G_FUSED_F16, t_o, bb.slot_ref(sq), bb.slot_ref(ss), t_y, 1, K, N, bb.slot_ref(sg), WT_REF_NONE, 0, 2)
+    return bb.build(), (t_qkv, t_a, t_o, t_y)
+
+
+@pytest.mark.parametrize("H,KVH,K,nslots,steps,res_kind", [(32, 8, 2560, 512, 67, "x"), (16, 8, 1024, 256, 9, "none"),
+                                                            (16, 8, 2048, 128, 4, "x")])
+def test_engine_runs_merge_with_oproj(engine, torch_dev, H, KVH, K, nslots, steps, res_kind):
+    """q|k|v GEMV -> ATTN_DECODE_QKV -> o-proj GEMV: with fusion on, the first launch runs
+    the GEMV and the chunk pass, the second the merge pass and the o-proj GEMV (x taken
+    from the merge workgroups' records; later steps replayed from a HIP graph). Every temp
+    bit-identical to the op-by-op runs over `steps` decode steps; a run that ends right
+    after the attention op (ops 0-1) still gets its merge pass; counters advance once
+    per fused step (step 1 runs ops 0-1 and 2-3 as two runs on the previous step's input)."""
+    rng = np.random.default_rng(H + K + steps + 7)
+    blob, temps = _decode_block_blob(rng, H, KVH, K, nslots, res_kind)
+    pb = engine.parse(blob)
+    xs = [(normal_f16(rng, 1, K) * np.float16(2)).astype(np.float16) for _ in range(steps)]
+    got = {}
+    for fusion in (False, True):
+        prev = engine.set_fusion(fusion)
+        try:
+            engine.state_reset()
+            n0, m0 = engine.qkv_attn_fused(), engine.merge_oproj_fused()
+            res = []
+            for s, x in enumerate(xs):
+                if s == 1:   # a run of the first two ops only (the last step's input), then the rest
+                    engine.run(pb, first=0, count=2)
+                    engine.run(pb, first=2, count=2)
+                else:
+                    engine.run_io(pb, x.tobytes(), temps[3])
+                res.append([engine.temp(t) for t in temps])
+            if fusion:
+                assert engine.qkv_attn_fused() - n0 == steps
+                assert engine.merge_oproj_fused() - m0 == steps - 1
+            else:
+                assert engine.qkv_attn_fused() == n0 and engine.merge_oproj_fused() == m0
+            got[fusion] = res
+        finally:
+            engine.set_fusion(prev)
+    names = ("qkv", "attention", "o-proj", "next GEMV")
+    for s in range(steps):
+        for name, a, b in zip(names, got[False][s], got[True][s]):
+            assert a == b, f"step {s}: {name} differs between the fused and the op-by-op run"
+
+
 def test_engine_decode_pair_error_keeps_its_index(engine, torch_dev):
     """A decode pair whose state is full (2 slots, third step) is not run in one launch:
     the GEMV runs alone and the attention op fails with its own 1-based index and the
