@@ -180,6 +180,8 @@ EXPORTS = {
     "gehtp_attn_decode_qkv": (_i, [_vp, _u32, _u32, _vp, _vp, C.c_float, C.c_float, _vp, _u32, _vp, _vp, _vp,
                                    _u32, _vp]),
     "gehtp_attn_qkv_fused_work_floats": (_u32, [_u32, _u32, _u32]),
+    "gehtp_qkv_attn_oproj_decode": (_i, [_vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, C.c_float, C.c_float,
+                                         _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _u32, _vp]),
     "gehtp_qkv_attn_decode": (_i, [_vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, C.c_float, C.c_float, _vp,
                                    _u32, _vp, _vp, _vp, _u32, _vp]),
     "gehtp_kv_append": (_i, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _vp]),

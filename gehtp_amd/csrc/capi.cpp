@@ -204,6 +204,30 @@ int gehtp_qkv_attn_decode(const void* x, const void* wq, const void* ws, const v
     return e == hipErrorNotSupported ? GEHTP_ENOTSUP : rc(e);
 }
 
+int gehtp_qkv_attn_oproj_decode(const void* x, const void* wq, const void* ws, const void* gamma, uint32_t K,
+                                void* qkv, uint32_t Hh, uint32_t KVH, const void* q_gamma, const void* k_gamma,
+                                float theta, float scale, void* ring, uint32_t state_bytes, void* count_dev,
+                                void* out, const void* wo_q, const void* wo_s, void* y, uint32_t N,
+                                const void* res, void* work, uint32_t work_floats, void* stream) {
+    const uint32_t slot_bytes = KVH * 128u * 4u;
+    if (!x || !wq || !ws || !qkv || !q_gamma || !k_gamma || !ring || !count_dev || !out || !wo_q || !wo_s || !y ||
+        !work || !KVH || Hh % KVH || !K || K % 64 || state_bytes % slot_bytes || !state_bytes || !al16(x) ||
+        !al16(wq) || !al16(wo_q) || (gamma && !al16(gamma)) || (reinterpret_cast<uintptr_t>(ws) & 1u) ||
+        (reinterpret_cast<uintptr_t>(wo_s) & 1u) || !al16(ring) || !al16(work) || !al16(out))
+        return GEHTP_EINVAL;
+    const uint32_t nslots = state_bytes / slot_bytes;
+    if (!qkv_attn_decode_supported(K, Hh, KVH, nslots) || !merge_oproj_supported(Hh, N)) return GEHTP_ENOTSUP;
+    hipError_t e = launch_qkv_attn_decode(H(x), static_cast<const uint8_t*>(wq), H(ws), H(gamma), K, Hm(qkv),
+                                          H(q_gamma), H(k_gamma), theta, static_cast<uint8_t*>(ring), slot_bytes,
+                                          nslots, static_cast<uint32_t*>(count_dev), Hm(out), Hh, KVH, scale,
+                                          static_cast<float*>(work), work_floats, S(stream), 0u, true);
+    if (e == hipSuccess)
+        e = launch_merge_oproj(static_cast<uint32_t*>(count_dev), Hm(out), Hh, KVH, nslots, theta,
+                               static_cast<float*>(work), work_floats, static_cast<const uint8_t*>(wo_q), H(wo_s),
+                               Hm(y), N, H(res), S(stream));
+    return e == hipErrorNotSupported ? GEHTP_ENOTSUP : rc(e);
+}
+
 int gehtp_attn_decode_noalloc(const void* q, const void* ring, uint32_t state_bytes, void* out, uint32_t n_kv,
                               uint32_t Hh, uint32_t KVH, uint32_t hd, float scale, void* stream) {
     const uint32_t slot_bytes = KVH * hd * 4u;

@@ -860,7 +860,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(
 // head each and, besides writing the attention output, publish it as tagged row-pair
 // records (tag: workspace word kWsSeqB + 1); workgroup H writes the RoPE records; the
 // GEMV workgroups behind them (gemv_rw_body, 4 waves, 2 passes) request their weights
-// at once and take x from those records. Waits go one way (GEMV on merge workgroups,
+// at once and take x from those records. (Dequantizing the weights while x is on its
+// way, with one pass per workgroup, was slower: 17.4 against 17.0 us for the 4B
+// q|k|v + attention + o-proj.) Waits go one way (GEMV on merge workgroups,
 // which never wait) and the host launches this only when the grid fits on the device
 // at once.
 struct MergeOprojArgs {

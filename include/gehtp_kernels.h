@@ -129,6 +129,18 @@ int gehtp_qkv_attn_decode(const void* x, const void* wq, const void* ws, const v
                           void* qkv, uint32_t H, uint32_t KVH, const void* q_gamma, const void* k_gamma,
                           float theta, float scale, void* ring, uint32_t state_bytes, void* count_dev,
                           void* out, void* work, uint32_t work_floats, void* stream);
+/* gehtp_qkv_attn_decode followed by the o-proj GEMV that reads its output (wo_q / wo_s:
+ * W4G weights of N rows of K = H*128; res: residual [N] or NULL; y: [N]), in two launches:
+ * the GEMV + chunk pass, then the merge pass + the o-proj GEMV. The bits of the three
+ * separate calls (out holds the attention output as well). GEHTP_ENOTSUP, launching
+ * nothing, for what either launch does not take. work: as gehtp_qkv_attn_decode. No
+ * counterpart in the reference: the engine performs its OP_W4G_FUSED_F16 ->
+ * OP_ATTN_DECODE_QKV_F16 -> OP_W4G_FUSED_F16 runs this way. */
+int gehtp_qkv_attn_oproj_decode(const void* x, const void* wq, const void* ws, const void* gamma, uint32_t K,
+                                void* qkv, uint32_t H, uint32_t KVH, const void* q_gamma, const void* k_gamma,
+                                float theta, float scale, void* ring, uint32_t state_bytes, void* count_dev,
+                                void* out, const void* wo_q, const void* wo_s, void* y, uint32_t N,
+                                const void* res, void* work, uint32_t work_floats, void* stream);
 /* Append n_tok tokens (k/v [n_tok, KVH*hd]) at positions pos..pos+n_tok-1 of the ring. */
 int gehtp_kv_append(void* ring, uint32_t state_bytes, const void* k, const void* v,
                     uint32_t kv_elems, uint32_t n_tok, uint32_t pos, void* stream);

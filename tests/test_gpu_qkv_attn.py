@@ -87,6 +87,57 @@ def test_qkv_attn_one_launch_matches_two_kernels(lib, oracle, torch_dev, H, KVH,
         assert head[2] == step + 1
 
 
+@pytest.mark.parametrize("H,KVH,K,nslots,pos0,with_res", [(32, 8, 2560, 4096, 2059, True),
+                                                          (16, 8, 1024, 256, 63, False),
+                                                          (8, 8, 2048, 128, 0, True)])
+def test_qkv_attn_oproj_two_launches_match_separate_calls(lib, torch_dev, H, KVH, K, nslots, pos0, with_res):
+    """gehtp_qkv_attn_oproj_decode (the q|k|v GEMV + chunk pass, then the merge pass + the
+    o-proj GEMV reading the attention output from the merge workgroups' records) against
+    gehtp_w4g_fused -> gehtp_attn_decode_qkv -> gehtp_w4g_fused over three steps: the
+    q|k|v row, the attention output, the o-proj output, the ring and the counter
+    bit-identical; no hand-off wait gave up."""
+    import torch
+    rng = np.random.default_rng(H * 11 + K + pos0)
+    hd = 128
+    N, kv_elems, Ko = (H + 2 * KVH) * hd, KVH * hd, H * hd
+    state_bytes = nslots * kv_elems * 4
+    _, wq, ws = w4g_weights(rng, N, K)
+    _, woq, wos = w4g_weights(rng, K, Ko)
+    wq_d, ws_d, woq_d, wos_d = (to_dev(a, torch_dev) for a in (wq, ws, woq, wos))
+    gam = to_dev(rng.uniform(0.2, 0.3, K).astype(np.float16), torch_dev)
+    qg = to_dev(rng.uniform(0.8, 1.2, hd).astype(np.float16), torch_dev)
+    kg = to_dev(rng.uniform(0.8, 1.2, hd).astype(np.float16), torch_dev)
+    ring_a = torch.from_numpy(normal_f16(rng, state_bytes // 2)).to(torch_dev)
+    ring_b = ring_a.clone()
+    count_a = torch.tensor([pos0], dtype=torch.int32, device=torch_dev)
+    count_b = count_a.clone()
+    wf = lib.gehtp_attn_qkv_fused_work_floats(nslots, H, KVH)
+    work_a = torch.zeros(wf, dtype=torch.float32, device=torch_dev)
+    work_b = torch.zeros(wf, dtype=torch.float32, device=torch_dev)
+    qkv_a, qkv_b = (torch.empty(N, dtype=torch.float16, device=torch_dev) for _ in range(2))
+    out_a, out_b = (torch.empty((H, hd), dtype=torch.float16, device=torch_dev) for _ in range(2))
+    y_a, y_b = (torch.empty(K, dtype=torch.float16, device=torch_dev) for _ in range(2))
+    for step in range(3):
+        x = to_dev((normal_f16(rng, 1, K) * np.float16(2)).astype(np.float16), torch_dev)
+        res = ptr(x) if with_res else None
+        assert lib.gehtp_w4g_fused(ptr(x), K, ptr(wq_d), ptr(ws_d), ptr(qkv_a), N, 1, N, K, ptr(gam), None, N, 0,
+                                   stream_ptr()) == 0
+        assert lib.gehtp_attn_decode_qkv(ptr(qkv_a), H, KVH, ptr(qg), ptr(kg), 1e6, SCALE, ptr(ring_a), state_bytes,
+                                         ptr(count_a), ptr(out_a), ptr(work_a), wf, stream_ptr()) == 0
+        assert lib.gehtp_w4g_fused(ptr(out_a), Ko, ptr(woq_d), ptr(wos_d), ptr(y_a), K, 1, K, Ko, None, res, K, 0,
+                                   stream_ptr()) == 0
+        rc = lib.gehtp_qkv_attn_oproj_decode(ptr(x), ptr(wq_d), ptr(ws_d), ptr(gam), K, ptr(qkv_b), H, KVH, ptr(qg),
+                                             ptr(kg), 1e6, SCALE, ptr(ring_b), state_bytes, ptr(count_b), ptr(out_b),
+                                             ptr(woq_d), ptr(wos_d), ptr(y_b), K, res, ptr(work_b), wf, stream_ptr())
+        assert rc == 0
+        _sync()
+        assert int(count_a.item()) == int(count_b.item()) == pos0 + step + 1
+        for name, a, b in (("q|k|v", qkv_a, qkv_b), ("attention", out_a, out_b), ("o-proj", y_a, y_b),
+                           ("ring", ring_a, ring_b)):
+            assert torch.equal(a, b), f"step {step}: {name} differs"
+        assert int(work_b[:4].cpu().view(torch.int32).numpy()[3]) == 0, "a hand-off wait gave up"
+
+
 def test_qkv_attn_one_launch_rejects_other_shapes(lib, torch_dev):
     """Shapes the one-launch form does not take return GEHTP_ENOTSUP and launch nothing
     (K = 1536 has no row-in-wave layout; a group of 3 query heads per kv head is not
