@@ -1109,7 +1109,17 @@ int op_w4g_fused(Ctx& cx) {
     if (g_merge_pending.op == cx.op) {   // left by the q|k|v GEMV two ops back
         const MergePending mp = g_merge_pending;
         g_merge_pending = MergePending{};
-        if (gemv_fits && M == 1 && a == mp.out && !gamma && !swiglu && ldy == N && ((uintptr_t)ws & 1u) == 0) {
+        // In that launch the merge workgroups store the attention output while the GEMV
+        // workgroups read the residual and store y: neither may share its bytes (a
+        // memory plan may place y over the attention output, dead after this op).
+        auto apart = [](const void* p, size_t np, const void* q, size_t nq) {
+            const uint8_t* a0 = static_cast<const uint8_t*>(p);
+            const uint8_t* b0 = static_cast<const uint8_t*>(q);
+            return a0 + np <= b0 || b0 + nq <= a0;
+        };
+        const size_t ob = (size_t)mp.H * 128u * 2u;
+        if (gemv_fits && M == 1 && a == mp.out && !gamma && !swiglu && ldy == N && ((uintptr_t)ws & 1u) == 0 &&
+            apart(y, (size_t)N * 2u, mp.out, ob) && (!res || apart(res, (size_t)N * 2u, mp.out, ob))) {
             CHECK_LAUNCH(launch_merge_oproj(mp.count, mp.out, mp.H, mp.KVH, mp.nslots, mp.theta, g.attn_work,
                                             g.attn_work_floats, wq, ws, y, N, res, g.stream));
             g.merge_oproj_fused++;

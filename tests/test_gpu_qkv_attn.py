@@ -212,9 +212,10 @@ def test_engine_runs_decode_pair_in_one_launch(engine, torch_dev, H, KVH, K, nsl
         assert got[False][s][1] == got[True][s][1], f"step {s}: attention output differs"
 
 
-def _decode_block_blob(rng, H, KVH, K, nslots, res_kind):
+def _decode_block_blob(rng, H, KVH, K, nslots, res_kind, plan_o_over_a=False):
     """q|k|v GEMV -> ATTN_DECODE_QKV -> o-proj GEMV (res_kind: 'x' = the block input as the
-    residual, 'none'), then a second GEMV reading the o-proj output."""
+    residual, 'none'), then a second GEMV reading the o-proj output. plan_o_over_a: a
+    TEMPOFF plan with the o-proj output at the attention output's offset."""
     hd = 128
     N, kv, Ko = (H + 2 * KVH) * hd, KVH * hd, H * hd
     _, wq, ws = w4g_weights(rng, N, K)
@@ -235,6 +236,14 @@ def _decode_block_blob(rng, H, KVH, K, nslots, res_kind):
     bb.op(OP.W4G_FUSED_F16, t_a, bb.slot_ref(soq), bb.slot_ref(sos), t_o, 1, Ko, K, WT_REF_NONE,
           bb.slot_ref(xs) if res_kind == "x" else WT_REF_NONE, 0, 2)
     bb.op(OP.W4G_FUSED_F16, t_o, bb.slot_ref(sq), bb.slot_ref(ss), t_y, 1, K, N, bb.slot_ref(sg), WT_REF_NONE, 0, 2)
+    if plan_o_over_a:
+        sizes = {t_qkv: N * 2, t_a: Ko * 2, t_o: K * 2, t_y: N * 2}
+        off, cap = {}, 0
+        for t in (t_qkv, t_a, t_y):
+            off[t] = cap
+            cap += (sizes[t] + 127) // 128 * 128
+        off[t_o] = off[t_a]
+        bb.set_tempoff(cap, [(t, off[t], sizes[t]) for t in sorted(sizes)])
     return bb.build(), (t_qkv, t_a, t_o, t_y)
 
 
@@ -277,6 +286,43 @@ def test_engine_runs_merge_with_oproj(engine, torch_dev, H, KVH, K, nslots, step
     for s in range(steps):
         for name, a, b in zip(names, got[False][s], got[True][s]):
             assert a == b, f"step {s}: {name} differs between the fused and the op-by-op run"
+
+
+def test_engine_merge_oproj_not_fused_when_output_overlaps(engine, torch_dev):
+    """A TEMPOFF plan that places the o-proj output over the attention output (dead after
+    the o-proj reads it; op by op that is legal): the merge pass may not share a launch
+    with that GEMV (its workgroups store the attention output while the GEMV's store y),
+    so the engine runs it alone; every temp equals the op-by-op run, the q|k|v GEMV +
+    chunk pass launch is still taken."""
+    rng = np.random.default_rng(41)
+    H, KVH, K, nslots, steps = 32, 8, 2560, 256, 3
+    blob_plain, temps = _decode_block_blob(rng, H, KVH, K, nslots, "x")
+    rng = np.random.default_rng(41)
+    bb_blob, temps2 = _decode_block_blob(rng, H, KVH, K, nslots, "x", plan_o_over_a=True)
+    assert temps == temps2
+    xs = [(normal_f16(rng, 1, K) * np.float16(2)).astype(np.float16) for _ in range(steps)]
+    got = {}
+    for name, blob, fusion in (("plain", blob_plain, False), ("aliased", bb_blob, True)):
+        prev = engine.set_fusion(fusion)
+        try:
+            engine.shutdown()
+            engine.state_reset()
+            pb = engine.parse(blob)
+            n0, m0 = engine.qkv_attn_fused(), engine.merge_oproj_fused()
+            res = []
+            for x in xs:
+                engine.run_io(pb, x.tobytes(), temps[3])
+                res.append([engine.temp(t) for t in (temps[0], temps[2], temps[3])])
+            if fusion:
+                assert engine.qkv_attn_fused() - n0 == steps
+                assert engine.merge_oproj_fused() == m0
+            got[name] = res
+            engine.shutdown()
+        finally:
+            engine.set_fusion(prev)
+    for s in range(steps):
+        for what, a, b in zip(("qkv", "o-proj", "next GEMV"), got["plain"][s], got["aliased"][s]):
+            assert a == b, f"step {s}: {what} differs"
 
 
 def test_engine_decode_pair_error_keeps_its_index(engine, torch_dev):
