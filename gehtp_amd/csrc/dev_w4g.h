@@ -82,9 +82,10 @@ __device__ __forceinline__ uint16_t silu_f16_expr(uint16_t hb) {
 // (and checks) its own.
 
 // Bound on the polls of one hand-off record: a wait that reaches it writes 1 to *err and
-// goes on (with whatever the record holds), so that every wave ends. ~1 us per poll, so
-// tens of ms.
+// goes on with two fp16 NaNs in place of the values (so the call's outputs show it), so
+// that every wave ends. ~1 us per poll, so tens of ms.
 constexpr uint32_t kHandoffSpins = 1u << 15;
+constexpr uint32_t kHandoffNaN2 = 0x7E007E00u;
 
 // The low 32 bits of record p once its high half carries tag: agent-scope atomic loads,
 // s_sleep(NAP) between them.
@@ -94,7 +95,7 @@ __device__ __forceinline__ uint32_t handoff_wait(const unsigned long long* p, ui
     for (uint32_t spin = 0; (uint32_t)(v >> 32) != tag; ++spin) {
         if (spin == kHandoffSpins) {
             *err = 1u;
-            break;
+            return kHandoffNaN2;
         }
         __builtin_amdgcn_s_sleep(NAP);
         v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
