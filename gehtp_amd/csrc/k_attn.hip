@@ -31,6 +31,9 @@ constexpr int KS = HD + 8;       // K tile row stride (halves)
 constexpr int VSR = HD + 32;     // V tile row stride (halves): 80 dwords, so the 4 rows x 64 bytes
                                  // that 32 lanes of a transposed read take hit 64 distinct banks
 constexpr float kLog2e = 1.4426950408889634f;
+// Buffer resource word 3 for raw dword loads on gfx9-family parts: data format 32
+// (bits 15..18 = 4); a raw load past the resource's byte count returns zeros.
+constexpr int kBufDword3 = 0x00020000;
 
 typedef short s4_t __attribute__((ext_vector_type(4)));
 
@@ -51,6 +54,9 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const _Float16* p) {
 // lane l^32. O^T = V^T P^T: the V^T operand comes from the row-major V tile through the
 // transposing LDS read, P^T straight from the score registers.
 //
+// The online softmax keeps a lazily moved reference max (see the stage code) and sums
+// the fp16 weights P.V consumes; K / V stage rows come in through buffer loads.
+//
 // Two halves of WPH waves split a tile's key stages: half p runs stages
 // [p*ns0, min(ns, (p+1)*ns0)) (ns0 = ceil(ns/2)) on its own LDS tiles, both halves in
 // lockstep (the shorter one idles through its last step), and half 1 hands its partial
@@ -70,7 +76,8 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
     __shared__ __align__(16) _Float16 kvbuf[(DB ? 2 : 1) * 2 * KV_HALF];   // [stage buffer][half]
     constexpr uint32_t QT = 32 * WPH, NT = 64 * WPH;   // queries per tile, threads per half
     constexpr int KR = KT * 16 / NT;                     // K / V rows per thread per stage
-    const uint32_t part = threadIdx.x / NT, tid = threadIdx.x % NT, lane = tid & 63, wave = tid >> 6;
+    const uint32_t part = __builtin_amdgcn_readfirstlane(threadIdx.x / NT), tid = threadIdx.x % NT, lane = tid & 63,
+                   wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     _Float16* const Ks0 = kvbuf + part * KV_HALF;   // stage buffer b at + 2 * b * KV_HALF
     const uint32_t n_qt = (S + QT - 1) / QT;
     const uint32_t qtile = n_qt - 1 - blockIdx.y;      // heaviest causal tiles first
@@ -99,17 +106,28 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
     float m_run = -INFINITY, l_run = 0.0f;
 
     const uint32_t kend = CAUSAL ? min(S, q0 + QT) : S;
-    // K and V rows of this thread's KR keys (stage-local key (tid>>4) + (NT/16)i, dims 8*ch..).
-    // Loads are unconditional (keys past S read row S-1; their scores are masked).
+    // K and V rows of this thread's KR keys (stage-local key (tid>>4) + (NT/16)i, dims 8*ch..),
+    // read as buffer loads whose resource spans the stage's rows below S: rows past S
+    // read as zeros (their scores are masked), and the per-thread byte offsets are fixed,
+    // so a stage's addresses cost scalar instructions only (kb < S, and the resource's
+    // byte count, at most KT rows, fits 32 bits for any row pitch below 2^25 halves).
     const uint32_t ch = tid & 15;
     u32x4 kv4[KR], vv4[KR];
+    const __half* const kh = k + (size_t)kvh * kvhs;
+    const __half* const vh = v + (size_t)kvh * kvhs;
+    uint32_t voff[KR];
+#pragma unroll
+    for (int i = 0; i < KR; ++i) voff[i] = (((tid >> 4) + (NT / 16) * i) * ldkv + ch * 8) * 2;
     auto load_kv = [&](uint32_t kb) {
+        const uint32_t nrec = min(S - kb, (uint32_t)KT) * ldkv * 2;
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(kh + (size_t)kb * ldkv), 0, nrec, kBufDword3);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(vh + (size_t)kb * ldkv), 0, nrec, kBufDword3);
 #pragma unroll
         for (int i = 0; i < KR; ++i) {
-            const uint32_t key = min(kb + (tid >> 4) + (NT / 16) * i, S - 1);
-            const size_t off = (size_t)key * ldkv + (size_t)kvh * kvhs + ch * 8;
-            kv4[i] = *reinterpret_cast<const u32x4*>(k + off);
-            vv4[i] = *reinterpret_cast<const u32x4*>(v + off);
+            kv4[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, voff[i], 0, 0));
+            vv4[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff[i], 0, 0));
         }
     };
     // This lane's address pattern for the transposed V reads (see lds_read_tr16): source
@@ -143,52 +161,107 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
         f16x_t s0, s1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) { s0[r] = 0.0f; s1[r] = 0.0f; }
+        // K fragments are requested two MFMA pairs ahead (the group barriers below hold
+        // the scheduler to that order).
+        h8_t kf0[HD / 16], kf1[HD / 16];
+        auto kread = [&](int kk) __attribute__((always_inline)) {
+            kf0[kk] = *reinterpret_cast<const h8_t*>(&Ks[(lane & 31) * KS + kk * 16 + hl * 8]);
+            kf1[kk] = *reinterpret_cast<const h8_t*>(&Ks[(32 + (lane & 31)) * KS + kk * 16 + hl * 8]);
+        };
+        kread(0);
+        kread(1);
 #pragma unroll
         for (int kk = 0; kk < HD / 16; ++kk) {
-            const h8_t kf0 = *reinterpret_cast<const h8_t*>(&Ks[(lane & 31) * KS + kk * 16 + hl * 8]);
-            const h8_t kf1 = *reinterpret_cast<const h8_t*>(&Ks[(32 + (lane & 31)) * KS + kk * 16 + hl * 8]);
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf0, qf[kk], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf1, qf[kk], s1, 0, 0, 0);
+            if (kk + 2 < HD / 16) kread(kk + 2);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf0[kk], qf[kk], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf1[kk], qf[kk], s1, 0, 0, 0);
         }
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         // s0[r] / s1[r]: key kb (+32) + 8*(r/4) + 4*hl + r%4, query my_q. Scores stay raw
         // (the launcher guarantees scale > 0, so max commutes with the scaling); a stage
         // wholly below the diagonal and inside S skips the mask (a wave-uniform test).
+        // The first P.V group's V^T operands are requested before the softmax runs.
+        u32x4 vpre[HD / 32];
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt) {
+            const _Float16* base = &Vs[tr_row * VSR + 32 * dt + tr_col];
+            const u32x2 lo = lds_read_tr16(base);
+            const u32x2 hi = lds_read_tr16(base + 8 * VSR);
+            vpre[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
         const bool full = kb + KT <= S && (!CAUSAL || kb + KT - 1 <= qw);
         // (scores are finite or -inf: the max is three-input v_max3 without NaN quieting)
         float mloc = -INFINITY;
-        if (!full) {
+        if (!full) {   // key kb + 4*hl + c is valid iff c <= lim
+            const int lim = (int)(CAUSAL ? min(my_q, S - 1) : S - 1) - (int)(kb + 4 * hl);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t key = kb + 8 * (r >> 2) + 4 * hl + (r & 3);
-                if (key >= S || (CAUSAL && key > my_q)) s0[r] = -INFINITY;
-                if (key + 32 >= S || (CAUSAL && key + 32 > my_q)) s1[r] = -INFINITY;
+                const int c = 8 * (r >> 2) + (r & 3);
+                if (c > lim) s0[r] = -INFINITY;
+                if (c + 32 > lim) s1[r] = -INFINITY;
             }
         }
+        {   // a max3 tree over the 32 scores (depth 4 instead of a 16-long chain)
+            float t1[12];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mloc = dev::max3_nonan(mloc, s0[r], s1[r]);
+            for (int i = 0; i < 10; ++i) {
+                const int a = 3 * i, b = 3 * i + 1, c = 3 * i + 2;
+                t1[i] = dev::max3_nonan(a < 16 ? s0[a] : s1[a - 16], b < 16 ? s0[b] : s1[b - 16], c < 16 ? s0[c] : s1[c - 16]);
+            }
+            t1[10] = s1[14];
+            t1[11] = s1[15];
+            const float u0 = dev::max3_nonan(t1[0], t1[1], t1[2]), u1 = dev::max3_nonan(t1[3], t1[4], t1[5]);
+            const float u2 = dev::max3_nonan(t1[6], t1[7], t1[8]), u3 = dev::max3_nonan(t1[9], t1[10], t1[11]);
+            mloc = dev::max3_nonan(dev::max3_nonan(u0, u1, u2), u3, mloc);
+        }
         {   // the other half of this query's keys sits in lane l ^ 32
             uint32_t x0 = __builtin_bit_cast(uint32_t, mloc), x1 = x0;
             dev::permlane32_swap(x0, x1);
             mloc = fmaxf(__builtin_bit_cast(float, x0), __builtin_bit_cast(float, x1));
         }
-        const float m_new = fmaxf(m_run, mloc);
+        const float m_top = fmaxf(m_run, mloc);
+        // Lazy rescaling: the reference max m_run moves only when this stage's max exceeds
+        // it by more than 8 in log2 units, so P stays below 2^8 (fp16 holds it) and O is
+        // rescaled in a few stages instead of almost every one. (m_top - m_run is NaN when
+        // both are -inf: no move.) The sum and O share the reference, so it cancels in O / l.
+        const bool grow = (m_top - m_run) * scale_log2 > 8.0f;
+        const float m_new = grow ? m_top : m_run;
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
         const float neg_ms = -m_use * scale_log2;
         // v_exp_f32 directly: results below 2^-126 flush to 0, which a softmax weight can
         // afford. p = 2^((s - m) * scale_log2) with the scaling folded into one fma.
-        const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, scale_log2, neg_ms));
-        float lsum = 0.0f;
+        const float alpha = grow ? __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, scale_log2, neg_ms)) : 1.0f;
         // P^T operand j (keys 16j .. 16j+15 of the stage): k-slot i of lane-half hl holds
         // key 16j + 8*(i/4) + 4*hl + i%4, i.e. score register 8*(j%2) + i of s0 / s1.
+        // The row sum adds the fp16 weights that P.V uses, two per v_dot2_f32_f16.
+        typedef _Float16 h2v_t __attribute__((ext_vector_type(2)));
+        typedef float f2v_t __attribute__((ext_vector_type(2)));
+        const h2v_t ones = {(_Float16)1.0f, (_Float16)1.0f};
         h8_t pb[4];
+        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale_log2, neg_ms));
-            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], scale_log2, neg_ms));
-            lsum += p0 + p1;
-            pb[r >> 3][r & 7] = (_Float16)p0;
-            pb[2 + (r >> 3)][r & 7] = (_Float16)p1;
+        for (int j = 0; j < 4; ++j) {
+            u32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 8 * (j & 1) + 2 * e;
+                const float a = j < 2 ? s0[r] : s1[r], b = j < 2 ? s0[r + 1] : s1[r + 1];
+                const f2v_t f = {__builtin_amdgcn_exp2f(__builtin_fmaf(a, scale_log2, neg_ms)),
+                                 __builtin_amdgcn_exp2f(__builtin_fmaf(b, scale_log2, neg_ms))};
+                const h2v_t hp = __builtin_convertvector(f, h2v_t);
+                ls[j] = __builtin_amdgcn_fdot2(hp, ones, ls[j], false);
+                w[e] = __builtin_bit_cast(uint32_t, hp);
+            }
+            pb[j] = __builtin_bit_cast(h8_t, w);
         }
+        float lsum = (ls[0] + ls[1]) + (ls[2] + ls[3]);
         {
             uint32_t x0 = __builtin_bit_cast(uint32_t, lsum), x1 = x0;
             dev::permlane32_swap(x0, x1);
@@ -196,7 +269,7 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
         }
         l_run = l_run * alpha + lsum;
         m_run = m_new;
-        if (__any(alpha != 1.0f)) {   // no lane's max grew: nothing to rescale
+        if (__any(grow)) {
 #pragma unroll
             for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
@@ -209,9 +282,14 @@ __global__ __launch_bounds__(128 * WPH) void attn_prefill_kernel(
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const _Float16* base = &Vs[(16 * j + tr_row) * VSR + 32 * dt + tr_col];
-                const u32x2 lo = lds_read_tr16(base);
-                const u32x2 hi = lds_read_tr16(base + 8 * VSR);
-                const u32x4 packed = {lo[0], lo[1], hi[0], hi[1]};
+                u32x4 packed;
+                if (j == 0) {
+                    packed = vpre[dt];
+                } else {
+                    const u32x2 lo = lds_read_tr16(base);
+                    const u32x2 hi = lds_read_tr16(base + 8 * VSR);
+                    packed = u32x4{lo[0], lo[1], hi[0], hi[1]};
+                }
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, packed), pb[j], o[dt], 0, 0, 0);
             }
         }
