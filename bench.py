@@ -59,7 +59,8 @@ def parse_args():
                     help="the four 4B prefill GEMM shapes (M = 2048) with random and with constant operands: "
                          "this build's W4A16 GEMM and torch's fp16 GEMM side by side; prints one JSON line")
     ap.add_argument("--only", default=None,
-                    help="with --kernel-configs: comma-separated subset of c1,c2,c3p,c3d,c4")
+                    help="with --kernel-configs: comma-separated subset of c1,c2,c3p,c3d,c4, or a4b (the 4B "
+                         "model's causal prefill attention, S 2048, 32 Q / 8 KV heads; not in the default set)")
     return ap.parse_args()
 
 
@@ -462,6 +463,8 @@ def kernel_configs(args) -> int:
           = 4.30 G
       c3d decode over 4096 keys of the ring, 16 Q / 8 KV heads: bytes K + V =
           4096*8*128*2*2 = 16,777,216 (the 4 KB query and output aside)
+      a4b (only when asked for) the 4B model's causal prefill, S=2048, 32 Q / 8 KV heads:
+          flops 34.4 G
     and config 4 end to end through the runlist engine (not a single kernel): one
     0.8B-class layer with its fp16 lm_head, a 512-token prefill (prompt embeddings
     resident in HBM) then 128 greedy decode steps chained on the device
@@ -574,6 +577,29 @@ def kernel_configs(args) -> int:
                                       "resident_tflops": round(flops / t_res / 1e12, 1)}
         log(f"c3 prefill: rotated {t_rot * 1e6:.2f} us ({flops / t_rot / 1e12:.0f} TFLOPS), "
             f"resident {t_res * 1e6:.2f} us")
+        del qq, kk, vv, oo
+
+    if "a4b" in only:   # opt-in: the 4B model's prefill attention shape, N(0, 1) inputs
+        S, H, KVH, copies = 2048, 32, 8, 8     # 8 x (16 + 4 + 4 + 16) MB = 320 MB
+        qq = torch.randn((copies, S, H, HD_ATTN), device=dev, generator=gen).half()
+        kk = torch.randn((copies, S, KVH, HD_ATTN), device=dev, generator=gen).half()
+        vv = torch.randn((copies, S, KVH, HD_ATTN), device=dev, generator=gen).half()
+        oo = torch.empty((copies, S, H, HD_ATTN), dtype=torch.float16, device=dev)
+        scale = float(np.float16(1.0 / np.sqrt(HD_ATTN)))
+        flops = 4.0 * H * HD_ATTN * S * (S + 1) / 2
+
+        def a4b(i):
+            assert lib.gehtp_attn_prefill(qq[i].data_ptr(), kk[i].data_ptr(), vv[i].data_ptr(), oo[i].data_ptr(), S,
+                                          H, KVH, HD_ATTN, scale, 1, sp) == 0
+        t_rot = timed(a4b, copies, 10)
+        t_res = timed(lambda i: a4b(0), 32, 5)
+        results["attn_prefill_4b"] = {"kernel": "attn_prefill_kernel<true, 4>", "S": S, "H": H, "KVH": KVH,
+                                      "flops": flops, "copies": copies, "rotated_us": round(t_rot * 1e6, 3),
+                                      "rotated_tflops": round(flops / t_rot / 1e12, 1),
+                                      "resident_us": round(t_res * 1e6, 3),
+                                      "resident_tflops": round(flops / t_res / 1e12, 1)}
+        log(f"4B prefill attention: rotated {t_rot * 1e6:.2f} us ({flops / t_rot / 1e12:.0f} TFLOPS), "
+            f"resident {t_res * 1e6:.2f} us ({flops / t_res / 1e12:.0f} TFLOPS)")
         del qq, kk, vv, oo
 
     if "c3d" in only:
