@@ -351,6 +351,28 @@ def test_attn_prefill(lib, oracle, torch_dev, S, H, KVH, causal):
             assert np.array_equal(got[0, h], v[0, h // rep])
 
 
+@pytest.mark.parametrize("ramp", [0.0, 4.0])
+def test_attn_prefill_wide_ragged(lib, oracle, torch_dev, ramp):
+    """The 128-query tiles (32 heads x 8 tiles cover the 256 CUs) at S = 1000: the last key
+    stage holds 40 keys, read as zero rows past S by the kernel's buffer loads and masked.
+    With ramp > 0 the keys are scaled by 1 + ramp * j / S, so later stages hold larger
+    scores: at ramp 4 the lazily kept reference max of about one row half in fourteen
+    moves after its first stage (the scores of a later stage exceed it by more than 8 in
+    log2 units), so O is rescaled mid-row there."""
+    import torch
+    rng = np.random.default_rng(77 + int(ramp * 10))
+    S, H, KVH, hd = 1000, 32, 8, 128
+    q, k, v = normal_f16(rng, S, H, hd), normal_f16(rng, S, KVH, hd), normal_f16(rng, S, KVH, hd)
+    if ramp:
+        k = (k.astype(np.float32) * (1.0 + ramp * np.arange(S, dtype=np.float32) / S)[:, None, None]).astype(np.float16)
+    out = torch.empty((S, H, hd), dtype=torch.float16, device=torch_dev)
+    assert lib.gehtp_attn_prefill(ptr(to_dev(q, torch_dev)), ptr(to_dev(k, torch_dev)), ptr(to_dev(v, torch_dev)),
+                                  ptr(out), S, H, KVH, hd, SCALE, 1, stream_ptr()) == 0
+    _sync()
+    assert_close(from_dev(out), oracle.attn_prefill(q, k, v, SCALE, True, threads=8),
+                 what=f"attn S={S} ramp={ramp}")
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_attn_prefill_tile_sizes(lib, oracle, torch_dev, causal):
     """The prefill runs 128-query tiles when heads x tiles cover the CUs (256 on MI355X),
