@@ -983,6 +983,7 @@ hipError_t launch_attn_prefill_hs(const __half* q, uint32_t ldq, uint32_t qhs, c
                                   uint32_t H, uint32_t KVH, uint32_t hd, float scale, bool causal, hipStream_t st) {
     if (hd != HD || !KVH || H % KVH) return hipErrorInvalidValue;
     if (!(scale > 0.0f && scale < INFINITY)) return hipErrorInvalidValue;   // the kernel's max needs scale > 0
+    if ((uint64_t)ldkv * 2u * KT > 0xFFFFFFFFull) return hipErrorInvalidValue;   // a stage's K / V bytes: 32-bit offsets
     if (!S || !H) return hipSuccess;
     // 128-query tiles (8-wave workgroups) while they give every CU one; else 64-query
     // tiles (4-wave workgroups) while those do; else 32-query tiles (2-wave workgroups).
