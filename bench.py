@@ -277,10 +277,11 @@ def main() -> int:
 
 
 def gemv_roofline(cfg, w, lib, reps):
-    """Roofline of the dominant decode kernel: the fused W4A16 GEMV exactly as one decode
-    token runs it (per layer: norm+qkv, o+residual, norm+gate/up+SwiGLU, down+residual;
-    the model's own weights), replayed back to back on torch's stream and timed with HIP
-    events on that stream. Returns (mean seconds per launch, mean algorithmic bytes per
+    """Roofline of the dominant decode kernel: the fused W4A16 GEMVs of one decode token
+    (per layer: norm+qkv, o+residual, norm+gate/up+SwiGLU, down+residual; the model's own
+    weights) as standalone launches (in the decode step itself the q|k|v and o-proj GEMVs
+    share their launches with the attention's chunk and merge passes), replayed back to
+    back on torch's stream and timed with HIP events on that stream. Returns (mean seconds per launch, mean algorithmic bytes per
     launch, GB/s). Algorithmic bytes: int4 weights + fp16 scales + activation in + out
     (+ gamma, + residual read)."""
     import torch
